@@ -1,0 +1,987 @@
+// defer_gpu.hip -- gfx950 implementation of the C ABI in include/defer_gpu.h.
+//
+// Three launch modes share the phase functions of phases.h:
+//   persistent: one cooperative kernel (one workgroup per CU) runs every op
+//               of a call; workgroups hand activations to each other through
+//               tagged mailboxes, so there is no grid barrier at all.
+//   graph:      one hipGraph per op (sampler, 6 phases x L, lm_head, commit),
+//               captured once per cache and replayed per token.
+//   eager:      the same kernels launched one by one.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+#include <vector>
+
+#include "../../include/defer_gpu.h"
+#include "phases.h"
+
+using namespace dg;
+
+// ------------------------------------------------------------------ errors
+
+static thread_local std::string g_last_error;
+
+static int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+#define HIP_TRY(expr)                                                                      \
+  do {                                                                                     \
+    hipError_t e_ = (expr);                                                                \
+    if (e_ != hipSuccess)                                                                  \
+      return fail(DEFER_GPU_E_HIP, "%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_), \
+                  __FILE__, __LINE__);                                                     \
+  } while (0)
+
+extern "C" const char* defer_gpu_last_error(void) { return g_last_error.c_str(); }
+
+// ------------------------------------------------------------------ kernels
+
+__device__ __forceinline__ Lds lds_init(const Dims& d) {
+  extern __shared__ float lds_raw[];
+  Lds s = lds_layout(lds_raw, d);
+  if (threadIdx.x == 0) s.ctl->abort_seen = 0;
+  __syncthreads();
+  return s;
+}
+
+__device__ bool forward_all(const Args& a, uint32_t tok, uint32_t pos, uint32_t tick, uint32_t wg,
+                            uint32_t G, const Lds& s) {
+  for (uint32_t l = 0; l < a.d.L; ++l) {
+    if (!phase_qkv(a, l, tick, pos, tok, wg, G, s)) return false;
+    if (!phase_attn(a, l, tick, pos, wg, G, s)) return false;
+    if (!phase_comb(a, l, tick, pos, wg, G, s)) return false;
+    if (!phase_o(a, l, tick, pos, tok, wg, G, s)) return false;
+    if (!phase_gu(a, l, tick, wg, G, s)) return false;
+    if (!phase_d(a, l, tick, wg, G, s)) return false;
+  }
+  return phase_lm(a, tick, wg, G, s);
+}
+
+__device__ __forceinline__ bool is_stop(const RunDesc& r, uint32_t tok) {
+  for (uint32_t k = 0; k < r.n_stop; ++k)
+    if (r.stop[k] == tok) return true;
+  return false;
+}
+
+// Every op of a run in one launch. All workgroups sample redundantly (same
+// inputs, same code, same token), so no broadcast is needed.
+__global__ __launch_bounds__(BLOCK) void k_persistent(Args a, const RunDesc* run) {
+  const Lds s = lds_init(a.d);
+  const RunDesc r = *run;
+  DevState* st = a.st;
+  uint32_t pos = st->pos, tick = st->tick;
+  const uint32_t wg = blockIdx.x, G = gridDim.x;
+  uint32_t i = 0;
+  uint32_t halted = 0;
+  for (; i < r.n_ops; ++i) {
+    uint32_t tok;
+    if (i >= r.sample_from) {
+      const uint32_t word = r.temperature != 0.0f ? r.words[i - r.sample_from] : 0u;
+      if (r.temperature != 0.0f && !sample_stage_a(a, tick, r.temperature, wg, G, s)) break;
+      if (!sample_stage_b(a, tick, r.temperature, word, s, &tok)) break;
+      if (r.mode == RUN_REPLAY) {
+        if (tok != r.tokens[i]) {
+          if (wg == 0 && threadIdx.x == 0) {
+            st->first_div = (long long)i;
+            st->sampled_div = tok;
+          }
+          halted = 1;
+          break;
+        }
+        tok = r.tokens[i];
+      } else if (wg == 0 && threadIdx.x == 0) {
+        r.out_tokens[i] = tok;
+      }
+    } else {
+      tok = r.tokens[i];
+    }
+    if (!forward_all(a, tok, pos, tick, wg, G, s)) break;
+    ++pos;
+    ++tick;
+    if (r.mode == RUN_GENERATE && is_stop(r, tok)) {
+      ++i;
+      halted = 1;
+      break;
+    }
+  }
+  if (wg == 0 && threadIdx.x == 0) {
+    st->pos = pos;
+    st->tick = tick;
+    st->n_done = i;
+    st->halt = halted;
+  }
+}
+
+// Per-run reset of the counters (pos / tick / token are kept).
+__global__ void k_begin(DevState* st) {
+  st->abort = 0;
+  st->halt = 0;
+  st->n_done = 0;
+  st->op = 0;
+  st->first_div = -1;
+  st->sampled_div = 0;
+}
+
+enum : uint32_t { PH_LM_KERNEL = 100 };
+
+__global__ __launch_bounds__(BLOCK) void k_phase(Args a, uint32_t ph, uint32_t layer) {
+  const Lds s = lds_init(a.d);
+  const DevState* st = a.st;
+  if (st->halt) return;
+  const uint32_t pos = st->pos, tick = st->tick, token = st->token;
+  const uint32_t wg = blockIdx.x, G = gridDim.x;
+  switch (ph) {
+    case PH_QKV: phase_qkv(a, layer, tick, pos, token, wg, G, s); break;
+    case PH_ATTN: phase_attn(a, layer, tick, pos, wg, G, s); break;
+    case PH_COMB: phase_comb(a, layer, tick, pos, wg, G, s); break;
+    case PH_O: phase_o(a, layer, tick, pos, token, wg, G, s); break;
+    case PH_GU: phase_gu(a, layer, tick, wg, G, s); break;
+    case PH_D: phase_d(a, layer, tick, wg, G, s); break;
+    case PH_LM_KERNEL: phase_lm(a, tick, wg, G, s); break;
+    default: break;
+  }
+}
+
+// Sampler stage A for the op in flight (no-op when it does not sample).
+__global__ __launch_bounds__(BLOCK) void k_samp_a(Args a, const RunDesc* run) {
+  const Lds s = lds_init(a.d);
+  const DevState* st = a.st;
+  if (st->halt) return;
+  const uint32_t i = st->op;
+  if (i < run->sample_from || run->temperature == 0.0f) return;
+  sample_stage_a(a, st->tick, run->temperature, blockIdx.x, gridDim.x, s);
+}
+
+// One workgroup: sampler stage B (if the op samples) and the token to feed.
+__global__ __launch_bounds__(BLOCK) void k_op(Args a, const RunDesc* run) {
+  const Lds s = lds_init(a.d);
+  DevState* st = a.st;
+  if (st->halt) return;
+  const RunDesc& r = *run;
+  const uint32_t i = st->op;
+  uint32_t tok;
+  if (i >= r.sample_from) {
+    const uint32_t word = r.temperature != 0.0f ? r.words[i - r.sample_from] : 0u;
+    if (!sample_stage_b(a, st->tick, r.temperature, word, s, &tok)) return;
+    if (r.mode == RUN_REPLAY) {
+      if (tok != r.tokens[i]) {
+        __syncthreads();
+        if (threadIdx.x == 0) {
+          st->first_div = (long long)i;
+          st->sampled_div = tok;
+          st->halt = 1;
+        }
+        return;
+      }
+      tok = r.tokens[i];
+    } else if (threadIdx.x == 0) {
+      r.out_tokens[i] = tok;
+    }
+  } else {
+    tok = r.tokens[i];
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) st->token = tok;
+}
+
+__global__ void k_commit(Args a, const RunDesc* run) {
+  DevState* st = a.st;
+  if (st->halt) return;
+  st->pos += 1;
+  st->tick += 1;
+  st->op += 1;
+  st->n_done += 1;
+  if (run->mode == RUN_GENERATE && is_stop(*run, st->token)) st->halt = 1;
+}
+
+// Strip the tags of logits (or any tagged vector) into plain floats.
+__global__ void k_untag(const u64* src, float* dst, uint32_t n) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = __uint_as_float((uint32_t)src[i]);
+}
+
+// Head-major cache rows -> the reference's [len, kv_dim] layout.
+__global__ void k_kv_gather(const float* src, float* dst, uint32_t len, uint32_t nkv, uint32_t hd,
+                            uint32_t cap, uint32_t kvs) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t kvd = nkv * hd;
+  if (i >= len * kvd) return;
+  const uint32_t t = i / kvd, r = i - t * kvd, g = r / hd, dd = r - g * hd;
+  dst[i] = src[((size_t)g * cap + t) * kvs + dd];
+}
+
+// ------------------------------------------------------------------ host side
+
+struct defer_gpu_model {
+  defer_gpu_config cfg;
+  Dims d;
+  int device = 0;
+  uint32_t G = 0;  // workgroups per phase (= CUs, capped by the smallest phase)
+  size_t lds_bytes = 0;
+  hipStream_t stream = nullptr;
+  float* wbuf = nullptr;
+  LayerW* d_layers = nullptr;
+  std::vector<LayerW> layers;
+  const float* embed = nullptr;
+  const float* norm = nullptr;
+  const float* head = nullptr;
+  float2* rope = nullptr;
+  uint32_t exec_mode = DEFER_GPU_EXEC_PERSISTENT;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  double last_ms = 0.0;
+};
+
+struct defer_gpu_cache {
+  const defer_gpu_model* m = nullptr;
+  uint32_t cap = 0;
+  float* kc = nullptr;
+  float* vc = nullptr;
+  u64* mb = nullptr;
+  size_t mb_words = 0;
+  DevState* st = nullptr;
+  RunDesc* d_run = nullptr;
+  uint32_t* d_mask = nullptr;
+  uint32_t* d_tokens = nullptr;
+  uint32_t* d_words = nullptr;
+  uint32_t* d_stop = nullptr;
+  uint32_t* d_out = nullptr;
+  size_t run_cap = 0;   // capacity of d_tokens / d_words / d_out
+  size_t stop_cap = 0;
+  float* d_logits = nullptr;
+  float* d_tmp = nullptr;  // kv gather staging
+  uint32_t pos = 0;        // host mirror of st->pos
+  uint32_t tick = 0;
+  bool has_logits = false;
+  hipGraphExec_t graph = nullptr;
+  Args args;
+};
+
+static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+extern "C" size_t defer_gpu_model_tensor_count(const defer_gpu_config* c) {
+  const size_t per_layer = c->has_bias ? 12 : 9;
+  return 1 + (size_t)c->num_layers * per_layer + 1 + (c->tie_word_embeddings ? 0 : 1);
+}
+
+static int validate(const defer_gpu_config* c) {
+  if (!c) return fail(DEFER_GPU_E_INVALID, "null config");
+  if (!c->vocab_size || !c->hidden_size || !c->intermediate_size || !c->num_layers ||
+      !c->num_heads || !c->head_dim || !c->max_seq_len)
+    return fail(DEFER_GPU_E_INVALID, "config has a zero size");
+  if (c->num_kv_heads == 0 || c->num_heads % c->num_kv_heads != 0)
+    return fail(DEFER_GPU_E_INVALID,
+                "num_attention_heads must be a multiple of num_key_value_heads");
+  if (c->head_dim % 2 != 0) return fail(DEFER_GPU_E_INVALID, "head_dim must be even for RoPE");
+  const uint32_t hd = c->head_dim;
+  if (hd % 4 != 0 || 64 % (hd / 4) != 0)
+    return fail(DEFER_GPU_E_INVALID, "head_dim %u unsupported (need 4*2^k, at most 256)", hd);
+  if (c->num_heads / c->num_kv_heads > MAX_GROUP)
+    return fail(DEFER_GPU_E_INVALID, "GQA group larger than %u", MAX_GROUP);
+  if (c->hidden_size % 4 || c->intermediate_size % 4)
+    return fail(DEFER_GPU_E_INVALID, "hidden and intermediate sizes must be multiples of 4");
+  const uint64_t q = (uint64_t)c->num_heads * hd;
+  const uint64_t mx = std::max<uint64_t>({c->hidden_size, q, c->intermediate_size});
+  if (mx > 32ull * BLOCK) return fail(DEFER_GPU_E_INVALID, "vector length %llu too large",
+                                      (unsigned long long)mx);
+  if (c->activation > 1) return fail(DEFER_GPU_E_INVALID, "unsupported activation");
+  return DEFER_GPU_OK;
+}
+
+extern "C" int defer_gpu_model_create(const defer_gpu_config* cfg, const float* const* tensors,
+                                      size_t n_tensors, uint32_t flags, defer_gpu_model** out) {
+  if (!out) return fail(DEFER_GPU_E_INVALID, "null output handle");
+  *out = nullptr;
+  int rc = validate(cfg);
+  if (rc) return rc;
+  (void)flags;
+  if (!tensors || n_tensors != defer_gpu_model_tensor_count(cfg))
+    return fail(DEFER_GPU_E_INVALID, "expected %zu tensors, got %zu",
+                defer_gpu_model_tensor_count(cfg), n_tensors);
+  for (size_t i = 0; i < n_tensors; ++i)
+    if (!tensors[i]) return fail(DEFER_GPU_E_INVALID, "tensor %zu is null", i);
+
+  defer_gpu_model* m = new defer_gpu_model();
+  m->cfg = *cfg;
+  Dims& d = m->d;
+  d.h = cfg->hidden_size;
+  d.nh = cfg->num_heads;
+  d.nkv = cfg->num_kv_heads;
+  d.hd = cfg->head_dim;
+  d.half = d.hd / 2;
+  d.ff = cfg->intermediate_size;
+  d.V = cfg->vocab_size;
+  d.L = cfg->num_layers;
+  d.q = d.nh * d.hd;
+  d.kv = d.nkv * d.hd;
+  d.qkv_rows = d.q + 2 * d.kv;
+  d.group = d.nh / d.nkv;
+  d.act = cfg->activation;
+  d.has_bias = cfg->has_bias;
+  d.tied = cfg->tie_word_embeddings;
+  d.kvs = std::max<uint32_t>(d.hd, 32);
+  d.nvc = (d.V + VCHUNK - 1) / VCHUNK;
+  d.eps = cfg->rms_norm_eps;
+  d.scale = 1.0f / sqrtf((float)d.hd);  // model.rs:426
+  d.cap = cfg->max_seq_len;
+
+  auto cleanup = [&](int code) {
+    defer_gpu_model_destroy(m);
+    return code;
+  };
+  hipError_t e = hipGetDevice(&m->device);
+  if (e != hipSuccess) return cleanup(fail(DEFER_GPU_E_HIP, "hipGetDevice: %s", hipGetErrorString(e)));
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, m->device);
+  if (e != hipSuccess)
+    return cleanup(fail(DEFER_GPU_E_HIP, "hipGetDeviceProperties: %s", hipGetErrorString(e)));
+  // Every workgroup must own work in every matvec phase (see phases.h): cap G
+  // by the smallest phase.
+  const uint32_t min_items = std::min({d.qkv_rows / 2, d.h, d.ff, d.nvc});
+  m->G = std::min<uint32_t>((uint32_t)prop.multiProcessorCount, min_items);
+
+  d.lds_vec = (std::max({d.h, d.q, d.ff}) + 3) & ~3u;
+  const uint32_t hs = d.hd + 2;
+  const uint32_t rmax = (d.h + m->G - 1) / m->G;
+  const uint32_t scr_attn = d.group * d.hd + 2 * d.hd + NWAVES * d.group * hs;
+  const uint32_t scr_o = INLINE_COMB_MAX + rmax;
+  const uint32_t scr_comb = MAX_ACHUNKS * hs;
+  const uint32_t scr_samp = 3 * d.nvc + VCHUNK + NWAVES + 2 + NWAVES * VCHUNK;
+  d.lds_scr = (std::max({scr_attn, scr_o, scr_comb, scr_samp, 2 * NWAVES}) + 3) & ~3u;
+  m->lds_bytes = (size_t)(4 + 64 + d.lds_vec + d.lds_scr) * sizeof(float);
+
+  // Weight layout: one allocation, each tensor 256-byte aligned; q/k/v rows
+  // are stored back to back as one [q + 2kv, h] matrix.
+  const size_t h = d.h, q = d.q, kv = d.kv, ff = d.ff, V = d.V;
+  size_t off = 0;
+  auto take = [&](size_t n) {
+    const size_t o = off;
+    off += align256(n * sizeof(float));
+    return o;
+  };
+  const size_t o_embed = take(V * h);
+  struct LOff { size_t an, qkv, b, wo, fn, wg, wu, wd; };
+  std::vector<LOff> lo(d.L);
+  for (uint32_t l = 0; l < d.L; ++l) {
+    lo[l].an = take(h);
+    lo[l].qkv = take((q + 2 * kv) * h);
+    lo[l].b = d.has_bias ? take(q + 2 * kv) : 0;
+    lo[l].wo = take(h * q);
+    lo[l].fn = take(h);
+    lo[l].wg = take(ff * h);
+    lo[l].wu = take(ff * h);
+    lo[l].wd = take(h * ff);
+  }
+  const size_t o_norm = take(h);
+  const size_t o_head = d.tied ? o_embed : take(V * h);
+  const size_t total = off;
+
+  e = hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) return cleanup(fail(DEFER_GPU_E_HIP, "stream: %s", hipGetErrorString(e)));
+  e = hipMalloc(&m->wbuf, total);
+  if (e != hipSuccess)
+    return cleanup(fail(DEFER_GPU_E_HIP, "hipMalloc(%zu) for weights: %s", total,
+                        hipGetErrorString(e)));
+  char* base = reinterpret_cast<char*>(m->wbuf);
+  auto up = [&](size_t o, const float* src, size_t n) {
+    return hipMemcpy(base + o, src, n * sizeof(float), hipMemcpyHostToDevice);
+  };
+  size_t k = 0;
+  e = up(o_embed, tensors[k++], V * h);
+  for (uint32_t l = 0; l < d.L && e == hipSuccess; ++l) {
+    e = up(lo[l].an, tensors[k++], h);
+    const float* wq = tensors[k++];
+    const float* bq = d.has_bias ? tensors[k++] : nullptr;
+    const float* wk = tensors[k++];
+    const float* bk = d.has_bias ? tensors[k++] : nullptr;
+    const float* wv = tensors[k++];
+    const float* bv = d.has_bias ? tensors[k++] : nullptr;
+    if (e == hipSuccess) e = up(lo[l].qkv, wq, q * h);
+    if (e == hipSuccess) e = up(lo[l].qkv + q * h * sizeof(float), wk, kv * h);
+    if (e == hipSuccess) e = up(lo[l].qkv + (q + kv) * h * sizeof(float), wv, kv * h);
+    if (d.has_bias) {
+      if (e == hipSuccess) e = up(lo[l].b, bq, q);
+      if (e == hipSuccess) e = up(lo[l].b + q * sizeof(float), bk, kv);
+      if (e == hipSuccess) e = up(lo[l].b + (q + kv) * sizeof(float), bv, kv);
+    }
+    if (e == hipSuccess) e = up(lo[l].wo, tensors[k++], h * q);
+    if (e == hipSuccess) e = up(lo[l].fn, tensors[k++], h);
+    if (e == hipSuccess) e = up(lo[l].wg, tensors[k++], ff * h);
+    if (e == hipSuccess) e = up(lo[l].wu, tensors[k++], ff * h);
+    if (e == hipSuccess) e = up(lo[l].wd, tensors[k++], h * ff);
+  }
+  if (e == hipSuccess) e = up(o_norm, tensors[k++], h);
+  if (e == hipSuccess && !d.tied) e = up(o_head, tensors[k++], V * h);
+  if (e != hipSuccess)
+    return cleanup(fail(DEFER_GPU_E_HIP, "weight upload: %s", hipGetErrorString(e)));
+
+  auto at = [&](size_t o) { return reinterpret_cast<const float*>(base + o); };
+  m->layers.resize(d.L);
+  for (uint32_t l = 0; l < d.L; ++l) {
+    LayerW& W = m->layers[l];
+    W.attn_norm = at(lo[l].an);
+    W.wqkv = at(lo[l].qkv);
+    W.bqkv = d.has_bias ? at(lo[l].b) : nullptr;
+    W.wo = at(lo[l].wo);
+    W.ffn_norm = at(lo[l].fn);
+    W.wg = at(lo[l].wg);
+    W.wu = at(lo[l].wu);
+    W.wd = at(lo[l].wd);
+  }
+  m->embed = at(o_embed);
+  m->norm = at(o_norm);
+  m->head = at(o_head);
+  e = hipMalloc(&m->d_layers, sizeof(LayerW) * d.L);
+  if (e == hipSuccess)
+    e = hipMemcpy(m->d_layers, m->layers.data(), sizeof(LayerW) * d.L, hipMemcpyHostToDevice);
+  if (e != hipSuccess) return cleanup(fail(DEFER_GPU_E_HIP, "layer table: %s", hipGetErrorString(e)));
+
+  // RoPE tables: inv_freq in f64 then f32 (model.rs:348-353); angle and
+  // cos/sin in f32 with the host libm (model.rs:438-445).
+  std::vector<float> inv_freq(d.half);
+  for (uint32_t i = 0; i < d.half; ++i) {
+    const double exponent = (double)(2 * i) / (double)d.hd;
+    inv_freq[i] = (float)(1.0 / pow((double)cfg->rope_theta, exponent));
+  }
+  std::vector<float2> rope((size_t)d.cap * d.half);
+  for (uint32_t p = 0; p < d.cap; ++p)
+    for (uint32_t i = 0; i < d.half; ++i) {
+      const float angle = (float)p * inv_freq[i];
+      rope[(size_t)p * d.half + i] = make_float2(cosf(angle), sinf(angle));
+    }
+  e = hipMalloc(&m->rope, rope.size() * sizeof(float2));
+  if (e == hipSuccess)
+    e = hipMemcpy(m->rope, rope.data(), rope.size() * sizeof(float2), hipMemcpyHostToDevice);
+  if (e != hipSuccess) return cleanup(fail(DEFER_GPU_E_HIP, "rope table: %s", hipGetErrorString(e)));
+
+  const void* kernels[] = {(const void*)k_persistent, (const void*)k_phase,
+                           (const void*)k_samp_a, (const void*)k_op};
+  for (const void* kf : kernels) {
+    e = hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)m->lds_bytes);
+    if (e != hipSuccess)
+      return cleanup(fail(DEFER_GPU_E_HIP, "LDS attribute (%zu bytes): %s", m->lds_bytes,
+                          hipGetErrorString(e)));
+  }
+  int occ = 0;
+  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_persistent, BLOCK, m->lds_bytes);
+  if (e != hipSuccess || occ < 1)
+    return cleanup(fail(DEFER_GPU_E_HIP, "persistent kernel does not fit a CU (occupancy %d)", occ));
+  if (hipEventCreate(&m->ev0) != hipSuccess || hipEventCreate(&m->ev1) != hipSuccess)
+    return cleanup(fail(DEFER_GPU_E_HIP, "event create"));
+  *out = m;
+  return DEFER_GPU_OK;
+}
+
+extern "C" void defer_gpu_model_destroy(defer_gpu_model* m) {
+  if (!m) return;
+  if (m->stream) (void)hipStreamSynchronize(m->stream);
+  (void)hipFree(m->wbuf);
+  (void)hipFree(m->d_layers);
+  (void)hipFree(m->rope);
+  if (m->ev0) (void)hipEventDestroy(m->ev0);
+  if (m->ev1) (void)hipEventDestroy(m->ev1);
+  if (m->stream) (void)hipStreamDestroy(m->stream);
+  delete m;
+}
+
+extern "C" int defer_gpu_model_set_exec(defer_gpu_model* m, uint32_t mode) {
+  if (!m || mode > DEFER_GPU_EXEC_EAGER) return fail(DEFER_GPU_E_INVALID, "bad exec mode");
+  m->exec_mode = mode;
+  return DEFER_GPU_OK;
+}
+
+extern "C" double defer_gpu_last_device_ms(const defer_gpu_model* m) { return m ? m->last_ms : 0.0; }
+
+// ------------------------------------------------------------------ caches
+
+static int cache_alloc(const defer_gpu_model* m, uint32_t cap, defer_gpu_cache* c) {
+  const Dims& d = m->d;
+  c->m = m;
+  c->cap = cap;
+  const size_t kvn = (size_t)d.L * d.nkv * cap * d.kvs;
+  HIP_TRY(hipMalloc(&c->kc, kvn * sizeof(float)));
+  HIP_TRY(hipMalloc(&c->vc, kvn * sizeof(float)));
+  const size_t hs = d.hd + 2;
+  const size_t words = d.qkv_rows + (size_t)d.nh * MAX_ACHUNKS * hs + d.q + d.h + d.h + d.ff +
+                       d.V + 3 * (size_t)d.nvc + 64;
+  c->mb_words = words;
+  HIP_TRY(hipMalloc(&c->mb, words * sizeof(u64)));
+  HIP_TRY(hipMemset(c->mb, 0, words * sizeof(u64)));
+  HIP_TRY(hipMalloc(&c->st, sizeof(DevState)));
+  HIP_TRY(hipMemset(c->st, 0, sizeof(DevState)));
+  HIP_TRY(hipMalloc(&c->d_run, sizeof(RunDesc)));
+  HIP_TRY(hipMalloc(&c->d_mask, ((cap + 31) / 32) * sizeof(uint32_t)));
+  HIP_TRY(hipMalloc(&c->d_logits, (size_t)d.V * sizeof(float)));
+  Args& a = c->args;
+  a.d = d;
+  a.d.cap = cap;
+  a.layers = m->d_layers;
+  a.embed = m->embed;
+  a.norm = m->norm;
+  a.head = m->head;
+  a.rope = m->rope;
+  a.kc = c->kc;
+  a.vc = c->vc;
+  u64* p = c->mb;
+  a.mb_qkv = p; p += d.qkv_rows;
+  a.mb_part = p; p += (size_t)d.nh * MAX_ACHUNKS * hs;
+  a.mb_att = p; p += d.q;
+  a.mb_xo = p; p += d.h;
+  a.mb_xd = p; p += d.h;
+  a.mb_g = p; p += d.ff;
+  a.mb_logit = p; p += d.V;
+  a.mb_vmax = p; p += d.nvc;
+  a.mb_varg = p; p += d.nvc;
+  a.mb_vsum = p; p += d.nvc;
+  a.st = c->st;
+  a.mask = nullptr;
+  return DEFER_GPU_OK;
+}
+
+static void cache_free(defer_gpu_cache* c) {
+  if (!c) return;
+  if (c->m && c->m->stream) (void)hipStreamSynchronize(c->m->stream);
+  if (c->graph) (void)hipGraphExecDestroy(c->graph);
+  (void)hipFree(c->kc);
+  (void)hipFree(c->vc);
+  (void)hipFree(c->mb);
+  (void)hipFree(c->st);
+  (void)hipFree(c->d_run);
+  (void)hipFree(c->d_mask);
+  (void)hipFree(c->d_tokens);
+  (void)hipFree(c->d_words);
+  (void)hipFree(c->d_stop);
+  (void)hipFree(c->d_out);
+  (void)hipFree(c->d_logits);
+  (void)hipFree(c->d_tmp);
+}
+
+extern "C" int defer_gpu_cache_create(const defer_gpu_model* m, uint32_t capacity,
+                                      defer_gpu_cache** out) {
+  if (!m || !out) return fail(DEFER_GPU_E_INVALID, "null argument");
+  *out = nullptr;
+  const uint32_t cap = capacity ? capacity : m->cfg.max_seq_len;
+  if (cap > m->cfg.max_seq_len)
+    return fail(DEFER_GPU_E_INVALID, "capacity %u exceeds max_seq_len %u", cap,
+                m->cfg.max_seq_len);
+  defer_gpu_cache* c = new defer_gpu_cache();
+  const int rc = cache_alloc(m, cap, c);
+  if (rc) {
+    cache_free(c);
+    delete c;
+    return rc;
+  }
+  *out = c;
+  return DEFER_GPU_OK;
+}
+
+extern "C" void defer_gpu_cache_destroy(defer_gpu_cache* c) {
+  if (!c) return;
+  cache_free(c);
+  delete c;
+}
+
+extern "C" uint32_t defer_gpu_cache_len(const defer_gpu_cache* c) { return c ? c->pos : 0; }
+
+static int push_state(defer_gpu_cache* c) {
+  DevState h;
+  HIP_TRY(hipMemcpy(&h, c->st, sizeof(h), hipMemcpyDeviceToHost));
+  h.pos = c->pos;
+  h.tick = c->tick;
+  HIP_TRY(hipMemcpy(c->st, &h, sizeof(h), hipMemcpyHostToDevice));
+  return DEFER_GPU_OK;
+}
+
+extern "C" int defer_gpu_cache_truncate(defer_gpu_cache* c, uint32_t n) {
+  if (!c) return fail(DEFER_GPU_E_INVALID, "null cache");
+  if (n >= c->pos) return DEFER_GPU_OK;
+  c->pos = n;
+  c->has_logits = false;
+  return push_state(c);
+}
+
+extern "C" int defer_gpu_cache_clone(const defer_gpu_cache* src, defer_gpu_cache** out) {
+  if (!src || !out) return fail(DEFER_GPU_E_INVALID, "null argument");
+  *out = nullptr;
+  defer_gpu_cache* c = new defer_gpu_cache();
+  int rc = cache_alloc(src->m, src->cap, c);
+  if (rc) {
+    cache_free(c);
+    delete c;
+    return rc;
+  }
+  const Dims& d = src->m->d;
+  const size_t kvn = (size_t)d.L * d.nkv * src->cap * d.kvs;
+  hipError_t e = hipMemcpy(c->kc, src->kc, kvn * sizeof(float), hipMemcpyDeviceToDevice);
+  if (e == hipSuccess) e = hipMemcpy(c->vc, src->vc, kvn * sizeof(float), hipMemcpyDeviceToDevice);
+  if (e == hipSuccess)
+    e = hipMemcpy(c->mb, src->mb, src->mb_words * sizeof(u64), hipMemcpyDeviceToDevice);
+  if (e == hipSuccess) e = hipMemcpy(c->st, src->st, sizeof(DevState), hipMemcpyDeviceToDevice);
+  if (e != hipSuccess) {
+    cache_free(c);
+    delete c;
+    return fail(DEFER_GPU_E_HIP, "cache clone: %s", hipGetErrorString(e));
+  }
+  c->pos = src->pos;
+  c->tick = src->tick;
+  c->has_logits = src->has_logits;
+  *out = c;
+  return DEFER_GPU_OK;
+}
+
+extern "C" int defer_gpu_cache_read(const defer_gpu_cache* cc, uint32_t layer, float* keys,
+                                    float* values) {
+  defer_gpu_cache* c = const_cast<defer_gpu_cache*>(cc);
+  if (!c) return fail(DEFER_GPU_E_INVALID, "null cache");
+  const Dims& d = c->m->d;
+  if (layer >= d.L) return fail(DEFER_GPU_E_INVALID, "layer %u out of range", layer);
+  const size_t n = (size_t)c->pos * d.kv;
+  if (n == 0) return DEFER_GPU_OK;
+  if (!c->d_tmp) HIP_TRY(hipMalloc(&c->d_tmp, (size_t)c->cap * d.kv * sizeof(float)));
+  const hipStream_t s = c->m->stream;
+  const size_t per_layer = (size_t)d.nkv * c->cap * d.kvs;
+  for (int which = 0; which < 2; ++which) {
+    float* dst = which ? values : keys;
+    if (!dst) continue;
+    const float* src = (which ? c->vc : c->kc) + layer * per_layer;
+    const uint32_t nb = (uint32_t)((n + 255) / 256);
+    k_kv_gather<<<nb, 256, 0, s>>>(src, c->d_tmp, c->pos, d.nkv, d.hd, c->cap, d.kvs);
+    HIP_TRY(hipGetLastError());
+    HIP_TRY(hipMemcpyAsync(dst, c->d_tmp, n * sizeof(float), hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+  }
+  return DEFER_GPU_OK;
+}
+
+// ------------------------------------------------------------------ runs
+
+static int ensure_run_buffers(defer_gpu_cache* c, size_t n_ops, size_t n_stop) {
+  if (n_ops > c->run_cap) {
+    (void)hipFree(c->d_tokens);
+    (void)hipFree(c->d_words);
+    (void)hipFree(c->d_out);
+    c->d_tokens = c->d_words = c->d_out = nullptr;
+    const size_t cap = std::max<size_t>(n_ops, 1024);
+    HIP_TRY(hipMalloc(&c->d_tokens, cap * sizeof(uint32_t)));
+    HIP_TRY(hipMalloc(&c->d_words, cap * sizeof(uint32_t)));
+    HIP_TRY(hipMalloc(&c->d_out, cap * sizeof(uint32_t)));
+    c->run_cap = cap;
+  }
+  if (n_stop > c->stop_cap || !c->d_stop) {
+    (void)hipFree(c->d_stop);
+    c->d_stop = nullptr;
+    const size_t cap = std::max<size_t>(n_stop, 16);
+    HIP_TRY(hipMalloc(&c->d_stop, cap * sizeof(uint32_t)));
+    c->stop_cap = cap;
+  }
+  return DEFER_GPU_OK;
+}
+
+static int launch_op_kernels(defer_gpu_cache* c, hipStream_t s) {
+  const defer_gpu_model* m = c->m;
+  const Dims& d = m->d;
+  const Args& a = c->args;
+  const uint32_t G = m->G;
+  const size_t lds = m->lds_bytes;
+  k_samp_a<<<G, BLOCK, lds, s>>>(a, c->d_run);
+  k_op<<<1, BLOCK, lds, s>>>(a, c->d_run);
+  for (uint32_t l = 0; l < d.L; ++l)
+    for (uint32_t ph = 0; ph < PH_PER_LAYER; ++ph) k_phase<<<G, BLOCK, lds, s>>>(a, ph, l);
+  k_phase<<<G, BLOCK, lds, s>>>(a, PH_LM_KERNEL, 0);
+  k_commit<<<1, 1, 0, s>>>(a, c->d_run);
+  HIP_TRY(hipGetLastError());
+  return DEFER_GPU_OK;
+}
+
+// Runs n_ops ops described by `r` (host copy, device pointers filled in).
+static int run_ops(defer_gpu_cache* c, RunDesc r, bool force_eager) {
+  defer_gpu_model* m = const_cast<defer_gpu_model*>(c->m);
+  const hipStream_t s = m->stream;
+  HIP_TRY(hipMemcpyAsync(c->d_run, &r, sizeof(r), hipMemcpyHostToDevice, s));
+  k_begin<<<1, 1, 0, s>>>(c->st);
+  HIP_TRY(hipGetLastError());
+  HIP_TRY(hipEventRecord(m->ev0, s));
+  const uint32_t mode = force_eager ? DEFER_GPU_EXEC_EAGER : m->exec_mode;
+  if (r.n_ops > 0) {
+    if (mode == DEFER_GPU_EXEC_PERSISTENT) {
+      Args a = c->args;
+      const RunDesc* dr = c->d_run;
+      void* params[] = {&a, &dr};
+      HIP_TRY(hipLaunchCooperativeKernel((const void*)k_persistent, dim3(m->G), dim3(BLOCK),
+                                         params, (unsigned)m->lds_bytes, s));
+    } else if (mode == DEFER_GPU_EXEC_GRAPH) {
+      if (!c->graph) {
+        hipGraph_t g;
+        HIP_TRY(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+        const int rc = launch_op_kernels(c, s);
+        hipError_t e = hipStreamEndCapture(s, &g);
+        if (rc) return rc;
+        if (e != hipSuccess) return fail(DEFER_GPU_E_HIP, "graph capture: %s", hipGetErrorString(e));
+        e = hipGraphInstantiate(&c->graph, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        if (e != hipSuccess)
+          return fail(DEFER_GPU_E_HIP, "graph instantiate: %s", hipGetErrorString(e));
+      }
+      for (uint32_t i = 0; i < r.n_ops; ++i) HIP_TRY(hipGraphLaunch(c->graph, s));
+    } else {
+      for (uint32_t i = 0; i < r.n_ops; ++i) {
+        const int rc = launch_op_kernels(c, s);
+        if (rc) return rc;
+      }
+    }
+  }
+  HIP_TRY(hipEventRecord(m->ev1, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  float ms = 0.0f;
+  HIP_TRY(hipEventElapsedTime(&ms, m->ev0, m->ev1));
+  m->last_ms = ms;
+  DevState h;
+  HIP_TRY(hipMemcpy(&h, c->st, sizeof(h), hipMemcpyDeviceToHost));
+  if (h.abort) {
+    c->has_logits = false;
+    return fail(DEFER_GPU_E_TIMEOUT, "a device-side wait exceeded its bound; cache state is undefined");
+  }
+  c->pos = h.pos;
+  c->tick = h.tick;
+  if (h.n_done > 0) c->has_logits = true;
+  return DEFER_GPU_OK;
+}
+
+static DevState read_state(defer_gpu_cache* c) {
+  DevState h;
+  memset(&h, 0, sizeof(h));
+  if (hipMemcpy(&h, c->st, sizeof(h), hipMemcpyDeviceToHost) != hipSuccess) h.first_div = -2;
+  return h;
+}
+
+static int check_pair(const defer_gpu_model* m, const defer_gpu_cache* c) {
+  if (!m || !c) return fail(DEFER_GPU_E_INVALID, "null model or cache");
+  if (c->m != m) return fail(DEFER_GPU_E_INVALID, "cache belongs to another model");
+  return DEFER_GPU_OK;
+}
+
+static int copy_logits(defer_gpu_cache* c, float* out) {
+  const Dims& d = c->m->d;
+  const hipStream_t s = c->m->stream;
+  k_untag<<<(d.V + 255) / 256, 256, 0, s>>>(c->args.mb_logit, c->d_logits, d.V);
+  HIP_TRY(hipGetLastError());
+  HIP_TRY(hipMemcpyAsync(out, c->d_logits, (size_t)d.V * sizeof(float), hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  return DEFER_GPU_OK;
+}
+
+extern "C" int defer_gpu_last_logits(const defer_gpu_cache* cc, float* logits_out) {
+  defer_gpu_cache* c = const_cast<defer_gpu_cache*>(cc);
+  if (!c || !logits_out) return fail(DEFER_GPU_E_INVALID, "null argument");
+  if (!c->has_logits) return fail(DEFER_GPU_E_NO_LOGITS, "no context: provide a non-empty prompt");
+  return copy_logits(c, logits_out);
+}
+
+static int feed_tokens(const defer_gpu_model* m, defer_gpu_cache* c, const uint32_t* tokens,
+                       size_t n, bool eager) {
+  for (size_t i = 0; i < n; ++i)
+    if (tokens[i] >= m->d.V) return fail(DEFER_GPU_E_TOKEN, "token id %u out of range", tokens[i]);
+  if ((size_t)c->pos + n > c->cap)
+    return fail(DEFER_GPU_E_CONTEXT, "context length %u exceeded", m->cfg.max_seq_len);
+  int rc = ensure_run_buffers(c, n, 0);
+  if (rc) return rc;
+  if (n) HIP_TRY(hipMemcpy(c->d_tokens, tokens, n * sizeof(uint32_t), hipMemcpyHostToDevice));
+  RunDesc r;
+  memset(&r, 0, sizeof(r));
+  r.n_ops = (uint32_t)n;
+  r.mode = RUN_FEED;
+  r.sample_from = (uint32_t)n;
+  r.tokens = c->d_tokens;
+  r.words = c->d_words;
+  r.stop = c->d_stop;
+  r.out_tokens = c->d_out;
+  return run_ops(c, r, eager);
+}
+
+extern "C" int defer_gpu_forward(const defer_gpu_model* m, defer_gpu_cache* c, uint32_t token,
+                                 const uint32_t* masked, size_t n_masked, float* logits_out,
+                                 float* trace_out) {
+  int rc = check_pair(m, c);
+  if (rc) return rc;
+  if (token >= m->d.V) return fail(DEFER_GPU_E_TOKEN, "token id %u out of range", token);
+  if (c->pos >= c->cap)
+    return fail(DEFER_GPU_E_CONTEXT, "context length %u exceeded", m->cfg.max_seq_len);
+  if (trace_out) return fail(DEFER_GPU_E_INVALID, "attention trace export is not built yet");
+  bool use_mask = false;
+  if (n_masked) {
+    std::vector<uint32_t> bits((c->cap + 31) / 32, 0u);
+    for (size_t i = 0; i < n_masked; ++i)
+      if (masked[i] < c->pos) {
+        bits[masked[i] >> 5] |= 1u << (masked[i] & 31);
+        use_mask = true;
+      }
+    if (use_mask)
+      HIP_TRY(hipMemcpy(c->d_mask, bits.data(), bits.size() * sizeof(uint32_t),
+                        hipMemcpyHostToDevice));
+  }
+  if (use_mask) c->args.mask = c->d_mask;
+  rc = feed_tokens(m, c, &token, 1, use_mask);
+  c->args.mask = nullptr;
+  if (rc) return rc;
+  return logits_out ? copy_logits(c, logits_out) : DEFER_GPU_OK;
+}
+
+extern "C" int defer_gpu_prompt(const defer_gpu_model* m, defer_gpu_cache* c,
+                                const uint32_t* tokens, size_t n_tokens) {
+  int rc = check_pair(m, c);
+  if (rc) return rc;
+  if (n_tokens && !tokens) return fail(DEFER_GPU_E_INVALID, "null tokens");
+  return feed_tokens(m, c, tokens, n_tokens, false);
+}
+
+static int check_temperature(float t) {
+  if (!(t >= 0.0f && isfinite(t)))
+    return fail(DEFER_GPU_E_INVALID, "temperature must be finite and >= 0");
+  return DEFER_GPU_OK;
+}
+
+extern "C" int defer_gpu_generate(const defer_gpu_model* m, defer_gpu_cache* c, uint32_t max_tokens,
+                                  float temperature, const uint32_t* rng_words,
+                                  const uint32_t* stop, size_t n_stop, uint32_t* tokens_out,
+                                  uint32_t* n_out) {
+  int rc = check_pair(m, c);
+  if (rc) return rc;
+  if (n_out) *n_out = 0;
+  rc = check_temperature(temperature);
+  if (rc) return rc;
+  if (max_tokens == 0) return DEFER_GPU_OK;
+  if (!c->has_logits) return fail(DEFER_GPU_E_NO_LOGITS, "no context: provide a non-empty prompt");
+  if (temperature != 0.0f && !rng_words) return fail(DEFER_GPU_E_INVALID, "null rng words");
+  if (!tokens_out) return fail(DEFER_GPU_E_INVALID, "null tokens_out");
+  const uint32_t room = c->cap - c->pos;
+  const uint32_t n = std::min(max_tokens, room);
+  if (n == 0) return fail(DEFER_GPU_E_CONTEXT, "context length %u exceeded", m->cfg.max_seq_len);
+  rc = ensure_run_buffers(c, n, n_stop);
+  if (rc) return rc;
+  if (temperature != 0.0f)
+    HIP_TRY(hipMemcpy(c->d_words, rng_words, n * sizeof(uint32_t), hipMemcpyHostToDevice));
+  if (n_stop) HIP_TRY(hipMemcpy(c->d_stop, stop, n_stop * sizeof(uint32_t), hipMemcpyHostToDevice));
+  RunDesc r;
+  memset(&r, 0, sizeof(r));
+  r.n_ops = n;
+  r.mode = RUN_GENERATE;
+  r.sample_from = 0;
+  r.temperature = temperature;
+  r.n_stop = (uint32_t)n_stop;
+  r.tokens = c->d_tokens;
+  r.words = c->d_words;
+  r.stop = c->d_stop;
+  r.out_tokens = c->d_out;
+  rc = run_ops(c, r, false);
+  if (rc) return rc;
+  const DevState h = read_state(c);
+  if (h.n_done) HIP_TRY(hipMemcpy(tokens_out, c->d_out, h.n_done * sizeof(uint32_t),
+                                  hipMemcpyDeviceToHost));
+  if (n_out) *n_out = h.n_done;
+  if (n < max_tokens && !h.halt)
+    return fail(DEFER_GPU_E_CONTEXT, "context length %u exceeded", m->cfg.max_seq_len);
+  return DEFER_GPU_OK;
+}
+
+extern "C" int defer_gpu_sample(const defer_gpu_model* m, defer_gpu_cache* c, float temperature,
+                                uint32_t rng_word, uint32_t* token_out) {
+  // A sample without the feed: run the sampler kernels alone on the current
+  // logits (stage A on all workgroups, stage B on one).
+  int rc = check_pair(m, c);
+  if (rc) return rc;
+  rc = check_temperature(temperature);
+  if (rc) return rc;
+  if (!c->has_logits) return fail(DEFER_GPU_E_NO_LOGITS, "no context: provide a non-empty prompt");
+  if (!token_out) return fail(DEFER_GPU_E_INVALID, "null token_out");
+  rc = ensure_run_buffers(c, 1, 0);
+  if (rc) return rc;
+  HIP_TRY(hipMemcpy(c->d_words, &rng_word, sizeof(uint32_t), hipMemcpyHostToDevice));
+  RunDesc r;
+  memset(&r, 0, sizeof(r));
+  r.n_ops = 1;
+  r.mode = RUN_GENERATE;
+  r.sample_from = 0;
+  r.temperature = temperature;
+  r.tokens = c->d_tokens;
+  r.words = c->d_words;
+  r.stop = c->d_stop;
+  r.out_tokens = c->d_out;
+  const hipStream_t s = m->stream;
+  HIP_TRY(hipMemcpyAsync(c->d_run, &r, sizeof(r), hipMemcpyHostToDevice, s));
+  k_begin<<<1, 1, 0, s>>>(c->st);
+  k_samp_a<<<m->G, BLOCK, m->lds_bytes, s>>>(c->args, c->d_run);
+  k_op<<<1, BLOCK, m->lds_bytes, s>>>(c->args, c->d_run);
+  HIP_TRY(hipGetLastError());
+  HIP_TRY(hipStreamSynchronize(s));
+  const DevState h = read_state(c);
+  if (h.abort) return fail(DEFER_GPU_E_TIMEOUT, "a device-side wait exceeded its bound");
+  HIP_TRY(hipMemcpy(token_out, c->d_out, sizeof(uint32_t), hipMemcpyDeviceToHost));
+  return DEFER_GPU_OK;
+}
+
+extern "C" int defer_gpu_step(const defer_gpu_model* m, defer_gpu_cache* c, float temperature,
+                              uint32_t rng_word, uint32_t* token_out) {
+  uint32_t n = 0;
+  const int rc = defer_gpu_generate(m, c, 1, temperature, &rng_word, nullptr, 0, token_out, &n);
+  if (rc) return rc;
+  if (n != 1) return fail(DEFER_GPU_E_CONTEXT, "context length %u exceeded", m->cfg.max_seq_len);
+  return DEFER_GPU_OK;
+}
+
+extern "C" int defer_gpu_replay(const defer_gpu_model* m, defer_gpu_cache* c,
+                                const uint32_t* history, size_t n_history, size_t prompt_len,
+                                float temperature, const uint32_t* rng_words, int64_t* first_div,
+                                uint32_t* sampled_at_div) {
+  int rc = check_pair(m, c);
+  if (rc) return rc;
+  rc = check_temperature(temperature);
+  if (rc) return rc;
+  if (first_div) *first_div = -1;
+  if (prompt_len > n_history) return fail(DEFER_GPU_E_INVALID, "prompt_len exceeds history");
+  if (c->pos != 0) return fail(DEFER_GPU_E_INVALID, "replay needs an empty cache");
+  if (n_history > prompt_len && prompt_len == 0)
+    return fail(DEFER_GPU_E_NO_LOGITS, "no context: provide a non-empty prompt");
+  if (n_history > prompt_len && temperature != 0.0f && !rng_words)
+    return fail(DEFER_GPU_E_INVALID, "null rng words");
+  for (size_t i = 0; i < n_history; ++i)
+    if (history[i] >= m->d.V) return fail(DEFER_GPU_E_TOKEN, "token id %u out of range", history[i]);
+  if (n_history > c->cap)
+    return fail(DEFER_GPU_E_CONTEXT, "context length %u exceeded", m->cfg.max_seq_len);
+  rc = ensure_run_buffers(c, n_history, 0);
+  if (rc) return rc;
+  if (n_history)
+    HIP_TRY(hipMemcpy(c->d_tokens, history, n_history * sizeof(uint32_t), hipMemcpyHostToDevice));
+  const size_t n_sampled = n_history - prompt_len;
+  if (n_sampled && temperature != 0.0f)
+    HIP_TRY(hipMemcpy(c->d_words, rng_words, n_sampled * sizeof(uint32_t), hipMemcpyHostToDevice));
+  RunDesc r;
+  memset(&r, 0, sizeof(r));
+  r.n_ops = (uint32_t)n_history;
+  r.mode = RUN_REPLAY;
+  r.sample_from = (uint32_t)prompt_len;
+  r.temperature = temperature;
+  r.tokens = c->d_tokens;
+  r.words = c->d_words;
+  r.stop = c->d_stop;
+  r.out_tokens = c->d_out;
+  rc = run_ops(c, r, false);
+  if (rc) return rc;
+  const DevState h = read_state(c);
+  if (h.first_div >= 0) {
+    if (first_div) *first_div = h.first_div;
+    if (sampled_at_div) *sampled_at_div = h.sampled_div;
+  }
+  return DEFER_GPU_OK;
+}

@@ -1,0 +1,243 @@
+// device.h -- device-side building blocks of the gfx950 forward pass.
+//
+// Tagged mailboxes. Every activation that crosses workgroups is stored as a
+// 64-bit word {generation:32, float bits:32} with an agent-scope relaxed
+// store (global_store_dwordx2 sc1) and read with agent-scope relaxed loads.
+// A consumer polls the words it needs until every tag equals the expected
+// generation, so no barrier, fence or read-modify-write atomic is needed:
+// the value and its readiness arrive in one access.
+//
+// Determinism. Every reduction below has a fixed shape that depends only on
+// the problem size: lane-strided partials in index order, an xor butterfly
+// across the 64 lanes of a wave, then wave partials summed in wave order.
+// Which workgroup computes an output never changes how it is computed, so
+// the persistent kernel and the per-phase kernels give identical bits.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dg {
+
+typedef unsigned long long u64;
+
+constexpr uint32_t WAVE = 64;
+constexpr uint32_t BLOCK = 512;
+constexpr uint32_t NWAVES = BLOCK / WAVE;
+constexpr uint32_t VCHUNK = 64;        // vocabulary rows per sampling chunk
+constexpr uint32_t ACHUNK = 64;        // attention positions per chunk (base size)
+constexpr uint32_t MAX_ACHUNKS = 8;    // attention chunks per head at most
+constexpr uint32_t INLINE_COMB_MAX = 8192;  // floats of partials combined inside the O phase
+constexpr uint32_t SPIN_LIMIT = 1u << 21;
+constexpr uint32_t NO_INDEX = 0xffffffffu;
+
+// ------------------------------------------------------------------ layout
+
+struct Dims {
+  uint32_t h, nh, nkv, hd, half, ff, V, L, q, kv, qkv_rows, group;
+  uint32_t act, has_bias, tied;
+  uint32_t cap;        // cache capacity (positions)
+  uint32_t kvs;        // KV row stride in floats (>= 32: rows never share a 128-byte line)
+  uint32_t nvc;        // number of vocabulary chunks
+  uint32_t lds_vec;    // floats of the input-vector LDS region
+  uint32_t lds_scr;    // floats of the scratch LDS region
+  float eps, scale;
+};
+
+struct LayerW {
+  const float* attn_norm;
+  const float* wqkv;  // [q + 2kv, h]: q rows, then k rows, then v rows
+  const float* bqkv;  // [q + 2kv] or null
+  const float* wo;    // [h, q]
+  const float* ffn_norm;
+  const float* wg;    // [ff, h]
+  const float* wu;    // [ff, h]
+  const float* wd;    // [h, ff]
+};
+
+// Phases of one layer, in order; generation numbers are derived from them.
+enum Phase : uint32_t { PH_QKV = 0, PH_ATTN = 1, PH_COMB = 2, PH_O = 3, PH_GU = 4, PH_D = 5 };
+constexpr uint32_t PH_PER_LAYER = 6;
+
+struct DevState {
+  uint32_t pos;      // cache length
+  uint32_t tick;     // number of forwards run on this cache (generation base)
+  uint32_t token;    // token of the forward in flight (per-phase kernels)
+  uint32_t abort;    // set when a wait exceeded SPIN_LIMIT
+  uint32_t halt;     // a run stopped early (divergence or stop token)
+  uint32_t n_done;   // ops completed in the current run
+  uint32_t op;       // op index of the forward in flight (per-phase kernels)
+  uint32_t sampled_div;
+  long long first_div;
+};
+
+// Describes a run of ops: op i optionally samples (i >= sample_from), then
+// feeds a token: the sampled one (generate) or tokens[i] (prompt, replay).
+enum RunMode : uint32_t { RUN_FEED = 0, RUN_GENERATE = 1, RUN_REPLAY = 2 };
+
+struct RunDesc {
+  uint32_t n_ops;
+  uint32_t mode;
+  uint32_t sample_from;
+  float temperature;
+  uint32_t n_stop;
+  const uint32_t* tokens;
+  const uint32_t* words;
+  const uint32_t* stop;
+  uint32_t* out_tokens;
+};
+
+struct Args {
+  Dims d;
+  const LayerW* layers;
+  const float* embed;
+  const float* norm;
+  const float* head;     // lm_head, or the embedding when tied
+  const float2* rope;    // [max_seq][half] (cos, sin)
+  float* kc;             // [L][nkv][cap][kvs]
+  float* vc;
+  u64* mb_qkv;           // [qkv_rows]
+  u64* mb_part;          // [nh][MAX_ACHUNKS][hd + 2]  (m, l, acc[hd])
+  u64* mb_att;           // [q] combined attention (separate-combine path)
+  u64* mb_xo;            // [h] residual after attention
+  u64* mb_xd;            // [h] residual after the MLP
+  u64* mb_g;             // [ff]
+  u64* mb_logit;         // [V]
+  u64* mb_vmax;          // [nvc] chunk max logit
+  u64* mb_varg;          // [nvc] chunk argmax (index bits)
+  u64* mb_vsum;          // [nvc] chunk sum of exp(logit/T - m)
+  DevState* st;
+  const uint32_t* mask;  // bitmask over positions, or null
+  RunDesc run;
+};
+
+__host__ __device__ inline uint32_t phases_per_tick(const Dims& d) {
+  return d.L * PH_PER_LAYER + 2;
+}
+__host__ __device__ inline uint32_t gen_of(const Dims& d, uint32_t tick, uint32_t layer,
+                                           uint32_t ph) {
+  return tick * phases_per_tick(d) + layer * PH_PER_LAYER + ph + 1u;
+}
+__host__ __device__ inline uint32_t gen_lm(const Dims& d, uint32_t tick) {
+  return tick * phases_per_tick(d) + d.L * PH_PER_LAYER + 1u;
+}
+__host__ __device__ inline uint32_t gen_sums(const Dims& d, uint32_t tick) {
+  return tick * phases_per_tick(d) + d.L * PH_PER_LAYER + 2u;
+}
+
+// Attention chunking: a function of the query position only, so results
+// depend on (pos, data) alone.
+__host__ __device__ inline uint32_t attn_chunk(uint32_t pos) {
+  const uint32_t ctx = pos + 1;
+  const uint32_t base = ACHUNK * MAX_ACHUNKS;
+  const uint32_t mult = (ctx + base - 1) / base;
+  return ACHUNK * (mult ? mult : 1);
+}
+__host__ __device__ inline uint32_t attn_nchunks(uint32_t pos) {
+  const uint32_t ch = attn_chunk(pos);
+  return (pos + 1 + ch - 1) / ch;
+}
+__host__ __device__ inline bool comb_inline(const Dims& d, uint32_t pos) {
+  return d.nh * attn_nchunks(pos) * (d.hd + 2) <= INLINE_COMB_MAX;
+}
+
+// --------------------------------------------------------- memory helpers
+
+__device__ __forceinline__ void mb_put(u64* slot, float v, uint32_t gen) {
+  const u64 w = ((u64)gen << 32) | (u64)__float_as_uint(v);
+  __hip_atomic_store(slot, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ u64 mb_load(const u64* slot) {
+  return __hip_atomic_load(const_cast<u64*>(slot), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coherent(float* p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_coherent_u32(const uint32_t* p) {
+  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coherent_u32(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float4 ld4(const float* p) {
+  return *reinterpret_cast<const float4*>(p);
+}
+
+// --------------------------------------------------------- reductions
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+// Sum over the block in a fixed tree; every thread gets the result.
+// `red` is LDS scratch of at least NWAVES floats (+1).
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float s = 0.0f;
+#pragma unroll
+  for (uint32_t w = 0; w < NWAVES; ++w) s += red[w];
+  return s;
+}
+
+// Per-lane partial of a row dot product: w[j] * x[j] for j = 4*lane + 256*k,
+// in ascending j, one fused multiply-add per element. K % 4 == 0.
+__device__ __forceinline__ float dot_partial(const float* __restrict__ w,
+                                             const float* __restrict__ x, uint32_t K,
+                                             uint32_t lane) {
+  float acc = 0.0f;
+  uint32_t j = lane * 4;
+  for (; j + 768 < K; j += 1024) {
+    const float4 a = ld4(w + j), b = ld4(w + j + 256), c = ld4(w + j + 512), e = ld4(w + j + 768);
+    const float4 xa = ld4(x + j), xb = ld4(x + j + 256), xc = ld4(x + j + 512),
+                 xe = ld4(x + j + 768);
+    acc = fmaf(a.x, xa.x, acc); acc = fmaf(a.y, xa.y, acc);
+    acc = fmaf(a.z, xa.z, acc); acc = fmaf(a.w, xa.w, acc);
+    acc = fmaf(b.x, xb.x, acc); acc = fmaf(b.y, xb.y, acc);
+    acc = fmaf(b.z, xb.z, acc); acc = fmaf(b.w, xb.w, acc);
+    acc = fmaf(c.x, xc.x, acc); acc = fmaf(c.y, xc.y, acc);
+    acc = fmaf(c.z, xc.z, acc); acc = fmaf(c.w, xc.w, acc);
+    acc = fmaf(e.x, xe.x, acc); acc = fmaf(e.y, xe.y, acc);
+    acc = fmaf(e.z, xe.z, acc); acc = fmaf(e.w, xe.w, acc);
+  }
+  for (; j < K; j += 256) {
+    const float4 a = ld4(w + j);
+    const float4 xa = ld4(x + j);
+    acc = fmaf(a.x, xa.x, acc); acc = fmaf(a.y, xa.y, acc);
+    acc = fmaf(a.z, xa.z, acc); acc = fmaf(a.w, xa.w, acc);
+  }
+  return acc;
+}
+
+__device__ __forceinline__ float dot_row(const float* __restrict__ w, const float* __restrict__ x,
+                                         uint32_t K, uint32_t lane) {
+  return wave_sum(dot_partial(w, x, K, lane));
+}
+
+// ----------------------------------------------------------- activation
+
+__device__ __forceinline__ float act_fn(float x, uint32_t act) {
+  if (act == 0) return x / (1.0f + expf(-x));  // silu, ops.rs:120-122
+  const float c = 0.7978846f;                  // gelu (tanh), ops.rs:125-128
+  return 0.5f * x * (1.0f + tanhf(c * (x + 0.044715f * x * x * x)));
+}
+
+// ------------------------------------------------------------- waiting
+
+// Shared between the polling helpers of one block (phases.h: wait_gather).
+struct WaitCtl {
+  int abort_seen;
+};
+
+}  // namespace dg

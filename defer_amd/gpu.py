@@ -1,0 +1,279 @@
+"""ctypes binding of the C ABI in include/defer_gpu.h (libdefer_gpu.so).
+
+Mirrors the reference's hot-path types: ``GpuModel`` stands for ``Model``
+(model.rs:271-280) and ``GpuCache`` for ``KvCache`` (model.rs:182-243), with
+the KV cache kept in HBM. The library is required: importing this module on a
+machine without the built ``libdefer_gpu.so`` raises, and there is no CPU
+fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional, Sequence
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libdefer_gpu.so")
+
+EXEC_PERSISTENT = 0
+EXEC_GRAPH = 1
+EXEC_EAGER = 2
+
+OK = 0
+E_INVALID = 1
+E_TOKEN = 2
+E_CONTEXT = 3
+E_HIP = 4
+E_NO_LOGITS = 5
+E_TIMEOUT = 6
+
+
+class DeferGpuError(RuntimeError):
+    """A non-zero status from the C ABI, with the library's message."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"defer_gpu error {code}: {msg}")
+        self.code = code
+
+
+class Config(ctypes.Structure):
+    """defer_gpu_config: Model::Config (model.rs:23-39)."""
+
+    _fields_ = [
+        ("vocab_size", ctypes.c_uint32),
+        ("hidden_size", ctypes.c_uint32),
+        ("intermediate_size", ctypes.c_uint32),
+        ("num_layers", ctypes.c_uint32),
+        ("num_heads", ctypes.c_uint32),
+        ("num_kv_heads", ctypes.c_uint32),
+        ("head_dim", ctypes.c_uint32),
+        ("rms_norm_eps", ctypes.c_float),
+        ("rope_theta", ctypes.c_float),
+        ("max_seq_len", ctypes.c_uint32),
+        ("tie_word_embeddings", ctypes.c_uint32),
+        ("activation", ctypes.c_uint32),
+        ("has_bias", ctypes.c_uint32),
+    ]
+
+    @classmethod
+    def from_dict(cls, d: dict) -> "Config":
+        c = cls()
+        for name, _ in cls._fields_:
+            setattr(c, name, d[name])
+        return c
+
+    def to_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libdefer_gpu.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is missing: build it first (python -c 'import __graft_entry__ as g; g.build()')"
+        )
+    L = ctypes.CDLL(LIB_PATH)
+    u32, f32, sz, vp = ctypes.c_uint32, ctypes.c_float, ctypes.c_size_t, ctypes.c_void_p
+    P = ctypes.POINTER
+    L.defer_gpu_model_create.argtypes = [P(Config), P(vp), sz, u32, P(vp)]
+    L.defer_gpu_model_create.restype = ctypes.c_int
+    L.defer_gpu_model_destroy.argtypes = [vp]
+    L.defer_gpu_model_destroy.restype = None
+    L.defer_gpu_model_tensor_count.argtypes = [P(Config)]
+    L.defer_gpu_model_tensor_count.restype = sz
+    L.defer_gpu_model_set_exec.argtypes = [vp, u32]
+    L.defer_gpu_model_set_exec.restype = ctypes.c_int
+    L.defer_gpu_cache_create.argtypes = [vp, u32, P(vp)]
+    L.defer_gpu_cache_create.restype = ctypes.c_int
+    L.defer_gpu_cache_destroy.argtypes = [vp]
+    L.defer_gpu_cache_destroy.restype = None
+    L.defer_gpu_cache_len.argtypes = [vp]
+    L.defer_gpu_cache_len.restype = u32
+    L.defer_gpu_cache_truncate.argtypes = [vp, u32]
+    L.defer_gpu_cache_truncate.restype = ctypes.c_int
+    L.defer_gpu_cache_clone.argtypes = [vp, P(vp)]
+    L.defer_gpu_cache_clone.restype = ctypes.c_int
+    L.defer_gpu_cache_read.argtypes = [vp, u32, vp, vp]
+    L.defer_gpu_cache_read.restype = ctypes.c_int
+    L.defer_gpu_forward.argtypes = [vp, vp, u32, vp, sz, vp, vp]
+    L.defer_gpu_forward.restype = ctypes.c_int
+    L.defer_gpu_last_logits.argtypes = [vp, vp]
+    L.defer_gpu_last_logits.restype = ctypes.c_int
+    L.defer_gpu_sample.argtypes = [vp, vp, f32, u32, P(u32)]
+    L.defer_gpu_sample.restype = ctypes.c_int
+    L.defer_gpu_step.argtypes = [vp, vp, f32, u32, P(u32)]
+    L.defer_gpu_step.restype = ctypes.c_int
+    L.defer_gpu_generate.argtypes = [vp, vp, u32, f32, vp, vp, sz, vp, P(u32)]
+    L.defer_gpu_generate.restype = ctypes.c_int
+    L.defer_gpu_prompt.argtypes = [vp, vp, vp, sz]
+    L.defer_gpu_prompt.restype = ctypes.c_int
+    L.defer_gpu_replay.argtypes = [vp, vp, vp, sz, sz, f32, vp, P(ctypes.c_int64), P(u32)]
+    L.defer_gpu_replay.restype = ctypes.c_int
+    L.defer_gpu_last_error.argtypes = []
+    L.defer_gpu_last_error.restype = ctypes.c_char_p
+    L.defer_gpu_last_device_ms.argtypes = [vp]
+    L.defer_gpu_last_device_ms.restype = ctypes.c_double
+    _lib = L
+    return L
+
+
+def _check(rc: int) -> None:
+    if rc != OK:
+        msg = lib().defer_gpu_last_error().decode(errors="replace")
+        raise DeferGpuError(rc, msg)
+
+
+def _u32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.uint32))
+
+
+def _ptr(a: Optional[np.ndarray]):
+    return None if a is None else ctypes.c_void_p(a.ctypes.data)
+
+
+def tensor_count(cfg: Config) -> int:
+    return int(lib().defer_gpu_model_tensor_count(ctypes.byref(cfg)))
+
+
+class GpuModel:
+    """Weights resident in HBM (Model::from_safetensors, model.rs:301-363)."""
+
+    def __init__(self, cfg: Config, tensors: Sequence[np.ndarray]):
+        self.cfg = cfg
+        arrs = [np.ascontiguousarray(t, dtype=np.float32) for t in tensors]
+        ptrs = (ctypes.c_void_p * len(arrs))(*[a.ctypes.data for a in arrs])
+        h = ctypes.c_void_p()
+        _check(lib().defer_gpu_model_create(ctypes.byref(cfg), ptrs, len(arrs), 0, ctypes.byref(h)))
+        self._h = h
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            lib().defer_gpu_model_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def vocab_size(self) -> int:
+        return int(self.cfg.vocab_size)
+
+    def set_exec(self, mode: int) -> None:
+        _check(lib().defer_gpu_model_set_exec(self._h, mode))
+
+    def new_cache(self, capacity: int = 0) -> "GpuCache":
+        return GpuCache(self, capacity)
+
+    def forward(self, token: int, cache: "GpuCache", masked: Sequence[int] = (),
+                logits: bool = True) -> Optional[np.ndarray]:
+        """Model::forward_ext (model.rs:394-520); logits copied out if asked."""
+        out = np.empty(self.vocab_size, dtype=np.float32) if logits else None
+        m = _u32(masked) if len(masked) else None
+        _check(lib().defer_gpu_forward(self._h, cache._h, int(token), _ptr(m),
+                                       0 if m is None else len(m), _ptr(out), None))
+        return out
+
+    def prompt(self, cache: "GpuCache", tokens: Sequence[int]) -> None:
+        t = _u32(tokens)
+        _check(lib().defer_gpu_prompt(self._h, cache._h, _ptr(t), len(t)))
+
+    def sample(self, cache: "GpuCache", temperature: float, word: int = 0) -> int:
+        out = ctypes.c_uint32()
+        _check(lib().defer_gpu_sample(self._h, cache._h, float(temperature), int(word) & 0xFFFFFFFF,
+                                      ctypes.byref(out)))
+        return int(out.value)
+
+    def step(self, cache: "GpuCache", temperature: float, word: int = 0) -> int:
+        out = ctypes.c_uint32()
+        _check(lib().defer_gpu_step(self._h, cache._h, float(temperature), int(word) & 0xFFFFFFFF,
+                                    ctypes.byref(out)))
+        return int(out.value)
+
+    def generate(self, cache: "GpuCache", max_tokens: int, temperature: float,
+                 words: Optional[Sequence[int]] = None, stop: Sequence[int] = ()) -> list:
+        w = _u32(words) if words is not None else None
+        if temperature != 0.0 and (w is None or len(w) < max_tokens):
+            raise ValueError("need one rng word per token when temperature > 0")
+        s = _u32(stop) if len(stop) else None
+        out = np.zeros(max(max_tokens, 1), dtype=np.uint32)
+        n = ctypes.c_uint32()
+        _check(lib().defer_gpu_generate(self._h, cache._h, int(max_tokens), float(temperature),
+                                        _ptr(w), _ptr(s), 0 if s is None else len(s), _ptr(out),
+                                        ctypes.byref(n)))
+        return [int(x) for x in out[: n.value]]
+
+    def replay(self, cache: "GpuCache", history: Sequence[int], prompt_len: int,
+               temperature: float, words: Optional[Sequence[int]] = None):
+        """Returns (first_divergence_index or -1, sampled token at it)."""
+        h = _u32(history)
+        w = _u32(words) if words is not None else None
+        fd = ctypes.c_int64(-1)
+        sd = ctypes.c_uint32(0)
+        _check(lib().defer_gpu_replay(self._h, cache._h, _ptr(h), len(h), int(prompt_len),
+                                      float(temperature), _ptr(w), ctypes.byref(fd),
+                                      ctypes.byref(sd)))
+        return int(fd.value), int(sd.value)
+
+    def last_device_ms(self) -> float:
+        return float(lib().defer_gpu_last_device_ms(self._h))
+
+
+class GpuCache:
+    """KvCache (model.rs:182-243), preallocated in HBM."""
+
+    def __init__(self, model: GpuModel, capacity: int = 0, _handle=None):
+        self.model = model
+        if _handle is not None:
+            self._h = _handle
+            return
+        h = ctypes.c_void_p()
+        _check(lib().defer_gpu_cache_create(model._h, int(capacity), ctypes.byref(h)))
+        self._h = h
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            lib().defer_gpu_cache_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __len__(self) -> int:
+        return int(lib().defer_gpu_cache_len(self._h))
+
+    def truncate(self, n: int) -> None:
+        _check(lib().defer_gpu_cache_truncate(self._h, int(n)))
+
+    def clone(self) -> "GpuCache":
+        h = ctypes.c_void_p()
+        _check(lib().defer_gpu_cache_clone(self._h, ctypes.byref(h)))
+        return GpuCache(self.model, _handle=h)
+
+    def read(self, layer: int):
+        """(keys, values) of one layer as [len, kv_dim] arrays."""
+        c = self.model.cfg
+        kvd = c.num_kv_heads * c.head_dim
+        n = len(self)
+        k = np.empty((n, kvd), dtype=np.float32)
+        v = np.empty((n, kvd), dtype=np.float32)
+        _check(lib().defer_gpu_cache_read(self._h, int(layer), _ptr(k), _ptr(v)))
+        return k, v
+
+    def last_logits(self) -> np.ndarray:
+        out = np.empty(self.model.vocab_size, dtype=np.float32)
+        _check(lib().defer_gpu_last_logits(self._h, _ptr(out)))
+        return out
