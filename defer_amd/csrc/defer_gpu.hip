@@ -57,15 +57,16 @@ __device__ __forceinline__ Lds lds_init(const Dims& d) {
   return s;
 }
 
-__device__ bool forward_all(const Args& a, uint32_t tok, uint32_t pos, uint32_t tick, uint32_t wg,
-                            uint32_t G, const Lds& s) {
+__device__ __forceinline__ bool forward_all(const Args& a, uint32_t tok, uint32_t pos, uint32_t tick,
+                                            uint32_t wg, uint32_t G, const Lds& s, Pf& pf) {
   for (uint32_t l = 0; l < a.d.L; ++l) {
-    if (!phase_qkv(a, l, tick, pos, tok, wg, G, s)) return false;
+    pf.next_layer = (l + 1 < a.d.L) ? l + 1 : 0;
+    if (!phase_qkv(a, l, tick, pos, tok, wg, G, s, pf)) return false;
     if (!phase_attn(a, l, tick, pos, wg, G, s)) return false;
     if (!phase_comb(a, l, tick, pos, wg, G, s)) return false;
-    if (!phase_o(a, l, tick, pos, tok, wg, G, s)) return false;
-    if (!phase_gu(a, l, tick, wg, G, s)) return false;
-    if (!phase_d(a, l, tick, wg, G, s)) return false;
+    if (!phase_o(a, l, tick, pos, tok, wg, G, s, pf)) return false;
+    if (!phase_gu(a, l, tick, wg, G, s, pf)) return false;
+    if (!phase_d(a, l, tick, wg, G, s, pf)) return false;
   }
   return phase_lm(a, tick, wg, G, s);
 }
@@ -78,12 +79,21 @@ __device__ __forceinline__ bool is_stop(const RunDesc& r, uint32_t tok) {
 
 // Every op of a run in one launch. All workgroups sample redundantly (same
 // inputs, same code, same token), so no broadcast is needed.
-__global__ __launch_bounds__(BLOCK) void k_persistent(Args a, const RunDesc* run) {
+__global__ __launch_bounds__(BLOCK) void k_persistent(const Args* __restrict__ ap,
+                                                      const RunDesc* __restrict__ run) {
+  const Args& a = *ap;
   const Lds s = lds_init(a.d);
   const RunDesc r = *run;
   DevState* st = a.st;
   uint32_t pos = st->pos, tick = st->tick;
   const uint32_t wg = blockIdx.x, G = gridDim.x;
+  lm_prime(a, s);
+  SlotSet slots;
+  slot_prime(a, slots, 0, wg, G);
+  Pf pf;
+  pf.on = true;
+  pf.SS = &slots;
+  pf.next_layer = 0;
   uint32_t i = 0;
   uint32_t halted = 0;
   for (; i < r.n_ops; ++i) {
@@ -108,7 +118,7 @@ __global__ __launch_bounds__(BLOCK) void k_persistent(Args a, const RunDesc* run
     } else {
       tok = r.tokens[i];
     }
-    if (!forward_all(a, tok, pos, tick, wg, G, s)) break;
+    if (!forward_all(a, tok, pos, tick, wg, G, s, pf)) break;
     ++pos;
     ++tick;
     if (r.mode == RUN_GENERATE && is_stop(r, tok)) {
@@ -137,26 +147,37 @@ __global__ void k_begin(DevState* st) {
 
 enum : uint32_t { PH_LM_KERNEL = 100 };
 
-__global__ __launch_bounds__(BLOCK) void k_phase(Args a, uint32_t ph, uint32_t layer) {
+__global__ __launch_bounds__(BLOCK) void k_phase(const Args* __restrict__ ap, uint32_t ph,
+                                                 uint32_t layer) {
+  const Args& a = *ap;
   const Lds s = lds_init(a.d);
   const DevState* st = a.st;
   if (st->halt) return;
   const uint32_t pos = st->pos, tick = st->tick, token = st->token;
   const uint32_t wg = blockIdx.x, G = gridDim.x;
+  Pf pf;
+  pf.on = false;
+  pf.SS = nullptr;
+  pf.next_layer = 0;
   switch (ph) {
-    case PH_QKV: phase_qkv(a, layer, tick, pos, token, wg, G, s); break;
+    case PH_QKV: phase_qkv(a, layer, tick, pos, token, wg, G, s, pf); break;
     case PH_ATTN: phase_attn(a, layer, tick, pos, wg, G, s); break;
     case PH_COMB: phase_comb(a, layer, tick, pos, wg, G, s); break;
-    case PH_O: phase_o(a, layer, tick, pos, token, wg, G, s); break;
-    case PH_GU: phase_gu(a, layer, tick, wg, G, s); break;
-    case PH_D: phase_d(a, layer, tick, wg, G, s); break;
-    case PH_LM_KERNEL: phase_lm(a, tick, wg, G, s); break;
+    case PH_O: phase_o(a, layer, tick, pos, token, wg, G, s, pf); break;
+    case PH_GU: phase_gu(a, layer, tick, wg, G, s, pf); break;
+    case PH_D: phase_d(a, layer, tick, wg, G, s, pf); break;
+    case PH_LM_KERNEL:
+      lm_prime(a, s);
+      phase_lm(a, tick, wg, G, s);
+      break;
     default: break;
   }
 }
 
 // Sampler stage A for the op in flight (no-op when it does not sample).
-__global__ __launch_bounds__(BLOCK) void k_samp_a(Args a, const RunDesc* run) {
+__global__ __launch_bounds__(BLOCK) void k_samp_a(const Args* __restrict__ ap,
+                                                  const RunDesc* __restrict__ run) {
+  const Args& a = *ap;
   const Lds s = lds_init(a.d);
   const DevState* st = a.st;
   if (st->halt) return;
@@ -166,7 +187,9 @@ __global__ __launch_bounds__(BLOCK) void k_samp_a(Args a, const RunDesc* run) {
 }
 
 // One workgroup: sampler stage B (if the op samples) and the token to feed.
-__global__ __launch_bounds__(BLOCK) void k_op(Args a, const RunDesc* run) {
+__global__ __launch_bounds__(BLOCK) void k_op(const Args* __restrict__ ap,
+                                              const RunDesc* __restrict__ run) {
+  const Args& a = *ap;
   const Lds s = lds_init(a.d);
   DevState* st = a.st;
   if (st->halt) return;
@@ -197,8 +220,8 @@ __global__ __launch_bounds__(BLOCK) void k_op(Args a, const RunDesc* run) {
   if (threadIdx.x == 0) st->token = tok;
 }
 
-__global__ void k_commit(Args a, const RunDesc* run) {
-  DevState* st = a.st;
+__global__ void k_commit(const Args* __restrict__ ap, const RunDesc* __restrict__ run) {
+  DevState* st = ap->st;
   if (st->halt) return;
   st->pos += 1;
   st->tick += 1;
@@ -266,7 +289,8 @@ struct defer_gpu_cache {
   uint32_t tick = 0;
   bool has_logits = false;
   hipGraphExec_t graph = nullptr;
-  Args args;
+  Args args;       // host copy
+  Args* d_args = nullptr;  // device copy the kernels read
 };
 
 static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -296,6 +320,8 @@ static int validate(const defer_gpu_config* c) {
   const uint64_t mx = std::max<uint64_t>({c->hidden_size, q, c->intermediate_size});
   if (mx > 32ull * BLOCK) return fail(DEFER_GPU_E_INVALID, "vector length %llu too large",
                                       (unsigned long long)mx);
+  if (c->hidden_size > (uint32_t)NWK * BLOCK)
+    return fail(DEFER_GPU_E_INVALID, "hidden_size %u above %u", c->hidden_size, NWK * BLOCK);
   if (c->activation > 1) return fail(DEFER_GPU_E_INVALID, "unsupported activation");
   return DEFER_GPU_OK;
 }
@@ -353,14 +379,16 @@ extern "C" int defer_gpu_model_create(const defer_gpu_config* cfg, const float* 
   m->G = std::min<uint32_t>((uint32_t)prop.multiProcessorCount, min_items);
 
   d.lds_vec = (std::max({d.h, d.q, d.ff}) + 3) & ~3u;
+  d.lds_vec2 = (2 * d.h + 3) & ~3u;
   const uint32_t hs = d.hd + 2;
   const uint32_t rmax = (d.h + m->G - 1) / m->G;
-  const uint32_t scr_attn = d.group * d.hd + 2 * d.hd + NWAVES * d.group * hs;
+  const uint32_t scr_attn = d.group * d.hd + 2 * d.hd + NWA * d.group * hs;
   const uint32_t scr_o = INLINE_COMB_MAX + rmax;
   const uint32_t scr_comb = MAX_ACHUNKS * hs;
   const uint32_t scr_samp = 3 * d.nvc + VCHUNK + NWAVES + 2 + NWAVES * VCHUNK;
-  d.lds_scr = (std::max({scr_attn, scr_o, scr_comb, scr_samp, 2 * NWAVES}) + 3) & ~3u;
-  m->lds_bytes = (size_t)(4 + 64 + d.lds_vec + d.lds_scr) * sizeof(float);
+  const uint32_t scr_lm = ((d.nvc + m->G - 1) / m->G) * VCHUNK;
+  d.lds_scr = (std::max({scr_attn, scr_o, scr_comb, scr_samp, scr_lm, 2 * NWAVES}) + 3) & ~3u;
+  m->lds_bytes = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr) * sizeof(float);
 
   // Weight layout: one allocation, each tensor 256-byte aligned; q/k/v rows
   // are stored back to back as one [q + 2kv, h] matrix.
@@ -398,28 +426,50 @@ extern "C" int defer_gpu_model_create(const defer_gpu_config* cfg, const float* 
   auto up = [&](size_t o, const float* src, size_t n) {
     return hipMemcpy(base + o, src, n * sizeof(float), hipMemcpyHostToDevice);
   };
+  // A matrix that consumes an RMSNorm output is stored with the norm weight
+  // folded into its columns, W'[r][j] = W[r][j] * w_norm[j], so the kernels
+  // compute (x * inv) * w_norm . W as inv * (W' . x). Unit norm weights leave
+  // the matrix bit-identical.
+  std::vector<float> stage;
+  auto up_folded = [&](size_t o, const float* src, size_t rows, const float* wn) {
+    bool unit = true;
+    for (size_t j = 0; j < h && unit; ++j) unit = (wn[j] == 1.0f);
+    if (unit) return up(o, src, rows * h);
+    const size_t chunk_rows = std::max<size_t>(1, (size_t)(4u << 20) / h);
+    stage.resize(chunk_rows * h);
+    for (size_t r0 = 0; r0 < rows; r0 += chunk_rows) {
+      const size_t nr = std::min(chunk_rows, rows - r0);
+      for (size_t r = 0; r < nr; ++r)
+        for (size_t j = 0; j < h; ++j) stage[r * h + j] = src[(r0 + r) * h + j] * wn[j];
+      const hipError_t er = up(o + r0 * h * sizeof(float), stage.data(), nr * h);
+      if (er != hipSuccess) return er;
+    }
+    return hipSuccess;
+  };
   size_t k = 0;
   e = up(o_embed, tensors[k++], V * h);
   for (uint32_t l = 0; l < d.L && e == hipSuccess; ++l) {
-    e = up(lo[l].an, tensors[k++], h);
+    const float* an = tensors[k++];
+    e = up(lo[l].an, an, h);
     const float* wq = tensors[k++];
     const float* bq = d.has_bias ? tensors[k++] : nullptr;
     const float* wk = tensors[k++];
     const float* bk = d.has_bias ? tensors[k++] : nullptr;
     const float* wv = tensors[k++];
     const float* bv = d.has_bias ? tensors[k++] : nullptr;
-    if (e == hipSuccess) e = up(lo[l].qkv, wq, q * h);
-    if (e == hipSuccess) e = up(lo[l].qkv + q * h * sizeof(float), wk, kv * h);
-    if (e == hipSuccess) e = up(lo[l].qkv + (q + kv) * h * sizeof(float), wv, kv * h);
+    if (e == hipSuccess) e = up_folded(lo[l].qkv, wq, q, an);
+    if (e == hipSuccess) e = up_folded(lo[l].qkv + q * h * sizeof(float), wk, kv, an);
+    if (e == hipSuccess) e = up_folded(lo[l].qkv + (q + kv) * h * sizeof(float), wv, kv, an);
     if (d.has_bias) {
       if (e == hipSuccess) e = up(lo[l].b, bq, q);
       if (e == hipSuccess) e = up(lo[l].b + q * sizeof(float), bk, kv);
       if (e == hipSuccess) e = up(lo[l].b + (q + kv) * sizeof(float), bv, kv);
     }
     if (e == hipSuccess) e = up(lo[l].wo, tensors[k++], h * q);
-    if (e == hipSuccess) e = up(lo[l].fn, tensors[k++], h);
-    if (e == hipSuccess) e = up(lo[l].wg, tensors[k++], ff * h);
-    if (e == hipSuccess) e = up(lo[l].wu, tensors[k++], ff * h);
+    const float* fnw = tensors[k++];
+    if (e == hipSuccess) e = up(lo[l].fn, fnw, h);
+    if (e == hipSuccess) e = up_folded(lo[l].wg, tensors[k++], ff, fnw);
+    if (e == hipSuccess) e = up_folded(lo[l].wu, tensors[k++], ff, fnw);
     if (e == hipSuccess) e = up(lo[l].wd, tensors[k++], h * ff);
   }
   if (e == hipSuccess) e = up(o_norm, tensors[k++], h);
@@ -547,6 +597,13 @@ static int cache_alloc(const defer_gpu_model* m, uint32_t cap, defer_gpu_cache* 
   a.mb_vsum = p; p += d.nvc;
   a.st = c->st;
   a.mask = nullptr;
+  HIP_TRY(hipMalloc(&c->d_args, sizeof(Args)));
+  HIP_TRY(hipMemcpy(c->d_args, &a, sizeof(Args), hipMemcpyHostToDevice));
+  return DEFER_GPU_OK;
+}
+
+static int sync_args(defer_gpu_cache* c) {
+  HIP_TRY(hipMemcpy(c->d_args, &c->args, sizeof(Args), hipMemcpyHostToDevice));
   return DEFER_GPU_OK;
 }
 
@@ -566,6 +623,7 @@ static void cache_free(defer_gpu_cache* c) {
   (void)hipFree(c->d_out);
   (void)hipFree(c->d_logits);
   (void)hipFree(c->d_tmp);
+  (void)hipFree(c->d_args);
 }
 
 extern "C" int defer_gpu_cache_create(const defer_gpu_model* m, uint32_t capacity,
@@ -692,7 +750,7 @@ static int ensure_run_buffers(defer_gpu_cache* c, size_t n_ops, size_t n_stop) {
 static int launch_op_kernels(defer_gpu_cache* c, hipStream_t s) {
   const defer_gpu_model* m = c->m;
   const Dims& d = m->d;
-  const Args& a = c->args;
+  const Args* a = c->d_args;
   const uint32_t G = m->G;
   const size_t lds = m->lds_bytes;
   k_samp_a<<<G, BLOCK, lds, s>>>(a, c->d_run);
@@ -716,7 +774,7 @@ static int run_ops(defer_gpu_cache* c, RunDesc r, bool force_eager) {
   const uint32_t mode = force_eager ? DEFER_GPU_EXEC_EAGER : m->exec_mode;
   if (r.n_ops > 0) {
     if (mode == DEFER_GPU_EXEC_PERSISTENT) {
-      Args a = c->args;
+      const Args* a = c->d_args;
       const RunDesc* dr = c->d_run;
       void* params[] = {&a, &dr};
       HIP_TRY(hipLaunchCooperativeKernel((const void*)k_persistent, dim3(m->G), dim3(BLOCK),
@@ -831,9 +889,17 @@ extern "C" int defer_gpu_forward(const defer_gpu_model* m, defer_gpu_cache* c, u
       HIP_TRY(hipMemcpy(c->d_mask, bits.data(), bits.size() * sizeof(uint32_t),
                         hipMemcpyHostToDevice));
   }
-  if (use_mask) c->args.mask = c->d_mask;
+  if (use_mask) {
+    c->args.mask = c->d_mask;
+    rc = sync_args(c);
+    if (rc) return rc;
+  }
   rc = feed_tokens(m, c, &token, 1, use_mask);
-  c->args.mask = nullptr;
+  if (use_mask) {
+    c->args.mask = nullptr;
+    const int rc2 = sync_args(c);
+    if (!rc) rc = rc2;
+  }
   if (rc) return rc;
   return logits_out ? copy_logits(c, logits_out) : DEFER_GPU_OK;
 }
@@ -921,8 +987,8 @@ extern "C" int defer_gpu_sample(const defer_gpu_model* m, defer_gpu_cache* c, fl
   const hipStream_t s = m->stream;
   HIP_TRY(hipMemcpyAsync(c->d_run, &r, sizeof(r), hipMemcpyHostToDevice, s));
   k_begin<<<1, 1, 0, s>>>(c->st);
-  k_samp_a<<<m->G, BLOCK, m->lds_bytes, s>>>(c->args, c->d_run);
-  k_op<<<1, BLOCK, m->lds_bytes, s>>>(c->args, c->d_run);
+  k_samp_a<<<m->G, BLOCK, m->lds_bytes, s>>>(c->d_args, c->d_run);
+  k_op<<<1, BLOCK, m->lds_bytes, s>>>(c->d_args, c->d_run);
   HIP_TRY(hipGetLastError());
   HIP_TRY(hipStreamSynchronize(s));
   const DevState h = read_state(c);

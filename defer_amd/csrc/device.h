@@ -25,8 +25,8 @@ constexpr uint32_t WAVE = 64;
 constexpr uint32_t BLOCK = 512;
 constexpr uint32_t NWAVES = BLOCK / WAVE;
 constexpr uint32_t VCHUNK = 64;        // vocabulary rows per sampling chunk
-constexpr uint32_t ACHUNK = 64;        // attention positions per chunk (base size)
-constexpr uint32_t MAX_ACHUNKS = 8;    // attention chunks per head at most
+constexpr uint32_t ACHUNK = 128;       // attention positions per chunk (base size)
+constexpr uint32_t MAX_ACHUNKS = 3;    // attention chunks per head at most
 constexpr uint32_t INLINE_COMB_MAX = 8192;  // floats of partials combined inside the O phase
 constexpr uint32_t SPIN_LIMIT = 1u << 21;
 constexpr uint32_t NO_INDEX = 0xffffffffu;
@@ -40,6 +40,7 @@ struct Dims {
   uint32_t kvs;        // KV row stride in floats (>= 32: rows never share a 128-byte line)
   uint32_t nvc;        // number of vocabulary chunks
   uint32_t lds_vec;    // floats of the input-vector LDS region
+  uint32_t lds_vec2;   // floats of the second vector region (h)
   uint32_t lds_scr;    // floats of the scratch LDS region
   float eps, scale;
 };
@@ -142,26 +143,65 @@ __host__ __device__ inline bool comb_inline(const Dims& d, uint32_t pos) {
 }
 
 // --------------------------------------------------------- memory helpers
+//
+// Explicit address spaces: pointers reach the kernels inside structs, so the
+// compiler would otherwise emit flat instructions, which count against both
+// the vector-memory and the LDS wait counters; a later LDS access would then
+// wait for every outstanding HBM load and undo the prefetching.
+
+#define AS_GLOBAL __attribute__((address_space(1)))
+#define AS_LDS __attribute__((address_space(3)))
+
+// Address-space casts go through an integer: a direct cast from a generic
+// pointer is dropped by the front end. A generic LDS address holds the LDS
+// offset in its low 32 bits (the same truncation the flat-to-LDS cast does).
+template <class T>
+__device__ __forceinline__ AS_GLOBAL T* gptr(T* p) {
+  return (AS_GLOBAL T*)(uintptr_t)p;
+}
+template <class T>
+__device__ __forceinline__ AS_LDS T* lptr(T* p) {
+  return (AS_LDS T*)(uintptr_t)(uint32_t)(uintptr_t)p;
+}
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float4 ldg4(const float* p) {
+  const v4f x = *gptr(reinterpret_cast<const v4f*>(p));
+  return make_float4(x.x, x.y, x.z, x.w);
+}
+__device__ __forceinline__ float ldg(const float* p) { return *gptr(p); }
+__device__ __forceinline__ float2 ldg2(const float2* p) {
+  const v2f x = *gptr(reinterpret_cast<const v2f*>(p));
+  return make_float2(x.x, x.y);
+}
+__device__ __forceinline__ uint32_t ldg_u32(const uint32_t* p) { return *gptr(p); }
+__device__ __forceinline__ float4 lds4(const float* p) {
+  const v4f x = *lptr(reinterpret_cast<const v4f*>(p));
+  return make_float4(x.x, x.y, x.z, x.w);
+}
+__device__ __forceinline__ float lds_ld(const float* p) { return *lptr(p); }
+__device__ __forceinline__ void lds_st(float* p, float v) { *lptr(p) = v; }
 
 __device__ __forceinline__ void mb_put(u64* slot, float v, uint32_t gen) {
   const u64 w = ((u64)gen << 32) | (u64)__float_as_uint(v);
-  __hip_atomic_store(slot, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(gptr(slot), w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ u64 mb_load(const u64* slot) {
-  return __hip_atomic_load(const_cast<u64*>(slot), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_load(gptr(const_cast<u64*>(slot)), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void st_coherent(float* p, float v) {
-  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
+  __hip_atomic_store(gptr(reinterpret_cast<uint32_t*>(p)), __float_as_uint(v), __ATOMIC_RELAXED,
                      __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ uint32_t ld_coherent_u32(const uint32_t* p) {
-  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_load(gptr(const_cast<uint32_t*>(p)), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void st_coherent_u32(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float4 ld4(const float* p) {
-  return *reinterpret_cast<const float4*>(p);
+  __hip_atomic_store(gptr(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // --------------------------------------------------------- reductions
@@ -183,46 +223,94 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
   v = wave_sum(v);
   __syncthreads();
-  if (lane == 0) red[wave] = v;
+  if (lane == 0) lds_st(red + wave, v);
   __syncthreads();
   float s = 0.0f;
 #pragma unroll
-  for (uint32_t w = 0; w < NWAVES; ++w) s += red[w];
+  for (uint32_t w = 0; w < NWAVES; ++w) s += lds_ld(red + w);
   return s;
 }
 
-// Per-lane partial of a row dot product: w[j] * x[j] for j = 4*lane + 256*k,
-// in ascending j, one fused multiply-add per element. K % 4 == 0.
+// Row dot products. Lane `lane` owns the float4s at j = 4*lane + 256*k of a
+// row; its partial sum runs over them in ascending j with one fused
+// multiply-add per element, then wave_sum() adds the 64 partials. That order
+// is the same however the loads are scheduled, so the helpers below (all
+// loads of a row issued at once, optionally before the row's input vector is
+// available) all give identical bits.
+constexpr int KF = 6;  // float4 per lane held in registers: rows of up to 1536 floats
+
+template <int NF>
+struct RowT {
+  float4 v[NF];
+};
+typedef RowT<KF> Row;
+
+template <int NF>
+__device__ __forceinline__ void row_load(RowT<NF>& r, const float* __restrict__ w, uint32_t K,
+                                         uint32_t lane) {
+#pragma unroll
+  for (int k = 0; k < NF; ++k) {
+    const uint32_t j = lane * 4 + 256u * k;
+    if (j < K) r.v[k] = ldg4(w + j);
+  }
+}
+
+template <int NF>
+__device__ __forceinline__ float row_fma(const RowT<NF>& r, const float* __restrict__ x,
+                                         uint32_t K, uint32_t lane, float acc) {
+#pragma unroll
+  for (int k = 0; k < NF; ++k) {
+    const uint32_t j = lane * 4 + 256u * k;
+    if (j < K) {
+      const float4 xv = lds4(x + j);
+      acc = fmaf(r.v[k].x, xv.x, acc);
+      acc = fmaf(r.v[k].y, xv.y, acc);
+      acc = fmaf(r.v[k].z, xv.z, acc);
+      acc = fmaf(r.v[k].w, xv.w, acc);
+    }
+  }
+  return acc;
+}
+
+// Lane partial of w . x given the row's first 256*NF floats already loaded
+// into `r`; longer rows stream the rest segment by segment through the same
+// registers (so `r` is consumed).
+template <int NF>
+__device__ __forceinline__ float dot_tail(RowT<NF>& r, const float* __restrict__ w,
+                                          const float* __restrict__ x, uint32_t K,
+                                          uint32_t lane) {
+  float acc = row_fma(r, x, K, lane, 0.0f);
+  for (uint32_t base = 256u * NF; base < K; base += 256u * NF) {
+    row_load(r, w + base, K - base, lane);
+    acc = row_fma(r, x + base, K - base, lane, acc);
+  }
+  return acc;
+}
+
 __device__ __forceinline__ float dot_partial(const float* __restrict__ w,
                                              const float* __restrict__ x, uint32_t K,
                                              uint32_t lane) {
-  float acc = 0.0f;
-  uint32_t j = lane * 4;
-  for (; j + 768 < K; j += 1024) {
-    const float4 a = ld4(w + j), b = ld4(w + j + 256), c = ld4(w + j + 512), e = ld4(w + j + 768);
-    const float4 xa = ld4(x + j), xb = ld4(x + j + 256), xc = ld4(x + j + 512),
-                 xe = ld4(x + j + 768);
-    acc = fmaf(a.x, xa.x, acc); acc = fmaf(a.y, xa.y, acc);
-    acc = fmaf(a.z, xa.z, acc); acc = fmaf(a.w, xa.w, acc);
-    acc = fmaf(b.x, xb.x, acc); acc = fmaf(b.y, xb.y, acc);
-    acc = fmaf(b.z, xb.z, acc); acc = fmaf(b.w, xb.w, acc);
-    acc = fmaf(c.x, xc.x, acc); acc = fmaf(c.y, xc.y, acc);
-    acc = fmaf(c.z, xc.z, acc); acc = fmaf(c.w, xc.w, acc);
-    acc = fmaf(e.x, xe.x, acc); acc = fmaf(e.y, xe.y, acc);
-    acc = fmaf(e.z, xe.z, acc); acc = fmaf(e.w, xe.w, acc);
-  }
-  for (; j < K; j += 256) {
-    const float4 a = ld4(w + j);
-    const float4 xa = ld4(x + j);
-    acc = fmaf(a.x, xa.x, acc); acc = fmaf(a.y, xa.y, acc);
-    acc = fmaf(a.z, xa.z, acc); acc = fmaf(a.w, xa.w, acc);
-  }
-  return acc;
+  Row r;
+  row_load(r, w, K, lane);
+  return dot_tail(r, w, x, K, lane);
 }
 
 __device__ __forceinline__ float dot_row(const float* __restrict__ w, const float* __restrict__ x,
                                          uint32_t K, uint32_t lane) {
   return wave_sum(dot_partial(w, x, K, lane));
+}
+
+// Norm weights of one vector, the thread's elements i = tid + BLOCK*k.
+constexpr int NWK = 8;  // vectors of up to 8 * BLOCK floats
+struct NormW {
+  float v[NWK];
+};
+__device__ __forceinline__ void norm_load(NormW& nw, const float* __restrict__ w, uint32_t n) {
+#pragma unroll
+  for (int k = 0; k < NWK; ++k) {
+    const uint32_t i = threadIdx.x + BLOCK * k;
+    if (i < n) nw.v[k] = ldg(w + i);
+  }
 }
 
 // ----------------------------------------------------------- activation

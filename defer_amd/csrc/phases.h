@@ -4,17 +4,32 @@
 // runs them back to back; the per-phase kernels run one each. Work items are
 // dealt round-robin (item = wg + G*k), and an item is always computed the
 // same way whoever computes it.
+//
+// Roles inside a workgroup (BLOCK = 512 threads = 8 waves):
+//  * waves 0..NPOLL-1 are pollers: in the matvec phases they alone read
+//    mailboxes, so their in-order load counter never holds a weight load
+//    and a poll completes as soon as its data is there;
+//  * waves NPOLL.. are compute waves: each owns the matvec items dealt to it
+//    and keeps the rows of its first NSLOT items in register slots, each
+//    refilled for the next layer right after use (persistent kernel only),
+//    so the weights of a phase are in registers before its inputs arrive.
 #pragma once
 
 #include "device.h"
 
 namespace dg {
 
+constexpr uint32_t NPOLL = 2;
+constexpr uint32_t NCW = NWAVES - NPOLL;
+constexpr uint32_t NSLOT = 2;
+constexpr int KS = 3;  // float4 per lane in half a slot: 768 floats
+
 struct Lds {
   WaitCtl* ctl;
-  float* red;  // 64 floats
-  float* vec;  // d.lds_vec floats: the matvec input vector
-  float* scr;  // d.lds_scr floats
+  float* red;   // 64 floats
+  float* vec;   // d.lds_vec floats: the matvec input vector
+  float* vec2;  // d.lds_vec2 floats: the normalised lm_head input
+  float* scr;   // d.lds_scr floats
 };
 
 __device__ inline Lds lds_layout(float* base, const Dims& d) {
@@ -22,7 +37,8 @@ __device__ inline Lds lds_layout(float* base, const Dims& d) {
   s.ctl = reinterpret_cast<WaitCtl*>(base);
   s.red = base + 4;
   s.vec = base + 4 + 64;
-  s.scr = s.vec + d.lds_vec;
+  s.vec2 = s.vec + d.lds_vec;
+  s.scr = s.vec2 + d.lds_vec2;
   return s;
 }
 
@@ -34,124 +50,376 @@ struct Gather {
   float* dst;
 };
 
-__device__ inline Gather gather_vec(const u64* src, uint32_t n, uint32_t gen, float* dst) {
+__device__ __forceinline__ Gather gather_strided(const u64* src, uint32_t seg_len, uint32_t n_seg,
+                                                 uint32_t src_stride, uint32_t gen, float* dst) {
   Gather g;
   g.src = src;
-  g.seg_len = n;
-  g.n_seg = 1;
-  g.src_stride = 0;
+  g.seg_len = seg_len;
+  g.n_seg = n_seg;
+  g.src_stride = src_stride;
   g.gen = gen;
   g.dst = dst;
   return g;
 }
+__device__ __forceinline__ Gather gather_vec(const u64* src, uint32_t n, uint32_t gen, float* dst) {
+  return gather_strided(src, n, 1, 0, gen, dst);
+}
+__device__ __forceinline__ Gather no_gather() { return gather_strided(nullptr, 0, 0, 0, 0, nullptr); }
 
-// Block-wide wait for up to three gathers at once (one polling loop, so the
-// round trips overlap). Returns false, uniformly, if the run was aborted.
-__device__ bool wait_gather(const Gather* gs, uint32_t ng, DevState* st, WaitCtl* ctl) {
+
+// Word offset of element e of a gather from its source.
+__device__ __forceinline__ uint32_t gather_off(const Gather& g, uint32_t e) {
+  if (g.n_seg <= 1) return e;
+  const uint32_t seg = e / g.seg_len;
+  return seg * g.src_stride + (e - seg * g.seg_len);
+}
+
+// One polling round of gather g for this lane: P words in flight.
+template <uint32_t P>
+struct PollState {
+  uint32_t pend;
+  u64 w[P > 0 ? P : 1];
+};
+
+template <uint32_t P>
+__device__ __forceinline__ void poll_init(PollState<P>& ps, const Gather& g, uint32_t n,
+                                          uint32_t base, uint32_t tid, uint32_t npl) {
+  ps.pend = 0;
+#pragma unroll
+  for (uint32_t k = 0; k < P; ++k)
+    if (base + tid + k * npl < n) ps.pend |= 1u << k;
+}
+template <uint32_t P>
+__device__ __forceinline__ void poll_issue(PollState<P>& ps, const Gather& g, uint32_t base,
+                                           uint32_t tid, uint32_t npl) {
+#pragma unroll
+  for (uint32_t k = 0; k < P; ++k)
+    if (ps.pend & (1u << k)) ps.w[k] = mb_load(g.src + gather_off(g, base + tid + k * npl));
+}
+template <uint32_t P>
+__device__ __forceinline__ void poll_check(PollState<P>& ps, const Gather& g, uint32_t base,
+                                           uint32_t tid, uint32_t npl) {
+#pragma unroll
+  for (uint32_t k = 0; k < P; ++k)
+    if ((ps.pend & (1u << k)) && (uint32_t)(ps.w[k] >> 32) == g.gen) {
+      lds_st(g.dst + base + tid + k * npl, __uint_as_float((uint32_t)ps.w[k]));
+      ps.pend &= ~(1u << k);
+    }
+}
+
+__device__ __forceinline__ uint32_t rounds_for(uint32_t n, uint32_t per_round) {
+  return per_round ? (n + per_round - 1) / per_round : (n ? 0xffffffffu : 0u);
+}
+
+// Wait until every element of up to three gathers carries its generation and
+// copy the values to LDS. Only the first `npoll_waves` waves read memory; a
+// polling lane keeps P0 + P1 + P2 words in flight per round (sized to the call
+// site), loops until its own words are all current, and the block then meets
+// at a barrier. Returns false (uniformly) if the run was aborted.
+template <uint32_t P0, uint32_t P1 = 0, uint32_t P2 = 0>
+__device__ __forceinline__ bool poll_gather(const Gather& g0, const Gather& g1, const Gather& g2,
+                                            uint32_t npoll_waves, DevState* st, WaitCtl* ctl) {
   const uint32_t tid = threadIdx.x;
-  // The destination LDS may still be read by slower waves of the previous
-  // phase: no wave writes it before every wave has arrived here.
+  const uint32_t npl = npoll_waves * WAVE;
+  // The destination LDS may still be read by the previous phase.
   __syncthreads();
-  uint32_t n[3] = {0, 0, 0};
-  uint32_t total = 0;
-  for (uint32_t k = 0; k < ng; ++k) {
-    n[k] = gs[k].seg_len * gs[k].n_seg;
-    total += n[k];
+  if (tid < npl) {
+    const uint32_t n0 = g0.seg_len * g0.n_seg, n1 = g1.seg_len * g1.n_seg;
+    const uint32_t n2 = g2.seg_len * g2.n_seg;
+    const uint32_t rounds = max(max(rounds_for(n0, P0 * npl), rounds_for(n1, P1 * npl)),
+                                rounds_for(n2, P2 * npl));
+    for (uint32_t r = 0; r < rounds; ++r) {
+      PollState<P0> s0;
+      PollState<P1> s1;
+      PollState<P2> s2;
+      poll_init(s0, g0, n0, r * P0 * npl, tid, npl);
+      poll_init(s1, g1, n1, r * P1 * npl, tid, npl);
+      poll_init(s2, g2, n2, r * P2 * npl, tid, npl);
+      for (uint32_t spins = 0;; ++spins) {
+        poll_issue(s0, g0, r * P0 * npl, tid, npl);
+        poll_issue(s1, g1, r * P1 * npl, tid, npl);
+        poll_issue(s2, g2, r * P2 * npl, tid, npl);
+        poll_check(s0, g0, r * P0 * npl, tid, npl);
+        poll_check(s1, g1, r * P1 * npl, tid, npl);
+        poll_check(s2, g2, r * P2 * npl, tid, npl);
+        if (__all((s0.pend | s1.pend | s2.pend) == 0)) break;
+        if (spins >= SPIN_LIMIT) {
+          st_coherent_u32(&st->abort, 1u);
+          ctl->abort_seen = 1;
+          break;
+        }
+        if ((spins & 63) == 63 && ld_coherent_u32(&st->abort)) {
+          ctl->abort_seen = 1;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+      if (ctl->abort_seen) break;
+    }
   }
-  const uint32_t nk = (total + BLOCK - 1) / BLOCK;
-  uint32_t pend = 0;
-  for (uint32_t k = 0; k < nk && k < 32; ++k)
-    if (tid + k * BLOCK < total) pend |= 1u << k;
-  for (uint32_t spins = 0;; ++spins) {
-    for (uint32_t k = 0; k < nk && k < 32; ++k) {
-      if (!(pend & (1u << k))) continue;
-      uint32_t e = tid + k * BLOCK;
-      uint32_t which = 0;
-      while (which + 1 < ng && e >= n[which]) {
-        e -= n[which];
-        ++which;
-      }
-      const Gather& g = gs[which];
-      const uint32_t seg = e / g.seg_len, off = e - seg * g.seg_len;
-      const u64 w = mb_load(g.src + (size_t)seg * g.src_stride + off);
-      if ((uint32_t)(w >> 32) == g.gen) {
-        g.dst[e] = __uint_as_float((uint32_t)w);
-        pend &= ~(1u << k);
-      }
-    }
-    if (tid == 0) {
-      if (spins >= SPIN_LIMIT) {
-        st_coherent_u32(&st->abort, 1u);
-        ctl->abort_seen = 1;
-      } else if ((spins & 63) == 63 && ld_coherent_u32(&st->abort)) {
-        ctl->abort_seen = 1;
-      }
-    }
-    const int pending = __syncthreads_count(pend != 0);
-    if (ctl->abort_seen) return false;
-    if (pending == 0) {
-      __syncthreads();
-      return true;
-    }
-    __builtin_amdgcn_s_sleep(1);
-  }
+  __syncthreads();
+  return ctl->abort_seen == 0;
 }
 
-// In-place RMSNorm of v[0..n) in LDS (ops.rs:84-95): inv = 1/sqrt(ss/n + eps),
-// out = x * inv * w. ss is a fixed-tree sum.
-__device__ void rmsnorm_lds(float* v, const float* __restrict__ w, uint32_t n, float eps,
-                            float* red) {
-  float ss = 0.0f;
-  for (uint32_t i = threadIdx.x; i < n; i += BLOCK) ss = fmaf(v[i], v[i], ss);
-  ss = block_sum(ss, red);
-  const float inv = 1.0f / sqrtf(ss / (float)n + eps);
-  for (uint32_t i = threadIdx.x; i < n; i += BLOCK) v[i] = v[i] * inv * w[i];
-  __syncthreads();
+template <uint32_t P0, uint32_t P1>
+__device__ __forceinline__ bool poll_gather(const Gather& g0, const Gather& g1, uint32_t npw,
+                                            DevState* st, WaitCtl* ctl) {
+  return poll_gather<P0, P1, 0>(g0, g1, no_gather(), npw, st, ctl);
+}
+template <uint32_t P0>
+__device__ __forceinline__ bool poll_gather(const Gather& g0, uint32_t npw, DevState* st,
+                                            WaitCtl* ctl) {
+  return poll_gather<P0, 0, 0>(g0, no_gather(), no_gather(), npw, st, ctl);
 }
 
-// x entering layer l: the embedding row (model.rs:428) or the last MLP output.
-__device__ bool load_x(const Args& a, uint32_t l, uint32_t tick, uint32_t token, float* dst,
-                       const Lds& s) {
+// Number of items i = wg + G*k below n owned by this workgroup.
+__device__ __forceinline__ uint32_t rows_owned(uint32_t n, uint32_t wg, uint32_t G) {
+  return wg < n ? (n - wg + G - 1) / G : 0;
+}
+
+// ------------------------------------------------------------- matvec items
+
+enum ItemKind : uint32_t { IK_QKV = 0, IK_O = 1, IK_GU = 2, IK_D = 3 };
+
+// The workgroup's items of every kind, numbered in order QKV, O, GU, D; item
+// number r belongs to compute wave r % NCW and lives in its slot r / NCW
+// (items with r / NCW >= NSLOT are loaded when used).
+struct Deal {
+  uint32_t base[4], cnt[4];
+};
+
+__device__ __forceinline__ Deal deal_of(const Dims& d, uint32_t wg, uint32_t G) {
+  Deal q;
+  q.cnt[IK_QKV] = rows_owned(d.qkv_rows / 2, wg, G);
+  q.cnt[IK_O] = rows_owned(d.h, wg, G);
+  q.cnt[IK_GU] = rows_owned(d.ff, wg, G);
+  q.cnt[IK_D] = rows_owned(d.h, wg, G);
+  q.base[0] = 0;
+  q.base[1] = q.cnt[0];
+  q.base[2] = q.base[1] + q.cnt[1];
+  q.base[3] = q.base[2] + q.cnt[2];
+  return q;
+}
+
+// Registers holding the first 1536 floats of one item: two rows of up to 768
+// (pairs) or one row split in halves.
+struct Slot {
+  RowT<KS> a, b;
+};
+
+// Row pointers and length of item k of a kind in layer l. Pairs give two
+// rows (QKV: rows i and i + hd/2 of one head; GU: gate and up row j).
+struct ItemRows {
+  const float* w0;
+  const float* w1;  // null for single-row kinds
+  uint32_t K;
+};
+
+__device__ __forceinline__ ItemRows item_rows(const Args& a, uint32_t kind, uint32_t l, uint32_t k,
+                                              uint32_t wg, uint32_t G) {
   const Dims& d = a.d;
-  if (l == 0) {
-    __syncthreads();  // dst may still be read by the previous phase
-    const float* e = a.embed + (size_t)token * d.h;
-    for (uint32_t i = threadIdx.x; i < d.h; i += BLOCK) dst[i] = e[i];
-    __syncthreads();
-    return true;
+  const LayerW& W = a.layers[l];
+  const uint32_t it = wg + G * k;
+  ItemRows r;
+  if (kind == IK_QKV) {
+    const uint32_t hb = it / d.half, i = it - hb * d.half;
+    const uint32_t r0 = hb * d.hd + i;
+    r.w0 = W.wqkv + (size_t)r0 * d.h;
+    r.w1 = W.wqkv + (size_t)(r0 + d.half) * d.h;
+    r.K = d.h;
+  } else if (kind == IK_O) {
+    r.w0 = W.wo + (size_t)it * d.q;
+    r.w1 = nullptr;
+    r.K = d.q;
+  } else if (kind == IK_GU) {
+    r.w0 = W.wg + (size_t)it * d.h;
+    r.w1 = W.wu + (size_t)it * d.h;
+    r.K = d.h;
+  } else {
+    r.w0 = W.wd + (size_t)it * d.ff;
+    r.w1 = nullptr;
+    r.K = d.ff;
   }
-  Gather g = gather_vec(a.mb_xd, d.h, gen_of(d, tick, l - 1, PH_D), dst);
-  return wait_gather(&g, 1, a.st, s.ctl);
+  return r;
+}
+
+__device__ __forceinline__ void slot_load(Slot& S, const ItemRows& r, uint32_t lane) {
+  row_load(S.a, r.w0, r.K, lane);
+  if (r.w1)
+    row_load(S.b, r.w1, r.K, lane);
+  else if (r.K > 256u * KS)
+    row_load(S.b, r.w0 + 256u * KS, r.K - 256u * KS, lane);
+}
+
+// Lane partial of w . x over a row whose first 256*KS floats are in `first`
+// and, when `second` is given, the next 256*KS in `second`; the rest streams.
+// Ascending j, one fma per element.
+__device__ __forceinline__ float dot_slot(RowT<KS>& first, RowT<KS>* second, const float* w,
+                                          const float* x, uint32_t K, uint32_t lane) {
+  float acc = row_fma(first, x, K, lane, 0.0f);
+  uint32_t base = 256u * KS;
+  if (second && base < K) {
+    acc = row_fma(*second, x + base, K - base, lane, acc);
+    base += 256u * KS;
+  }
+  for (; base < K; base += 256u * KS) {
+    row_load(first, w + base, K - base, lane);
+    acc = row_fma(first, x + base, K - base, lane, acc);
+  }
+  return acc;
+}
+
+// Lane partial of x . x over the lane's elements of a length-K vector, in
+// the order the dot products visit them.
+__device__ __forceinline__ float sumsq_lane(const float* x, uint32_t K, uint32_t lane) {
+  float ss = 0.0f;
+  for (uint32_t j = lane * 4; j < K; j += 256) {
+    const float4 v = lds4(x + j);
+    ss = fmaf(v.x, v.x, ss);
+    ss = fmaf(v.y, v.y, ss);
+    ss = fmaf(v.z, v.z, ss);
+    ss = fmaf(v.w, v.w, ss);
+  }
+  return ss;
+}
+
+// 1/rms of the length-n vector in LDS (ops.rs:84-95: 1/sqrt(ss/n + eps)).
+// The RMSNorm weight is folded into the consuming matrix columns at load
+// time, so the normalised dot product is inv * (W' . x).
+__device__ __forceinline__ float rms_inv(const float* x, uint32_t n, float eps, uint32_t lane) {
+  const float ss = wave_sum(sumsq_lane(x, n, lane));
+  return 1.0f / sqrtf(ss / (float)n + eps);
+}
+
+// Runs body(k, si) for every item of `kind` dealt to compute wave cw, in item
+// order; si is the item's slot (>= NSLOT: no slot).
+template <class F>
+__device__ __forceinline__ void for_items(const Deal& q, uint32_t kind, uint32_t cw, F body) {
+  const uint32_t b = q.base[kind], n = q.cnt[kind];
+  uint32_t k = (cw + NCW - b % NCW) % NCW;  // first k with (b + k) % NCW == cw
+  for (; k < n; k += NCW) body(k, (b + k) / NCW);
+}
+
+struct SlotSet {
+  Slot s[NSLOT];
+};
+
+// Calls f(slot si) with a statically indexed slot (so slots stay in
+// registers).
+template <class F>
+__device__ __forceinline__ void with_slot(SlotSet& SS, uint32_t si, F f) {
+  static_assert(NSLOT >= 1 && NSLOT <= 3, "with_slot covers up to three slots");
+  if (si == 0)
+    f(SS.s[0]);
+  else if (NSLOT >= 2 && si == 1)
+    f(SS.s[NSLOT >= 2 ? 1 : 0]);
+  else if (NSLOT >= 3)
+    f(SS.s[NSLOT >= 3 ? 2 : 0]);
+}
+
+// Prefetch state of the calling wave.
+struct Pf {
+  bool on;              // the slots hold this layer's rows (persistent kernel)
+  SlotSet* SS;          // this wave's slots
+  uint32_t next_layer;  // layer the refills load
+};
+
+// Refill the slots of compute wave cw that hold items of `kind` with layer
+// l's rows (persistent kernel, right after they were consumed).
+__device__ __forceinline__ void slot_refill(const Args& a, const Deal& q, const Pf& pf, uint32_t cw,
+                                            uint32_t kind, uint32_t wg, uint32_t G, uint32_t lane) {
+  if (!pf.on) return;
+  for_items(q, kind, cw, [&](uint32_t k, uint32_t si) {
+    if (si >= NSLOT) return;
+    const ItemRows r = item_rows(a, kind, pf.next_layer, k, wg, G);
+    with_slot(*pf.SS, si, [&](Slot& S) { slot_load(S, r, lane); });
+  });
+}
+
+// Dot products of one item whose rows are in S against the LDS vector x:
+// y0 (and y1 for pairs). S is consumed.
+__device__ __forceinline__ void slot_dot(Slot& S, const ItemRows& r, const float* x, uint32_t lane,
+                                         float* y0, float* y1) {
+  if (r.w1) {
+    *y0 = wave_sum(dot_slot(S.a, nullptr, r.w0, x, r.K, lane));
+    *y1 = wave_sum(dot_slot(S.b, nullptr, r.w1, x, r.K, lane));
+  } else {
+    *y0 = wave_sum(dot_slot(S.a, &S.b, r.w0, x, r.K, lane));
+    *y1 = 0.0f;
+  }
+}
+
+// Item k of a kind: from its prefetched slot, or loaded now.
+__device__ __forceinline__ void item_dot(const Args& a, uint32_t kind, uint32_t l, uint32_t k,
+                                         uint32_t si, const Pf& pf, const float* x, uint32_t wg,
+                                         uint32_t G, uint32_t lane, float* y0, float* y1) {
+  const ItemRows r = item_rows(a, kind, l, k, wg, G);
+  if (pf.on && si < NSLOT) {
+    with_slot(*pf.SS, si, [&](Slot& S) { slot_dot(S, r, x, lane, y0, y1); });
+  } else {
+    Slot T;
+    slot_load(T, r, lane);
+    slot_dot(T, r, x, lane, y0, y1);
+  }
+}
+
+// Fill the calling compute wave's slots with their items' rows of layer l
+// (persistent kernel start).
+__device__ __forceinline__ void slot_prime(const Args& a, SlotSet& SS, uint32_t l, uint32_t wg,
+                                           uint32_t G) {
+  const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+  if (wave < NPOLL) return;
+  const Deal q = deal_of(a.d, wg, G);
+  Pf pf;
+  pf.on = true;
+  pf.SS = &SS;
+  pf.next_layer = l;
+  for (uint32_t kind = 0; kind < 4; ++kind) slot_refill(a, q, pf, wave - NPOLL, kind, wg, G, lane);
 }
 
 // ------------------------------------------------------------------ QKV
 
 // rmsnorm -> q/k/v rows (+bias) -> RoPE on q and k (model.rs:460-465) ->
-// k, v appended to the cache at `pos` (model.rs:466-467). Work item = a pair
-// of rows (i, i + hd/2) of one head, so RoPE needs no exchange.
-__device__ bool phase_qkv(const Args& a, uint32_t l, uint32_t tick, uint32_t pos, uint32_t token,
-                          uint32_t wg, uint32_t G, const Lds& s) {
+// k, v appended to the cache at `pos` (model.rs:466-467). Item = a pair of
+// rows (i, i + hd/2) of one head, so RoPE needs no exchange.
+__device__ __forceinline__ bool phase_qkv(const Args& a, uint32_t l, uint32_t tick, uint32_t pos,
+                                          uint32_t token, uint32_t wg, uint32_t G, const Lds& s,
+                                          const Pf& pf) {
   const Dims& d = a.d;
-  const LayerW& W = a.layers[l];
-  if (!load_x(a, l, tick, token, s.vec, s)) return false;
-  rmsnorm_lds(s.vec, W.attn_norm, d.h, d.eps, s.red);
   const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
-  const uint32_t P = d.qkv_rows / 2;
+  if (l == 0) {
+    // The embedding row (model.rs:428), read by the pollers only.
+    __syncthreads();
+    const float* e = a.embed + (size_t)token * d.h;
+    for (uint32_t i = threadIdx.x; i < d.h && threadIdx.x < NPOLL * WAVE; i += NPOLL * WAVE)
+      lds_st(s.vec + i, ldg(e + i));
+    __syncthreads();
+  } else if (!poll_gather<8>(gather_vec(a.mb_xd, d.h, gen_of(d, tick, l - 1, PH_D), s.vec), NPOLL,
+                          a.st, s.ctl)) {
+    return false;
+  }
+  if (wave < NPOLL) return true;
+  const uint32_t cw = wave - NPOLL;
+  const Deal q = deal_of(d, wg, G);
+  if (q.cnt[IK_QKV] == 0) return true;
+  const float inv = rms_inv(s.vec, d.h, d.eps, lane);
   const uint32_t gen = gen_of(d, tick, l, PH_QKV);
+  const LayerW& W = a.layers[l];
   const float2* rp = a.rope + (size_t)pos * d.half;
-  for (uint32_t k = wave; wg + G * k < P; k += NWAVES) {
+  for_items(q, IK_QKV, cw, [&](uint32_t k, uint32_t si) {
+    float y0, y1;
+    item_dot(a, IK_QKV, l, k, si, pf, s.vec, wg, G, lane, &y0, &y1);
     const uint32_t p = wg + G * k;
     const uint32_t hb = p / d.half, i = p - hb * d.half;
     const uint32_t r0 = hb * d.hd + i, r1 = r0 + d.half;
-    const float p0 = dot_partial(W.wqkv + (size_t)r0 * d.h, s.vec, d.h, lane);
-    const float p1 = dot_partial(W.wqkv + (size_t)r1 * d.h, s.vec, d.h, lane);
-    float y0 = wave_sum(p0), y1 = wave_sum(p1);
+    y0 *= inv;
+    y1 *= inv;
     if (W.bqkv) {
-      y0 += W.bqkv[r0];
-      y1 += W.bqkv[r1];
+      y0 += ldg(W.bqkv + r0);
+      y1 += ldg(W.bqkv + r1);
     }
     if (hb < d.nh + d.nkv) {
-      const float2 cs = rp[i];
+      const float2 cs = ldg2(rp + i);
       const float a0 = y0 * cs.x - y1 * cs.y;
       const float a1 = y1 * cs.x + y0 * cs.y;
       y0 = a0;
@@ -168,19 +436,84 @@ __device__ bool phase_qkv(const Args& a, uint32_t l, uint32_t tick, uint32_t pos
       st_coherent(row + i, y0);
       st_coherent(row + i + d.half, y1);
     }
-  }
+  });
   return true;
 }
 
 // ------------------------------------------------------------ attention
 
-constexpr uint32_t MAX_GROUP = 8;
+constexpr uint32_t MAX_GROUP = 4;
+constexpr uint32_t ATT_PF = 4;  // position iterations whose K/V rows a lane holds at once
+// Waves that compute attention (all of them; a fixed number, so the merge
+// order does not depend on the launch).
+constexpr uint32_t NWA = NWAVES;
+
+// K/V rows (this lane's float4) of positions t, t + stride, ... for ATT_PF
+// iterations; rows at or past `pos` come from LDS, not the cache.
+__device__ __forceinline__ void load_kv(const float* kb, const float* vb, float4* kr, float4* vr,
+                                        uint32_t t, uint32_t stride, uint32_t t1, uint32_t pos,
+                                        uint32_t kvs, uint32_t sub) {
+#pragma unroll
+  for (uint32_t it = 0; it < ATT_PF; ++it) {
+    const uint32_t tt = t + stride * it;
+    if (tt < t1 && tt < pos) {
+      kr[it] = ldg4(kb + (size_t)tt * kvs + sub * 4);
+      vr[it] = ldg4(vb + (size_t)tt * kvs + sub * 4);
+    }
+  }
+}
+
+// Online-softmax state of one query head over this lane group's positions.
+struct AttState {
+  float m, l, acc[4];
+};
+
+// Folds ATT_PF iterations (positions t0 + gi + NG*(base + it)) into st.
+__device__ __forceinline__ void att_batch(AttState& st, const float4* kr, const float4* vr,
+                                          const float* qh, const float* kn, const float* vn,
+                                          const uint32_t* mask, float scale, uint32_t t_first,
+                                          uint32_t NG, uint32_t t1, uint32_t pos, uint32_t sub,
+                                          uint32_t LP) {
+#pragma unroll
+  for (uint32_t it = 0; it < ATT_PF; ++it) {
+    const uint32_t t = t_first + NG * it;
+    if (t >= t1) continue;
+    const bool cur = (t == pos);
+    const float4 kk = cur ? lds4(kn + sub * 4) : kr[it];
+    const float4 vv = cur ? lds4(vn + sub * 4) : vr[it];
+    const bool masked = mask && t < pos && ((ldg_u32(mask + (t >> 5)) >> (t & 31)) & 1u);
+    const float4 qq = lds4(qh + sub * 4);
+    float p = qq.x * kk.x;
+    p = fmaf(qq.y, kk.y, p);
+    p = fmaf(qq.z, kk.z, p);
+    p = fmaf(qq.w, kk.w, p);
+    for (uint32_t o = LP / 2; o > 0; o >>= 1) p += __shfl_xor(p, o);
+    const float sc = masked ? -INFINITY : p * scale;
+    if (sc > st.m) {
+      const float r = (st.m == -INFINITY) ? 0.0f : expf(st.m - sc);
+      st.l *= r;
+      st.acc[0] *= r;
+      st.acc[1] *= r;
+      st.acc[2] *= r;
+      st.acc[3] *= r;
+      st.m = sc;
+    }
+    const float e = (sc == -INFINITY) ? 0.0f : expf(sc - st.m);
+    st.l += e;
+    st.acc[0] = fmaf(e, vv.x, st.acc[0]);
+    st.acc[1] = fmaf(e, vv.y, st.acc[1]);
+    st.acc[2] = fmaf(e, vv.z, st.acc[2]);
+    st.acc[3] = fmaf(e, vv.w, st.acc[3]);
+  }
+}
 
 // Split-context attention for one (kv head, chunk) item: scores, softmax
 // partials (max m, sum l, unnormalised acc) for each query head of the GQA
-// group (model.rs:471-497). K/V rows of the chunk are read once per group.
-__device__ bool phase_attn(const Args& a, uint32_t l, uint32_t tick, uint32_t pos, uint32_t wg,
-                           uint32_t G, const Lds& s) {
+// group (model.rs:471-497). A chunk's K/V rows are loaded once and reused for
+// every head of the group when they fit the lane's registers; longer chunks
+// stream them again per head.
+__device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t tick, uint32_t pos,
+                                           uint32_t wg, uint32_t G, const Lds& s) {
   const Dims& d = a.d;
   const uint32_t nch = attn_nchunks(pos), CH = attn_chunk(pos);
   const uint32_t n_items = d.nkv * nch;
@@ -190,8 +523,8 @@ __device__ bool phase_attn(const Args& a, uint32_t l, uint32_t tick, uint32_t po
   float* qs = s.scr;            // [grp*hd]
   float* kn = qs + grp * hd;    // [hd]
   float* vn = kn + hd;          // [hd]
-  float* wp = vn + hd;          // [NWAVES][grp][hd+2]
-  const uint32_t LP = hd / 4, PPI = WAVE / LP, NG = NWAVES * PPI;
+  float* wp = vn + hd;          // [NWA][grp][hd+2]
+  const uint32_t LP = hd / 4, PPI = WAVE / LP, NG = NWA * PPI;
   const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
   const uint32_t sub = lane % LP;
   const uint32_t gi = wave * PPI + lane / LP;
@@ -199,80 +532,54 @@ __device__ bool phase_attn(const Args& a, uint32_t l, uint32_t tick, uint32_t po
     const uint32_t g = item / nch, c = item - g * nch;
     const uint32_t t0 = c * CH;
     const uint32_t t1 = min(t0 + CH, pos + 1);
-    Gather gs[3];
-    gs[0] = gather_vec(a.mb_qkv + (size_t)g * grp * hd, grp * hd, gen_in, qs);
-    gs[1] = gather_vec(a.mb_qkv + d.q + g * hd, hd, gen_in, kn);
-    gs[2] = gather_vec(a.mb_qkv + d.q + d.kv + g * hd, hd, gen_in, vn);
-    if (!wait_gather(gs, 3, a.st, s.ctl)) return false;
     const float* kb = a.kc + ((size_t)l * d.nkv + g) * d.cap * d.kvs;
     const float* vb = a.vc + ((size_t)l * d.nkv + g) * d.cap * d.kvs;
-    float m[MAX_GROUP], ls[MAX_GROUP], acc[MAX_GROUP][4];
-#pragma unroll
-    for (uint32_t j = 0; j < MAX_GROUP; ++j) {
-      m[j] = -INFINITY;
-      ls[j] = 0.0f;
-      acc[j][0] = acc[j][1] = acc[j][2] = acc[j][3] = 0.0f;
-    }
-    for (uint32_t t = t0 + gi; t < t1; t += NG) {
-      const bool cur = (t == pos);
-      const float4 kk = cur ? ld4(kn + sub * 4) : ld4(kb + (size_t)t * d.kvs + sub * 4);
-      const float4 vv = cur ? ld4(vn + sub * 4) : ld4(vb + (size_t)t * d.kvs + sub * 4);
-      const bool masked = a.mask && t < pos && ((a.mask[t >> 5] >> (t & 31)) & 1u);
-#pragma unroll
-      for (uint32_t j = 0; j < MAX_GROUP; ++j) {
-        if (j >= grp) break;
-        const float4 qq = ld4(qs + j * hd + sub * 4);
-        float p = qq.x * kk.x;
-        p = fmaf(qq.y, kk.y, p);
-        p = fmaf(qq.z, kk.z, p);
-        p = fmaf(qq.w, kk.w, p);
-        for (uint32_t o = LP / 2; o > 0; o >>= 1) p += __shfl_xor(p, o);
-        const float sc = masked ? -INFINITY : p * d.scale;
-        if (sc > m[j]) {
-          const float r = (m[j] == -INFINITY) ? 0.0f : expf(m[j] - sc);
-          ls[j] *= r;
-          acc[j][0] *= r;
-          acc[j][1] *= r;
-          acc[j][2] *= r;
-          acc[j][3] *= r;
-          m[j] = sc;
-        }
-        const float e = (sc == -INFINITY) ? 0.0f : expf(sc - m[j]);
-        ls[j] += e;
-        acc[j][0] = fmaf(e, vv.x, acc[j][0]);
-        acc[j][1] = fmaf(e, vv.y, acc[j][1]);
-        acc[j][2] = fmaf(e, vv.z, acc[j][2]);
-        acc[j][3] = fmaf(e, vv.w, acc[j][3]);
+    // The first batch of historical K/V rows is issued before waiting for
+    // this token's q/k/v.
+    float4 kr[ATT_PF], vr[ATT_PF];
+    load_kv(kb, vb, kr, vr, t0 + gi, NG, t1, pos, d.kvs, sub);
+    if (!poll_gather<2, 1, 1>(gather_vec(a.mb_qkv + (size_t)g * grp * hd, grp * hd, gen_in, qs),
+                              gather_vec(a.mb_qkv + d.q + g * hd, hd, gen_in, kn),
+                              gather_vec(a.mb_qkv + d.q + d.kv + g * hd, hd, gen_in, vn), NPOLL,
+                              a.st, s.ctl))
+      return false;
+    const uint32_t n_iter = (t1 - t0 + NG - 1) / NG;
+    for (uint32_t j = 0; j < grp; ++j) {
+      AttState st;
+      st.m = -INFINITY;
+      st.l = 0.0f;
+      st.acc[0] = st.acc[1] = st.acc[2] = st.acc[3] = 0.0f;
+      for (uint32_t base = 0; base < n_iter; base += ATT_PF) {
+        if (n_iter > ATT_PF && (base > 0 || j > 0))
+          load_kv(kb, vb, kr, vr, t0 + gi + NG * base, NG, t1, pos, d.kvs, sub);
+        att_batch(st, kr, vr, qs + j * hd, kn, vn, a.mask, d.scale, t0 + gi + NG * base, NG, t1,
+                  pos, sub, LP);
       }
-    }
-    // Merge the position groups of this wave (lanes with the same `sub`).
-#pragma unroll
-    for (uint32_t j = 0; j < MAX_GROUP; ++j) {
-      if (j >= grp) break;
+      // Merge the position groups of this wave (lanes with the same `sub`).
       for (uint32_t o = LP; o < WAVE; o <<= 1) {
-        const float m2 = __shfl_xor(m[j], o), l2 = __shfl_xor(ls[j], o);
-        const float b0 = __shfl_xor(acc[j][0], o), b1 = __shfl_xor(acc[j][1], o);
-        const float b2 = __shfl_xor(acc[j][2], o), b3 = __shfl_xor(acc[j][3], o);
-        const float mn = fmaxf(m[j], m2);
-        const float s1 = (m[j] == -INFINITY) ? 0.0f : expf(m[j] - mn);
+        const float m2 = __shfl_xor(st.m, o), l2 = __shfl_xor(st.l, o);
+        const float b0 = __shfl_xor(st.acc[0], o), b1 = __shfl_xor(st.acc[1], o);
+        const float b2 = __shfl_xor(st.acc[2], o), b3 = __shfl_xor(st.acc[3], o);
+        const float mn = fmaxf(st.m, m2);
+        const float s1 = (st.m == -INFINITY) ? 0.0f : expf(st.m - mn);
         const float s2 = (m2 == -INFINITY) ? 0.0f : expf(m2 - mn);
-        ls[j] = ls[j] * s1 + l2 * s2;
-        acc[j][0] = acc[j][0] * s1 + b0 * s2;
-        acc[j][1] = acc[j][1] * s1 + b1 * s2;
-        acc[j][2] = acc[j][2] * s1 + b2 * s2;
-        acc[j][3] = acc[j][3] * s1 + b3 * s2;
-        m[j] = mn;
+        st.l = st.l * s1 + l2 * s2;
+        st.acc[0] = st.acc[0] * s1 + b0 * s2;
+        st.acc[1] = st.acc[1] * s1 + b1 * s2;
+        st.acc[2] = st.acc[2] * s1 + b2 * s2;
+        st.acc[3] = st.acc[3] * s1 + b3 * s2;
+        st.m = mn;
       }
       if (lane < LP) {
         float* dst = wp + (wave * grp + j) * hs;
         if (lane == 0) {
-          dst[0] = m[j];
-          dst[1] = ls[j];
+          lds_st(dst + 0, st.m);
+          lds_st(dst + 1, st.l);
         }
-        dst[2 + sub * 4 + 0] = acc[j][0];
-        dst[2 + sub * 4 + 1] = acc[j][1];
-        dst[2 + sub * 4 + 2] = acc[j][2];
-        dst[2 + sub * 4 + 3] = acc[j][3];
+        lds_st(dst + 2 + sub * 4 + 0, st.acc[0]);
+        lds_st(dst + 2 + sub * 4 + 1, st.acc[1]);
+        lds_st(dst + 2 + sub * 4 + 2, st.acc[2]);
+        lds_st(dst + 2 + sub * 4 + 3, st.acc[3]);
       }
     }
     __syncthreads();
@@ -280,13 +587,14 @@ __device__ bool phase_attn(const Args& a, uint32_t l, uint32_t tick, uint32_t po
     for (uint32_t u = threadIdx.x; u < grp * hd; u += BLOCK) {
       const uint32_t j = u / hd, dd = u - j * hd;
       float M = -INFINITY;
-      for (uint32_t w = 0; w < NWAVES; ++w) M = fmaxf(M, wp[(w * grp + j) * hs]);
+      for (uint32_t w = 0; w < NWA; ++w) M = fmaxf(M, lds_ld(wp + (w * grp + j) * hs));
       float Ls = 0.0f, A = 0.0f;
-      for (uint32_t w = 0; w < NWAVES; ++w) {
+      for (uint32_t w = 0; w < NWA; ++w) {
         const float* src = wp + (w * grp + j) * hs;
-        const float sw = (src[0] == -INFINITY) ? 0.0f : expf(src[0] - M);
-        Ls = Ls + src[1] * sw;
-        A = A + src[2 + dd] * sw;
+        const float mw = lds_ld(src);
+        const float sw = (mw == -INFINITY) ? 0.0f : expf(mw - M);
+        Ls = Ls + lds_ld(src + 1) * sw;
+        A = A + lds_ld(src + 2 + dd) * sw;
       }
       const uint32_t hh = g * grp + j;
       u64* out = a.mb_part + ((size_t)hh * MAX_ACHUNKS + c) * hs;
@@ -296,7 +604,6 @@ __device__ bool phase_attn(const Args& a, uint32_t l, uint32_t tick, uint32_t po
         mb_put(out + 1, Ls, gen_out);
       }
     }
-    __syncthreads();
   }
   return true;
 }
@@ -306,120 +613,128 @@ __device__ bool phase_attn(const Args& a, uint32_t l, uint32_t tick, uint32_t po
 __device__ __forceinline__ float combine_one(const float* part, uint32_t nch, uint32_t hs,
                                              uint32_t dd) {
   float M = -INFINITY;
-  for (uint32_t c = 0; c < nch; ++c) M = fmaxf(M, part[c * hs]);
+  for (uint32_t c = 0; c < nch; ++c) M = fmaxf(M, lds_ld(part + c * hs));
   float Ls = 0.0f, A = 0.0f;
   for (uint32_t c = 0; c < nch; ++c) {
     const float* p = part + c * hs;
-    const float sc = (p[0] == -INFINITY) ? 0.0f : expf(p[0] - M);
-    Ls = Ls + p[1] * sc;
-    A = A + p[2 + dd] * sc;
+    const float mc = lds_ld(p);
+    const float sc = (mc == -INFINITY) ? 0.0f : expf(mc - M);
+    Ls = Ls + lds_ld(p + 1) * sc;
+    A = A + lds_ld(p + 2 + dd) * sc;
   }
   return A / Ls;
 }
 
 // Separate combine (used when the partials of all heads do not fit the O
 // phase's LDS budget): item = one query head.
-__device__ bool phase_comb(const Args& a, uint32_t l, uint32_t tick, uint32_t pos, uint32_t wg,
-                           uint32_t G, const Lds& s) {
+__device__ __forceinline__ bool phase_comb(const Args& a, uint32_t l, uint32_t tick, uint32_t pos,
+                                           uint32_t wg, uint32_t G, const Lds& s) {
   const Dims& d = a.d;
   if (comb_inline(d, pos)) return true;
   const uint32_t nch = attn_nchunks(pos), hs = d.hd + 2;
   const uint32_t gen_in = gen_of(d, tick, l, PH_ATTN), gen_out = gen_of(d, tick, l, PH_COMB);
   for (uint32_t hh = wg; hh < d.nh; hh += G) {
-    Gather g = gather_vec(a.mb_part + (size_t)hh * MAX_ACHUNKS * hs, nch * hs, gen_in, s.scr);
-    if (!wait_gather(&g, 1, a.st, s.ctl)) return false;
+    if (!poll_gather<4>(gather_vec(a.mb_part + (size_t)hh * MAX_ACHUNKS * hs, nch * hs, gen_in, s.scr),
+                     NPOLL, a.st, s.ctl))
+      return false;
     for (uint32_t dd = threadIdx.x; dd < d.hd; dd += BLOCK)
       mb_put(a.mb_att + hh * d.hd + dd, combine_one(s.scr, nch, hs, dd), gen_out);
-    __syncthreads();
   }
   return true;
-}
-
-// Number of rows r = wg + G*k below n owned by this workgroup.
-__device__ __forceinline__ uint32_t rows_owned(uint32_t n, uint32_t wg, uint32_t G) {
-  return wg < n ? (n - wg + G - 1) / G : 0;
 }
 
 // ------------------------------------------------------------ O projection
 
 // x_o = x + Wo . att (model.rs:498-499), with the attention combine done
-// in the prologue when it fits.
-__device__ bool phase_o(const Args& a, uint32_t l, uint32_t tick, uint32_t pos, uint32_t token,
-                        uint32_t wg, uint32_t G, const Lds& s) {
+// after the poll when it fits.
+__device__ __forceinline__ bool phase_o(const Args& a, uint32_t l, uint32_t tick, uint32_t pos,
+                                        uint32_t token, uint32_t wg, uint32_t G, const Lds& s,
+                                        const Pf& pf) {
   const Dims& d = a.d;
-  const LayerW& W = a.layers[l];
   const uint32_t nch = attn_nchunks(pos), hs = d.hd + 2;
   const bool inl = comb_inline(d, pos);
-  const uint32_t R = rows_owned(d.h, wg, G);
+  const Deal q = deal_of(d, wg, G);
+  const uint32_t R = q.cnt[IK_O];
+  const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
   float* part = s.scr;
   float* xres = s.scr + (inl ? d.nh * nch * hs : 0);
-  Gather gs[2];
-  uint32_t ng = 0;
-  if (inl)
-    gs[ng++] = {a.mb_part, nch * hs, d.nh, MAX_ACHUNKS * hs, gen_of(d, tick, l, PH_ATTN), part};
-  else
-    gs[ng++] = gather_vec(a.mb_att, d.q, gen_of(d, tick, l, PH_COMB), s.vec);
-  if (l > 0 && R > 0) gs[ng++] = {a.mb_xd + wg, 1, R, G, gen_of(d, tick, l - 1, PH_D), xres};
-  if (!wait_gather(gs, ng, a.st, s.ctl)) return false;
+  const Gather ga =
+      inl ? gather_strided(a.mb_part, nch * hs, d.nh, MAX_ACHUNKS * hs, gen_of(d, tick, l, PH_ATTN),
+                           part)
+          : gather_vec(a.mb_att, d.q, gen_of(d, tick, l, PH_COMB), s.vec);
+  const Gather gr = (l > 0 && R > 0)
+                        ? gather_strided(a.mb_xd + wg, 1, R, G, gen_of(d, tick, l - 1, PH_D), xres)
+                        : no_gather();
+  if (!poll_gather<12, 1>(ga, gr, NPOLL, a.st, s.ctl)) return false;
+  // QKV slots were consumed before the attention; refill them now that the
+  // attention's K/V reads are done (next layer, or the next token's layer 0).
+  if (pf.on && wave >= NPOLL)
+    slot_refill(a, q, pf, wave - NPOLL, IK_QKV, wg, G, lane);
   if (l == 0)
     for (uint32_t k = threadIdx.x; k < R; k += BLOCK)
-      xres[k] = a.embed[(size_t)token * d.h + wg + G * k];
+      lds_st(xres + k, ldg(a.embed + (size_t)token * d.h + wg + G * k));
   if (inl)
     for (uint32_t u = threadIdx.x; u < d.q; u += BLOCK) {
       const uint32_t hh = u / d.hd, dd = u - hh * d.hd;
-      s.vec[u] = combine_one(part + hh * nch * hs, nch, hs, dd);
+      lds_st(s.vec + u, combine_one(part + hh * nch * hs, nch, hs, dd));
     }
   __syncthreads();
-  const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+  if (wave < NPOLL) return true;
+  const uint32_t cw = wave - NPOLL;
   const uint32_t gen = gen_of(d, tick, l, PH_O);
-  for (uint32_t k = wave; k < R; k += NWAVES) {
-    const uint32_t i = wg + G * k;
-    const float y = dot_row(W.wo + (size_t)i * d.q, s.vec, d.q, lane);
-    if (lane == 0) mb_put(a.mb_xo + i, xres[k] + y, gen);
-  }
+  for_items(q, IK_O, cw, [&](uint32_t k, uint32_t si) {
+    float y, unused;
+    item_dot(a, IK_O, l, k, si, pf, s.vec, wg, G, lane, &y, &unused);
+    if (lane == 0) mb_put(a.mb_xo + wg + G * k, lds_ld(xres + k) + y, gen);
+  });
+  slot_refill(a, q, pf, cw, IK_O, wg, G, lane);
   return true;
 }
 
 // ------------------------------------------------------------ MLP
 
 // rmsnorm -> g = act(Wg.x) * (Wu.x) (model.rs:502-509).
-__device__ bool phase_gu(const Args& a, uint32_t l, uint32_t tick, uint32_t wg, uint32_t G,
-                         const Lds& s) {
+__device__ __forceinline__ bool phase_gu(const Args& a, uint32_t l, uint32_t tick, uint32_t wg,
+                                         uint32_t G, const Lds& s, const Pf& pf) {
   const Dims& d = a.d;
-  const LayerW& W = a.layers[l];
-  Gather g = gather_vec(a.mb_xo, d.h, gen_of(d, tick, l, PH_O), s.vec);
-  if (!wait_gather(&g, 1, a.st, s.ctl)) return false;
-  rmsnorm_lds(s.vec, W.ffn_norm, d.h, d.eps, s.red);
   const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+  if (!poll_gather<8>(gather_vec(a.mb_xo, d.h, gen_of(d, tick, l, PH_O), s.vec), NPOLL, a.st, s.ctl))
+    return false;
+  if (wave < NPOLL) return true;
+  const uint32_t cw = wave - NPOLL;
+  const Deal q = deal_of(d, wg, G);
+  const float inv = rms_inv(s.vec, d.h, d.eps, lane);
   const uint32_t gen = gen_of(d, tick, l, PH_GU);
-  for (uint32_t k = wave; wg + G * k < d.ff; k += NWAVES) {
-    const uint32_t j = wg + G * k;
-    const float pg = dot_partial(W.wg + (size_t)j * d.h, s.vec, d.h, lane);
-    const float pu = dot_partial(W.wu + (size_t)j * d.h, s.vec, d.h, lane);
-    const float gate = wave_sum(pg), up = wave_sum(pu);
-    if (lane == 0) mb_put(a.mb_g + j, act_fn(gate, d.act) * up, gen);
-  }
+  for_items(q, IK_GU, cw, [&](uint32_t k, uint32_t si) {
+    float gate, up;
+    item_dot(a, IK_GU, l, k, si, pf, s.vec, wg, G, lane, &gate, &up);
+    if (lane == 0) mb_put(a.mb_g + wg + G * k, act_fn(gate * inv, d.act) * (up * inv), gen);
+  });
+  slot_refill(a, q, pf, cw, IK_GU, wg, G, lane);
   return true;
 }
 
 // x_d = x_o + Wd . g (model.rs:510-511).
-__device__ bool phase_d(const Args& a, uint32_t l, uint32_t tick, uint32_t wg, uint32_t G,
-                        const Lds& s) {
+__device__ __forceinline__ bool phase_d(const Args& a, uint32_t l, uint32_t tick, uint32_t wg,
+                                        uint32_t G, const Lds& s, const Pf& pf) {
   const Dims& d = a.d;
-  const LayerW& W = a.layers[l];
-  const uint32_t R = rows_owned(d.h, wg, G);
-  Gather gs[2];
-  uint32_t ng = 0;
-  gs[ng++] = gather_vec(a.mb_g, d.ff, gen_of(d, tick, l, PH_GU), s.vec);
-  if (R > 0) gs[ng++] = {a.mb_xo + wg, 1, R, G, gen_of(d, tick, l, PH_O), s.scr};
-  if (!wait_gather(gs, ng, a.st, s.ctl)) return false;
+  const Deal q = deal_of(d, wg, G);
+  const uint32_t R = q.cnt[IK_D];
   const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+  const Gather gr = R > 0 ? gather_strided(a.mb_xo + wg, 1, R, G, gen_of(d, tick, l, PH_O), s.scr)
+                          : no_gather();
+  if (!poll_gather<12, 1>(gather_vec(a.mb_g, d.ff, gen_of(d, tick, l, PH_GU), s.vec), gr, NPOLL, a.st,
+                   s.ctl))
+    return false;
+  if (wave < NPOLL) return true;
+  const uint32_t cw = wave - NPOLL;
   const uint32_t gen = gen_of(d, tick, l, PH_D);
-  for (uint32_t k = wave; k < R; k += NWAVES) {
-    const uint32_t i = wg + G * k;
-    const float y = dot_row(W.wd + (size_t)i * d.ff, s.vec, d.ff, lane);
-    if (lane == 0) mb_put(a.mb_xd + i, s.scr[k] + y, gen);
-  }
+  for_items(q, IK_D, cw, [&](uint32_t k, uint32_t si) {
+    float y, unused;
+    item_dot(a, IK_D, l, k, si, pf, s.vec, wg, G, lane, &y, &unused);
+    if (lane == 0) mb_put(a.mb_xd + wg + G * k, lds_ld(s.scr + k) + y, gen);
+  });
+  slot_refill(a, q, pf, cw, IK_D, wg, G, lane);
   return true;
 }
 
@@ -433,60 +748,93 @@ __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t b
   return v > bv || (v == bv && i < bi);
 }
 
+constexpr int LMF = 4;  // float4 per lane per lm_head row held in registers (h <= 1024 in one go)
+
+// The final RMSNorm weight, kept in LDS for the kernel's lifetime (the
+// lm_head may be the tied embedding, so it cannot be folded into the rows).
+__device__ __forceinline__ void lm_prime(const Args& a, const Lds& s) {
+  for (uint32_t i = threadIdx.x; i < a.d.h && threadIdx.x < NPOLL * WAVE; i += NPOLL * WAVE)
+    lds_st(s.vec2 + a.d.h + i, ldg(a.norm + i));
+  __syncthreads();
+}
+
 // rmsnorm(final) -> logits = H . x (model.rs:515-519), plus each vocabulary
-// chunk's (max, argmax) for the sampler.
-__device__ bool phase_lm(const Args& a, uint32_t tick, uint32_t wg, uint32_t G, const Lds& s) {
+// chunk's (max, argmax) for the sampler. The workgroup owns chunks
+// c = wg + G*k; every wave computes rows, two at a time, with the next two
+// rows in flight. logit = inv * (H . (x * w_norm)).
+__device__ __forceinline__ bool phase_lm(const Args& a, uint32_t tick, uint32_t wg, uint32_t G,
+                                         const Lds& s) {
   const Dims& d = a.d;
-  Gather g = gather_vec(a.mb_xd, d.h, gen_of(d, tick, d.L - 1, PH_D), s.vec);
-  if (!wait_gather(&g, 1, a.st, s.ctl)) return false;
-  rmsnorm_lds(s.vec, a.norm, d.h, d.eps, s.red);
   const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+  const uint32_t nown = wg < d.nvc ? (d.nvc - wg + G - 1) / G : 0;
+  const uint32_t nrows = nown * VCHUNK;  // local rows r -> chunk r / VCHUNK
+  float* lg = s.scr;                     // [nrows] logits of this workgroup
+  float* xs = s.vec2;                    // x * w_norm
+  const float* nrm = s.vec2 + d.h;       // final norm weight (lm_prime)
+  auto vocab_row = [&](uint32_t r) { return (wg + G * (r / VCHUNK)) * VCHUNK + r % VCHUNK; };
+  RowT<LMF> A0, A1, B0, B1;
+  auto load_pair = [&](RowT<LMF>& x0, RowT<LMF>& x1, uint32_t r0) {
+    const uint32_t r1 = r0 + NWAVES;
+    if (r0 < nrows && vocab_row(r0) < d.V)
+      row_load(x0, a.head + (size_t)vocab_row(r0) * d.h, d.h, lane);
+    if (r1 < nrows && vocab_row(r1) < d.V)
+      row_load(x1, a.head + (size_t)vocab_row(r1) * d.h, d.h, lane);
+  };
+  load_pair(A0, A1, wave);
+  if (!poll_gather<8>(gather_vec(a.mb_xd, d.h, gen_of(d, tick, d.L - 1, PH_D), s.vec), NPOLL, a.st,
+                   s.ctl))
+    return false;
+  for (uint32_t i = threadIdx.x; i < d.h; i += BLOCK) lds_st(xs + i, lds_ld(s.vec + i) * lds_ld(nrm + i));
+  __syncthreads();
+  const float inv = rms_inv(s.vec, d.h, d.eps, lane);
   const uint32_t gen = gen_lm(d, tick);
-  float* wbest = s.scr;  // [NWAVES] values, then [NWAVES] indices
-  for (uint32_t c = wg; c < d.nvc; c += G) {
-    const uint32_t v0 = c * VCHUNK, v1 = min(v0 + VCHUNK, d.V);
+  for (uint32_t r0 = wave; r0 < nrows; r0 += 2 * NWAVES) {
+    const uint32_t r1 = r0 + NWAVES;
+    load_pair(B0, B1, r0 + 2 * NWAVES);
+    const uint32_t v0 = vocab_row(r0), v1 = vocab_row(r1);
+    if (v0 < d.V) {
+      const float y = inv * wave_sum(dot_tail(A0, a.head + (size_t)v0 * d.h, xs, d.h, lane));
+      if (lane == 0) {
+        lds_st(lg + r0, y);
+        mb_put(a.mb_logit + v0, y, gen);
+      }
+    }
+    if (r1 < nrows && v1 < d.V) {
+      const float y = inv * wave_sum(dot_tail(A1, a.head + (size_t)v1 * d.h, xs, d.h, lane));
+      if (lane == 0) {
+        lds_st(lg + r1, y);
+        mb_put(a.mb_logit + v1, y, gen);
+      }
+    }
+    A0 = B0;
+    A1 = B1;
+  }
+  __syncthreads();
+  // Chunk (max, argmax): one wave per chunk, one lane per row.
+  for (uint32_t k = wave; k < nown; k += NWAVES) {
+    const uint32_t c = wg + G * k;
+    const uint32_t v = c * VCHUNK + lane;
     float bv = -INFINITY;
     uint32_t bi = NO_INDEX;
-    uint32_t v = v0 + wave;
-    for (; v + 3 * NWAVES < v1; v += 4 * NWAVES) {
-      const float p0 = dot_partial(a.head + (size_t)v * d.h, s.vec, d.h, lane);
-      const float p1 = dot_partial(a.head + (size_t)(v + NWAVES) * d.h, s.vec, d.h, lane);
-      const float p2 = dot_partial(a.head + (size_t)(v + 2 * NWAVES) * d.h, s.vec, d.h, lane);
-      const float p3 = dot_partial(a.head + (size_t)(v + 3 * NWAVES) * d.h, s.vec, d.h, lane);
-      const float y0 = wave_sum(p0), y1 = wave_sum(p1), y2 = wave_sum(p2), y3 = wave_sum(p3);
-      if (lane == 0) {
-        mb_put(a.mb_logit + v, y0, gen);
-        mb_put(a.mb_logit + v + NWAVES, y1, gen);
-        mb_put(a.mb_logit + v + 2 * NWAVES, y2, gen);
-        mb_put(a.mb_logit + v + 3 * NWAVES, y3, gen);
+    if (v < d.V) {
+      const float y = lds_ld(lg + k * VCHUNK + lane);
+      if (!isnan(y)) {
+        bv = y;
+        bi = v;
       }
-      if (!isnan(y0) && better(y0, v, bv, bi)) { bv = y0; bi = v; }
-      if (!isnan(y1) && better(y1, v + NWAVES, bv, bi)) { bv = y1; bi = v + NWAVES; }
-      if (!isnan(y2) && better(y2, v + 2 * NWAVES, bv, bi)) { bv = y2; bi = v + 2 * NWAVES; }
-      if (!isnan(y3) && better(y3, v + 3 * NWAVES, bv, bi)) { bv = y3; bi = v + 3 * NWAVES; }
     }
-    for (; v < v1; v += NWAVES) {
-      const float y = dot_row(a.head + (size_t)v * d.h, s.vec, d.h, lane);
-      if (lane == 0) mb_put(a.mb_logit + v, y, gen);
-      if (!isnan(y) && better(y, v, bv, bi)) { bv = y; bi = v; }
+    for (int o = 32; o > 0; o >>= 1) {
+      const float v2 = __shfl_xor(bv, o);
+      const uint32_t i2 = __shfl_xor(bi, o);
+      if (better(v2, i2, bv, bi)) {
+        bv = v2;
+        bi = i2;
+      }
     }
     if (lane == 0) {
-      wbest[wave] = bv;
-      reinterpret_cast<uint32_t*>(wbest)[NWAVES + wave] = bi;
+      mb_put(a.mb_vmax + c, bv, gen);
+      mb_put(a.mb_varg + c, __uint_as_float(bi), gen);
     }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      float cv = -INFINITY;
-      uint32_t ci = NO_INDEX;
-      for (uint32_t w = 0; w < NWAVES; ++w) {
-        const float wv = wbest[w];
-        const uint32_t wi = reinterpret_cast<const uint32_t*>(wbest)[NWAVES + w];
-        if (better(wv, wi, cv, ci)) { cv = wv; ci = wi; }
-      }
-      mb_put(a.mb_vmax + c, cv, gen);
-      mb_put(a.mb_varg + c, __uint_as_float(ci), gen);
-    }
-    __syncthreads();
   }
   return true;
 }
@@ -494,7 +842,7 @@ __device__ bool phase_lm(const Args& a, uint32_t tick, uint32_t wg, uint32_t G, 
 // ------------------------------------------------------------ sampler
 
 // Global (max, argmax) over the chunk partials already in LDS.
-__device__ void global_argmax(const float* vmx, const float* varg, uint32_t nvc, float* red,
+__device__ __forceinline__ void global_argmax(const float* vmx, const float* varg, uint32_t nvc, float* red,
                               float* bv_out, uint32_t* bi_out) {
   float bv = -INFINITY;
   uint32_t bi = NO_INDEX;
@@ -539,7 +887,7 @@ __device__ __forceinline__ float exp_term(float logit, float T, float m) {
 
 // Sampler stage A (temperature > 0): the global max m from the chunk maxima,
 // then exp-sums of this workgroup's chunks, published for stage B.
-__device__ bool sample_stage_a(const Args& a, uint32_t tick, float T, uint32_t wg, uint32_t G,
+__device__ __forceinline__ bool sample_stage_a(const Args& a, uint32_t tick, float T, uint32_t wg, uint32_t G,
                                const Lds& s) {
   const Dims& d = a.d;
   const uint32_t nvc = d.nvc;
@@ -547,8 +895,9 @@ __device__ bool sample_stage_a(const Args& a, uint32_t tick, float T, uint32_t w
   float* vmx = s.scr;
   float* varg = vmx + nvc;
   float* chunk = varg + nvc;  // [NWAVES][VCHUNK]
-  Gather gs[2] = {gather_vec(a.mb_vmax, nvc, gl, vmx), gather_vec(a.mb_varg, nvc, gl, varg)};
-  if (!wait_gather(gs, 2, a.st, s.ctl)) return false;
+  if (!poll_gather<4, 4>(gather_vec(a.mb_vmax, nvc, gl, vmx), gather_vec(a.mb_varg, nvc, gl, varg),
+                   NWAVES, a.st, s.ctl))
+    return false;
   float bv;
   uint32_t bi;
   global_argmax(vmx, varg, nvc, s.red, &bv, &bi);
@@ -558,19 +907,15 @@ __device__ bool sample_stage_a(const Args& a, uint32_t tick, float T, uint32_t w
   for (uint32_t k0 = 0; k0 < nown; k0 += NWAVES) {
     const uint32_t nb = min(NWAVES, nown - k0);
     // chunks wg + G*(k0 + b), b < nb; the last one may be short
-    Gather g = {a.mb_logit + (size_t)(wg + G * k0) * VCHUNK, VCHUNK, nb, G * VCHUNK, gl, chunk};
+    const u64* src0 = a.mb_logit + (size_t)(wg + G * k0) * VCHUNK;
     const uint32_t clast = wg + G * (k0 + nb - 1);
-    if ((clast + 1) * VCHUNK > d.V) {
-      // short last chunk: gather it separately so no slot past V is read
-      Gather g2[2];
-      uint32_t ng = 0;
-      if (nb > 1) g2[ng++] = {g.src, VCHUNK, nb - 1, G * VCHUNK, gl, chunk};
-      g2[ng++] = gather_vec(a.mb_logit + (size_t)clast * VCHUNK, d.V - clast * VCHUNK, gl,
-                            chunk + (nb - 1) * VCHUNK);
-      if (!wait_gather(g2, ng, a.st, s.ctl)) return false;
-    } else if (!wait_gather(&g, 1, a.st, s.ctl)) {
-      return false;
-    }
+    // a short last chunk is gathered separately so no slot past V is read
+    const bool short_last = (clast + 1) * VCHUNK > d.V;
+    const Gather ga = gather_strided(src0, VCHUNK, short_last ? nb - 1 : nb, G * VCHUNK, gl, chunk);
+    const Gather gb = short_last ? gather_vec(a.mb_logit + (size_t)clast * VCHUNK,
+                                              d.V - clast * VCHUNK, gl, chunk + (nb - 1) * VCHUNK)
+                                 : no_gather();
+    if (!poll_gather<2, 1>(ga, gb, NWAVES, a.st, s.ctl)) return false;
     if (wave < nb) {
       const uint32_t c = wg + G * (k0 + wave);
       const uint32_t v = c * VCHUNK + lane;
@@ -600,7 +945,7 @@ __device__ __forceinline__ float wave_scan(float x) {
 // scanned element by element, p_v = exp(l_v/T - m) * (1/total), returning
 // the first v with p_v > 0 and r < cumulative, else the last v with p_v > 0.
 // A degenerate total (not > 0, or not finite) falls back to argmax.
-__device__ bool sample_stage_b(const Args& a, uint32_t tick, float T, uint32_t word,
+__device__ __forceinline__ bool sample_stage_b(const Args& a, uint32_t tick, float T, uint32_t word,
                                const Lds& s, uint32_t* tok_out) {
   const Dims& d = a.d;
   const uint32_t nvc = d.nvc;
@@ -610,12 +955,10 @@ __device__ bool sample_stage_b(const Args& a, uint32_t tick, float T, uint32_t w
   float* vsum = varg + nvc;
   float* chunk = vsum + nvc;  // [VCHUNK]
   float* wtot = chunk + VCHUNK;  // [NWAVES + 2]
-  Gather gs[3];
-  uint32_t ng = 0;
-  gs[ng++] = gather_vec(a.mb_vmax, nvc, gl, vmx);
-  gs[ng++] = gather_vec(a.mb_varg, nvc, gl, varg);
-  if (T != 0.0f) gs[ng++] = gather_vec(a.mb_vsum, nvc, gsum, vsum);
-  if (!wait_gather(gs, ng, a.st, s.ctl)) return false;
+  if (!poll_gather<4, 4, 4>(gather_vec(a.mb_vmax, nvc, gl, vmx), gather_vec(a.mb_varg, nvc, gl, varg),
+                   T != 0.0f ? gather_vec(a.mb_vsum, nvc, gsum, vsum) : no_gather(), NWAVES, a.st,
+                   s.ctl))
+    return false;
   float bv;
   uint32_t bi;
   global_argmax(vmx, varg, nvc, s.red, &bv, &bi);
@@ -676,8 +1019,7 @@ __device__ bool sample_stage_b(const Args& a, uint32_t tick, float T, uint32_t w
   // Element scan from chunk cstar onwards (normally one chunk).
   for (uint32_t c = cstar; c < nvc; ++c) {
     const uint32_t v0 = c * VCHUNK, nv = min(VCHUNK, d.V - v0);
-    Gather g = gather_vec(a.mb_logit + v0, nv, gl, chunk);
-    if (!wait_gather(&g, 1, a.st, s.ctl)) return false;
+    if (!poll_gather<1>(gather_vec(a.mb_logit + v0, nv, gl, chunk), NWAVES, a.st, s.ctl)) return false;
     const float p = (lane < nv) ? exp_term(chunk[lane], T, m) * inv : 0.0f;
     const float sc = wave_scan(p > 0.0f ? p : 0.0f);
     const bool hit = p > 0.0f && r < run + sc;
@@ -694,8 +1036,7 @@ __device__ bool sample_stage_b(const Args& a, uint32_t tick, float T, uint32_t w
   for (uint32_t cc = nvc; cc-- > 0;) {
     if (!(vsum[cc] > 0.0f)) continue;
     const uint32_t v0 = cc * VCHUNK, nv = min(VCHUNK, d.V - v0);
-    Gather g = gather_vec(a.mb_logit + v0, nv, gl, chunk);
-    if (!wait_gather(&g, 1, a.st, s.ctl)) return false;
+    if (!poll_gather<1>(gather_vec(a.mb_logit + v0, nv, gl, chunk), NWAVES, a.st, s.ctl)) return false;
     const float p = (lane < nv) ? exp_term(chunk[lane], T, m) * inv : 0.0f;
     const unsigned long long nz = __ballot(p > 0.0f);
     __syncthreads();
