@@ -58,22 +58,22 @@ __device__ __forceinline__ Lds lds_init(const Dims& d) {
 }
 
 __device__ __forceinline__ bool forward_all(const Args& a, uint32_t tok, uint32_t pos, uint32_t tick,
-                                            uint32_t wg, uint32_t G, const Lds& s, Pf& pf) {
+                                            uint32_t wg, uint32_t G, const Lds& s,
+                                            const Stager& sg) {
   for (uint32_t l = 0; l < a.d.L; ++l) {
-    pf.next_layer = (l + 1 < a.d.L) ? l + 1 : 0;
-    if (!phase_qkv(a, l, tick, pos, tok, wg, G, s, pf)) return false;
+    if (!phase_qkv(a, l, tick, pos, tok, wg, G, s, sg)) return false;
     if (!phase_attn(a, l, tick, pos, wg, G, s)) return false;
     if (!phase_comb(a, l, tick, pos, wg, G, s)) return false;
-    if (!phase_o(a, l, tick, pos, tok, wg, G, s, pf)) return false;
-    if (!phase_gu(a, l, tick, wg, G, s, pf)) return false;
-    if (!phase_d(a, l, tick, wg, G, s, pf)) return false;
+    if (!phase_o(a, l, tick, pos, tok, wg, G, s, sg)) return false;
+    if (!phase_gu(a, l, tick, wg, G, s, sg)) return false;
+    if (!phase_d(a, l, tick, wg, G, s, sg)) return false;
   }
-  return phase_lm(a, tick, wg, G, s);
+  return phase_lm(a, tick, wg, G, s, sg);
 }
 
 __device__ __forceinline__ bool is_stop(const RunDesc& r, uint32_t tok) {
   for (uint32_t k = 0; k < r.n_stop; ++k)
-    if (r.stop[k] == tok) return true;
+    if (cptr(r.stop)[k] == tok) return true;
   return false;
 }
 
@@ -85,25 +85,25 @@ __global__ __launch_bounds__(BLOCK) void k_persistent(const Args* __restrict__ a
   const Lds s = lds_init(a.d);
   const RunDesc r = *run;
   DevState* st = a.st;
-  uint32_t pos = st->pos, tick = st->tick;
+  uint32_t pos = cptr(st)->pos, tick = cptr(st)->tick;
   const uint32_t wg = blockIdx.x, G = gridDim.x;
   lm_prime(a, s);
-  SlotSet slots;
-  slot_prime(a, slots, 0, wg, G);
-  Pf pf;
-  pf.on = true;
-  pf.SS = &slots;
-  pf.next_layer = 0;
+  // Weight rows are staged in LDS when a layer's share fits: the loaders
+  // request layer 0's QKV, O and GU rows now (the D rows follow at the first
+  // QKV phase, as in every later layer).
+  const Stager sg = make_stager(a, s, wg, G, a.d.lds_stg != 0);
+  if (sg.on && sg.loader)
+    for (uint32_t k = 0; k < 3; ++k) stage_issue(sg, k, 0);
   uint32_t i = 0;
   uint32_t halted = 0;
   for (; i < r.n_ops; ++i) {
     uint32_t tok;
     if (i >= r.sample_from) {
-      const uint32_t word = r.temperature != 0.0f ? r.words[i - r.sample_from] : 0u;
+      const uint32_t word = r.temperature != 0.0f ? cptr(r.words)[i - r.sample_from] : 0u;
       if (r.temperature != 0.0f && !sample_stage_a(a, tick, r.temperature, wg, G, s)) break;
       if (!sample_stage_b(a, tick, r.temperature, word, s, &tok)) break;
       if (r.mode == RUN_REPLAY) {
-        if (tok != r.tokens[i]) {
+        if (tok != cptr(r.tokens)[i]) {
           if (wg == 0 && threadIdx.x == 0) {
             st->first_div = (long long)i;
             st->sampled_div = tok;
@@ -111,14 +111,14 @@ __global__ __launch_bounds__(BLOCK) void k_persistent(const Args* __restrict__ a
           halted = 1;
           break;
         }
-        tok = r.tokens[i];
+        tok = cptr(r.tokens)[i];
       } else if (wg == 0 && threadIdx.x == 0) {
         r.out_tokens[i] = tok;
       }
     } else {
-      tok = r.tokens[i];
+      tok = cptr(r.tokens)[i];
     }
-    if (!forward_all(a, tok, pos, tick, wg, G, s, pf)) break;
+    if (!forward_all(a, tok, pos, tick, wg, G, s, sg)) break;
     ++pos;
     ++tick;
     if (r.mode == RUN_GENERATE && is_stop(r, tok)) {
@@ -133,6 +133,8 @@ __global__ __launch_bounds__(BLOCK) void k_persistent(const Args* __restrict__ a
     st->n_done = i;
     st->halt = halted;
   }
+  // Staged loads of a layer that will not run land before the wave ends.
+  if (sg.on && sg.loader) stage_wait(0);
 }
 
 // Per-run reset of the counters (pos / tick / token are kept).
@@ -155,20 +157,17 @@ __global__ __launch_bounds__(BLOCK) void k_phase(const Args* __restrict__ ap, ui
   if (st->halt) return;
   const uint32_t pos = st->pos, tick = st->tick, token = st->token;
   const uint32_t wg = blockIdx.x, G = gridDim.x;
-  Pf pf;
-  pf.on = false;
-  pf.SS = nullptr;
-  pf.next_layer = 0;
+  const Stager sg = make_stager(a, s, wg, G, false);
   switch (ph) {
-    case PH_QKV: phase_qkv(a, layer, tick, pos, token, wg, G, s, pf); break;
+    case PH_QKV: phase_qkv(a, layer, tick, pos, token, wg, G, s, sg); break;
     case PH_ATTN: phase_attn(a, layer, tick, pos, wg, G, s); break;
     case PH_COMB: phase_comb(a, layer, tick, pos, wg, G, s); break;
-    case PH_O: phase_o(a, layer, tick, pos, token, wg, G, s, pf); break;
-    case PH_GU: phase_gu(a, layer, tick, wg, G, s, pf); break;
-    case PH_D: phase_d(a, layer, tick, wg, G, s, pf); break;
+    case PH_O: phase_o(a, layer, tick, pos, token, wg, G, s, sg); break;
+    case PH_GU: phase_gu(a, layer, tick, wg, G, s, sg); break;
+    case PH_D: phase_d(a, layer, tick, wg, G, s, sg); break;
     case PH_LM_KERNEL:
       lm_prime(a, s);
-      phase_lm(a, tick, wg, G, s);
+      phase_lm(a, tick, wg, G, s, sg);
       break;
     default: break;
   }
@@ -209,7 +208,7 @@ __global__ __launch_bounds__(BLOCK) void k_op(const Args* __restrict__ ap,
         }
         return;
       }
-      tok = r.tokens[i];
+      tok = cptr(r.tokens)[i];
     } else if (threadIdx.x == 0) {
       r.out_tokens[i] = tok;
     }
@@ -295,6 +294,9 @@ struct defer_gpu_cache {
 
 static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
+// LDS of one gfx950 compute unit, all of which a workgroup may take.
+static constexpr size_t LDS_BYTES_MAX = 160 * 1024;
+
 extern "C" size_t defer_gpu_model_tensor_count(const defer_gpu_config* c) {
   const size_t per_layer = c->has_bias ? 12 : 9;
   return 1 + (size_t)c->num_layers * per_layer + 1 + (c->tie_word_embeddings ? 0 : 1);
@@ -310,8 +312,8 @@ static int validate(const defer_gpu_config* c) {
                 "num_attention_heads must be a multiple of num_key_value_heads");
   if (c->head_dim % 2 != 0) return fail(DEFER_GPU_E_INVALID, "head_dim must be even for RoPE");
   const uint32_t hd = c->head_dim;
-  if (hd % 4 != 0 || 64 % (hd / 4) != 0)
-    return fail(DEFER_GPU_E_INVALID, "head_dim %u unsupported (need 4*2^k, at most 256)", hd);
+  if (hd < 16 || hd > 256 || (hd & (hd - 1)) != 0)
+    return fail(DEFER_GPU_E_INVALID, "head_dim %u unsupported (need 16 * 2^k, at most 256)", hd);
   if (c->num_heads / c->num_kv_heads > MAX_GROUP)
     return fail(DEFER_GPU_E_INVALID, "GQA group larger than %u", MAX_GROUP);
   if (c->hidden_size % 4 || c->intermediate_size % 4)
@@ -382,13 +384,36 @@ extern "C" int defer_gpu_model_create(const defer_gpu_config* cfg, const float* 
   d.lds_vec2 = (2 * d.h + 3) & ~3u;
   const uint32_t hs = d.hd + 2;
   const uint32_t rmax = (d.h + m->G - 1) / m->G;
-  const uint32_t scr_attn = d.group * d.hd + 2 * d.hd + NWA * d.group * hs;
+  const uint32_t scr_attn = MAX_GROUP * d.hd + 2 * d.hd + 2 * MAX_GROUP +
+                            MAX_GROUP * attn_chunk(d.cap - 1) + NWA * 256 * d.group;
   const uint32_t scr_o = INLINE_COMB_MAX + rmax;
   const uint32_t scr_comb = MAX_ACHUNKS * hs;
-  const uint32_t scr_samp = 3 * d.nvc + VCHUNK + NWAVES + 2 + NWAVES * VCHUNK;
+  const uint32_t scr_samp = 3 * d.nvc + VCHUNK + NWAVES + 2 + NWA * VCHUNK;
   const uint32_t scr_lm = ((d.nvc + m->G - 1) / m->G) * VCHUNK;
   d.lds_scr = (std::max({scr_attn, scr_o, scr_comb, scr_samp, scr_lm, 2 * NWAVES}) + 3) & ~3u;
-  m->lds_bytes = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr) * sizeof(float);
+  // Publish list: one entry per matvec result of a phase (four per QKV item).
+  {
+    const uint32_t per_wg[4] = {4 * ((d.qkv_rows / 2 + m->G - 1) / m->G), (d.h + m->G - 1) / m->G,
+                                (d.ff + m->G - 1) / m->G, (d.h + m->G - 1) / m->G};
+    d.lds_pub = std::max({per_wg[0], per_wg[1], per_wg[2], per_wg[3]});
+  }
+  // Weight staging for the persistent kernel: each kind's rows of one layer
+  // for the workgroup with the most items, if that fits the CU's LDS.
+  {
+    const uint32_t n_items[4] = {d.qkv_rows / 2, d.h, d.ff, d.h};
+    const uint32_t rows[4] = {2, 1, 2, 1};
+    const uint32_t K[4] = {d.h, d.q, d.h, d.ff};
+    uint32_t stg = 0;
+    for (int k = 0; k < 4; ++k) {
+      d.stg_off[k] = stg;
+      stg += (n_items[k] + m->G - 1) / m->G * rows[k] * K[k];
+    }
+    const size_t base = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr) * sizeof(float) +
+                        (size_t)d.lds_pub * 2 * sizeof(u64);
+    d.lds_stg = (base + (size_t)stg * sizeof(float) <= LDS_BYTES_MAX) ? stg : 0;
+  }
+  m->lds_bytes = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr + d.lds_stg) * sizeof(float) +
+                 (size_t)d.lds_pub * 2 * sizeof(u64);
 
   // Weight layout: one allocation, each tensor 256-byte aligned; q/k/v rows
   // are stored back to back as one [q + 2kv, h] matrix.

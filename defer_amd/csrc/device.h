@@ -26,8 +26,8 @@ constexpr uint32_t BLOCK = 512;
 constexpr uint32_t NWAVES = BLOCK / WAVE;
 constexpr uint32_t VCHUNK = 64;        // vocabulary rows per sampling chunk
 constexpr uint32_t ACHUNK = 128;       // attention positions per chunk (base size)
-constexpr uint32_t MAX_ACHUNKS = 3;    // attention chunks per head at most
-constexpr uint32_t INLINE_COMB_MAX = 8192;  // floats of partials combined inside the O phase
+constexpr uint32_t MAX_ACHUNKS = 16;   // attention chunks per head at most
+constexpr uint32_t INLINE_COMB_MAX = 1536;  // floats of partials combined inside the O phase
 constexpr uint32_t SPIN_LIMIT = 1u << 21;
 constexpr uint32_t NO_INDEX = 0xffffffffu;
 
@@ -42,6 +42,9 @@ struct Dims {
   uint32_t lds_vec;    // floats of the input-vector LDS region
   uint32_t lds_vec2;   // floats of the second vector region (h)
   uint32_t lds_scr;    // floats of the scratch LDS region
+  uint32_t lds_stg;    // floats of the weight staging region (0: rows are not staged)
+  uint32_t stg_off[4]; // float offset of each item kind's rows in the staging region
+  uint32_t lds_pub;    // entries of the publish list
   float eps, scale;
 };
 
@@ -150,6 +153,7 @@ __host__ __device__ inline bool comb_inline(const Dims& d, uint32_t pos) {
 // wait for every outstanding HBM load and undo the prefetching.
 
 #define AS_GLOBAL __attribute__((address_space(1)))
+#define AS_CONST __attribute__((address_space(4)))
 #define AS_LDS __attribute__((address_space(3)))
 
 // Address-space casts go through an integer: a direct cast from a generic
@@ -158,6 +162,13 @@ __host__ __device__ inline bool comb_inline(const Dims& d, uint32_t pos) {
 template <class T>
 __device__ __forceinline__ AS_GLOBAL T* gptr(T* p) {
   return (AS_GLOBAL T*)(uintptr_t)p;
+}
+// Read-only data the whole kernel shares (the layer table): through the
+// constant address space, so wave-uniform reads become scalar loads, which
+// never enter the vector-memory counter.
+template <class T>
+__device__ __forceinline__ const AS_CONST T* cptr(const T* p) {
+  return (const AS_CONST T*)(uintptr_t)p;
 }
 template <class T>
 __device__ __forceinline__ AS_LDS T* lptr(T* p) {
@@ -206,15 +217,81 @@ __device__ __forceinline__ void st_coherent_u32(uint32_t* p, uint32_t v) {
 
 // --------------------------------------------------------- reductions
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+// Lane permutations through DPP (a VALU operand modifier: a few cycles, no
+// LDS round trip). Controls: quad_perm [1,0,3,2] and [2,3,0,1], mirror within
+// 8 and 16 lanes, and the row broadcasts of lane 15 / 31 into later rows.
+enum : uint32_t {
+  DPP_QUAD_X1 = 0xB1,
+  DPP_QUAD_X2 = 0x4E,
+  DPP_HALF_MIRROR = 0x141,
+  DPP_MIRROR = 0x140,
+  DPP_BCAST15 = 0x142,
+  DPP_BCAST31 = 0x143,
+};
+
+// v from the lane DPP control CTRL names; lanes of rows outside ROWS get old.
+template <uint32_t CTRL, uint32_t ROWS = 0xF>
+__device__ __forceinline__ float dpp_f(float old, float v) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROWS, 0xF, false));
+}
+template <uint32_t CTRL, uint32_t ROWS = 0xF>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t old, uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, ROWS, 0xF, false);
+}
+
+// Sum over aligned groups of n lanes (n = 1, 2, 4, 8 or 16): a butterfly in
+// which the two lanes of each pair add the same two values, so every lane of
+// a group ends with the same bits.
+__device__ __forceinline__ float group_sum(float v, uint32_t n) {
+  if (n >= 2) v += dpp_f<DPP_QUAD_X1>(0.0f, v);
+  if (n >= 4) v += dpp_f<DPP_QUAD_X2>(0.0f, v);
+  if (n >= 8) v += dpp_f<DPP_HALF_MIRROR>(0.0f, v);
+  if (n >= 16) v += dpp_f<DPP_MIRROR>(0.0f, v);
   return v;
 }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+__device__ __forceinline__ float row_max(float v) {
+  v = fmaxf(v, dpp_f<DPP_QUAD_X1>(v, v));
+  v = fmaxf(v, dpp_f<DPP_QUAD_X2>(v, v));
+  v = fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v, v));
+  v = fmaxf(v, dpp_f<DPP_MIRROR>(v, v));
   return v;
+}
+
+// Sum over the wave in a fixed tree: rows of 16 (group_sum), then
+// row1 += row0, row3 += row2, row3 += row1; lane 63's value, to every lane.
+__device__ __forceinline__ float wave_sum(float v) {
+  v = group_sum(v, 16);
+  v += dpp_f<DPP_BCAST15, 0xA>(0.0f, v);
+  v += dpp_f<DPP_BCAST31, 0xC>(0.0f, v);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), WAVE - 1));
+}
+// wave_sum of N values at once, stage by stage, so the N dependency chains
+// interleave (same tree, same bits as wave_sum).
+template <int N>
+__device__ __forceinline__ void wave_sum_n(float* v) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_f<DPP_QUAD_X1>(0.0f, v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_f<DPP_QUAD_X2>(0.0f, v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_f<DPP_HALF_MIRROR>(0.0f, v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_f<DPP_MIRROR>(0.0f, v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_f<DPP_BCAST15, 0xA>(0.0f, v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_f<DPP_BCAST31, 0xC>(0.0f, v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    v[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[i]), WAVE - 1));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = row_max(v);
+  v = fmaxf(v, dpp_f<DPP_BCAST15, 0xA>(v, v));
+  v = fmaxf(v, dpp_f<DPP_BCAST31, 0xC>(v, v));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), WAVE - 1));
 }
 
 // Sum over the block in a fixed tree; every thread gets the result.

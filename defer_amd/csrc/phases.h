@@ -6,13 +6,17 @@
 // same way whoever computes it.
 //
 // Roles inside a workgroup (BLOCK = 512 threads = 8 waves):
-//  * waves 0..NPOLL-1 are pollers: in the matvec phases they alone read
-//    mailboxes, so their in-order load counter never holds a weight load
-//    and a poll completes as soon as its data is there;
-//  * waves NPOLL.. are compute waves: each owns the matvec items dealt to it
-//    and keeps the rows of its first NSLOT items in register slots, each
-//    refilled for the next layer right after use (persistent kernel only),
-//    so the weights of a phase are in registers before its inputs arrive.
+//  * pollers (waves 0..NPOLL-1) alone read mailboxes in the matvec phases,
+//    so a poll round waits for nothing but its own words;
+//  * compute waves (the next NCW) compute the matvec items dealt to them;
+//  * loaders (the last NLOAD waves) stage weight rows into LDS with direct
+//    global->LDS loads (persistent kernel only, when a layer's share of the
+//    workgroup fits): each kind's rows for the next layer are requested as
+//    soon as this layer's rows of that kind have been used, and a loader
+//    waits for them (exact vector-memory counts) only at the barrier before
+//    their use. Loaders issue no other memory instruction, so those counts
+//    hold, and no other wave ever waits for a weight load.
+// Attention, lm_head and the sampler run on pollers and compute waves.
 #pragma once
 
 #include "device.h"
@@ -20,9 +24,10 @@
 namespace dg {
 
 constexpr uint32_t NPOLL = 2;
-constexpr uint32_t NCW = NWAVES - NPOLL;
-constexpr uint32_t NSLOT = 2;
-constexpr int KS = 3;  // float4 per lane in half a slot: 768 floats
+constexpr uint32_t NCW = 4;
+constexpr uint32_t NLOAD = NWAVES - NPOLL - NCW;
+constexpr uint32_t NWA = NPOLL + NCW;  // waves 0..NWA-1 compute attention, lm_head, sampler
+static_assert(NLOAD == 2, "two loader waves");
 
 struct Lds {
   WaitCtl* ctl;
@@ -30,6 +35,8 @@ struct Lds {
   float* vec;   // d.lds_vec floats: the matvec input vector
   float* vec2;  // d.lds_vec2 floats: the normalised lm_head input
   float* scr;   // d.lds_scr floats
+  float* stg;   // d.lds_stg floats: staged weight rows (persistent kernel)
+  u64* pub;     // d.lds_pub entries of {word, address}: results the pollers store
 };
 
 __device__ inline Lds lds_layout(float* base, const Dims& d) {
@@ -39,6 +46,8 @@ __device__ inline Lds lds_layout(float* base, const Dims& d) {
   s.vec = base + 4 + 64;
   s.vec2 = s.vec + d.lds_vec;
   s.scr = s.vec2 + d.lds_vec2;
+  s.stg = s.scr + d.lds_scr;
+  s.pub = reinterpret_cast<u64*>(s.stg + d.lds_stg);
   return s;
 }
 
@@ -111,18 +120,29 @@ __device__ __forceinline__ uint32_t rounds_for(uint32_t n, uint32_t per_round) {
   return per_round ? (n + per_round - 1) / per_round : (n ? 0xffffffffu : 0u);
 }
 
+// Work other waves do around a poll's first barrier (the barrier after which
+// the previous phase's compute is over): pre_b1 runs before it, post_b1
+// after it, while the pollers poll.
+struct NoHook {
+  __device__ __forceinline__ void pre_b1() const {}
+  __device__ __forceinline__ void post_b1() const {}
+};
+
 // Wait until every element of up to three gathers carries its generation and
 // copy the values to LDS. Only the first `npoll_waves` waves read memory; a
 // polling lane keeps P0 + P1 + P2 words in flight per round (sized to the call
 // site), loops until its own words are all current, and the block then meets
 // at a barrier. Returns false (uniformly) if the run was aborted.
-template <uint32_t P0, uint32_t P1 = 0, uint32_t P2 = 0>
+template <uint32_t P0, uint32_t P1 = 0, uint32_t P2 = 0, class H = NoHook>
 __device__ __forceinline__ bool poll_gather(const Gather& g0, const Gather& g1, const Gather& g2,
-                                            uint32_t npoll_waves, DevState* st, WaitCtl* ctl) {
+                                            uint32_t npoll_waves, DevState* st, WaitCtl* ctl,
+                                            const H& hook = H()) {
   const uint32_t tid = threadIdx.x;
   const uint32_t npl = npoll_waves * WAVE;
+  hook.pre_b1();
   // The destination LDS may still be read by the previous phase.
   __syncthreads();
+  hook.post_b1();
   if (tid < npl) {
     const uint32_t n0 = g0.seg_len * g0.n_seg, n1 = g1.seg_len * g1.n_seg;
     const uint32_t n2 = g2.seg_len * g2.n_seg;
@@ -161,15 +181,15 @@ __device__ __forceinline__ bool poll_gather(const Gather& g0, const Gather& g1, 
   return ctl->abort_seen == 0;
 }
 
-template <uint32_t P0, uint32_t P1>
+template <uint32_t P0, uint32_t P1, class H = NoHook>
 __device__ __forceinline__ bool poll_gather(const Gather& g0, const Gather& g1, uint32_t npw,
-                                            DevState* st, WaitCtl* ctl) {
-  return poll_gather<P0, P1, 0>(g0, g1, no_gather(), npw, st, ctl);
+                                            DevState* st, WaitCtl* ctl, const H& hook = H()) {
+  return poll_gather<P0, P1, 0, H>(g0, g1, no_gather(), npw, st, ctl, hook);
 }
-template <uint32_t P0>
+template <uint32_t P0, class H = NoHook>
 __device__ __forceinline__ bool poll_gather(const Gather& g0, uint32_t npw, DevState* st,
-                                            WaitCtl* ctl) {
-  return poll_gather<P0, 0, 0>(g0, no_gather(), no_gather(), npw, st, ctl);
+                                            WaitCtl* ctl, const H& hook = H()) {
+  return poll_gather<P0, 0, 0, H>(g0, no_gather(), no_gather(), npw, st, ctl, hook);
 }
 
 // Number of items i = wg + G*k below n owned by this workgroup.
@@ -177,38 +197,76 @@ __device__ __forceinline__ uint32_t rows_owned(uint32_t n, uint32_t wg, uint32_t
   return wg < n ? (n - wg + G - 1) / G : 0;
 }
 
+// ------------------------------------------------------------ publishing
+//
+// Compute waves hand their results to the pollers through LDS instead of
+// storing them: a wave's vector-memory counter then never holds a store, so
+// no later wait of a compute wave can stall on one. A phase ends with a
+// barrier, after which the pollers issue the stores of entries [0, n).
+
+// Entry i: a tagged mailbox word for `slot`.
+__device__ __forceinline__ void pub_word(const Lds& s, uint32_t i, u64* slot, float v, uint32_t gen) {
+  AS_LDS u64* e = lptr(s.pub + 2 * i);
+  e[0] = ((u64)gen << 32) | (u64)__float_as_uint(v);
+  e[1] = (u64)(uintptr_t)slot;
+}
+// Entry i: a plain float for `p` (address bit 0 marks the kind).
+__device__ __forceinline__ void pub_float(const Lds& s, uint32_t i, float* p, float v) {
+  AS_LDS u64* e = lptr(s.pub + 2 * i);
+  e[0] = (u64)__float_as_uint(v);
+  e[1] = (u64)(uintptr_t)p | 1u;
+}
+__device__ __forceinline__ void pub_none(const Lds& s, uint32_t i) { lptr(s.pub + 2 * i)[1] = 0; }
+
+// The barrier that ends a matvec phase, then the pollers' stores.
+__device__ __forceinline__ void pub_flush(const Lds& s, uint32_t n) {
+  __syncthreads();
+  if (threadIdx.x >= NPOLL * WAVE) return;
+  for (uint32_t i = threadIdx.x; i < n; i += NPOLL * WAVE) {
+    const AS_LDS u64* e = lptr(s.pub + 2 * i);
+    const u64 w = e[0], addr = e[1];
+    if (addr & 1u)
+      st_coherent(reinterpret_cast<float*>((uintptr_t)(addr & ~(u64)1)), __uint_as_float((uint32_t)w));
+    else if (addr)
+      __hip_atomic_store(gptr(reinterpret_cast<u64*>((uintptr_t)addr)), w, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 // ------------------------------------------------------------- matvec items
 
 enum ItemKind : uint32_t { IK_QKV = 0, IK_O = 1, IK_GU = 2, IK_D = 3 };
 
-// The workgroup's items of every kind, numbered in order QKV, O, GU, D; item
-// number r belongs to compute wave r % NCW and lives in its slot r / NCW
-// (items with r / NCW >= NSLOT are loaded when used).
-struct Deal {
-  uint32_t base[4], cnt[4];
-};
-
-__device__ __forceinline__ Deal deal_of(const Dims& d, uint32_t wg, uint32_t G) {
-  Deal q;
-  q.cnt[IK_QKV] = rows_owned(d.qkv_rows / 2, wg, G);
-  q.cnt[IK_O] = rows_owned(d.h, wg, G);
-  q.cnt[IK_GU] = rows_owned(d.ff, wg, G);
-  q.cnt[IK_D] = rows_owned(d.h, wg, G);
-  q.base[0] = 0;
-  q.base[1] = q.cnt[0];
-  q.base[2] = q.base[1] + q.cnt[1];
-  q.base[3] = q.base[2] + q.cnt[2];
-  return q;
+// Items of each kind: QKV pairs (rows i, i + hd/2 of one head, so RoPE needs
+// no exchange), O rows, GU pairs (gate row j, up row j), D rows. Item k of a
+// kind owned by workgroup wg is number wg + G*k; compute wave k % NCW
+// computes it and loader k % NLOAD stages it.
+__device__ __forceinline__ uint32_t kind_items(const Dims& d, uint32_t kind) {
+  return kind == IK_QKV ? d.qkv_rows / 2 : (kind == IK_GU ? d.ff : d.h);
+}
+__device__ __forceinline__ uint32_t kind_k(const Dims& d, uint32_t kind) {
+  return kind == IK_O ? d.q : (kind == IK_D ? d.ff : d.h);
+}
+__device__ __forceinline__ uint32_t kind_rows(uint32_t kind) {
+  return (kind == IK_QKV || kind == IK_GU) ? 2u : 1u;
 }
 
-// Registers holding the first 1536 floats of one item: two rows of up to 768
-// (pairs) or one row split in halves.
-struct Slot {
-  RowT<KS> a, b;
-};
+// The layer table entry of layer l (scalar loads: see cptr).
+__device__ __forceinline__ LayerW layer_w(const Args& a, uint32_t l) {
+  const AS_CONST LayerW* p = cptr(a.layers) + l;
+  LayerW W;
+  W.attn_norm = p->attn_norm;
+  W.wqkv = p->wqkv;
+  W.bqkv = p->bqkv;
+  W.wo = p->wo;
+  W.ffn_norm = p->ffn_norm;
+  W.wg = p->wg;
+  W.wu = p->wu;
+  W.wd = p->wd;
+  return W;
+}
 
-// Row pointers and length of item k of a kind in layer l. Pairs give two
-// rows (QKV: rows i and i + hd/2 of one head; GU: gate and up row j).
+// Row pointers and length of item k of a kind in layer l.
 struct ItemRows {
   const float* w0;
   const float* w1;  // null for single-row kinds
@@ -218,7 +276,7 @@ struct ItemRows {
 __device__ __forceinline__ ItemRows item_rows(const Args& a, uint32_t kind, uint32_t l, uint32_t k,
                                               uint32_t wg, uint32_t G) {
   const Dims& d = a.d;
-  const LayerW& W = a.layers[l];
+  const LayerW W = layer_w(a, l);
   const uint32_t it = wg + G * k;
   ItemRows r;
   if (kind == IK_QKV) {
@@ -243,28 +301,143 @@ __device__ __forceinline__ ItemRows item_rows(const Args& a, uint32_t kind, uint
   return r;
 }
 
-__device__ __forceinline__ void slot_load(Slot& S, const ItemRows& r, uint32_t lane) {
-  row_load(S.a, r.w0, r.K, lane);
-  if (r.w1)
-    row_load(S.b, r.w1, r.K, lane);
-  else if (r.K > 256u * KS)
-    row_load(S.b, r.w0 + 256u * KS, r.K - 256u * KS, lane);
+// Staging of the workgroup's rows in LDS (persistent kernel). Kind X's items
+// sit back to back at s.stg + d.stg_off[X], item k's rows contiguous.
+struct Stager {
+  bool on;             // rows are staged (else compute waves load them)
+  const Args* a;
+  float* stg;
+  uint32_t wg, G, ld;  // ld: this wave's loader index (loaders only)
+  bool loader;
+  // Loads a loader may leave in flight when kind X's rows must have landed:
+  // at the first barrier of X's phase, the batches requested after X's are
+  // those of the two kinds whose phases came since (the kind before X is
+  // requested only after that barrier).
+  uint32_t wait[4];
+};
+
+// 16 bytes per lane from global memory straight into LDS: lane i's bytes
+// land at LDS byte address lds_base + 16*i (lds_base is wave-uniform). M0,
+// which the instruction takes the LDS address from, is saved and restored.
+// The compiler does not see this load, so it never waits for it: loaders
+// wait explicitly (stage_wait).
+__device__ __forceinline__ void dma16(const float* src, uint32_t lds_base) {
+  uint32_t m0_saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(m0_saved)
+      : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_base))
+      : "memory");
 }
 
-// Lane partial of w . x over a row whose first 256*KS floats are in `first`
-// and, when `second` is given, the next 256*KS in `second`; the rest streams.
-// Ascending j, one fma per element.
-__device__ __forceinline__ float dot_slot(RowT<KS>& first, RowT<KS>* second, const float* w,
-                                          const float* x, uint32_t K, uint32_t lane) {
-  float acc = row_fma(first, x, K, lane, 0.0f);
-  uint32_t base = 256u * KS;
-  if (second && base < K) {
-    acc = row_fma(*second, x + base, K - base, lane, acc);
-    base += 256u * KS;
+// s_waitcnt vmcnt(n) for a run-time n (clamped to the counter's 63).
+__device__ __forceinline__ void stage_wait(uint32_t n) {
+#define DG_VMW(N) \
+  case N:         \
+    asm volatile("s_waitcnt vmcnt(" #N ")" ::: "memory"); \
+    break;
+  switch (n < 63u ? n : 63u) {
+    DG_VMW(0) DG_VMW(1) DG_VMW(2) DG_VMW(3) DG_VMW(4) DG_VMW(5) DG_VMW(6) DG_VMW(7)
+    DG_VMW(8) DG_VMW(9) DG_VMW(10) DG_VMW(11) DG_VMW(12) DG_VMW(13) DG_VMW(14) DG_VMW(15)
+    DG_VMW(16) DG_VMW(17) DG_VMW(18) DG_VMW(19) DG_VMW(20) DG_VMW(21) DG_VMW(22) DG_VMW(23)
+    DG_VMW(24) DG_VMW(25) DG_VMW(26) DG_VMW(27) DG_VMW(28) DG_VMW(29) DG_VMW(30) DG_VMW(31)
+    DG_VMW(32) DG_VMW(33) DG_VMW(34) DG_VMW(35) DG_VMW(36) DG_VMW(37) DG_VMW(38) DG_VMW(39)
+    DG_VMW(40) DG_VMW(41) DG_VMW(42) DG_VMW(43) DG_VMW(44) DG_VMW(45) DG_VMW(46) DG_VMW(47)
+    DG_VMW(48) DG_VMW(49) DG_VMW(50) DG_VMW(51) DG_VMW(52) DG_VMW(53) DG_VMW(54) DG_VMW(55)
+    DG_VMW(56) DG_VMW(57) DG_VMW(58) DG_VMW(59) DG_VMW(60) DG_VMW(61) DG_VMW(62)
+    default:
+      asm volatile("s_waitcnt vmcnt(63)" ::: "memory");
+      break;
   }
-  for (; base < K; base += 256u * KS) {
-    row_load(first, w + base, K - base, lane);
-    acc = row_fma(first, x + base, K - base, lane, acc);
+#undef DG_VMW
+}
+
+// Loads one loader wave issues for its items of a kind: 1 KB per load.
+__device__ __forceinline__ uint32_t stage_loads(const Dims& d, uint32_t kind, uint32_t wg,
+                                                uint32_t G, uint32_t ld) {
+  const uint32_t cnt = rows_owned(kind_items(d, kind), wg, G);
+  const uint32_t mine = cnt > ld ? (cnt - ld + NLOAD - 1) / NLOAD : 0;
+  return mine * kind_rows(kind) * ((kind_k(d, kind) + 255) / 256);
+}
+
+__device__ __forceinline__ Stager make_stager(const Args& a, const Lds& s, uint32_t wg, uint32_t G,
+                                              bool on) {
+  Stager sg;
+  sg.on = on;
+  sg.a = &a;
+  sg.stg = s.stg;
+  sg.wg = wg;
+  sg.G = G;
+  const uint32_t wave = threadIdx.x / WAVE;
+  sg.loader = wave >= NWA;
+  sg.ld = sg.loader ? wave - NWA : 0;
+  uint32_t n[4], tot = 0;
+  for (uint32_t k = 0; k < 4; ++k) {
+    n[k] = stage_loads(a.d, k, wg, G, sg.ld);
+    tot += n[k];
+  }
+  for (uint32_t k = 0; k < 4; ++k) sg.wait[k] = tot - n[k] - n[(k + 3) % 4];
+  return sg;
+}
+
+// Loader: request this wave's items of `kind`, layer l.
+__device__ __forceinline__ void stage_issue(const Stager& sg, uint32_t kind, uint32_t l) {
+  const Args& a = *sg.a;
+  const Dims& d = a.d;
+  const uint32_t lane = threadIdx.x % WAVE;
+  const uint32_t cnt = rows_owned(kind_items(d, kind), sg.wg, sg.G);
+  const uint32_t K = kind_k(d, kind), nr = kind_rows(kind), nseg = (K + 255) / 256;
+  const uint32_t base = (uint32_t)(uintptr_t)(sg.stg + d.stg_off[kind]);
+  for (uint32_t k = sg.ld; k < cnt; k += NLOAD) {
+    const ItemRows r = item_rows(a, kind, l, k, sg.wg, sg.G);
+    for (uint32_t row = 0; row < nr; ++row) {
+      const float* src = row ? r.w1 : r.w0;
+      const uint32_t dst = base + ((k * nr + row) * K) * 4u;
+      for (uint32_t sgm = 0; sgm < nseg; ++sgm) {
+        const uint32_t rem = K - sgm * 256;
+        if (rem >= 256 || lane * 4 < rem) dma16(src + sgm * 256 + lane * 4, dst + sgm * 1024);
+      }
+    }
+  }
+}
+
+// What the loader waves do at a matvec phase's first barrier: before it,
+// wait until at most `wait` of their loads are in flight (none if NO_WAIT);
+// after it, request kind `issue` of layer `layer` (none if issue >= 4).
+constexpr uint32_t NO_WAIT = 0xffffffffu;
+struct LoadOp {
+  uint32_t issue, layer, wait;
+};
+__device__ __forceinline__ LoadOp no_load() {
+  LoadOp o;
+  o.issue = 4;
+  o.layer = 0;
+  o.wait = NO_WAIT;
+  return o;
+}
+
+// Staged rows of item k of a kind (pairs: second row at +K).
+__device__ __forceinline__ const float* staged_item(const Stager& sg, uint32_t kind, uint32_t k) {
+  const Dims& d = sg.a->d;
+  return sg.stg + d.stg_off[kind] + k * kind_rows(kind) * kind_k(d, kind);
+}
+
+// Lane partial of w . x with both in LDS: ascending j, one fma per element
+// (the order row_fma / dot_partial use, so staged and direct rows give the
+// same bits).
+__device__ __forceinline__ float dot_lds(const float* w, const float* x, uint32_t K,
+                                         uint32_t lane) {
+  float acc = 0.0f;
+  for (uint32_t j = lane * 4; j < K; j += 256) {
+    const float4 wv = lds4(w + j), xv = lds4(x + j);
+    acc = fmaf(wv.x, xv.x, acc);
+    acc = fmaf(wv.y, xv.y, acc);
+    acc = fmaf(wv.z, xv.z, acc);
+    acc = fmaf(wv.w, xv.w, acc);
   }
   return acc;
 }
@@ -273,7 +446,17 @@ __device__ __forceinline__ float dot_slot(RowT<KS>& first, RowT<KS>* second, con
 // the order the dot products visit them.
 __device__ __forceinline__ float sumsq_lane(const float* x, uint32_t K, uint32_t lane) {
   float ss = 0.0f;
-  for (uint32_t j = lane * 4; j < K; j += 256) {
+  uint32_t j = lane * 4;
+  // Four reads in flight, then the fmas in order.
+  for (; j + 768 < K; j += 1024) {
+    const float4 v0 = lds4(x + j), v1 = lds4(x + j + 256), v2 = lds4(x + j + 512),
+                 v3 = lds4(x + j + 768);
+    ss = fmaf(v0.x, v0.x, ss); ss = fmaf(v0.y, v0.y, ss); ss = fmaf(v0.z, v0.z, ss); ss = fmaf(v0.w, v0.w, ss);
+    ss = fmaf(v1.x, v1.x, ss); ss = fmaf(v1.y, v1.y, ss); ss = fmaf(v1.z, v1.z, ss); ss = fmaf(v1.w, v1.w, ss);
+    ss = fmaf(v2.x, v2.x, ss); ss = fmaf(v2.y, v2.y, ss); ss = fmaf(v2.z, v2.z, ss); ss = fmaf(v2.w, v2.w, ss);
+    ss = fmaf(v3.x, v3.x, ss); ss = fmaf(v3.y, v3.y, ss); ss = fmaf(v3.z, v3.z, ss); ss = fmaf(v3.w, v3.w, ss);
+  }
+  for (; j < K; j += 256) {
     const float4 v = lds4(x + j);
     ss = fmaf(v.x, v.x, ss);
     ss = fmaf(v.y, v.y, ss);
@@ -291,227 +474,389 @@ __device__ __forceinline__ float rms_inv(const float* x, uint32_t n, float eps, 
   return 1.0f / sqrtf(ss / (float)n + eps);
 }
 
-// Runs body(k, si) for every item of `kind` dealt to compute wave cw, in item
-// order; si is the item's slot (>= NSLOT: no slot).
-template <class F>
-__device__ __forceinline__ void for_items(const Deal& q, uint32_t kind, uint32_t cw, F body) {
-  const uint32_t b = q.base[kind], n = q.cnt[kind];
-  uint32_t k = (cw + NCW - b % NCW) % NCW;  // first k with (b + k) % NCW == cw
-  for (; k < n; k += NCW) body(k, (b + k) / NCW);
+// Dot products of NR LDS rows w[r] with the LDS vector x, all loads issued
+// before the first multiply (NF = float4 per lane covering K <= 256*NF).
+// Per row: ascending j, one fma per element -- the order dot_lds / row_fma
+// use -- then the wave tree.
+template <int NF, int NR>
+__device__ __forceinline__ void dot_rows_lds(const float* const* w, const float* x, uint32_t K,
+                                             uint32_t lane, float* out) {
+  float4 xv[NF];
+#pragma unroll
+  for (int i = 0; i < NF; ++i) {
+    const uint32_t j = lane * 4 + 256u * i;
+    if (j < K) xv[i] = lds4(x + j);
+  }
+  float4 wv[NR][NF];
+#pragma unroll
+  for (int r = 0; r < NR; ++r)
+#pragma unroll
+    for (int i = 0; i < NF; ++i) {
+      const uint32_t j = lane * 4 + 256u * i;
+      if (j < K) wv[r][i] = lds4(w[r] + j);
+    }
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NF; ++i) {
+      const uint32_t j = lane * 4 + 256u * i;
+      if (j < K) {
+        acc = fmaf(wv[r][i].x, xv[i].x, acc);
+        acc = fmaf(wv[r][i].y, xv[i].y, acc);
+        acc = fmaf(wv[r][i].z, xv[i].z, acc);
+        acc = fmaf(wv[r][i].w, xv[i].w, acc);
+      }
+    }
+    out[r] = acc;
+  }
+  wave_sum_n<NR>(out);
 }
 
-struct SlotSet {
-  Slot s[NSLOT];
-};
-
-// Calls f(slot si) with a statically indexed slot (so slots stay in
-// registers).
-template <class F>
-__device__ __forceinline__ void with_slot(SlotSet& SS, uint32_t si, F f) {
-  static_assert(NSLOT >= 1 && NSLOT <= 3, "with_slot covers up to three slots");
-  if (si == 0)
-    f(SS.s[0]);
-  else if (NSLOT >= 2 && si == 1)
-    f(SS.s[NSLOT >= 2 ? 1 : 0]);
-  else if (NSLOT >= 3)
-    f(SS.s[NSLOT >= 3 ? 2 : 0]);
-}
-
-// Prefetch state of the calling wave.
-struct Pf {
-  bool on;              // the slots hold this layer's rows (persistent kernel)
-  SlotSet* SS;          // this wave's slots
-  uint32_t next_layer;  // layer the refills load
-};
-
-// Refill the slots of compute wave cw that hold items of `kind` with layer
-// l's rows (persistent kernel, right after they were consumed).
-__device__ __forceinline__ void slot_refill(const Args& a, const Deal& q, const Pf& pf, uint32_t cw,
-                                            uint32_t kind, uint32_t wg, uint32_t G, uint32_t lane) {
-  if (!pf.on) return;
-  for_items(q, kind, cw, [&](uint32_t k, uint32_t si) {
-    if (si >= NSLOT) return;
-    const ItemRows r = item_rows(a, kind, pf.next_layer, k, wg, G);
-    with_slot(*pf.SS, si, [&](Slot& S) { slot_load(S, r, lane); });
-  });
-}
-
-// Dot products of one item whose rows are in S against the LDS vector x:
-// y0 (and y1 for pairs). S is consumed.
-__device__ __forceinline__ void slot_dot(Slot& S, const ItemRows& r, const float* x, uint32_t lane,
-                                         float* y0, float* y1) {
-  if (r.w1) {
-    *y0 = wave_sum(dot_slot(S.a, nullptr, r.w0, x, r.K, lane));
-    *y1 = wave_sum(dot_slot(S.b, nullptr, r.w1, x, r.K, lane));
-  } else {
-    *y0 = wave_sum(dot_slot(S.a, &S.b, r.w0, x, r.K, lane));
-    *y1 = 0.0f;
+// The same for any K (rows longer than 8 float4 per lane go through the
+// serial loop).
+template <int NR>
+__device__ __forceinline__ void dot_rows_any(const float* const* w, const float* x, uint32_t K,
+                                             uint32_t lane, float* out) {
+  switch ((K + 255) / 256) {
+    case 1: dot_rows_lds<1, NR>(w, x, K, lane, out); return;
+    case 2: dot_rows_lds<2, NR>(w, x, K, lane, out); return;
+    case 3: dot_rows_lds<3, NR>(w, x, K, lane, out); return;
+    case 4: dot_rows_lds<4, NR>(w, x, K, lane, out); return;
+    case 5: dot_rows_lds<5, NR>(w, x, K, lane, out); return;
+    case 6: dot_rows_lds<6, NR>(w, x, K, lane, out); return;
+    default:
+#pragma unroll
+      for (int r = 0; r < NR; ++r) out[r] = wave_sum(dot_lds(w[r], x, K, lane));
   }
 }
 
-// Item k of a kind: from its prefetched slot, or loaded now.
-__device__ __forceinline__ void item_dot(const Args& a, uint32_t kind, uint32_t l, uint32_t k,
-                                         uint32_t si, const Pf& pf, const float* x, uint32_t wg,
-                                         uint32_t G, uint32_t lane, float* y0, float* y1) {
-  const ItemRows r = item_rows(a, kind, l, k, wg, G);
-  if (pf.on && si < NSLOT) {
-    with_slot(*pf.SS, si, [&](Slot& S) { slot_dot(S, r, x, lane, y0, y1); });
-  } else {
-    Slot T;
-    slot_load(T, r, lane);
-    slot_dot(T, r, x, lane, y0, y1);
-  }
+// A compute wave's first pass of a staged matvec phase: up to two items
+// (four rows for pair kinds), whose rows it reads from LDS into registers
+// while the pollers wait for the phase's input, so only the input vector is
+// read after the barrier. 8 float4 per lane: 2 per row for pairs (K <= 512),
+// 4 per row otherwise (K <= 1024); longer rows read the rest from LDS later.
+constexpr int PRE_F4 = 8;
+__host__ __device__ constexpr int pre_nr(bool pair) { return pair ? 4 : 2; }
+__host__ __device__ constexpr int pre_nf(bool pair) { return pair ? 2 : 4; }
+struct Preload {
+  float4 w[PRE_F4];
+  uint32_t k, k2;  // items of the pass (k2 == k: no second item)
+  bool any;        // the wave has an item
+};
+
+template <bool PAIR>
+__device__ __forceinline__ void preload_rows(Preload& P, const Stager& sg, uint32_t kind,
+                                             uint32_t cw, uint32_t lane) {
+  constexpr int NR = pre_nr(PAIR), NF = pre_nf(PAIR);
+  const Dims& d = sg.a->d;
+  const uint32_t cnt = rows_owned(kind_items(d, kind), sg.wg, sg.G);
+  const uint32_t K = kind_k(d, kind);
+  P.any = cw < cnt;
+  if (!P.any) return;
+  P.k = cw;
+  P.k2 = cw + NCW < cnt ? cw + NCW : cw;
+  const float* w1 = staged_item(sg, kind, P.k);
+  const float* w2 = staged_item(sg, kind, P.k2);
+  const float* rows[4] = {w1, PAIR ? w1 + K : w2, w2, w2 + K};
+#pragma unroll
+  for (int r = 0; r < NR; ++r)
+#pragma unroll
+    for (int i = 0; i < NF; ++i) {
+      const uint32_t j = lane * 4 + 256u * i;
+      if (j < K) P.w[r * NF + i] = lds4(rows[r] + j);
+    }
 }
 
-// Fill the calling compute wave's slots with their items' rows of layer l
-// (persistent kernel start).
-__device__ __forceinline__ void slot_prime(const Args& a, SlotSet& SS, uint32_t l, uint32_t wg,
-                                           uint32_t G) {
-  const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
-  if (wave < NPOLL) return;
-  const Deal q = deal_of(a.d, wg, G);
-  Pf pf;
-  pf.on = true;
-  pf.SS = &SS;
-  pf.next_layer = l;
-  for (uint32_t kind = 0; kind < 4; ++kind) slot_refill(a, q, pf, wave - NPOLL, kind, wg, G, lane);
+// Row r of the pass dotted with x: the preloaded float4s, then (longer
+// rows) the rest from LDS, in ascending j.
+template <bool PAIR>
+__device__ __forceinline__ float pass_dot(const Preload& P, int r, const float* row,
+                                          const float4* xv, const float* x, uint32_t K,
+                                          uint32_t lane) {
+  constexpr int NF = pre_nf(PAIR);
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NF; ++i) {
+    const uint32_t j = lane * 4 + 256u * i;
+    if (j < K) {
+      const float4 w = P.w[r * NF + i];
+      acc = fmaf(w.x, xv[i].x, acc);
+      acc = fmaf(w.y, xv[i].y, acc);
+      acc = fmaf(w.z, xv[i].z, acc);
+      acc = fmaf(w.w, xv[i].w, acc);
+    }
+  }
+  for (uint32_t j = lane * 4 + 256u * NF; j < K; j += 256) {
+    const float4 wv = lds4(row + j), xx = lds4(x + j);
+    acc = fmaf(wv.x, xx.x, acc);
+    acc = fmaf(wv.y, xx.y, acc);
+    acc = fmaf(wv.z, xx.z, acc);
+    acc = fmaf(wv.w, xx.w, acc);
+  }
+  return acc;
+}
+
+// Barrier work of a staged matvec phase: loaders wait for this kind's rows
+// before the first barrier and request the previous kind's after it;
+// compute waves then preload their first pass.
+struct MvHook {
+  const Stager* sg;
+  LoadOp op;
+  Preload* pre;
+  uint32_t kind;
+  __device__ __forceinline__ void pre_b1() const {
+    if (sg->on && sg->loader && op.wait != NO_WAIT) stage_wait(op.wait);
+  }
+  __device__ __forceinline__ void post_b1() const {
+    if (!sg->on) return;
+    const uint32_t wave = threadIdx.x / WAVE;
+    if (sg->loader) {
+      if (op.issue < 4) stage_issue(*sg, op.issue, op.layer);
+    } else if (wave >= NPOLL) {
+      if (kind_rows(kind) == 2)
+        preload_rows<true>(*pre, *sg, kind, wave - NPOLL, threadIdx.x % WAVE);
+      else
+        preload_rows<false>(*pre, *sg, kind, wave - NPOLL, threadIdx.x % WAVE);
+    }
+  }
+};
+
+__device__ __forceinline__ MvHook mv_hook(const Stager& sg, LoadOp op, Preload& P, uint32_t kind) {
+  MvHook h;
+  h.sg = &sg;
+  h.op = op;
+  h.pre = &P;
+  h.kind = kind;
+  return h;
+}
+
+// body(k, y0, y1) for every item k of `kind` dealt to compute wave cw, with
+// its dot products against the LDS vector x (y1 = 0 for single-row kinds).
+// Staged: the preloaded first pass, then further passes of two items read
+// from LDS. Otherwise the rows are loaded from memory now.
+template <class F>
+__device__ __forceinline__ void items_dot(const Args& a, uint32_t kind, uint32_t cw, uint32_t l,
+                                          const Stager& sg, const Preload& P, const float* x,
+                                          uint32_t wg, uint32_t G, uint32_t lane, F body) {
+  const uint32_t cnt = rows_owned(kind_items(a.d, kind), wg, G);
+  const uint32_t K = kind_k(a.d, kind);
+  const bool pair = kind_rows(kind) == 2;
+  if (sg.on) {
+    if (!P.any) return;
+    const float* w1 = staged_item(sg, kind, P.k);
+    const float* w2 = staged_item(sg, kind, P.k2);
+    if (pair) {
+      constexpr int NF = pre_nf(true);
+      float4 xv[NF];
+#pragma unroll
+      for (int i = 0; i < NF; ++i) {
+        const uint32_t j = lane * 4 + 256u * i;
+        if (j < K) xv[i] = lds4(x + j);
+      }
+      float y[4];
+      y[0] = pass_dot<true>(P, 0, w1, xv, x, K, lane);
+      y[1] = pass_dot<true>(P, 1, w1 + K, xv, x, K, lane);
+      y[2] = pass_dot<true>(P, 2, w2, xv, x, K, lane);
+      y[3] = pass_dot<true>(P, 3, w2 + K, xv, x, K, lane);
+      wave_sum_n<4>(y);
+      body(P.k, y[0], y[1]);
+      if (P.k2 != P.k) body(P.k2, y[2], y[3]);
+    } else {
+      constexpr int NF = pre_nf(false);
+      float4 xv[NF];
+#pragma unroll
+      for (int i = 0; i < NF; ++i) {
+        const uint32_t j = lane * 4 + 256u * i;
+        if (j < K) xv[i] = lds4(x + j);
+      }
+      float y[2];
+      y[0] = pass_dot<false>(P, 0, w1, xv, x, K, lane);
+      y[1] = pass_dot<false>(P, 1, w2, xv, x, K, lane);
+      wave_sum_n<2>(y);
+      body(P.k, y[0], 0.0f);
+      if (P.k2 != P.k) body(P.k2, y[1], 0.0f);
+    }
+    for (uint32_t k = cw + 2 * NCW; k < cnt; k += 2 * NCW) {
+      const uint32_t k2 = k + NCW < cnt ? k + NCW : k;
+      const float* v1 = staged_item(sg, kind, k);
+      const float* v2 = staged_item(sg, kind, k2);
+      if (pair) {
+        const float* rows[4] = {v1, v1 + K, v2, v2 + K};
+        float y[4];
+        dot_rows_any<4>(rows, x, K, lane, y);
+        body(k, y[0], y[1]);
+        if (k2 != k) body(k2, y[2], y[3]);
+      } else {
+        const float* rows[2] = {v1, v2};
+        float y[2];
+        dot_rows_any<2>(rows, x, K, lane, y);
+        body(k, y[0], 0.0f);
+        if (k2 != k) body(k2, y[1], 0.0f);
+      }
+    }
+    return;
+  }
+  for (uint32_t k = cw; k < cnt; k += NCW) {
+    float p0, p1 = 0.0f;
+    const ItemRows r = item_rows(a, kind, l, k, wg, G);
+    if (r.w1) {
+      Row A, B;
+      row_load(A, r.w0, r.K, lane);
+      row_load(B, r.w1, r.K, lane);
+      p0 = dot_tail(A, r.w0, x, r.K, lane);
+      p1 = dot_tail(B, r.w1, x, r.K, lane);
+    } else {
+      p0 = dot_partial(r.w0, x, r.K, lane);
+    }
+    const float y0 = wave_sum(p0);
+    const float y1 = r.w1 ? wave_sum(p1) : 0.0f;
+    body(k, y0, y1);
+  }
 }
 
 // ------------------------------------------------------------------ QKV
 
+// What the QKV epilogue of item k needs from memory: the RoPE rotation
+// (cos, sin) and the biases of its two rows.
+__device__ __forceinline__ float4 qkv_epi_load(const Args& a, uint32_t l, uint32_t pos, uint32_t k,
+                                               uint32_t wg, uint32_t G) {
+  const Dims& d = a.d;
+  const uint32_t p = wg + G * k;
+  const uint32_t hb = p / d.half, i = p - hb * d.half;
+  const uint32_t r0 = hb * d.hd + i;
+  float4 e = make_float4(1.0f, 0.0f, 0.0f, 0.0f);
+  if (hb < d.nh + d.nkv) {
+    const float2 cs = ldg2(a.rope + (size_t)pos * d.half + i);
+    e.x = cs.x;
+    e.y = cs.y;
+  }
+  const float* b = (cptr(a.layers) + l)->bqkv;
+  if (b) {
+    e.z = ldg(b + r0);
+    e.w = ldg(b + r0 + d.half);
+  }
+  return e;
+}
+
+constexpr uint32_t QKV_PRE = 2;  // epilogue inputs a compute wave loads before the wait
+
 // rmsnorm -> q/k/v rows (+bias) -> RoPE on q and k (model.rs:460-465) ->
-// k, v appended to the cache at `pos` (model.rs:466-467). Item = a pair of
-// rows (i, i + hd/2) of one head, so RoPE needs no exchange.
+// k, v appended to the cache at `pos` (model.rs:466-467).
 __device__ __forceinline__ bool phase_qkv(const Args& a, uint32_t l, uint32_t tick, uint32_t pos,
                                           uint32_t token, uint32_t wg, uint32_t G, const Lds& s,
-                                          const Pf& pf) {
+                                          const Stager& sg) {
   const Dims& d = a.d;
   const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+  const bool compute = wave >= NPOLL && wave < NWA;
+  const uint32_t cw = wave - NPOLL;  // meaningful for compute waves only
+  const uint32_t cnt = rows_owned(d.qkv_rows / 2, wg, G);
+  // The epilogue inputs of the wave's first items are loaded before the wait.
+  float4 pre[QKV_PRE];
+  if (compute) {
+#pragma unroll
+    for (uint32_t u = 0; u < QKV_PRE; ++u) {
+      const uint32_t k = cw + NCW * u;
+      if (k < cnt) pre[u] = qkv_epi_load(a, l, pos, k, wg, G);
+    }
+  }
+  Preload P;
+  LoadOp op = no_load();
+  if (sg.on) {
+    op.issue = IK_D;  // the previous layer's D rows are used: this layer's
+    op.layer = l;
+    op.wait = sg.wait[IK_QKV];
+  }
+  const MvHook hk = mv_hook(sg, op, P, IK_QKV);
   if (l == 0) {
     // The embedding row (model.rs:428), read by the pollers only.
+    hk.pre_b1();
     __syncthreads();
+    hk.post_b1();
     const float* e = a.embed + (size_t)token * d.h;
     for (uint32_t i = threadIdx.x; i < d.h && threadIdx.x < NPOLL * WAVE; i += NPOLL * WAVE)
       lds_st(s.vec + i, ldg(e + i));
     __syncthreads();
   } else if (!poll_gather<8>(gather_vec(a.mb_xd, d.h, gen_of(d, tick, l - 1, PH_D), s.vec), NPOLL,
-                          a.st, s.ctl)) {
+                             a.st, s.ctl, hk)) {
     return false;
   }
-  if (wave < NPOLL) return true;
-  const uint32_t cw = wave - NPOLL;
-  const Deal q = deal_of(d, wg, G);
-  if (q.cnt[IK_QKV] == 0) return true;
-  const float inv = rms_inv(s.vec, d.h, d.eps, lane);
-  const uint32_t gen = gen_of(d, tick, l, PH_QKV);
-  const LayerW& W = a.layers[l];
-  const float2* rp = a.rope + (size_t)pos * d.half;
-  for_items(q, IK_QKV, cw, [&](uint32_t k, uint32_t si) {
-    float y0, y1;
-    item_dot(a, IK_QKV, l, k, si, pf, s.vec, wg, G, lane, &y0, &y1);
-    const uint32_t p = wg + G * k;
-    const uint32_t hb = p / d.half, i = p - hb * d.half;
-    const uint32_t r0 = hb * d.hd + i, r1 = r0 + d.half;
-    y0 *= inv;
-    y1 *= inv;
-    if (W.bqkv) {
-      y0 += ldg(W.bqkv + r0);
-      y1 += ldg(W.bqkv + r1);
-    }
-    if (hb < d.nh + d.nkv) {
-      const float2 cs = ldg2(rp + i);
-      const float a0 = y0 * cs.x - y1 * cs.y;
-      const float a1 = y1 * cs.x + y0 * cs.y;
-      y0 = a0;
-      y1 = a1;
-    }
-    if (lane == 0) {
-      mb_put(a.mb_qkv + r0, y0, gen);
-      mb_put(a.mb_qkv + r1, y1, gen);
-    }
-    if (hb >= d.nh && lane == 1) {
-      const bool is_k = hb < d.nh + d.nkv;
-      const uint32_t g = is_k ? hb - d.nh : hb - d.nh - d.nkv;
-      float* row = (is_k ? a.kc : a.vc) + (((size_t)l * d.nkv + g) * d.cap + pos) * d.kvs;
-      st_coherent(row + i, y0);
-      st_coherent(row + i + d.half, y1);
-    }
-  });
+  if (compute && cnt > 0) {
+    const float inv = rms_inv(s.vec, d.h, d.eps, lane);
+    const uint32_t gen = gen_of(d, tick, l, PH_QKV);
+    items_dot(a, IK_QKV, cw, l, sg, P, s.vec, wg, G, lane, [&](uint32_t k, float y0, float y1) {
+      const uint32_t u = (k - cw) / NCW;
+      float4 e;
+      if (u == 0)
+        e = pre[0];
+      else if (u == 1)
+        e = pre[1];
+      else
+        e = qkv_epi_load(a, l, pos, k, wg, G);
+      const uint32_t p = wg + G * k;
+      const uint32_t hb = p / d.half, i = p - hb * d.half;
+      const uint32_t r0 = hb * d.hd + i, r1 = r0 + d.half;
+      y0 = y0 * inv + e.z;
+      y1 = y1 * inv + e.w;
+      float a0 = y0, a1 = y1;
+      if (hb < d.nh + d.nkv) {
+        a0 = y0 * e.x - y1 * e.y;
+        a1 = y1 * e.x + y0 * e.y;
+      }
+      if (lane == 0) {
+        pub_word(s, 4 * k, a.mb_qkv + r0, a0, gen);
+        pub_word(s, 4 * k + 1, a.mb_qkv + r1, a1, gen);
+        if (hb >= d.nh) {
+          const bool is_k = hb < d.nh + d.nkv;
+          const uint32_t g = is_k ? hb - d.nh : hb - d.nh - d.nkv;
+          float* row = (is_k ? a.kc : a.vc) + (((size_t)l * d.nkv + g) * d.cap + pos) * d.kvs;
+          pub_float(s, 4 * k + 2, row + i, a0);
+          pub_float(s, 4 * k + 3, row + i + d.half, a1);
+        } else {
+          pub_none(s, 4 * k + 2);
+          pub_none(s, 4 * k + 3);
+        }
+      }
+    });
+  }
+  pub_flush(s, 4 * cnt);
   return true;
 }
 
 // ------------------------------------------------------------ attention
 
 constexpr uint32_t MAX_GROUP = 4;
-constexpr uint32_t ATT_PF = 4;  // position iterations whose K/V rows a lane holds at once
-// Waves that compute attention (all of them; a fixed number, so the merge
-// order does not depend on the launch).
-constexpr uint32_t NWA = NWAVES;
+constexpr uint32_t VU = 2;  // V float4 a lane keeps in flight
 
-// K/V rows (this lane's float4) of positions t, t + stride, ... for ATT_PF
-// iterations; rows at or past `pos` come from LDS, not the cache.
-__device__ __forceinline__ void load_kv(const float* kb, const float* vb, float4* kr, float4* vr,
-                                        uint32_t t, uint32_t stride, uint32_t t1, uint32_t pos,
-                                        uint32_t kvs, uint32_t sub) {
-#pragma unroll
-  for (uint32_t it = 0; it < ATT_PF; ++it) {
-    const uint32_t tt = t + stride * it;
-    if (tt < t1 && tt < pos) {
-      kr[it] = ldg4(kb + (size_t)tt * kvs + sub * 4);
-      vr[it] = ldg4(vb + (size_t)tt * kvs + sub * 4);
-    }
-  }
-}
-
-// Online-softmax state of one query head over this lane group's positions.
-struct AttState {
-  float m, l, acc[4];
+// Lane geometry of the attention (head_dim = 16 * 2^k, at most 256). Every
+// lane holds float4 pieces of rows:
+//  score pass: lps = head_dim/16 lanes per position, 4 float4 each; a wave
+//              scores pw = WAVE/lps positions, the block NWA*pw per pass;
+//  value pass: lv = head_dim/4 lanes per position, 1 float4 each; a wave
+//              takes pv = WAVE/lv positions per step.
+struct AttGeo {
+  uint32_t lps, pw, lv, pv;
 };
-
-// Folds ATT_PF iterations (positions t0 + gi + NG*(base + it)) into st.
-__device__ __forceinline__ void att_batch(AttState& st, const float4* kr, const float4* vr,
-                                          const float* qh, const float* kn, const float* vn,
-                                          const uint32_t* mask, float scale, uint32_t t_first,
-                                          uint32_t NG, uint32_t t1, uint32_t pos, uint32_t sub,
-                                          uint32_t LP) {
-#pragma unroll
-  for (uint32_t it = 0; it < ATT_PF; ++it) {
-    const uint32_t t = t_first + NG * it;
-    if (t >= t1) continue;
-    const bool cur = (t == pos);
-    const float4 kk = cur ? lds4(kn + sub * 4) : kr[it];
-    const float4 vv = cur ? lds4(vn + sub * 4) : vr[it];
-    const bool masked = mask && t < pos && ((ldg_u32(mask + (t >> 5)) >> (t & 31)) & 1u);
-    const float4 qq = lds4(qh + sub * 4);
-    float p = qq.x * kk.x;
-    p = fmaf(qq.y, kk.y, p);
-    p = fmaf(qq.z, kk.z, p);
-    p = fmaf(qq.w, kk.w, p);
-    for (uint32_t o = LP / 2; o > 0; o >>= 1) p += __shfl_xor(p, o);
-    const float sc = masked ? -INFINITY : p * scale;
-    if (sc > st.m) {
-      const float r = (st.m == -INFINITY) ? 0.0f : expf(st.m - sc);
-      st.l *= r;
-      st.acc[0] *= r;
-      st.acc[1] *= r;
-      st.acc[2] *= r;
-      st.acc[3] *= r;
-      st.m = sc;
-    }
-    const float e = (sc == -INFINITY) ? 0.0f : expf(sc - st.m);
-    st.l += e;
-    st.acc[0] = fmaf(e, vv.x, st.acc[0]);
-    st.acc[1] = fmaf(e, vv.y, st.acc[1]);
-    st.acc[2] = fmaf(e, vv.z, st.acc[2]);
-    st.acc[3] = fmaf(e, vv.w, st.acc[3]);
-  }
+__device__ __forceinline__ AttGeo att_geo(uint32_t hd) {
+  AttGeo g;
+  g.lps = hd / 16;
+  g.pw = WAVE / g.lps;
+  g.lv = hd / 4;
+  g.pv = WAVE / g.lv;
+  return g;
 }
 
-// Split-context attention for one (kv head, chunk) item: scores, softmax
-// partials (max m, sum l, unnormalised acc) for each query head of the GQA
-// group (model.rs:471-497). A chunk's K/V rows are loaded once and reused for
-// every head of the group when they fit the lane's registers; longer chunks
-// stream them again per head.
+// Split-context attention for one (kv head, chunk) item (model.rs:471-497):
+// for each query head j of the GQA group, the chunk's softmax partials
+// m_j = max score, l_j = sum exp(score - m_j), acc_j = sum exp(score - m_j) v.
+//  1. scores of every position of the chunk into LDS (each K row read once
+//     for the whole group);
+//  2. wave j: m_j, exp in place, l_j (lane-strided partials, wave tree);
+//  3. exp-weighted V rows (each read once for the group), one partial per
+//     (wave, position lane group), summed in that order.
+// Every order above depends on (pos, head_dim) only. Heads beyond the group
+// size are computed on whatever LDS holds and never stored, which keeps
+// every loop's trip count a compile-time constant.
 __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t tick, uint32_t pos,
                                            uint32_t wg, uint32_t G, const Lds& s) {
   const Dims& d = a.d;
@@ -520,88 +865,159 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
   const uint32_t gen_in = gen_of(d, tick, l, PH_QKV);
   const uint32_t gen_out = gen_of(d, tick, l, PH_ATTN);
   const uint32_t hd = d.hd, grp = d.group, hs = hd + 2;
-  float* qs = s.scr;            // [grp*hd]
-  float* kn = qs + grp * hd;    // [hd]
-  float* vn = kn + hd;          // [hd]
-  float* wp = vn + hd;          // [NWA][grp][hd+2]
-  const uint32_t LP = hd / 4, PPI = WAVE / LP, NG = NWA * PPI;
+  const AttGeo ge = att_geo(hd);
+  float* qs = s.scr;                      // [MAX_GROUP*hd] (rows >= grp: don't care)
+  float* kn = qs + MAX_GROUP * hd;        // [hd]
+  float* vn = kn + hd;                    // [hd]
+  float* ml = vn + hd;                    // [2*MAX_GROUP]
+  float* sc = ml + 2 * MAX_GROUP;         // [MAX_GROUP][CH]
+  float* wp = sc + MAX_GROUP * CH;        // [NWA][grp][hd]
   const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
-  const uint32_t sub = lane % LP;
-  const uint32_t gi = wave * PPI + lane / LP;
+  const uint32_t ps = lane / ge.lps, sub = lane % ge.lps;
+  const uint32_t pl = lane / ge.lv, dl = lane % ge.lv;
+  const uint32_t sstep = NWA * ge.pw, vstep = NWA * ge.pv;
+  const bool att = wave < NWA;  // loader waves only meet the barriers
+  const uint32_t tw = wave * ge.pw + ps;  // this lane's position offset in a score pass
+  const uint32_t vw = wave * ge.pv + pl;  // ... and in a value step
   for (uint32_t item = wg; item < n_items; item += G) {
     const uint32_t g = item / nch, c = item - g * nch;
     const uint32_t t0 = c * CH;
     const uint32_t t1 = min(t0 + CH, pos + 1);
-    const float* kb = a.kc + ((size_t)l * d.nkv + g) * d.cap * d.kvs;
-    const float* vb = a.vc + ((size_t)l * d.nkv + g) * d.cap * d.kvs;
-    // The first batch of historical K/V rows is issued before waiting for
-    // this token's q/k/v.
-    float4 kr[ATT_PF], vr[ATT_PF];
-    load_kv(kb, vb, kr, vr, t0 + gi, NG, t1, pos, d.kvs, sub);
+    const float* kb = a.kc + ((size_t)l * d.nkv + g) * d.cap * d.kvs + sub * 16;
+    const float* vb = a.vc + ((size_t)l * d.nkv + g) * d.cap * d.kvs + dl * 4;
+    // The chunk's first K rows (score pass) and V rows (value pass) of the
+    // history are requested before waiting for this token's q/k/v.
+    float4 kr[4];
+    if (att && t0 + tw < t1 && t0 + tw < pos) {
+      const float* r = kb + (size_t)(t0 + tw) * d.kvs;
+#pragma unroll
+      for (uint32_t i = 0; i < 4; ++i) kr[i] = ldg4(r + 4 * i);
+    }
+    float4 vr[VU];
+#pragma unroll
+    for (uint32_t u = 0; u < VU; ++u) {
+      const uint32_t t = t0 + vw + u * vstep;
+      if (att && t < t1 && t < pos) vr[u] = ldg4(vb + (size_t)t * d.kvs);
+    }
     if (!poll_gather<2, 1, 1>(gather_vec(a.mb_qkv + (size_t)g * grp * hd, grp * hd, gen_in, qs),
                               gather_vec(a.mb_qkv + d.q + g * hd, hd, gen_in, kn),
                               gather_vec(a.mb_qkv + d.q + d.kv + g * hd, hd, gen_in, vn), NPOLL,
                               a.st, s.ctl))
       return false;
-    const uint32_t n_iter = (t1 - t0 + NG - 1) / NG;
-    for (uint32_t j = 0; j < grp; ++j) {
-      AttState st;
-      st.m = -INFINITY;
-      st.l = 0.0f;
-      st.acc[0] = st.acc[1] = st.acc[2] = st.acc[3] = 0.0f;
-      for (uint32_t base = 0; base < n_iter; base += ATT_PF) {
-        if (n_iter > ATT_PF && (base > 0 || j > 0))
-          load_kv(kb, vb, kr, vr, t0 + gi + NG * base, NG, t1, pos, d.kvs, sub);
-        att_batch(st, kr, vr, qs + j * hd, kn, vn, a.mask, d.scale, t0 + gi + NG * base, NG, t1,
-                  pos, sub, LP);
+    // 1. scores
+    for (uint32_t pb = t0; att && pb < t1; pb += sstep) {
+      const uint32_t ts = pb + tw;
+      const bool live = ts < t1;
+      if (ts == pos) {
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) kr[i] = lds4(kn + sub * 16 + 4 * i);
       }
-      // Merge the position groups of this wave (lanes with the same `sub`).
-      for (uint32_t o = LP; o < WAVE; o <<= 1) {
-        const float m2 = __shfl_xor(st.m, o), l2 = __shfl_xor(st.l, o);
-        const float b0 = __shfl_xor(st.acc[0], o), b1 = __shfl_xor(st.acc[1], o);
-        const float b2 = __shfl_xor(st.acc[2], o), b3 = __shfl_xor(st.acc[3], o);
-        const float mn = fmaxf(st.m, m2);
-        const float s1 = (st.m == -INFINITY) ? 0.0f : expf(st.m - mn);
-        const float s2 = (m2 == -INFINITY) ? 0.0f : expf(m2 - mn);
-        st.l = st.l * s1 + l2 * s2;
-        st.acc[0] = st.acc[0] * s1 + b0 * s2;
-        st.acc[1] = st.acc[1] * s1 + b1 * s2;
-        st.acc[2] = st.acc[2] * s1 + b2 * s2;
-        st.acc[3] = st.acc[3] * s1 + b3 * s2;
-        st.m = mn;
-      }
-      if (lane < LP) {
-        float* dst = wp + (wave * grp + j) * hs;
-        if (lane == 0) {
-          lds_st(dst + 0, st.m);
-          lds_st(dst + 1, st.l);
+      const bool masked = live && a.mask && ts < pos &&
+                          ((ldg_u32(a.mask + (ts >> 5)) >> (ts & 31)) & 1u);
+      // One head at a time keeps the live registers to this lane's K piece.
+#pragma unroll 1
+      for (uint32_t j = 0; j < grp; ++j) {
+        float acc = 0.0f;
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) {
+          const float4 qq = lds4(qs + j * hd + sub * 16 + 4 * i);
+          acc = fmaf(qq.x, kr[i].x, acc);
+          acc = fmaf(qq.y, kr[i].y, acc);
+          acc = fmaf(qq.z, kr[i].z, acc);
+          acc = fmaf(qq.w, kr[i].w, acc);
         }
-        lds_st(dst + 2 + sub * 4 + 0, st.acc[0]);
-        lds_st(dst + 2 + sub * 4 + 1, st.acc[1]);
-        lds_st(dst + 2 + sub * 4 + 2, st.acc[2]);
-        lds_st(dst + 2 + sub * 4 + 3, st.acc[3]);
+        const float v = group_sum(acc, ge.lps);
+        if (live && sub == 0) lds_st(sc + j * CH + (ts - t0), masked ? -INFINITY : v * d.scale);
+      }
+      const uint32_t tn = ts + sstep;
+      if (tn < t1 && tn < pos) {
+        const float* r = kb + (size_t)tn * d.kvs;
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) kr[i] = ldg4(r + 4 * i);
       }
     }
     __syncthreads();
-    // Merge the waves in wave order and publish the chunk's partials.
-    for (uint32_t u = threadIdx.x; u < grp * hd; u += BLOCK) {
-      const uint32_t j = u / hd, dd = u - j * hd;
-      float M = -INFINITY;
-      for (uint32_t w = 0; w < NWA; ++w) M = fmaxf(M, lds_ld(wp + (w * grp + j) * hs));
-      float Ls = 0.0f, A = 0.0f;
-      for (uint32_t w = 0; w < NWA; ++w) {
-        const float* src = wp + (w * grp + j) * hs;
-        const float mw = lds_ld(src);
-        const float sw = (mw == -INFINITY) ? 0.0f : expf(mw - M);
-        Ls = Ls + lds_ld(src + 1) * sw;
-        A = A + lds_ld(src + 2 + dd) * sw;
+    // 2. softmax statistics, one wave per query head
+    const uint32_t n = t1 - t0;
+    if (wave < grp) {
+      float* sh = sc + wave * CH;
+      float m = -INFINITY;
+      for (uint32_t i = lane; i < n; i += WAVE) m = fmaxf(m, lds_ld(sh + i));
+      m = wave_max(m);
+      float ls = 0.0f;
+      for (uint32_t i = lane; i < n; i += WAVE) {
+        const float e = (m == -INFINITY) ? 0.0f : expf(lds_ld(sh + i) - m);
+        lds_st(sh + i, e);
+        ls += e;
       }
+      ls = wave_sum(ls);
+      if (lane == 0) {
+        lds_st(ml + 2 * wave, m);
+        lds_st(ml + 2 * wave + 1, ls);
+      }
+    }
+    __syncthreads();
+    // 3. exp-weighted V rows: positions t0 + vw + k*vstep, k = 0, 1, ...
+    float4 acc[MAX_GROUP];
+#pragma unroll
+    for (uint32_t j = 0; j < MAX_GROUP; ++j) acc[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const uint32_t nk = att && t0 + vw < t1 ? (t1 - t0 - vw + vstep - 1) / vstep : 0;
+    for (uint32_t k0 = 0; k0 < nk; k0 += VU) {
+#pragma unroll
+      for (uint32_t u = 0; u < VU; ++u) {
+        const uint32_t k = k0 + u;
+        if (k < nk) {
+          const uint32_t t = t0 + vw + k * vstep;
+          const float4 v = (t == pos) ? lds4(vn + dl * 4) : vr[u];
+          const uint32_t tf = t + VU * vstep;
+          if (k + VU < nk && tf < pos) vr[u] = ldg4(vb + (size_t)tf * d.kvs);
+#pragma unroll
+          for (uint32_t j = 0; j < MAX_GROUP; ++j) {
+            const float p = lds_ld(sc + j * CH + (t - t0));
+            acc[j].x = fmaf(p, v.x, acc[j].x);
+            acc[j].y = fmaf(p, v.y, acc[j].y);
+            acc[j].z = fmaf(p, v.z, acc[j].z);
+            acc[j].w = fmaf(p, v.w, acc[j].w);
+          }
+        }
+      }
+    }
+    // The wave's position groups (lanes lv apart) in a butterfly, then one
+    // partial per wave.
+    for (uint32_t o = ge.lv; o < WAVE; o <<= 1) {
+#pragma unroll
+      for (uint32_t j = 0; j < MAX_GROUP; ++j)
+        if (j < grp) {
+          acc[j].x += __shfl_xor(acc[j].x, o);
+          acc[j].y += __shfl_xor(acc[j].y, o);
+          acc[j].z += __shfl_xor(acc[j].z, o);
+          acc[j].w += __shfl_xor(acc[j].w, o);
+        }
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < MAX_GROUP; ++j)
+      if (att && pl == 0 && j < grp) {
+        float* dst = wp + (wave * grp + j) * hd + dl * 4;
+        lds_st(dst + 0, acc[j].x);
+        lds_st(dst + 1, acc[j].y);
+        lds_st(dst + 2, acc[j].z);
+        lds_st(dst + 3, acc[j].w);
+      }
+    __syncthreads();
+    for (uint32_t u = threadIdx.x; threadIdx.x < NPOLL * WAVE && u < grp * hd; u += NPOLL * WAVE) {
+      const uint32_t j = u / hd, dd = u - j * hd;
+      float pw[NWA];
+#pragma unroll
+      for (uint32_t w = 0; w < NWA; ++w) pw[w] = lds_ld(wp + (w * grp + j) * hd + dd);
+      float A = 0.0f;
+#pragma unroll
+      for (uint32_t w = 0; w < NWA; ++w) A += pw[w];
       const uint32_t hh = g * grp + j;
       u64* out = a.mb_part + ((size_t)hh * MAX_ACHUNKS + c) * hs;
       mb_put(out + 2 + dd, A, gen_out);
       if (dd == 0) {
-        mb_put(out + 0, M, gen_out);
-        mb_put(out + 1, Ls, gen_out);
+        mb_put(out + 0, lds_ld(ml + 2 * j), gen_out);
+        mb_put(out + 1, lds_ld(ml + 2 * j + 1), gen_out);
       }
     }
   }
@@ -612,6 +1028,10 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
 // att[d] = sum_c acc_c[d] e^(m_c - M) / sum_c l_c e^(m_c - M).
 __device__ __forceinline__ float combine_one(const float* part, uint32_t nch, uint32_t hs,
                                              uint32_t dd) {
+  if (nch == 1) {  // one chunk: its own max, weight exp(0) = 1
+    const float Ls = lds_ld(part + 1) * 1.0f, A = lds_ld(part + 2 + dd) * 1.0f;
+    return A / Ls;
+  }
   float M = -INFINITY;
   for (uint32_t c = 0; c < nch; ++c) M = fmaxf(M, lds_ld(part + c * hs));
   float Ls = 0.0f, A = 0.0f;
@@ -649,12 +1069,11 @@ __device__ __forceinline__ bool phase_comb(const Args& a, uint32_t l, uint32_t t
 // after the poll when it fits.
 __device__ __forceinline__ bool phase_o(const Args& a, uint32_t l, uint32_t tick, uint32_t pos,
                                         uint32_t token, uint32_t wg, uint32_t G, const Lds& s,
-                                        const Pf& pf) {
+                                        const Stager& sg) {
   const Dims& d = a.d;
   const uint32_t nch = attn_nchunks(pos), hs = d.hd + 2;
   const bool inl = comb_inline(d, pos);
-  const Deal q = deal_of(d, wg, G);
-  const uint32_t R = q.cnt[IK_O];
+  const uint32_t R = rows_owned(d.h, wg, G);
   const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
   float* part = s.scr;
   float* xres = s.scr + (inl ? d.nh * nch * hs : 0);
@@ -665,29 +1084,32 @@ __device__ __forceinline__ bool phase_o(const Args& a, uint32_t l, uint32_t tick
   const Gather gr = (l > 0 && R > 0)
                         ? gather_strided(a.mb_xd + wg, 1, R, G, gen_of(d, tick, l - 1, PH_D), xres)
                         : no_gather();
-  if (!poll_gather<12, 1>(ga, gr, NPOLL, a.st, s.ctl)) return false;
-  // QKV slots were consumed before the attention; refill them now that the
-  // attention's K/V reads are done (next layer, or the next token's layer 0).
-  if (pf.on && wave >= NPOLL)
-    slot_refill(a, q, pf, wave - NPOLL, IK_QKV, wg, G, lane);
-  if (l == 0)
-    for (uint32_t k = threadIdx.x; k < R; k += BLOCK)
-      lds_st(xres + k, ldg(a.embed + (size_t)token * d.h + wg + G * k));
+  // Layer 0's residual is the embedding row: its words are loaded before the
+  // wait (pollers, one word per thread).
+  float emb = 0.0f;
+  if (l == 0 && threadIdx.x < R) emb = ldg(a.embed + (size_t)token * d.h + wg + G * threadIdx.x);
+  Preload P;
+  LoadOp op = no_load();
+  if (sg.on) {
+    op.issue = IK_QKV;  // the QKV rows are used: request the next layer's
+    op.layer = l + 1 < d.L ? l + 1 : 0;
+    op.wait = sg.wait[IK_O];
+  }
+  if (!poll_gather<12, 1>(ga, gr, NPOLL, a.st, s.ctl, mv_hook(sg, op, P, IK_O))) return false;
+  if (l == 0 && threadIdx.x < R) lds_st(xres + threadIdx.x, emb);
   if (inl)
-    for (uint32_t u = threadIdx.x; u < d.q; u += BLOCK) {
+    for (uint32_t u = threadIdx.x; u < d.q && threadIdx.x < NWA * WAVE; u += NWA * WAVE) {
       const uint32_t hh = u / d.hd, dd = u - hh * d.hd;
       lds_st(s.vec + u, combine_one(part + hh * nch * hs, nch, hs, dd));
     }
   __syncthreads();
-  if (wave < NPOLL) return true;
-  const uint32_t cw = wave - NPOLL;
-  const uint32_t gen = gen_of(d, tick, l, PH_O);
-  for_items(q, IK_O, cw, [&](uint32_t k, uint32_t si) {
-    float y, unused;
-    item_dot(a, IK_O, l, k, si, pf, s.vec, wg, G, lane, &y, &unused);
-    if (lane == 0) mb_put(a.mb_xo + wg + G * k, lds_ld(xres + k) + y, gen);
-  });
-  slot_refill(a, q, pf, cw, IK_O, wg, G, lane);
+  if (wave >= NPOLL && wave < NWA) {
+    const uint32_t gen = gen_of(d, tick, l, PH_O);
+    items_dot(a, IK_O, wave - NPOLL, l, sg, P, s.vec, wg, G, lane, [&](uint32_t k, float y, float) {
+      if (lane == 0) pub_word(s, k, a.mb_xo + wg + G * k, lds_ld(xres + k) + y, gen);
+    });
+  }
+  pub_flush(s, R);
   return true;
 }
 
@@ -695,46 +1117,57 @@ __device__ __forceinline__ bool phase_o(const Args& a, uint32_t l, uint32_t tick
 
 // rmsnorm -> g = act(Wg.x) * (Wu.x) (model.rs:502-509).
 __device__ __forceinline__ bool phase_gu(const Args& a, uint32_t l, uint32_t tick, uint32_t wg,
-                                         uint32_t G, const Lds& s, const Pf& pf) {
+                                         uint32_t G, const Lds& s, const Stager& sg) {
   const Dims& d = a.d;
   const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
-  if (!poll_gather<8>(gather_vec(a.mb_xo, d.h, gen_of(d, tick, l, PH_O), s.vec), NPOLL, a.st, s.ctl))
+  Preload P;
+  LoadOp op = no_load();
+  if (sg.on) {
+    op.issue = IK_O;
+    op.layer = l + 1 < d.L ? l + 1 : 0;
+    op.wait = sg.wait[IK_GU];
+  }
+  if (!poll_gather<8>(gather_vec(a.mb_xo, d.h, gen_of(d, tick, l, PH_O), s.vec), NPOLL, a.st, s.ctl,
+                      mv_hook(sg, op, P, IK_GU)))
     return false;
-  if (wave < NPOLL) return true;
-  const uint32_t cw = wave - NPOLL;
-  const Deal q = deal_of(d, wg, G);
-  const float inv = rms_inv(s.vec, d.h, d.eps, lane);
-  const uint32_t gen = gen_of(d, tick, l, PH_GU);
-  for_items(q, IK_GU, cw, [&](uint32_t k, uint32_t si) {
-    float gate, up;
-    item_dot(a, IK_GU, l, k, si, pf, s.vec, wg, G, lane, &gate, &up);
-    if (lane == 0) mb_put(a.mb_g + wg + G * k, act_fn(gate * inv, d.act) * (up * inv), gen);
-  });
-  slot_refill(a, q, pf, cw, IK_GU, wg, G, lane);
+  if (wave >= NPOLL && wave < NWA) {
+    const float inv = rms_inv(s.vec, d.h, d.eps, lane);
+    const uint32_t gen = gen_of(d, tick, l, PH_GU);
+    items_dot(a, IK_GU, wave - NPOLL, l, sg, P, s.vec, wg, G, lane,
+              [&](uint32_t k, float gate, float up) {
+                if (lane == 0)
+                  pub_word(s, k, a.mb_g + wg + G * k, act_fn(gate * inv, d.act) * (up * inv), gen);
+              });
+  }
+  pub_flush(s, rows_owned(d.ff, wg, G));
   return true;
 }
 
 // x_d = x_o + Wd . g (model.rs:510-511).
 __device__ __forceinline__ bool phase_d(const Args& a, uint32_t l, uint32_t tick, uint32_t wg,
-                                        uint32_t G, const Lds& s, const Pf& pf) {
+                                        uint32_t G, const Lds& s, const Stager& sg) {
   const Dims& d = a.d;
-  const Deal q = deal_of(d, wg, G);
-  const uint32_t R = q.cnt[IK_D];
+  const uint32_t R = rows_owned(d.h, wg, G);
   const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
   const Gather gr = R > 0 ? gather_strided(a.mb_xo + wg, 1, R, G, gen_of(d, tick, l, PH_O), s.scr)
                           : no_gather();
-  if (!poll_gather<12, 1>(gather_vec(a.mb_g, d.ff, gen_of(d, tick, l, PH_GU), s.vec), gr, NPOLL, a.st,
-                   s.ctl))
+  Preload P;
+  LoadOp op = no_load();
+  if (sg.on) {
+    op.issue = IK_GU;
+    op.layer = l + 1 < d.L ? l + 1 : 0;
+    op.wait = sg.wait[IK_D];
+  }
+  if (!poll_gather<12, 1>(gather_vec(a.mb_g, d.ff, gen_of(d, tick, l, PH_GU), s.vec), gr, NPOLL,
+                          a.st, s.ctl, mv_hook(sg, op, P, IK_D)))
     return false;
-  if (wave < NPOLL) return true;
-  const uint32_t cw = wave - NPOLL;
-  const uint32_t gen = gen_of(d, tick, l, PH_D);
-  for_items(q, IK_D, cw, [&](uint32_t k, uint32_t si) {
-    float y, unused;
-    item_dot(a, IK_D, l, k, si, pf, s.vec, wg, G, lane, &y, &unused);
-    if (lane == 0) mb_put(a.mb_xd + wg + G * k, lds_ld(s.scr + k) + y, gen);
-  });
-  slot_refill(a, q, pf, cw, IK_D, wg, G, lane);
+  if (wave >= NPOLL && wave < NWA) {
+    const uint32_t gen = gen_of(d, tick, l, PH_D);
+    items_dot(a, IK_D, wave - NPOLL, l, sg, P, s.vec, wg, G, lane, [&](uint32_t k, float y, float) {
+      if (lane == 0) pub_word(s, k, a.mb_xd + wg + G * k, lds_ld(s.scr + k) + y, gen);
+    });
+  }
+  pub_flush(s, R);
   return true;
 }
 
@@ -763,7 +1196,7 @@ __device__ __forceinline__ void lm_prime(const Args& a, const Lds& s) {
 // c = wg + G*k; every wave computes rows, two at a time, with the next two
 // rows in flight. logit = inv * (H . (x * w_norm)).
 __device__ __forceinline__ bool phase_lm(const Args& a, uint32_t tick, uint32_t wg, uint32_t G,
-                                         const Lds& s) {
+                                         const Lds& s, const Stager& sg) {
   const Dims& d = a.d;
   const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
   const uint32_t nown = wg < d.nvc ? (d.nvc - wg + G - 1) / G : 0;
@@ -773,24 +1206,25 @@ __device__ __forceinline__ bool phase_lm(const Args& a, uint32_t tick, uint32_t 
   const float* nrm = s.vec2 + d.h;       // final norm weight (lm_prime)
   auto vocab_row = [&](uint32_t r) { return (wg + G * (r / VCHUNK)) * VCHUNK + r % VCHUNK; };
   RowT<LMF> A0, A1, B0, B1;
+  const bool lmw = wave < NWA;  // loader waves only meet the barriers
   auto load_pair = [&](RowT<LMF>& x0, RowT<LMF>& x1, uint32_t r0) {
-    const uint32_t r1 = r0 + NWAVES;
+    const uint32_t r1 = r0 + NWA;
     if (r0 < nrows && vocab_row(r0) < d.V)
       row_load(x0, a.head + (size_t)vocab_row(r0) * d.h, d.h, lane);
     if (r1 < nrows && vocab_row(r1) < d.V)
       row_load(x1, a.head + (size_t)vocab_row(r1) * d.h, d.h, lane);
   };
-  load_pair(A0, A1, wave);
+  if (lmw) load_pair(A0, A1, wave);
   if (!poll_gather<8>(gather_vec(a.mb_xd, d.h, gen_of(d, tick, d.L - 1, PH_D), s.vec), NPOLL, a.st,
-                   s.ctl))
+                      s.ctl))
     return false;
   for (uint32_t i = threadIdx.x; i < d.h; i += BLOCK) lds_st(xs + i, lds_ld(s.vec + i) * lds_ld(nrm + i));
   __syncthreads();
   const float inv = rms_inv(s.vec, d.h, d.eps, lane);
   const uint32_t gen = gen_lm(d, tick);
-  for (uint32_t r0 = wave; r0 < nrows; r0 += 2 * NWAVES) {
-    const uint32_t r1 = r0 + NWAVES;
-    load_pair(B0, B1, r0 + 2 * NWAVES);
+  for (uint32_t r0 = wave; lmw && r0 < nrows; r0 += 2 * NWA) {
+    const uint32_t r1 = r0 + NWA;
+    load_pair(B0, B1, r0 + 2 * NWA);
     const uint32_t v0 = vocab_row(r0), v1 = vocab_row(r1);
     if (v0 < d.V) {
       const float y = inv * wave_sum(dot_tail(A0, a.head + (size_t)v0 * d.h, xs, d.h, lane));
@@ -811,7 +1245,7 @@ __device__ __forceinline__ bool phase_lm(const Args& a, uint32_t tick, uint32_t 
   }
   __syncthreads();
   // Chunk (max, argmax): one wave per chunk, one lane per row.
-  for (uint32_t k = wave; k < nown; k += NWAVES) {
+  for (uint32_t k = wave; lmw && k < nown; k += NWA) {
     const uint32_t c = wg + G * k;
     const uint32_t v = c * VCHUNK + lane;
     float bv = -INFINITY;
@@ -894,9 +1328,9 @@ __device__ __forceinline__ bool sample_stage_a(const Args& a, uint32_t tick, flo
   const uint32_t gl = gen_lm(d, tick - 1u), gsum = gen_sums(d, tick);
   float* vmx = s.scr;
   float* varg = vmx + nvc;
-  float* chunk = varg + nvc;  // [NWAVES][VCHUNK]
+  float* chunk = varg + nvc;  // [NWA][VCHUNK]
   if (!poll_gather<4, 4>(gather_vec(a.mb_vmax, nvc, gl, vmx), gather_vec(a.mb_varg, nvc, gl, varg),
-                   NWAVES, a.st, s.ctl))
+                   NWA, a.st, s.ctl))
     return false;
   float bv;
   uint32_t bi;
@@ -904,8 +1338,8 @@ __device__ __forceinline__ bool sample_stage_a(const Args& a, uint32_t tick, flo
   const float m = (bi == NO_INDEX) ? -INFINITY : bv / T;
   const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
   const uint32_t nown = wg < nvc ? (nvc - wg + G - 1) / G : 0;
-  for (uint32_t k0 = 0; k0 < nown; k0 += NWAVES) {
-    const uint32_t nb = min(NWAVES, nown - k0);
+  for (uint32_t k0 = 0; k0 < nown; k0 += NWA) {
+    const uint32_t nb = min(NWA, nown - k0);
     // chunks wg + G*(k0 + b), b < nb; the last one may be short
     const u64* src0 = a.mb_logit + (size_t)(wg + G * k0) * VCHUNK;
     const uint32_t clast = wg + G * (k0 + nb - 1);
@@ -915,7 +1349,7 @@ __device__ __forceinline__ bool sample_stage_a(const Args& a, uint32_t tick, flo
     const Gather gb = short_last ? gather_vec(a.mb_logit + (size_t)clast * VCHUNK,
                                               d.V - clast * VCHUNK, gl, chunk + (nb - 1) * VCHUNK)
                                  : no_gather();
-    if (!poll_gather<2, 1>(ga, gb, NWAVES, a.st, s.ctl)) return false;
+    if (!poll_gather<2, 1>(ga, gb, NWA, a.st, s.ctl)) return false;
     if (wave < nb) {
       const uint32_t c = wg + G * (k0 + wave);
       const uint32_t v = c * VCHUNK + lane;
@@ -956,7 +1390,7 @@ __device__ __forceinline__ bool sample_stage_b(const Args& a, uint32_t tick, flo
   float* chunk = vsum + nvc;  // [VCHUNK]
   float* wtot = chunk + VCHUNK;  // [NWAVES + 2]
   if (!poll_gather<4, 4, 4>(gather_vec(a.mb_vmax, nvc, gl, vmx), gather_vec(a.mb_varg, nvc, gl, varg),
-                   T != 0.0f ? gather_vec(a.mb_vsum, nvc, gsum, vsum) : no_gather(), NWAVES, a.st,
+                   T != 0.0f ? gather_vec(a.mb_vsum, nvc, gsum, vsum) : no_gather(), NWA, a.st,
                    s.ctl))
     return false;
   float bv;
@@ -1019,7 +1453,7 @@ __device__ __forceinline__ bool sample_stage_b(const Args& a, uint32_t tick, flo
   // Element scan from chunk cstar onwards (normally one chunk).
   for (uint32_t c = cstar; c < nvc; ++c) {
     const uint32_t v0 = c * VCHUNK, nv = min(VCHUNK, d.V - v0);
-    if (!poll_gather<1>(gather_vec(a.mb_logit + v0, nv, gl, chunk), NWAVES, a.st, s.ctl)) return false;
+    if (!poll_gather<1>(gather_vec(a.mb_logit + v0, nv, gl, chunk), NWA, a.st, s.ctl)) return false;
     const float p = (lane < nv) ? exp_term(chunk[lane], T, m) * inv : 0.0f;
     const float sc = wave_scan(p > 0.0f ? p : 0.0f);
     const bool hit = p > 0.0f && r < run + sc;
@@ -1036,7 +1470,7 @@ __device__ __forceinline__ bool sample_stage_b(const Args& a, uint32_t tick, flo
   for (uint32_t cc = nvc; cc-- > 0;) {
     if (!(vsum[cc] > 0.0f)) continue;
     const uint32_t v0 = cc * VCHUNK, nv = min(VCHUNK, d.V - v0);
-    if (!poll_gather<1>(gather_vec(a.mb_logit + v0, nv, gl, chunk), NWAVES, a.st, s.ctl)) return false;
+    if (!poll_gather<1>(gather_vec(a.mb_logit + v0, nv, gl, chunk), NWA, a.st, s.ctl)) return false;
     const float p = (lane < nv) ? exp_term(chunk[lane], T, m) * inv : 0.0f;
     const unsigned long long nz = __ballot(p > 0.0f);
     __syncthreads();
