@@ -57,7 +57,8 @@ def build_host() -> str:
     )
     tmp = out + ".tmp"
     _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra",
-          "-I", os.path.join(ROOT, "include"), "-o", tmp, *srcs])
+          "-I", os.path.join(ROOT, "include"), "-o", tmp, *srcs,
+          "-L", PKG, "-ldefer_gpu", "-Wl,-rpath,$ORIGIN"])
     os.replace(tmp, out)
     return out
 

@@ -1,0 +1,141 @@
+"""GPU: the host Session over the device path, the WAL round trip, longer
+contexts (several attention chunks, separate combine), and the staged
+persistent kernel against the per-phase kernels on the 135M shape.
+
+Bars as in test_gpu_forward.py: tokens identical to the oracle, logits within
+1e-3, and bit-identical results among GPU runs.
+"""
+import numpy as np
+import pytest
+
+import oracle_py as O
+from defer_amd import gpu as G
+from defer_amd import host as H
+from defer_amd import synthetic
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_TOL = 1e-3
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+@pytest.fixture(scope="module")
+def tiny():
+    cfg = synthetic.CONFIGS["tiny"]
+    w = synthetic.make_weights(cfg, 77)
+    return cfg, w, G.GpuModel(G.Config.from_dict(cfg), w), O.OracleModel(cfg, w)
+
+
+@pytest.fixture(scope="module")
+def m135():
+    cfg = synthetic.CONFIGS["smollm2-135m"]
+    w = synthetic.make_weights(cfg, 0)
+    return cfg, w, G.GpuModel(G.Config.from_dict(cfg), w), O.OracleModel(cfg, w)
+
+
+def test_session_sampling_matches_oracle(tiny):
+    cfg, w, gm, om = tiny
+    say("tiny: host session, prompt 9 + 50 at T=0.8 seed 5, vs oracle")
+    prompt = [int(x) for x in synthetic.make_prompt(cfg["vocab_size"], 9, seed=1)]
+    s = H.Session(gm, H.seed_from_u64(5), 0.8)
+    s.prompt(prompt)
+    toks = s.generate(50)
+    otoks, words, _ = om.generate(om.new_cache(), O.seed_from_u64(5), 0.8, prompt, 50)
+    assert toks == otoks
+    assert s.rng_word_pos == words == 50
+    assert s.history == prompt + toks and s.prompt_len == 9
+
+
+def test_session_steps_equal_generate(tiny):
+    cfg, w, gm, om = tiny
+    say("tiny: 20 single steps vs one generate of 20")
+    prompt = [3, 1, 4, 1, 5]
+    a = H.Session(gm, H.seed_from_u64(9), 0.6)
+    a.prompt(prompt)
+    steps = [a.step() for _ in range(20)]
+    b = H.Session(gm, H.seed_from_u64(9), 0.6)
+    b.prompt(prompt)
+    assert b.generate(20) == steps
+    assert a.rng_word_pos == b.rng_word_pos == 20
+    with pytest.raises(H.DeferHostError, match="after generation started"):
+        a.prompt([1])
+
+
+def test_wal_checkout_rebuilds_cache_and_detects_divergence(tiny, tmp_path):
+    cfg, w, gm, om = tiny
+    say("tiny: generate 40 at T=0.7 into a WAL, checkout, tamper, checkout")
+    seed = H.seed_from_u64(123)
+    prompt = [10, 20, 30, 40, 50, 60]
+    live = H.Session(gm, seed, 0.7)
+    live.prompt(prompt)
+    toks = live.generate(40)
+    p = str(tmp_path / "s.wal")
+    wal = H.Wal.create(p, bytes(32), seed, 0.7, len(prompt), 0, prompt)
+    for i, t in enumerate(toks):
+        wal.append(t, i + 1)
+    wal.close()
+    log = H.Wal.read(p)
+    rep = H.Session.checkout(gm, log["base_seed"], log["temperature"], log["history"],
+                             log["prompt_len"], log["rng_word_pos"])
+    assert rep.history == live.history and rep.rng_word_pos == live.rng_word_pos
+    for layer in range(cfg["num_layers"]):
+        for x, y in zip(rep.cache.read(layer), live.cache.read(layer)):
+            assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
+    assert np.array_equal(rep.cache.last_logits().view(np.uint32),
+                          live.cache.last_logits().view(np.uint32))
+    bad = list(log["history"])
+    bad[20] = (bad[20] + 1) % cfg["vocab_size"]
+    with pytest.raises(H.Divergence, match=f"at position 20, checkpoint recorded {bad[20]}"):
+        H.Session.checkout(gm, seed, 0.7, bad, len(prompt), 40)
+    with pytest.raises(H.DeferHostError, match="inconsistent"):
+        H.Session.checkout(gm, seed, 0.7, log["history"], len(prompt), 39)
+
+
+def test_masked_forward_matches_oracle(tiny):
+    cfg, w, gm, om = tiny
+    say("tiny: forward with masked positions vs oracle")
+    gc, oc = gm.new_cache(), om.new_cache()
+    for t in range(1, 9):
+        gm.forward(t, gc, logits=False)
+        om.forward(t, oc)
+    lg = gm.forward(11, gc, masked=[0, 3, 5])
+    lo = om.forward(11, oc, masked=[0, 3, 5])
+    assert float(np.max(np.abs(lg - lo))) <= LOGIT_TOL
+
+
+def test_135m_long_prompt_split_attention_and_combine(m135):
+    """300 positions: several attention chunks and the separate combine phase."""
+    cfg, w, gm, om = m135
+    say("135m: prompt 300 + 6 greedy vs oracle (oracle side takes ~15 s)")
+    prompt = synthetic.make_prompt(cfg["vocab_size"], 300, seed=21)
+    gc = gm.new_cache()
+    gm.prompt(gc, prompt)
+    toks = gm.generate(gc, 6, 0.0)
+    otoks, _, olog = om.generate(om.new_cache(), bytes(32), 0.0, prompt, 6)
+    d = float(np.max(np.abs(gc.last_logits() - olog)))
+    say(f"135m at 306 positions: max|dlogit| = {d:.3e}")
+    assert toks == otoks
+    assert d <= LOGIT_TOL
+
+
+def test_135m_persistent_and_phase_kernels_bit_identical(m135):
+    cfg, w, gm, om = m135
+    say("135m: prompt 40 + 24 at T=0.7, persistent (staged) vs eager kernels")
+    prompt = synthetic.make_prompt(cfg["vocab_size"], 40, seed=8)
+    words = H.chacha8_words(H.seed_from_u64(3), 0, 24)
+    res = {}
+    for mode in (G.EXEC_PERSISTENT, G.EXEC_EAGER):
+        gm.set_exec(mode)
+        c = gm.new_cache()
+        gm.prompt(c, prompt)
+        toks = gm.generate(c, 24, 0.7, words)
+        res[mode] = (toks, c.last_logits(), c.read(7))
+    gm.set_exec(G.EXEC_PERSISTENT)
+    a, b = res[G.EXEC_PERSISTENT], res[G.EXEC_EAGER]
+    assert a[0] == b[0]
+    assert np.array_equal(a[1].view(np.uint32), b[1].view(np.uint32))
+    for x, y in zip(a[2], b[2]):
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32))

@@ -1,0 +1,158 @@
+"""The C++ host library on the CPU: hashes, the ChaCha8 word source, the WAL
+format, and that both libraries export every function their headers declare.
+(Session tests need the GPU and live in test_gpu_session.py.)"""
+import ctypes
+import hashlib
+import os
+import re
+import struct
+import zlib
+
+import numpy as np
+import pytest
+
+import oracle_py as O
+from defer_amd import gpu as G
+from defer_amd import host as H
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared(header: str, prefix: str):
+    text = open(os.path.join(ROOT, "include", header)).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(" + prefix + r"\w+)\s*\(", text)))
+
+
+@pytest.mark.parametrize("header,prefix,path", [
+    ("defer_gpu.h", "defer_gpu_", G.LIB_PATH),
+    ("defer_host.h", "defer_host_", H.LIB_PATH),
+])
+def test_library_exports_every_declared_symbol(header, prefix, path):
+    names = _declared(header, prefix)
+    assert len(names) > 5
+    if prefix == "defer_host_":
+        G.lib()  # dependency
+    lib = ctypes.CDLL(path)
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+# ------------------------------------------------------------------ hashes
+
+def test_crc32_check_value():  # crc32.rs:34
+    assert H.crc32(b"123456789") == 0xCBF43926
+
+
+def test_sha256_fips_vectors():  # sha256.rs:141-158
+    assert H.sha256(b"abc").hex() == "ba7816bf8f01cfea414140de5dae2223b00361a396177a9cb410ff61f20015ad"
+    assert H.sha256(b"").hex() == "e3b0c44298fc1c149afbf4c8996fb92427ae41e4649b934ca495991b7852b855"
+    assert H.sha256(b"abcdbcdecdefdefgefghfghighijhijkijkljklmklmnlmnomnopnopq").hex() == \
+        "248d6a61d20638b8e5c026930c3e6039a33ce45964ff2167f6ecedd419db06c1"
+
+
+def test_hashes_match_zlib_and_hashlib_at_block_edges():
+    rng = np.random.default_rng(3)
+    for n in (0, 1, 55, 56, 57, 63, 64, 65, 119, 120, 128, 1000, 4099):
+        d = rng.integers(0, 256, n, dtype=np.uint8).tobytes()
+        assert H.crc32(d) == zlib.crc32(d)
+        assert H.sha256(d) == hashlib.sha256(d).digest()
+
+
+# --------------------------------------------------------------- randomness
+
+def test_host_chacha8_keystream_kat():
+    want = bytes.fromhex(
+        "3e00ef2f895f40d67f5bb8e81f09a5a12c840ec3ce9a7f3b181be188ef711a1e"
+        "984ce172b9216f419f445367456d5619314a42a3da86b001387bfdb80e0cfe42")
+    assert H.chacha8_words(bytes(32), 0, 16).tobytes() == want
+
+
+def test_host_words_agree_with_oracle_at_any_offset():
+    seed = H.seed_from_u64(42)
+    assert seed == O.seed_from_u64(42)
+    for start in (0, 5, 16, 31, 1000):
+        w = H.chacha8_words(seed, start, 40)
+        assert [int(x) for x in w] == [O.chacha8_word(seed, start + i) for i in range(40)]
+
+
+def test_words_per_sample():  # sampler.rs:15-21
+    assert H.words_per_sample(0.0) == 0
+    assert H.words_per_sample(0.7) == 1
+
+
+# -------------------------------------------------------------------- WAL
+
+SIG, SEED = bytes([1] * 32), bytes([2] * 32)
+
+
+def test_wal_write_read_torn_resume(tmp_path):  # wal.rs:272-301
+    p = str(tmp_path / "x.wal")
+    w = H.Wal.create(p, SIG, SEED, 0.5, 3, 0, [10, 11, 12])
+    for i, t in enumerate([5, 6, 7]):
+        w.append(t, i + 1)
+    w.close()
+    with open(p, "ab") as f:
+        f.write(bytes([1, 2, 3, 4, 5]))
+    log = H.Wal.read(p)
+    assert log["torn_tail"]
+    assert log["history"] == [10, 11, 12, 5, 6, 7]
+    assert log["rng_word_pos"] == 3
+    assert log["prompt_len"] == 3 and log["temperature"] == 0.5
+    w = H.Wal.resume(p, durable=True)
+    assert w.next_step == 6
+    w.append(8, 4)
+    w.close()
+    log = H.Wal.read(p)
+    assert not log["torn_tail"] and log["history"][-1] == 8
+
+
+def test_wal_byte_layout(tmp_path):  # wal.rs:8-31
+    p = str(tmp_path / "y.wal")
+    prefix = [7, 8, 9, 10]
+    w = H.Wal.create(p, SIG, SEED, 0.7, 2, 0, prefix)
+    w.append(99, 1)
+    w.close()
+    b = open(p, "rb").read()
+    hdr = 104 + 4 * len(prefix)
+    assert len(b) == hdr + 4 + 29
+    assert b[:8] == b"DEFERWAL" and struct.unpack_from("<I", b, 8)[0] == 1
+    assert b[12:44] == SIG and b[44:76] == SEED
+    assert struct.unpack_from("<f", b, 76)[0] == np.float32(0.7)
+    assert struct.unpack_from("<I", b, 80)[0] == 2
+    assert b[84:100] == bytes(16)
+    assert struct.unpack_from("<I", b, 100)[0] == len(prefix)
+    assert list(struct.unpack_from("<4I", b, 104)) == prefix
+    assert struct.unpack_from("<I", b, hdr)[0] == zlib.crc32(b[:hdr])
+    rec = b[hdr + 4:]
+    assert rec[0] == 1 and struct.unpack_from("<II", rec, 1) == (4, 99)
+    assert int.from_bytes(rec[9:25], "little") == 1
+    assert struct.unpack_from("<I", rec, 25)[0] == zlib.crc32(rec[:25])
+
+
+def test_wal_rejects_bad_header_and_inconsistent_records(tmp_path):
+    p = str(tmp_path / "z.wal")
+    w = H.Wal.create(p, SIG, SEED, 0.7, 1, 0, [1])
+    w.append(3, 1)
+    w.append(4, 5)  # rng position must advance by one word per sample
+    w.close()
+    with pytest.raises(H.DeferHostError, match="inconsistent"):
+        H.Wal.read(p)
+    b = bytearray(open(p, "rb").read())
+    b[20] ^= 0xFF
+    open(p, "wb").write(bytes(b))
+    with pytest.raises(H.DeferHostError, match="checksum"):
+        H.Wal.read(p)
+    open(p, "wb").write(b"not a wal at all, not at all, not at all" * 4)
+    with pytest.raises(H.DeferHostError, match="not a defer WAL"):
+        H.Wal.read(p)
+
+
+def test_wal_greedy_records_keep_rng_position(tmp_path):
+    p = str(tmp_path / "g.wal")
+    w = H.Wal.create(p, SIG, SEED, 0.0, 2, 0, [1, 2])
+    for t in (3, 4, 5):
+        w.append(t, 0)
+    w.close()
+    log = H.Wal.read(p)
+    assert log["history"] == [1, 2, 3, 4, 5] and log["rng_word_pos"] == 0

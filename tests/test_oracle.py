@@ -1,0 +1,273 @@
+"""The oracle (CPU restatement of the reference) pinned against known answers.
+
+Known-answer tests come from the reference's own unit tests (ops.rs:188-252,
+sampler.rs:116-162), from RFC 8439 and the ChaCha8 reference keystream, and
+from closed forms. The structure of the forward pass (GQA head mapping,
+half-split RoPE, append-before-attend) is pinned by an independent float64
+numpy forward on the tiny config. Nothing here needs a GPU.
+"""
+import math
+import struct
+
+import numpy as np
+import pytest
+
+import oracle_py as O
+from defer_amd import synthetic
+
+
+# ------------------------------------------------------------------ ops.rs KATs
+
+def test_matmul_small():  # ops.rs:189-195
+    out = O.matmul_sequential([1, 2, 3, 4, 5, 6], [7, 8, 9, 10, 11, 12], 2, 2, 3)
+    assert list(out) == [58.0, 64.0, 139.0, 154.0]
+
+
+def test_linear_matches_matmul():  # ops.rs:197-205
+    out = O.linear([1.0, 0.5, -1.0], [1, 2, 3, 4, 5, 6], bias=[0.5, -0.5], out_dim=2)
+    assert list(out) == [1.0 + 1.0 - 3.0 + 0.5, 4.0 + 2.5 - 6.0 - 0.5]
+
+
+def test_blocked_linear_bit_identical_to_sequential():  # ops.rs:207-224
+    in_dim, out_dim = 37, 11
+    w = np.array([((i * 7919) % 1000) * 1e-3 - 0.5 for i in range(in_dim * out_dim)], dtype=np.float32)
+    x = np.array([((i * 104729) % 997) * 1e-2 - 4.0 for i in range(in_dim)], dtype=np.float32)
+    b = np.array([i * 0.1 for i in range(out_dim)], dtype=np.float32)
+    out = O.linear(x, w, bias=b, out_dim=out_dim)
+    for o in range(out_dim):
+        s = np.float32(0.0)
+        for i in range(in_dim):
+            s = np.float32(s + np.float32(w[o * in_dim + i] * x[i]))
+        s = np.float32(s + b[o])
+        assert out[o].view(np.uint32) == s.view(np.uint32)
+
+
+def test_norms():  # ops.rs:227-238
+    x = np.array([1.0, 2.0, 3.0, 4.0], dtype=np.float32)
+    out = O.rmsnorm(x, np.ones(4, dtype=np.float32), 0.0)
+    rms = math.sqrt(30.0 / 4.0)
+    assert np.max(np.abs(out - x / rms)) < 1e-6
+    ln = O.layernorm(x, np.ones(4, dtype=np.float32), np.zeros(4, dtype=np.float32), 0.0)
+    assert abs(float(np.sum(ln))) < 1e-5
+
+
+def test_activations_and_softmax():  # ops.rs:241-252
+    assert O.silu(0.0) == 0.0
+    assert abs(O.gelu(1.0) - 0.841192) < 1e-4
+    v = O.softmax([1.0, 2.0, 3.0])
+    assert abs(float(np.sum(v)) - 1.0) < 1e-6
+    assert v[2] > v[1] > v[0]
+    a = O.add_inplace([1.0, 2.0], [1.0, 1.0])
+    a = O.mul_inplace(a, [2.0, 3.0])
+    assert list(a) == [4.0, 9.0]
+
+
+def test_linear_one_hot_returns_a_column_exactly():
+    rng = np.random.default_rng(0)
+    w = rng.standard_normal((7, 13)).astype(np.float32)
+    for j in range(13):
+        x = np.zeros(13, dtype=np.float32)
+        x[j] = 1.0
+        out = O.linear(x, w.ravel(), out_dim=7)
+        assert np.array_equal(out.view(np.uint32), w[:, j].copy().view(np.uint32))
+
+
+# -------------------------------------------------------------- sampler.rs KATs
+
+def test_argmax_ties_nan_and_neg_inf():  # sampler.rs:120-124
+    assert O.argmax([1.0, 3.0, 3.0, 2.0]) == 1
+    assert O.argmax([float("nan"), 0.0, 0.0]) == 1
+    assert O.argmax([float("-inf")] * 3) == 0
+
+
+def test_greedy_does_not_touch_rng():  # sampler.rs:126-133, verification.rs:80
+    cfg = synthetic.CONFIGS["tiny"]
+    om = O.OracleModel(cfg, synthetic.make_weights(cfg, 5))
+    _, words, _ = om.generate(om.new_cache(), O.seed_from_u64(1), 0.0, [1, 2, 3], 10)
+    assert words == 0
+
+
+def test_exactly_one_word_per_sample():  # sampler.rs:135-148
+    cfg = synthetic.CONFIGS["tiny"]
+    om = O.OracleModel(cfg, synthetic.make_weights(cfg, 5))
+    _, words, _ = om.generate(om.new_cache(), O.seed_from_u64(7), 0.7, [1, 2, 3], 9)
+    assert words == 9
+
+
+def test_sampling_reproducible_and_distributed():  # sampler.rs:150-162
+    logits = [0.0, 1.0, 2.0, 3.0]
+    seed = O.seed_from_u64(42)
+    run = [O.sample_token(logits, 1.0, O.chacha8_word(seed, i)) for i in range(2000)]
+    again = [O.sample_token(logits, 1.0, O.chacha8_word(seed, i)) for i in range(2000)]
+    assert run == again
+    counts = np.bincount(run, minlength=4)
+    assert counts[3] > counts[2] > counts[1] > counts[0] > 0
+
+
+def test_uniform_logits_give_uniform_probabilities():
+    p = O.softmax_with_temperature([0.25] * 8, 0.7)
+    assert np.all(p == np.float32(0.125))
+
+
+def test_unit_f32_is_24_bit_fraction():
+    assert O.unit_f32(0) == 0.0
+    assert O.unit_f32(0xFFFFFFFF) == (2**24 - 1) / 2**24
+    assert O.unit_f32(0x00000100) == 2**-24
+
+
+def test_degenerate_temperature_distribution_falls_back_to_argmax():  # sampler.rs:64-66
+    assert O.sample_token([float("-inf")] * 4, 0.7, 123456) == 0
+    assert O.sample_token([float("nan"), 5.0], 0.7, 0xFFFFFFFF) == 1
+
+
+# ----------------------------------------------------------------- ChaCha KATs
+
+def _le_bytes(words):
+    return b"".join(struct.pack("<I", w) for w in words)
+
+
+def test_chacha20_block_rfc8439_2_3_2():
+    # RFC 8439 section 2.3.2: key 00..1f, counter 1, nonce 00000009 0000004a 00000000.
+    # With the 64-bit counter layout, word 13 holds the first nonce word and
+    # words 14-15 the rest.
+    key = [int.from_bytes(bytes(range(4 * i, 4 * i + 4)), "little") for i in range(8)]
+    out = O.chacha_block(key, 1 | (0x09000000 << 32), 0x4A000000, 20)
+    assert out == [0xE4E7F110, 0x15593BD1, 0x1FDD0F50, 0xC47120A3, 0xC7F4D1C7, 0x0368C033,
+                   0x9AAA2204, 0x4E6CD4C3, 0x466482D2, 0x09AA9F07, 0x05D7C214, 0xA2028BD9,
+                   0xD19C12B5, 0xB94E16DE, 0xE883D0CB, 0x4E3C50A2]
+
+
+def test_chacha8_zero_key_keystream():
+    # The published ChaCha8 keystream for the all-zero key and nonce, block 0.
+    want = bytes.fromhex(
+        "3e00ef2f895f40d67f5bb8e81f09a5a12c840ec3ce9a7f3b181be188ef711a1e"
+        "984ce172b9216f419f445367456d5619314a42a3da86b001387bfdb80e0cfe42")
+    assert _le_bytes(O.chacha_block([0] * 8, 0, 0, 8)) == want
+
+
+def test_chacha8_word_stream_indexing():
+    seed = bytes(range(32))
+    key = list(struct.unpack("<8I", seed))
+    for n in (0, 1, 15, 16, 17, 33, 1000):
+        assert O.chacha8_word(seed, n) == O.chacha_block(key, n // 16, 0, 8)[n % 16]
+
+
+# ------------------------------------------------- forward pass (tiny, float64)
+
+def _rope_tables(hd, theta, pos):
+    half = hd // 2
+    inv = np.array([np.float32(1.0 / theta ** (2 * i / hd)) for i in range(half)], dtype=np.float32)
+    ang = (np.float32(pos) * inv).astype(np.float32)
+    return np.cos(ang.astype(np.float64)), np.sin(ang.astype(np.float64))
+
+
+def _numpy_forward(cfg, w, tokens):
+    """Llama forward in float64, written from the model definition: RMSNorm,
+    q/k/v, half-split RoPE on q and k, k/v appended before attending, GQA
+    (query head h reads kv head h // group), softmax, o, SwiGLU, tied head."""
+    h, L = cfg["hidden_size"], cfg["num_layers"]
+    nh, nkv, hd = cfg["num_heads"], cfg["num_kv_heads"], cfg["head_dim"]
+    eps, theta = cfg["rms_norm_eps"], cfg["rope_theta"]
+    grp, half = nh // nkv, hd // 2
+    W = [np.asarray(t, dtype=np.float64) for t in w]
+    emb, i = W[0], 1
+    layers = []
+    for _ in range(L):
+        layers.append(W[i:i + 9])
+        i += 9
+    norm = W[i]
+    head = emb if cfg["tie_word_embeddings"] else W[i + 1]
+    K = [[] for _ in range(L)]
+    Vc = [[] for _ in range(L)]
+    rms = lambda x, g: x / np.sqrt(np.mean(x * x) + eps) * g  # noqa: E731
+    out = []
+    for pos, tok in enumerate(tokens):
+        x = emb[tok].copy()
+        c, s = _rope_tables(hd, theta, pos)
+        for l, (an, wq, wk, wv, wo, fn, wg, wu, wd) in enumerate(layers):
+            xn = rms(x, an)
+            q, k, v = wq @ xn, wk @ xn, wv @ xn
+
+            def rope(vec, nheads):
+                vec = vec.reshape(nheads, hd).copy()
+                a, b = vec[:, :half].copy(), vec[:, half:].copy()
+                vec[:, :half] = a * c - b * s
+                vec[:, half:] = b * c + a * s
+                return vec
+
+            q, k = rope(q, nh), rope(k, nkv)
+            K[l].append(k)
+            Vc[l].append(v.reshape(nkv, hd))
+            ks, vs = np.stack(K[l]), np.stack(Vc[l])
+            att = np.empty((nh, hd))
+            for hh in range(nh):
+                g = hh // grp
+                sc = ks[:, g, :] @ q[hh] / math.sqrt(hd)
+                p = np.exp(sc - sc.max())
+                p /= p.sum()
+                att[hh] = p @ vs[:, g, :]
+            x = x + wo @ att.ravel()
+            xn = rms(x, fn)
+            gt, up = wg @ xn, wu @ xn
+            x = x + wd @ (gt / (1.0 + np.exp(-gt)) * up)
+        out.append(head @ rms(x, norm))
+    return out
+
+
+def test_tiny_forward_matches_float64_model():
+    cfg = synthetic.CONFIGS["tiny"]
+    w = synthetic.make_weights(cfg, 1234)
+    om = O.OracleModel(cfg, w)
+    toks = list(synthetic.make_prompt(cfg["vocab_size"], 9, seed=4))
+    ref = _numpy_forward(cfg, w, toks)
+    c = om.new_cache()
+    for t, r in zip(toks, ref):
+        lg = om.forward(int(t), c).astype(np.float64)
+        assert np.max(np.abs(lg - r)) <= 1e-4 * (1.0 + np.max(np.abs(r)))
+
+
+def test_first_position_attends_to_itself_only():
+    """At pos 0 the softmax has one term: probability exactly 1.0, so the
+    attention output is V[0] bit for bit whatever q and k are."""
+    cfg = synthetic.CONFIGS["tiny"]
+    om = O.OracleModel(cfg, synthetic.make_weights(cfg, 9))
+    _, tr = om.forward(17, om.new_cache(), trace=True)
+    assert tr.shape == (cfg["num_layers"], cfg["num_heads"], 1)
+    assert np.all(tr == np.float32(1.0))
+
+
+def test_masked_positions_get_zero_probability():  # model.rs:478-484
+    cfg = synthetic.CONFIGS["tiny"]
+    om = O.OracleModel(cfg, synthetic.make_weights(cfg, 9))
+    c = om.new_cache()
+    for t in (3, 4, 5):
+        om.forward(t, c)
+    _, tr = om.forward(6, c, masked=[0, 2], trace=True)
+    assert np.all(tr[:, :, 0] == 0.0) and np.all(tr[:, :, 2] == 0.0)
+    assert np.allclose(tr.sum(axis=2), 1.0, atol=1e-6)
+
+
+def test_range_errors_leave_the_cache_untouched():  # model.rs:417-422
+    cfg = dict(synthetic.CONFIGS["tiny"])
+    om = O.OracleModel(cfg, synthetic.make_weights(cfg, 9))
+    c = om.new_cache()
+    om.forward(1, c)
+    with pytest.raises(ValueError):
+        om.forward(cfg["vocab_size"], c)
+    assert len(c) == 1
+
+
+def test_checkout_replay_of_generated_session_and_divergence():
+    cfg = synthetic.CONFIGS["tiny"]
+    om = O.OracleModel(cfg, synthetic.make_weights(cfg, 9))
+    seed = O.seed_from_u64(11)
+    prompt = [5, 6, 7, 8]
+    toks, words, last = om.generate(om.new_cache(), seed, 0.8, prompt, 20)
+    assert words == 20
+    hist = prompt + toks
+    fd, _, last2 = om.checkout(om.new_cache(), seed, 0.8, hist, len(prompt))
+    assert fd == -1 and np.array_equal(last.view(np.uint32), last2.view(np.uint32))
+    bad = list(hist)
+    bad[10] = (bad[10] + 1) % cfg["vocab_size"]
+    fd, sampled, _ = om.checkout(om.new_cache(), seed, 0.8, bad, len(prompt))
+    assert fd == 10 and sampled == hist[10]
