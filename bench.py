@@ -53,6 +53,18 @@ def algorithmic_bytes(cfg: dict, weight_bytes: int, first_pos: int, n_pos: int) 
     return total
 
 
+def measured_traffic() -> int | None:
+    """HBM bytes per replay launch from the committed rocprofv3 PMC summary
+    (FETCH_SIZE and WRITE_SIZE, each scaled by a 1 GiB copy's reading)."""
+    p = os.path.join(ROOT, "profiles", "k_persistent_replay_135m.md")
+    if not os.path.exists(p):
+        return None
+    for line in open(p):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":")[1])
+    return None
+
+
 def cpu_baseline(cfg: dict, weights, history, budget_s: float = 12.0) -> dict:
     """The oracle (C, one thread) replaying the session's first positions
     until `budget_s` of CPU work is spent."""
@@ -84,7 +96,20 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only copy MIB MiB device-to-device once (calibrates HBM byte counters)")
     args = ap.parse_args()
+    if args.copy_probe:
+        import torch
+
+        n = args.copy_probe * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": n * 4}), flush=True)
+        return 0
     if args.gpus != 1:
         print(f"bench.py runs on one GPU; --gpus {args.gpus} is not supported "
               "(the single-GPU path is the whole product; see DESIGN.md for how it would shard)",
@@ -178,9 +203,12 @@ def main() -> int:
             "peak": PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
         },
     }
+    # Device objects are released here, not during interpreter shutdown.
+    live.close()
+    model.close()
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(cfg, weights, log["history"])
     print(json.dumps(line), flush=True)
@@ -188,4 +216,6 @@ def main() -> int:
 
 
 if __name__ == "__main__":
-    sys.exit(main())
+    rc = main()
+    if rc:
+        sys.exit(rc)
