@@ -139,3 +139,23 @@ def test_135m_persistent_and_phase_kernels_bit_identical(m135):
     assert np.array_equal(a[1].view(np.uint32), b[1].view(np.uint32))
     for x, y in zip(a[2], b[2]):
         assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
+
+
+def test_360m_rows_loaded_directly_greedy_parity():
+    """The 360M shape does not fit the LDS staging: compute waves load their
+    rows from HBM (same arithmetic order)."""
+    cfg = synthetic.CONFIGS["smollm2-360m"]
+    w = synthetic.make_weights(cfg, 0)
+    gm, om = G.GpuModel(G.Config.from_dict(cfg), w), O.OracleModel(cfg, w)
+    say("360m: prompt 24 + 8 greedy vs oracle")
+    prompt = synthetic.make_prompt(cfg["vocab_size"], 24, seed=2)
+    c = gm.new_cache(64)
+    gm.prompt(c, prompt)
+    toks = gm.generate(c, 8, 0.0)
+    otoks, _, olog = om.generate(om.new_cache(), bytes(32), 0.0, prompt, 8)
+    d = float(np.max(np.abs(c.last_logits() - olog)))
+    say(f"360m max|dlogit| = {d:.3e}")
+    assert toks == otoks
+    assert d <= LOGIT_TOL
+    c.close()
+    gm.close()
