@@ -45,7 +45,9 @@ def _run(cmd, cwd=ROOT):
 def build_gpu() -> str:
     out = os.path.join(PKG, "libdefer_gpu.so")
     tmp = out + ".tmp"
-    _run([HIPCC, *GPU_FLAGS, "-o", tmp, os.path.join(CSRC, "defer_gpu.hip")])
+    srcs = [os.path.join(CSRC, "defer_gpu.hip")] + sorted(
+        os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.startswith("kernels_") and f.endswith(".hip"))
+    _run([HIPCC, *GPU_FLAGS, "-o", tmp, *srcs])
     os.replace(tmp, out)
     return out
 

@@ -23,6 +23,13 @@
 
 using namespace dg;
 
+// Persistent kernels specialised for known model shapes (kernels_*.hip).
+namespace dg135 {
+struct Args;
+struct RunDesc;
+__global__ void k_persistent(const Args* ap, const RunDesc* run);
+}  // namespace dg135
+
 // ------------------------------------------------------------------ errors
 
 static thread_local std::string g_last_error;
@@ -49,93 +56,7 @@ extern "C" const char* defer_gpu_last_error(void) { return g_last_error.c_str();
 
 // ------------------------------------------------------------------ kernels
 
-__device__ __forceinline__ Lds lds_init(const Dims& d) {
-  extern __shared__ float lds_raw[];
-  Lds s = lds_layout(lds_raw, d);
-  if (threadIdx.x == 0) s.ctl->abort_seen = 0;
-  __syncthreads();
-  return s;
-}
-
-__device__ __forceinline__ bool forward_all(const Args& a, uint32_t tok, uint32_t pos, uint32_t tick,
-                                            uint32_t wg, uint32_t G, const Lds& s,
-                                            const Stager& sg) {
-  for (uint32_t l = 0; l < a.d.L; ++l) {
-    if (!phase_qkv(a, l, tick, pos, tok, wg, G, s, sg)) return false;
-    if (!phase_attn(a, l, tick, pos, wg, G, s)) return false;
-    if (!phase_comb(a, l, tick, pos, wg, G, s)) return false;
-    if (!phase_o(a, l, tick, pos, tok, wg, G, s, sg)) return false;
-    if (!phase_gu(a, l, tick, wg, G, s, sg)) return false;
-    if (!phase_d(a, l, tick, wg, G, s, sg)) return false;
-  }
-  return phase_lm(a, tick, wg, G, s, sg);
-}
-
-__device__ __forceinline__ bool is_stop(const RunDesc& r, uint32_t tok) {
-  for (uint32_t k = 0; k < r.n_stop; ++k)
-    if (cptr(r.stop)[k] == tok) return true;
-  return false;
-}
-
-// Every op of a run in one launch. All workgroups sample redundantly (same
-// inputs, same code, same token), so no broadcast is needed.
-__global__ __launch_bounds__(BLOCK) void k_persistent(const Args* __restrict__ ap,
-                                                      const RunDesc* __restrict__ run) {
-  const Args& a = *ap;
-  const Lds s = lds_init(a.d);
-  const RunDesc r = *run;
-  DevState* st = a.st;
-  uint32_t pos = cptr(st)->pos, tick = cptr(st)->tick;
-  const uint32_t wg = blockIdx.x, G = gridDim.x;
-  lm_prime(a, s);
-  // Weight rows are staged in LDS when a layer's share fits: the loaders
-  // request layer 0's QKV, O and GU rows now (the D rows follow at the first
-  // QKV phase, as in every later layer).
-  const Stager sg = make_stager(a, s, wg, G, a.d.lds_stg != 0);
-  if (sg.on && sg.loader)
-    for (uint32_t k = 0; k < 3; ++k) stage_issue(sg, k, 0);
-  uint32_t i = 0;
-  uint32_t halted = 0;
-  for (; i < r.n_ops; ++i) {
-    uint32_t tok;
-    if (i >= r.sample_from) {
-      const uint32_t word = r.temperature != 0.0f ? cptr(r.words)[i - r.sample_from] : 0u;
-      if (r.temperature != 0.0f && !sample_stage_a(a, tick, r.temperature, wg, G, s)) break;
-      if (!sample_stage_b(a, tick, r.temperature, word, s, &tok)) break;
-      if (r.mode == RUN_REPLAY) {
-        if (tok != cptr(r.tokens)[i]) {
-          if (wg == 0 && threadIdx.x == 0) {
-            st->first_div = (long long)i;
-            st->sampled_div = tok;
-          }
-          halted = 1;
-          break;
-        }
-        tok = cptr(r.tokens)[i];
-      } else if (wg == 0 && threadIdx.x == 0) {
-        r.out_tokens[i] = tok;
-      }
-    } else {
-      tok = cptr(r.tokens)[i];
-    }
-    if (!forward_all(a, tok, pos, tick, wg, G, s, sg)) break;
-    ++pos;
-    ++tick;
-    if (r.mode == RUN_GENERATE && is_stop(r, tok)) {
-      ++i;
-      halted = 1;
-      break;
-    }
-  }
-  if (wg == 0 && threadIdx.x == 0) {
-    st->pos = pos;
-    st->tick = tick;
-    st->n_done = i;
-    st->halt = halted;
-  }
-  // Staged loads of a layer that will not run land before the wave ends.
-  if (sg.on && sg.loader) stage_wait(0);
-}
+#include "persistent.h"
 
 // Per-run reset of the counters (pos / tick / token are kept).
 __global__ void k_begin(DevState* st) {
@@ -262,9 +183,19 @@ struct defer_gpu_model {
   const float* head = nullptr;
   float2* rope = nullptr;
   uint32_t exec_mode = DEFER_GPU_EXEC_PERSISTENT;
+  const void* persistent = nullptr;  // the persistent kernel for this shape
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   double last_ms = 0.0;
 };
+
+// A persistent kernel compiled for this exact shape, if there is one.
+static const void* persistent_kernel_for(const Dims& d) {
+  const bool smollm2_135m = d.h == 576 && d.nh == 9 && d.nkv == 3 && d.hd == 64 &&
+                            d.ff == 1536 && d.V == 49152 && d.L == 30 && d.act == 0 &&
+                            d.has_bias == 0 && d.tied == 1;
+  if (smollm2_135m) return (const void*)dg135::k_persistent;
+  return (const void*)k_persistent;
+}
 
 struct defer_gpu_cache {
   const defer_gpu_model* m = nullptr;
@@ -541,7 +472,8 @@ extern "C" int defer_gpu_model_create(const defer_gpu_config* cfg, const float* 
     e = hipMemcpy(m->rope, rope.data(), rope.size() * sizeof(float2), hipMemcpyHostToDevice);
   if (e != hipSuccess) return cleanup(fail(DEFER_GPU_E_HIP, "rope table: %s", hipGetErrorString(e)));
 
-  const void* kernels[] = {(const void*)k_persistent, (const void*)k_phase,
+  m->persistent = persistent_kernel_for(d);
+  const void* kernels[] = {m->persistent, (const void*)k_phase,
                            (const void*)k_samp_a, (const void*)k_op};
   for (const void* kf : kernels) {
     e = hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)m->lds_bytes);
@@ -550,7 +482,7 @@ extern "C" int defer_gpu_model_create(const defer_gpu_config* cfg, const float* 
                           hipGetErrorString(e)));
   }
   int occ = 0;
-  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_persistent, BLOCK, m->lds_bytes);
+  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, m->persistent, BLOCK, m->lds_bytes);
   if (e != hipSuccess || occ < 1)
     return cleanup(fail(DEFER_GPU_E_HIP, "persistent kernel does not fit a CU (occupancy %d)", occ));
   if (hipEventCreate(&m->ev0) != hipSuccess || hipEventCreate(&m->ev1) != hipSuccess)
@@ -802,7 +734,7 @@ static int run_ops(defer_gpu_cache* c, RunDesc r, bool force_eager) {
       const Args* a = c->d_args;
       const RunDesc* dr = c->d_run;
       void* params[] = {&a, &dr};
-      HIP_TRY(hipLaunchCooperativeKernel((const void*)k_persistent, dim3(m->G), dim3(BLOCK),
+      HIP_TRY(hipLaunchCooperativeKernel(m->persistent, dim3(m->G), dim3(BLOCK),
                                          params, (unsigned)m->lds_bytes, s));
     } else if (mode == DEFER_GPU_EXEC_GRAPH) {
       if (!c->graph) {

@@ -17,7 +17,14 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-namespace dg {
+// The device code is compiled once generically (namespace dg, every model
+// dimension read at run time) and once per specialised model shape (its own
+// namespace, DG_NS, with the shape's dimensions as compile-time constants).
+#ifndef DG_NS
+#define DG_NS dg
+#endif
+
+namespace DG_NS {
 
 typedef unsigned long long u64;
 
@@ -127,6 +134,35 @@ __host__ __device__ inline uint32_t gen_lm(const Dims& d, uint32_t tick) {
 }
 __host__ __device__ inline uint32_t gen_sums(const Dims& d, uint32_t tick) {
   return tick * phases_per_tick(d) + d.L * PH_PER_LAYER + 2u;
+}
+
+// The dimensions device code computes with. In a shape-specialised build the
+// model's dimensions are compile-time constants (loops unroll, index
+// arithmetic folds); the per-cache and per-launch fields (capacity, LDS
+// layout) always come from the arguments. The values are identical either
+// way, so specialised and generic kernels produce the same bits.
+__device__ __forceinline__ Dims shape_dims(const Dims& r) {
+  Dims d = r;
+#if defined(DG_SHAPE_SMOLLM2_135M)
+  d.h = 576;
+  d.nh = 9;
+  d.nkv = 3;
+  d.hd = 64;
+  d.half = 32;
+  d.ff = 1536;
+  d.V = 49152;
+  d.L = 30;
+  d.q = 576;
+  d.kv = 192;
+  d.qkv_rows = 960;
+  d.group = 3;
+  d.act = 0;
+  d.has_bias = 0;
+  d.tied = 1;
+  d.kvs = 64;
+  d.nvc = 768;
+#endif
+  return d;
 }
 
 // Attention chunking: a function of the query position only, so results
@@ -405,4 +441,4 @@ struct WaitCtl {
   int abort_seen;
 };
 
-}  // namespace dg
+}  // namespace DG_NS

@@ -1,0 +1,99 @@
+// persistent.h -- the persistent kernel (every op of a call in one launch)
+// and the LDS set-up the other kernels share. Included once per device
+// namespace: generically (dg) and per specialised model shape.
+#pragma once
+
+#include "phases.h"
+
+namespace DG_NS {
+
+__device__ __forceinline__ Lds lds_init(const Dims& d) {
+  extern __shared__ float lds_raw[];
+  Lds s = lds_layout(lds_raw, d);
+  if (threadIdx.x == 0) s.ctl->abort_seen = 0;
+  __syncthreads();
+  return s;
+}
+
+__device__ __forceinline__ bool forward_all(const Args& a, uint32_t tok, uint32_t pos, uint32_t tick,
+                                            uint32_t wg, uint32_t G, const Lds& s,
+                                            const Stager& sg) {
+  const uint32_t L = shape_dims(a.d).L;
+  for (uint32_t l = 0; l < L; ++l) {
+    if (!phase_qkv(a, l, tick, pos, tok, wg, G, s, sg)) return false;
+    if (!phase_attn(a, l, tick, pos, wg, G, s)) return false;
+    if (!phase_comb(a, l, tick, pos, wg, G, s)) return false;
+    if (!phase_o(a, l, tick, pos, tok, wg, G, s, sg)) return false;
+    if (!phase_gu(a, l, tick, wg, G, s, sg)) return false;
+    if (!phase_d(a, l, tick, wg, G, s, sg)) return false;
+  }
+  return phase_lm(a, tick, wg, G, s, sg);
+}
+
+__device__ __forceinline__ bool is_stop(const RunDesc& r, uint32_t tok) {
+  for (uint32_t k = 0; k < r.n_stop; ++k)
+    if (cptr(r.stop)[k] == tok) return true;
+  return false;
+}
+
+// Every op of a run in one launch. All workgroups sample redundantly (same
+// inputs, same code, same token), so no broadcast is needed.
+__global__ __launch_bounds__(BLOCK) void k_persistent(const Args* __restrict__ ap,
+                                                      const RunDesc* __restrict__ run) {
+  const Args& a = *ap;
+  const Lds s = lds_init(a.d);
+  const RunDesc r = *run;
+  DevState* st = a.st;
+  uint32_t pos = cptr(st)->pos, tick = cptr(st)->tick;
+  const uint32_t wg = blockIdx.x, G = gridDim.x;
+  lm_prime(a, s);
+  // Weight rows are staged in LDS when a layer's share fits: the loaders
+  // request layer 0's QKV, O and GU rows now (the D rows follow at the first
+  // QKV phase, as in every later layer).
+  const Stager sg = make_stager(a, s, wg, G, a.d.lds_stg != 0);
+  if (sg.on && sg.loader)
+    for (uint32_t k = 0; k < 3; ++k) stage_issue(sg, k, 0);
+  uint32_t i = 0;
+  uint32_t halted = 0;
+  for (; i < r.n_ops; ++i) {
+    uint32_t tok;
+    if (i >= r.sample_from) {
+      const uint32_t word = r.temperature != 0.0f ? cptr(r.words)[i - r.sample_from] : 0u;
+      if (r.temperature != 0.0f && !sample_stage_a(a, tick, r.temperature, wg, G, s)) break;
+      if (!sample_stage_b(a, tick, r.temperature, word, s, &tok)) break;
+      if (r.mode == RUN_REPLAY) {
+        if (tok != cptr(r.tokens)[i]) {
+          if (wg == 0 && threadIdx.x == 0) {
+            st->first_div = (long long)i;
+            st->sampled_div = tok;
+          }
+          halted = 1;
+          break;
+        }
+        tok = cptr(r.tokens)[i];
+      } else if (wg == 0 && threadIdx.x == 0) {
+        r.out_tokens[i] = tok;
+      }
+    } else {
+      tok = cptr(r.tokens)[i];
+    }
+    if (!forward_all(a, tok, pos, tick, wg, G, s, sg)) break;
+    ++pos;
+    ++tick;
+    if (r.mode == RUN_GENERATE && is_stop(r, tok)) {
+      ++i;
+      halted = 1;
+      break;
+    }
+  }
+  if (wg == 0 && threadIdx.x == 0) {
+    st->pos = pos;
+    st->tick = tick;
+    st->n_done = i;
+    st->halt = halted;
+  }
+  // Staged loads of a layer that will not run land before the wave ends.
+  if (sg.on && sg.loader) stage_wait(0);
+}
+
+}  // namespace DG_NS

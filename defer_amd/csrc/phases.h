@@ -21,7 +21,7 @@
 
 #include "device.h"
 
-namespace dg {
+namespace DG_NS {
 
 constexpr uint32_t NPOLL = 2;
 constexpr uint32_t NCW = 4;
@@ -275,7 +275,7 @@ struct ItemRows {
 
 __device__ __forceinline__ ItemRows item_rows(const Args& a, uint32_t kind, uint32_t l, uint32_t k,
                                               uint32_t wg, uint32_t G) {
-  const Dims& d = a.d;
+  const Dims d = shape_dims(a.d);
   const LayerW W = layer_w(a, l);
   const uint32_t it = wg + G * k;
   ItemRows r;
@@ -377,7 +377,7 @@ __device__ __forceinline__ Stager make_stager(const Args& a, const Lds& s, uint3
   sg.ld = sg.loader ? wave - NWA : 0;
   uint32_t n[4], tot = 0;
   for (uint32_t k = 0; k < 4; ++k) {
-    n[k] = stage_loads(a.d, k, wg, G, sg.ld);
+    n[k] = stage_loads(shape_dims(a.d), k, wg, G, sg.ld);
     tot += n[k];
   }
   for (uint32_t k = 0; k < 4; ++k) sg.wait[k] = tot - n[k] - n[(k + 3) % 4];
@@ -387,7 +387,7 @@ __device__ __forceinline__ Stager make_stager(const Args& a, const Lds& s, uint3
 // Loader: request this wave's items of `kind`, layer l.
 __device__ __forceinline__ void stage_issue(const Stager& sg, uint32_t kind, uint32_t l) {
   const Args& a = *sg.a;
-  const Dims& d = a.d;
+  const Dims d = shape_dims(a.d);
   const uint32_t lane = threadIdx.x % WAVE;
   const uint32_t cnt = rows_owned(kind_items(d, kind), sg.wg, sg.G);
   const uint32_t K = kind_k(d, kind), nr = kind_rows(kind), nseg = (K + 255) / 256;
@@ -422,7 +422,7 @@ __device__ __forceinline__ LoadOp no_load() {
 
 // Staged rows of item k of a kind (pairs: second row at +K).
 __device__ __forceinline__ const float* staged_item(const Stager& sg, uint32_t kind, uint32_t k) {
-  const Dims& d = sg.a->d;
+  const Dims d = shape_dims(sg.a->d);
   return sg.stg + d.stg_off[kind] + k * kind_rows(kind) * kind_k(d, kind);
 }
 
@@ -549,7 +549,7 @@ template <bool PAIR>
 __device__ __forceinline__ void preload_rows(Preload& P, const Stager& sg, uint32_t kind,
                                              uint32_t cw, uint32_t lane) {
   constexpr int NR = pre_nr(PAIR), NF = pre_nf(PAIR);
-  const Dims& d = sg.a->d;
+  const Dims d = shape_dims(sg.a->d);
   const uint32_t cnt = rows_owned(kind_items(d, kind), sg.wg, sg.G);
   const uint32_t K = kind_k(d, kind);
   P.any = cw < cnt;
@@ -639,8 +639,9 @@ template <class F>
 __device__ __forceinline__ void items_dot(const Args& a, uint32_t kind, uint32_t cw, uint32_t l,
                                           const Stager& sg, const Preload& P, const float* x,
                                           uint32_t wg, uint32_t G, uint32_t lane, F body) {
-  const uint32_t cnt = rows_owned(kind_items(a.d, kind), wg, G);
-  const uint32_t K = kind_k(a.d, kind);
+  const Dims dd = shape_dims(a.d);
+  const uint32_t cnt = rows_owned(kind_items(dd, kind), wg, G);
+  const uint32_t K = kind_k(dd, kind);
   const bool pair = kind_rows(kind) == 2;
   if (sg.on) {
     if (!P.any) return;
@@ -721,7 +722,7 @@ __device__ __forceinline__ void items_dot(const Args& a, uint32_t kind, uint32_t
 // (cos, sin) and the biases of its two rows.
 __device__ __forceinline__ float4 qkv_epi_load(const Args& a, uint32_t l, uint32_t pos, uint32_t k,
                                                uint32_t wg, uint32_t G) {
-  const Dims& d = a.d;
+  const Dims d = shape_dims(a.d);
   const uint32_t p = wg + G * k;
   const uint32_t hb = p / d.half, i = p - hb * d.half;
   const uint32_t r0 = hb * d.hd + i;
@@ -746,7 +747,7 @@ constexpr uint32_t QKV_PRE = 2;  // epilogue inputs a compute wave loads before 
 __device__ __forceinline__ bool phase_qkv(const Args& a, uint32_t l, uint32_t tick, uint32_t pos,
                                           uint32_t token, uint32_t wg, uint32_t G, const Lds& s,
                                           const Stager& sg) {
-  const Dims& d = a.d;
+  const Dims d = shape_dims(a.d);
   const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
   const bool compute = wave >= NPOLL && wave < NWA;
   const uint32_t cw = wave - NPOLL;  // meaningful for compute waves only
@@ -859,7 +860,7 @@ __device__ __forceinline__ AttGeo att_geo(uint32_t hd) {
 // every loop's trip count a compile-time constant.
 __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t tick, uint32_t pos,
                                            uint32_t wg, uint32_t G, const Lds& s) {
-  const Dims& d = a.d;
+  const Dims d = shape_dims(a.d);
   const uint32_t nch = attn_nchunks(pos), CH = attn_chunk(pos);
   const uint32_t n_items = d.nkv * nch;
   const uint32_t gen_in = gen_of(d, tick, l, PH_QKV);
@@ -1049,7 +1050,7 @@ __device__ __forceinline__ float combine_one(const float* part, uint32_t nch, ui
 // phase's LDS budget): item = one query head.
 __device__ __forceinline__ bool phase_comb(const Args& a, uint32_t l, uint32_t tick, uint32_t pos,
                                            uint32_t wg, uint32_t G, const Lds& s) {
-  const Dims& d = a.d;
+  const Dims d = shape_dims(a.d);
   if (comb_inline(d, pos)) return true;
   const uint32_t nch = attn_nchunks(pos), hs = d.hd + 2;
   const uint32_t gen_in = gen_of(d, tick, l, PH_ATTN), gen_out = gen_of(d, tick, l, PH_COMB);
@@ -1070,7 +1071,7 @@ __device__ __forceinline__ bool phase_comb(const Args& a, uint32_t l, uint32_t t
 __device__ __forceinline__ bool phase_o(const Args& a, uint32_t l, uint32_t tick, uint32_t pos,
                                         uint32_t token, uint32_t wg, uint32_t G, const Lds& s,
                                         const Stager& sg) {
-  const Dims& d = a.d;
+  const Dims d = shape_dims(a.d);
   const uint32_t nch = attn_nchunks(pos), hs = d.hd + 2;
   const bool inl = comb_inline(d, pos);
   const uint32_t R = rows_owned(d.h, wg, G);
@@ -1118,7 +1119,7 @@ __device__ __forceinline__ bool phase_o(const Args& a, uint32_t l, uint32_t tick
 // rmsnorm -> g = act(Wg.x) * (Wu.x) (model.rs:502-509).
 __device__ __forceinline__ bool phase_gu(const Args& a, uint32_t l, uint32_t tick, uint32_t wg,
                                          uint32_t G, const Lds& s, const Stager& sg) {
-  const Dims& d = a.d;
+  const Dims d = shape_dims(a.d);
   const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
   Preload P;
   LoadOp op = no_load();
@@ -1146,7 +1147,7 @@ __device__ __forceinline__ bool phase_gu(const Args& a, uint32_t l, uint32_t tic
 // x_d = x_o + Wd . g (model.rs:510-511).
 __device__ __forceinline__ bool phase_d(const Args& a, uint32_t l, uint32_t tick, uint32_t wg,
                                         uint32_t G, const Lds& s, const Stager& sg) {
-  const Dims& d = a.d;
+  const Dims d = shape_dims(a.d);
   const uint32_t R = rows_owned(d.h, wg, G);
   const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
   const Gather gr = R > 0 ? gather_strided(a.mb_xo + wg, 1, R, G, gen_of(d, tick, l, PH_O), s.scr)
@@ -1186,8 +1187,9 @@ constexpr int LMF = 4;  // float4 per lane per lm_head row held in registers (h 
 // The final RMSNorm weight, kept in LDS for the kernel's lifetime (the
 // lm_head may be the tied embedding, so it cannot be folded into the rows).
 __device__ __forceinline__ void lm_prime(const Args& a, const Lds& s) {
-  for (uint32_t i = threadIdx.x; i < a.d.h && threadIdx.x < NPOLL * WAVE; i += NPOLL * WAVE)
-    lds_st(s.vec2 + a.d.h + i, ldg(a.norm + i));
+  const uint32_t h = shape_dims(a.d).h;
+  for (uint32_t i = threadIdx.x; i < h && threadIdx.x < NPOLL * WAVE; i += NPOLL * WAVE)
+    lds_st(s.vec2 + h + i, ldg(a.norm + i));
   __syncthreads();
 }
 
@@ -1197,7 +1199,7 @@ __device__ __forceinline__ void lm_prime(const Args& a, const Lds& s) {
 // rows in flight. logit = inv * (H . (x * w_norm)).
 __device__ __forceinline__ bool phase_lm(const Args& a, uint32_t tick, uint32_t wg, uint32_t G,
                                          const Lds& s, const Stager& sg) {
-  const Dims& d = a.d;
+  const Dims d = shape_dims(a.d);
   const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
   const uint32_t nown = wg < d.nvc ? (d.nvc - wg + G - 1) / G : 0;
   const uint32_t nrows = nown * VCHUNK;  // local rows r -> chunk r / VCHUNK
@@ -1323,7 +1325,7 @@ __device__ __forceinline__ float exp_term(float logit, float T, float m) {
 // then exp-sums of this workgroup's chunks, published for stage B.
 __device__ __forceinline__ bool sample_stage_a(const Args& a, uint32_t tick, float T, uint32_t wg, uint32_t G,
                                const Lds& s) {
-  const Dims& d = a.d;
+  const Dims d = shape_dims(a.d);
   const uint32_t nvc = d.nvc;
   const uint32_t gl = gen_lm(d, tick - 1u), gsum = gen_sums(d, tick);
   float* vmx = s.scr;
@@ -1381,7 +1383,7 @@ __device__ __forceinline__ float wave_scan(float x) {
 // A degenerate total (not > 0, or not finite) falls back to argmax.
 __device__ __forceinline__ bool sample_stage_b(const Args& a, uint32_t tick, float T, uint32_t word,
                                const Lds& s, uint32_t* tok_out) {
-  const Dims& d = a.d;
+  const Dims d = shape_dims(a.d);
   const uint32_t nvc = d.nvc;
   const uint32_t gl = gen_lm(d, tick - 1u), gsum = gen_sums(d, tick);
   float* vmx = s.scr;
@@ -1483,4 +1485,4 @@ __device__ __forceinline__ bool sample_stage_b(const Args& a, uint32_t tick, flo
   return true;
 }
 
-}  // namespace dg
+}  // namespace DG_NS
