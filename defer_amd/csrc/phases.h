@@ -2,7 +2,7 @@
 // workgroup-level device functions. Each takes (wg, G): the calling
 // workgroup and how many workgroups share the phase. The persistent kernel
 // runs them back to back; the per-phase kernels run one each. Work items are
-// dealt round-robin (item = wg + G*k), and an item is always computed the
+// dealt in contiguous blocks (item_of), and an item is always computed the
 // same way whoever computes it.
 //
 // Roles inside a workgroup (BLOCK = 512 threads = 8 waves):
@@ -192,9 +192,17 @@ __device__ __forceinline__ bool poll_gather(const Gather& g0, uint32_t npw, DevS
   return poll_gather<P0, 0, 0, H>(g0, no_gather(), no_gather(), npw, st, ctl, hook);
 }
 
-// Number of items i = wg + G*k below n owned by this workgroup.
+// Number of the n items of a phase dealt to workgroup wg: n / G, plus one for
+// the first n % G workgroups.
 __device__ __forceinline__ uint32_t rows_owned(uint32_t n, uint32_t wg, uint32_t G) {
   return wg < n ? (n - wg + G - 1) / G : 0;
+}
+// Item k (k < rows_owned) of workgroup wg. Each workgroup's items are
+// contiguous, so its results fill whole mailbox lines and a reader's line
+// holds the words of one or two writers, not of eight.
+__device__ __forceinline__ uint32_t item_of(uint32_t n, uint32_t wg, uint32_t G, uint32_t k) {
+  const uint32_t q = n / G, r = n - q * G;
+  return wg * q + min(wg, r) + k;
 }
 
 // ------------------------------------------------------------ publishing
@@ -239,8 +247,8 @@ enum ItemKind : uint32_t { IK_QKV = 0, IK_O = 1, IK_GU = 2, IK_D = 3 };
 
 // Items of each kind: QKV pairs (rows i, i + hd/2 of one head, so RoPE needs
 // no exchange), O rows, GU pairs (gate row j, up row j), D rows. Item k of a
-// kind owned by workgroup wg is number wg + G*k; compute wave k % NCW
-// computes it and loader k % NLOAD stages it.
+// kind owned by workgroup wg is number item_of(n, wg, G, k); compute wave
+// k % NCW computes it and loader k % NLOAD stages it.
 __device__ __forceinline__ uint32_t kind_items(const Dims& d, uint32_t kind) {
   return kind == IK_QKV ? d.qkv_rows / 2 : (kind == IK_GU ? d.ff : d.h);
 }
@@ -277,7 +285,7 @@ __device__ __forceinline__ ItemRows item_rows(const Args& a, uint32_t kind, uint
                                               uint32_t wg, uint32_t G) {
   const Dims d = shape_dims(a.d);
   const LayerW W = layer_w(a, l);
-  const uint32_t it = wg + G * k;
+  const uint32_t it = item_of(kind_items(d, kind), wg, G, k);
   ItemRows r;
   if (kind == IK_QKV) {
     const uint32_t hb = it / d.half, i = it - hb * d.half;
@@ -723,7 +731,7 @@ __device__ __forceinline__ void items_dot(const Args& a, uint32_t kind, uint32_t
 __device__ __forceinline__ float4 qkv_epi_load(const Args& a, uint32_t l, uint32_t pos, uint32_t k,
                                                uint32_t wg, uint32_t G) {
   const Dims d = shape_dims(a.d);
-  const uint32_t p = wg + G * k;
+  const uint32_t p = item_of(d.qkv_rows / 2, wg, G, k);
   const uint32_t hb = p / d.half, i = p - hb * d.half;
   const uint32_t r0 = hb * d.hd + i;
   float4 e = make_float4(1.0f, 0.0f, 0.0f, 0.0f);
@@ -794,7 +802,7 @@ __device__ __forceinline__ bool phase_qkv(const Args& a, uint32_t l, uint32_t ti
         e = pre[1];
       else
         e = qkv_epi_load(a, l, pos, k, wg, G);
-      const uint32_t p = wg + G * k;
+      const uint32_t p = item_of(d.qkv_rows / 2, wg, G, k);
       const uint32_t hb = p / d.half, i = p - hb * d.half;
       const uint32_t r0 = hb * d.hd + i, r1 = r0 + d.half;
       y0 = y0 * inv + e.z;
@@ -1083,12 +1091,12 @@ __device__ __forceinline__ bool phase_o(const Args& a, uint32_t l, uint32_t tick
                            part)
           : gather_vec(a.mb_att, d.q, gen_of(d, tick, l, PH_COMB), s.vec);
   const Gather gr = (l > 0 && R > 0)
-                        ? gather_strided(a.mb_xd + wg, 1, R, G, gen_of(d, tick, l - 1, PH_D), xres)
+                        ? gather_vec(a.mb_xd + item_of(d.h, wg, G, 0), R, gen_of(d, tick, l - 1, PH_D), xres)
                         : no_gather();
   // Layer 0's residual is the embedding row: its words are loaded before the
   // wait (pollers, one word per thread).
   float emb = 0.0f;
-  if (l == 0 && threadIdx.x < R) emb = ldg(a.embed + (size_t)token * d.h + wg + G * threadIdx.x);
+  if (l == 0 && threadIdx.x < R) emb = ldg(a.embed + (size_t)token * d.h + item_of(d.h, wg, G, threadIdx.x));
   Preload P;
   LoadOp op = no_load();
   if (sg.on) {
@@ -1107,7 +1115,7 @@ __device__ __forceinline__ bool phase_o(const Args& a, uint32_t l, uint32_t tick
   if (wave >= NPOLL && wave < NWA) {
     const uint32_t gen = gen_of(d, tick, l, PH_O);
     items_dot(a, IK_O, wave - NPOLL, l, sg, P, s.vec, wg, G, lane, [&](uint32_t k, float y, float) {
-      if (lane == 0) pub_word(s, k, a.mb_xo + wg + G * k, lds_ld(xres + k) + y, gen);
+      if (lane == 0) pub_word(s, k, a.mb_xo + item_of(d.h, wg, G, k), lds_ld(xres + k) + y, gen);
     });
   }
   pub_flush(s, R);
@@ -1137,7 +1145,7 @@ __device__ __forceinline__ bool phase_gu(const Args& a, uint32_t l, uint32_t tic
     items_dot(a, IK_GU, wave - NPOLL, l, sg, P, s.vec, wg, G, lane,
               [&](uint32_t k, float gate, float up) {
                 if (lane == 0)
-                  pub_word(s, k, a.mb_g + wg + G * k, act_fn(gate * inv, d.act) * (up * inv), gen);
+                  pub_word(s, k, a.mb_g + item_of(d.ff, wg, G, k), act_fn(gate * inv, d.act) * (up * inv), gen);
               });
   }
   pub_flush(s, rows_owned(d.ff, wg, G));
@@ -1150,7 +1158,7 @@ __device__ __forceinline__ bool phase_d(const Args& a, uint32_t l, uint32_t tick
   const Dims d = shape_dims(a.d);
   const uint32_t R = rows_owned(d.h, wg, G);
   const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
-  const Gather gr = R > 0 ? gather_strided(a.mb_xo + wg, 1, R, G, gen_of(d, tick, l, PH_O), s.scr)
+  const Gather gr = R > 0 ? gather_vec(a.mb_xo + item_of(d.h, wg, G, 0), R, gen_of(d, tick, l, PH_O), s.scr)
                           : no_gather();
   Preload P;
   LoadOp op = no_load();
@@ -1165,7 +1173,7 @@ __device__ __forceinline__ bool phase_d(const Args& a, uint32_t l, uint32_t tick
   if (wave >= NPOLL && wave < NWA) {
     const uint32_t gen = gen_of(d, tick, l, PH_D);
     items_dot(a, IK_D, wave - NPOLL, l, sg, P, s.vec, wg, G, lane, [&](uint32_t k, float y, float) {
-      if (lane == 0) pub_word(s, k, a.mb_xd + wg + G * k, lds_ld(s.scr + k) + y, gen);
+      if (lane == 0) pub_word(s, k, a.mb_xd + item_of(d.h, wg, G, k), lds_ld(s.scr + k) + y, gen);
     });
   }
   pub_flush(s, R);
