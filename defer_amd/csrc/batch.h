@@ -1,0 +1,366 @@
+// batch.h -- the batched forward: B rows, each a (cache, position, token),
+// step through the model together and every matrix product is an MFMA GEMM.
+//
+// Batch invariance. Every output element of every matrix product is computed
+// in the one order the one-token path uses (device.h, "Row dot products"):
+// 64 lane-strided segments s, segment s holding the elements
+// 256*i + 4*s + c (i ascending, c = 0..3), each segment a chain of fused
+// multiply-adds from +0, then the complete binary tree over the 64 segment
+// sums. v_mfma_f32_16x16x4_f32 computes, for each output, exactly
+// fma(a3,b3,fma(a2,b2,fma(a1,b1,fma(a0,b0,c)))) -- four links of such a
+// chain -- so chaining MFMAs over a segment's chunks reproduces its sum bit
+// for bit, and the tree is then formed from the 64 segment accumulators. The
+// result of a row depends on that row's inputs only: not on B, not on the
+// other rows, not on the tiling. Everything else a row goes through
+// (RMSNorm, RoPE, attention, combine, residuals, activation, sampling) runs
+// the same expressions as the one-token path, or the very same functions.
+#pragma once
+
+#include "phases.h"
+
+namespace dg {
+
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------ panel layout
+//
+// GEMM operands are stored as panels: a matrix of R rows and K columns
+// becomes [ceil(R/16)][nch = ceil(K/256)][4 slices][64 lanes][16 floats],
+// lane l = r + 16c of slice w of chunk i holding element
+// (16*T + r, 256*i + 64*w + 4*s + c) for s = 0..15, zero outside the
+// matrix. That is the MFMA operand (A for weights, B for activations) of
+// segment 16w + s: one wave reads its slice of a chunk as 4 KB contiguous.
+
+constexpr uint32_t PANEL_TILE = 4096;  // floats per (16-row tile, chunk)
+
+__host__ __device__ inline uint32_t panel_chunks(uint32_t K) { return (K + 255) / 256; }
+__host__ __device__ inline size_t panel_floats(uint32_t R, uint32_t K) {
+  return (size_t)((R + 15) / 16) * panel_chunks(K) * PANEL_TILE;
+}
+
+// Rows [0, R0) from src0, rows [R0, R) from src1 (row r - R0): a stacked
+// matrix without a stacked copy. ld: row stride of both sources.
+__global__ void k_to_panel(const float* __restrict__ src0, const float* __restrict__ src1,
+                           uint32_t R0, uint32_t R, uint32_t K, uint32_t ld,
+                           float* __restrict__ dst) {
+  const size_t n = panel_floats(R, K);
+  const uint32_t nch = panel_chunks(K);
+  for (size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x; e < n;
+       e += (size_t)gridDim.x * blockDim.x) {
+    const uint32_t s = (uint32_t)(e % 16), l = (uint32_t)((e / 16) % 64),
+                   w = (uint32_t)((e / 1024) % 4);
+    const size_t rest = e / PANEL_TILE;
+    const uint32_t i = (uint32_t)(rest % nch);
+    const size_t r = (rest / nch) * 16 + l % 16;
+    const uint32_t k = 256 * i + 64 * w + 4 * s + l / 16;
+    float v = 0.0f;
+    if (r < R && k < K) v = r < R0 ? src0[r * ld + k] : src1[(r - R0) * ld + k];
+    dst[e] = v;
+  }
+}
+
+// ------------------------------------------------------------------ GEMM
+
+enum GemmOut : uint32_t {
+  GO_PLAIN = 0,  // Y[b][o] = y
+  GO_RESID = 1,  // Y[b][o] = Y[b][o] + y   (the residual stream, in place)
+  GO_TAG = 2,    // T[b][o] = tag(gen[b], scale[b] * y)  (tagged logits)
+};
+
+// Complete binary tree over 16 values in index order.
+__device__ __forceinline__ f4v tree16(const f4v* a) {
+  f4v p[8], q[4];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) p[k] = a[2 * k] + a[2 * k + 1];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) q[k] = p[2 * k] + p[2 * k + 1];
+  return (q[0] + q[1]) + (q[2] + q[3]);
+}
+
+// Y[b][o] = W[o] . X[b] for o < M, b < B, K columns. Workgroup (T, g): rows
+// 16T.., column tiles g*TN..; wave w chains segments 16w..16w+15 of every
+// output of the block (its slice of each chunk), reduces them with tree16
+// (the first four levels of the 64-leaf tree), and the four waves' sums
+// are added as (w0 + w1) + (w2 + w3) -- the remaining two levels.
+template <int TN, uint32_t OUT>
+__global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ Wp, uint32_t M, uint32_t K,
+                                              const float* __restrict__ Xp, uint32_t B,
+                                              float* __restrict__ Y, uint32_t ldy,
+                                              const float* __restrict__ scale,
+                                              const uint32_t* __restrict__ gen) {
+  __shared__ f4v red[4][TN][64];
+  const uint32_t wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+  const uint32_t T = blockIdx.x, C0 = blockIdx.y * TN;
+  const uint32_t nch = panel_chunks(K), nct = (B + 15) / 16;
+  f4v acc[TN][16];
+#pragma unroll
+  for (int t = 0; t < TN; ++t)
+#pragma unroll
+    for (int s = 0; s < 16; ++s) acc[t][s] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+  const float* wp = Wp + ((size_t)T * nch * 4 + wave) * 1024 + lane * 16;
+  const float* xp[TN];
+#pragma unroll
+  for (int t = 0; t < TN; ++t) {
+    const uint32_t ct = min(C0 + t, nct - 1);  // past the last tile: read a real one, never used
+    xp[t] = Xp + ((size_t)ct * nch * 4 + wave) * 1024 + lane * 16;
+  }
+  for (uint32_t i = 0; i < nch; ++i) {
+    const uint32_t kb = 256 * i + 64 * wave;
+    if (kb >= K) break;
+    float4 a[4], b[TN][4];
+    const float4* wa = reinterpret_cast<const float4*>(wp + (size_t)i * PANEL_TILE);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) a[q] = wa[q];
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+      const float4* xb = reinterpret_cast<const float4*>(xp[t] + (size_t)i * PANEL_TILE);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) b[t][q] = xb[q];
+    }
+    const uint32_t ns = min(16u, (K - kb + 3) / 4);  // segments with an element in this slice
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      if ((uint32_t)s < ns) {
+        const float av = (&a[s / 4].x)[s % 4];
+#pragma unroll
+        for (int t = 0; t < TN; ++t)
+          acc[t][s] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, (&b[t][s / 4].x)[s % 4], acc[t][s],
+                                                           0, 0, 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < TN; ++t) red[wave][t][lane] = tree16(acc[t]);
+  __syncthreads();
+  for (uint32_t idx = threadIdx.x; idx < TN * 64u; idx += 256) {
+    const uint32_t t = idx / 64, l = idx % 64;
+    const f4v r = (red[0][t][l] + red[1][t][l]) + (red[2][t][l] + red[3][t][l]);
+    const uint32_t b = (C0 + t) * 16 + l % 16;
+    const uint32_t o = T * 16 + 4 * (l / 16);
+    if (b >= B) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (o + j >= M) continue;
+      const size_t at = (size_t)b * ldy + o + j;
+      if (OUT == GO_PLAIN) {
+        Y[at] = r[j];
+      } else if (OUT == GO_RESID) {
+        Y[at] = Y[at] + r[j];
+      } else {
+        const float v = scale[b] * r[j];
+        reinterpret_cast<u64*>(Y)[at] = ((u64)gen[b] << 32) | (u64)__float_as_uint(v);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------- rows
+
+// One row of a batch: the cache it extends, at which position and
+// generation base, with which token.
+struct BRow {
+  float* kc;
+  float* vc;
+  uint32_t cap, pos, tick, token;
+};
+
+// X[b] = E[token_b] (model.rs:428).
+__global__ void k_b_embed(const BRow* __restrict__ rows, const float* __restrict__ embed, uint32_t h,
+                          float* __restrict__ X) {
+  const uint32_t b = blockIdx.x;
+  const float* e = embed + (size_t)rows[b].token * h;
+  for (uint32_t i = threadIdx.x; i < h; i += blockDim.x) X[(size_t)b * h + i] = e[i];
+}
+
+// inv[b] = 1/rms(X[b]) in the order of rms_inv: each lane's elements
+// 4*lane + 256*k ascending, then wave_sum. One wave per row.
+__global__ __launch_bounds__(256) void k_b_rms(const float* __restrict__ X, uint32_t B, uint32_t n,
+                                               float eps, float* __restrict__ inv) {
+  const uint32_t b = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+  if (b >= B) return;
+  const float* x = X + (size_t)b * n;
+  float ss = 0.0f;
+  for (uint32_t j = lane * 4; j < n; j += 256) {
+    const float4 v = *reinterpret_cast<const float4*>(x + j);
+    ss = fmaf(v.x, v.x, ss);
+    ss = fmaf(v.y, v.y, ss);
+    ss = fmaf(v.z, v.z, ss);
+    ss = fmaf(v.w, v.w, ss);
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) inv[b] = 1.0f / sqrtf(ss / (float)n + eps);
+}
+
+// QKV epilogue of the one-token path (phase_qkv), per (row, pair): scale,
+// bias, RoPE; q/k/v words tagged for the attention item; k, v into the
+// row's cache at its position.
+__global__ void k_b_qkv_epi(const Args* __restrict__ ap, const BRow* __restrict__ rows, uint32_t l,
+                            const float* __restrict__ Y, uint32_t ldy, const float* __restrict__ inv,
+                            u64* __restrict__ qkvt, uint32_t ldq) {
+  const Dims& d = ap->d;
+  const uint32_t b = blockIdx.y;
+  const uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= d.qkv_rows / 2) return;
+  const BRow r = rows[b];
+  const uint32_t hb = p / d.half, i = p - hb * d.half;
+  const uint32_t r0 = hb * d.hd + i, r1 = r0 + d.half;
+  float4 e = make_float4(1.0f, 0.0f, 0.0f, 0.0f);
+  if (hb < d.nh + d.nkv) {
+    const float2 cs = ap->rope[(size_t)r.pos * d.half + i];
+    e.x = cs.x;
+    e.y = cs.y;
+  }
+  const float* bias = ap->layers[l].bqkv;
+  if (bias) {
+    e.z = bias[r0];
+    e.w = bias[r0 + d.half];
+  }
+  const float iv = inv[b];
+  float y0 = Y[(size_t)b * ldy + r0], y1 = Y[(size_t)b * ldy + r1];
+  y0 = y0 * iv + e.z;
+  y1 = y1 * iv + e.w;
+  float a0 = y0, a1 = y1;
+  if (hb < d.nh + d.nkv) {
+    a0 = y0 * e.x - y1 * e.y;
+    a1 = y1 * e.x + y0 * e.y;
+  }
+  const u64 g = (u64)gen_of(d, r.tick, l, PH_QKV) << 32;
+  qkvt[(size_t)b * ldq + r0] = g | __float_as_uint(a0);
+  qkvt[(size_t)b * ldq + r1] = g | __float_as_uint(a1);
+  if (hb >= d.nh) {
+    const bool is_k = hb < d.nh + d.nkv;
+    const uint32_t gi = is_k ? hb - d.nh : hb - d.nh - d.nkv;
+    float* row = (is_k ? r.kc : r.vc) + (((size_t)l * d.nkv + gi) * r.cap + r.pos) * d.kvs;
+    row[i] = a0;
+    row[i + d.half] = a1;
+  }
+}
+
+// LDS of the batched kernels that run one-token functions: no weight
+// staging (lds_stg = 0 in the row Args).
+__device__ __forceinline__ Lds lds_init_rows(const Dims& d) {
+  extern __shared__ float lds_raw[];
+  Lds s = lds_layout(lds_raw, d);
+  if (threadIdx.x == 0) s.ctl->abort_seen = 0;
+  __syncthreads();
+  return s;
+}
+
+// Attention items of every row: workgroup (x, b) runs item x of row b with
+// the one-token path's phase_attn (reading the row's tagged q/k/v, writing
+// its tagged partials).
+__global__ __launch_bounds__(BLOCK) void k_b_attn(const Args* __restrict__ rargs,
+                                                  const BRow* __restrict__ rows, uint32_t l) {
+  const Args& a = rargs[blockIdx.y];
+  const Lds s = lds_init_rows(a.d);
+  const BRow r = rows[blockIdx.y];
+  phase_attn(a, l, r.tick, r.pos, blockIdx.x, gridDim.x, s);
+}
+
+// Combine of the chunk partials (combine_one, as the O phase does), per
+// (head, row), into plain att[b][q].
+__global__ __launch_bounds__(BLOCK) void k_b_comb(const Args* __restrict__ rargs,
+                                                  const BRow* __restrict__ rows, uint32_t l,
+                                                  float* __restrict__ att, uint32_t lda) {
+  const Args& a = rargs[blockIdx.y];
+  const Lds s = lds_init_rows(a.d);
+  const BRow r = rows[blockIdx.y];
+  const Dims& d = a.d;
+  const uint32_t hh = blockIdx.x, nch = attn_nchunks(r.pos), hs = d.hd + 2;
+  if (!poll_gather<4>(gather_vec(a.mb_part + (size_t)hh * MAX_ACHUNKS * hs, nch * hs,
+                                 gen_of(d, r.tick, l, PH_ATTN), s.scr),
+                      NPOLL, a.st, s.ctl))
+    return;
+  for (uint32_t dd = threadIdx.x; dd < d.hd; dd += BLOCK)
+    att[(size_t)blockIdx.y * lda + hh * d.hd + dd] = combine_one(s.scr, nch, hs, dd);
+}
+
+// g = act(gate * inv) * (up * inv) (phase_gu); Y holds gate rows then up rows.
+__global__ void k_b_act(const float* __restrict__ Y, uint32_t ldy, const float* __restrict__ inv,
+                        uint32_t ff, uint32_t act, float* __restrict__ G, uint32_t ldg_) {
+  const uint32_t b = blockIdx.y;
+  const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= ff) return;
+  const float iv = inv[b];
+  const float gate = Y[(size_t)b * ldy + j], up = Y[(size_t)b * ldy + ff + j];
+  G[(size_t)b * ldg_ + j] = act_fn(gate * iv, act) * (up * iv);
+}
+
+// Final norm of the rows that need logits (phase_lm): xs = x * w_norm and
+// inv = 1/rms(x) in rms_inv's order. One wave per logits row; sel[i] is its
+// batch row.
+__global__ __launch_bounds__(64) void k_b_final(const float* __restrict__ X,
+                                                const uint32_t* __restrict__ sel, uint32_t h,
+                                                const float* __restrict__ nrm, float eps,
+                                                float* __restrict__ XS, float* __restrict__ linv) {
+  const uint32_t i = blockIdx.x, lane = threadIdx.x;
+  const float* x = X + (size_t)sel[i] * h;
+  float* xs = XS + (size_t)i * h;
+  float ss = 0.0f;
+  for (uint32_t j = lane * 4; j < h; j += 256) {
+    const float4 v = *reinterpret_cast<const float4*>(x + j);
+    ss = fmaf(v.x, v.x, ss);
+    ss = fmaf(v.y, v.y, ss);
+    ss = fmaf(v.z, v.z, ss);
+    ss = fmaf(v.w, v.w, ss);
+    xs[j] = v.x * nrm[j];
+    xs[j + 1] = v.y * nrm[j + 1];
+    xs[j + 2] = v.z * nrm[j + 2];
+    xs[j + 3] = v.w * nrm[j + 3];
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) linv[i] = 1.0f / sqrtf(ss / (float)h + eps);
+}
+
+// Chunk (max, argmax) of the tagged logits of each logits row, tagged for
+// the sampler (phase_lm's chunk step; argmax is a total order, so any tree
+// gives its answer). One wave per (chunk, row).
+__global__ __launch_bounds__(256) void k_b_chunkmax(const Dims d, const u64* __restrict__ logt,
+                                                    const uint32_t* __restrict__ gen,
+                                                    u64* __restrict__ vmax, u64* __restrict__ varg,
+                                                    uint32_t nlm) {
+  const uint32_t c = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+  const uint32_t i = blockIdx.y;
+  if (c >= d.nvc || i >= nlm) return;
+  const uint32_t v = c * VCHUNK + lane;
+  float bv = -INFINITY;
+  uint32_t bi = NO_INDEX;
+  if (v < d.V) {
+    const float y = __uint_as_float((uint32_t)logt[(size_t)i * d.V + v]);
+    if (!isnan(y)) {
+      bv = y;
+      bi = v;
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    const float v2 = __shfl_xor(bv, o);
+    const uint32_t i2 = __shfl_xor(bi, o);
+    if (better(v2, i2, bv, bi)) {
+      bv = v2;
+      bi = i2;
+    }
+  }
+  if (lane == 0) {
+    const u64 g = (u64)gen[i] << 32;
+    vmax[(size_t)i * d.nvc + c] = g | __float_as_uint(bv);
+    varg[(size_t)i * d.nvc + c] = g | bi;
+  }
+}
+
+// One sampling op per workgroup (the one-token sampler, stages A and B on
+// one workgroup): op j samples logits row lrow[j] for generation base
+// tick[j] with rng word words[j]; the token goes to out[j].
+__global__ __launch_bounds__(BLOCK) void k_b_sample(const Args* __restrict__ largs,
+                                                    const uint32_t* __restrict__ tick,
+                                                    const uint32_t* __restrict__ words, float T,
+                                                    uint32_t* __restrict__ out) {
+  const uint32_t j = blockIdx.x;
+  const Args& a = largs[j];
+  const Lds s = lds_init_rows(a.d);
+  if (T != 0.0f && !sample_stage_a(a, tick[j], T, 0, 1, s)) return;
+  uint32_t tok = 0;
+  if (!sample_stage_b(a, tick[j], T, T != 0.0f ? words[j] : 0u, s, &tok)) return;
+  if (threadIdx.x == 0) out[j] = tok;
+}
+
+}  // namespace dg

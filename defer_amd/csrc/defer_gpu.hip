@@ -57,6 +57,7 @@ extern "C" const char* defer_gpu_last_error(void) { return g_last_error.c_str();
 // ------------------------------------------------------------------ kernels
 
 #include "persistent.h"
+#include "batch.h"
 
 // Per-run reset of the counters (pos / tick / token are kept).
 __global__ void k_begin(DevState* st) {
@@ -186,6 +187,13 @@ struct defer_gpu_model {
   const void* persistent = nullptr;  // the persistent kernel for this shape
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   double last_ms = 0.0;
+  // Batched path (built on first use): weight panels and the workspace.
+  uint32_t batch_min = 16;
+  size_t lds_rows = 0;  // LDS of the batched kernels that run one-token functions
+  float* panels = nullptr;
+  std::vector<const float*> p_qkv, p_o, p_gu, p_d;
+  const float* p_lm = nullptr;
+  struct BatchWs* bw = nullptr;
 };
 
 // A persistent kernel compiled for this exact shape, if there is one.
@@ -345,6 +353,7 @@ extern "C" int defer_gpu_model_create(const defer_gpu_config* cfg, const float* 
   }
   m->lds_bytes = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr + d.lds_stg) * sizeof(float) +
                  (size_t)d.lds_pub * 2 * sizeof(u64);
+  m->lds_rows = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr) * sizeof(float);
 
   // Weight layout: one allocation, each tensor 256-byte aligned; q/k/v rows
   // are stored back to back as one [q + 2kv, h] matrix.
@@ -481,6 +490,14 @@ extern "C" int defer_gpu_model_create(const defer_gpu_config* cfg, const float* 
       return cleanup(fail(DEFER_GPU_E_HIP, "LDS attribute (%zu bytes): %s", m->lds_bytes,
                           hipGetErrorString(e)));
   }
+  const void* row_kernels[] = {(const void*)k_b_attn, (const void*)k_b_comb,
+                               (const void*)k_b_sample};
+  for (const void* kf : row_kernels) {
+    e = hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)m->lds_rows);
+    if (e != hipSuccess)
+      return cleanup(fail(DEFER_GPU_E_HIP, "LDS attribute (%zu bytes): %s", m->lds_rows,
+                          hipGetErrorString(e)));
+  }
   int occ = 0;
   e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, m->persistent, BLOCK, m->lds_bytes);
   if (e != hipSuccess || occ < 1)
@@ -491,9 +508,13 @@ extern "C" int defer_gpu_model_create(const defer_gpu_config* cfg, const float* 
   return DEFER_GPU_OK;
 }
 
+static void batch_ws_free(defer_gpu_model* m);
+
 extern "C" void defer_gpu_model_destroy(defer_gpu_model* m) {
   if (!m) return;
   if (m->stream) (void)hipStreamSynchronize(m->stream);
+  batch_ws_free(m);
+  (void)hipFree(m->panels);
   (void)hipFree(m->wbuf);
   (void)hipFree(m->d_layers);
   (void)hipFree(m->rope);
@@ -861,11 +882,41 @@ extern "C" int defer_gpu_forward(const defer_gpu_model* m, defer_gpu_cache* c, u
   return logits_out ? copy_logits(c, logits_out) : DEFER_GPU_OK;
 }
 
+static bool use_batch(const defer_gpu_model* m, size_t n);
+static int feed_batched(defer_gpu_model* m, defer_gpu_cache* c, const uint32_t* tokens, size_t n);
+static int replay_batched(defer_gpu_model* m, defer_gpu_cache* c, const uint32_t* history,
+                          size_t n, size_t plen, float T, const uint32_t* words,
+                          int64_t* first_div, uint32_t* sampled_at_div);
+
+// Device time of a host-driven sequence of launches on the model's stream.
+template <class F>
+static int timed(const defer_gpu_model* mc, F body) {
+  defer_gpu_model* m = const_cast<defer_gpu_model*>(mc);
+  HIP_TRY(hipEventRecord(m->ev0, m->stream));
+  const int rc = body();
+  if (rc) return rc;
+  HIP_TRY(hipEventRecord(m->ev1, m->stream));
+  HIP_TRY(hipEventSynchronize(m->ev1));
+  float ms = 0.0f;
+  HIP_TRY(hipEventElapsedTime(&ms, m->ev0, m->ev1));
+  m->last_ms = ms;
+  return DEFER_GPU_OK;
+}
+
 extern "C" int defer_gpu_prompt(const defer_gpu_model* m, defer_gpu_cache* c,
                                 const uint32_t* tokens, size_t n_tokens) {
   int rc = check_pair(m, c);
   if (rc) return rc;
   if (n_tokens && !tokens) return fail(DEFER_GPU_E_INVALID, "null tokens");
+  if (use_batch(m, n_tokens)) {
+    for (size_t i = 0; i < n_tokens; ++i)
+      if (tokens[i] >= m->d.V) return fail(DEFER_GPU_E_TOKEN, "token id %u out of range", tokens[i]);
+    if ((size_t)c->pos + n_tokens > c->cap)
+      return fail(DEFER_GPU_E_CONTEXT, "context length %u exceeded", m->cfg.max_seq_len);
+    return timed(m, [&] {
+      return feed_batched(const_cast<defer_gpu_model*>(m), c, tokens, n_tokens);
+    });
+  }
   return feed_tokens(m, c, tokens, n_tokens, false);
 }
 
@@ -982,6 +1033,11 @@ extern "C" int defer_gpu_replay(const defer_gpu_model* m, defer_gpu_cache* c,
     if (history[i] >= m->d.V) return fail(DEFER_GPU_E_TOKEN, "token id %u out of range", history[i]);
   if (n_history > c->cap)
     return fail(DEFER_GPU_E_CONTEXT, "context length %u exceeded", m->cfg.max_seq_len);
+  if (use_batch(m, n_history))
+    return timed(m, [&] {
+      return replay_batched(const_cast<defer_gpu_model*>(m), c, history, n_history, prompt_len,
+                            temperature, rng_words, first_div, sampled_at_div);
+    });
   rc = ensure_run_buffers(c, n_history, 0);
   if (rc) return rc;
   if (n_history)
@@ -1005,6 +1061,474 @@ extern "C" int defer_gpu_replay(const defer_gpu_model* m, defer_gpu_cache* c,
   if (h.first_div >= 0) {
     if (first_div) *first_div = h.first_div;
     if (sampled_at_div) *sampled_at_div = h.sampled_div;
+  }
+  return DEFER_GPU_OK;
+}
+
+// ------------------------------------------------------------------ batches
+
+// Rows per batched launch sequence; longer runs go in slices (a slice's
+// attention reads the cache the earlier slices wrote).
+static constexpr uint32_t BATCH_MAX_ROWS = 2048;
+
+struct BatchWs {
+  uint32_t rows = 0, lm = 0;  // capacities
+  float *X = nullptr, *Y = nullptr, *G = nullptr, *ATT = nullptr, *INV = nullptr, *XP = nullptr;
+  float *XS = nullptr, *LINV = nullptr;
+  u64 *QKVT = nullptr, *PART = nullptr, *LOGT = nullptr, *VMAX = nullptr, *VARG = nullptr,
+      *VSUM = nullptr;
+  BRow* drows = nullptr;
+  Args* rargs = nullptr;
+  Args* largs = nullptr;
+  uint32_t *sel = nullptr, *lgen = nullptr, *stick = nullptr, *swords = nullptr, *sout = nullptr;
+  DevState* st = nullptr;
+};
+
+static void batch_ws_release(BatchWs* w) {
+  if (!w) return;
+  void* ps[] = {w->X, w->Y, w->G, w->ATT, w->INV, w->XP, w->XS, w->LINV, w->QKVT, w->PART,
+                w->LOGT, w->VMAX, w->VARG, w->VSUM, w->drows, w->rargs, w->largs, w->sel,
+                w->lgen, w->stick, w->swords, w->sout, w->st};
+  for (void* p : ps) (void)hipFree(p);
+  *w = BatchWs();
+}
+
+static void batch_ws_free(defer_gpu_model* m) {
+  if (!m->bw) return;
+  batch_ws_release(m->bw);
+  delete m->bw;
+  m->bw = nullptr;
+}
+
+static uint32_t batch_ldy(const Dims& d) { return std::max({d.qkv_rows, 2 * d.ff, d.h}); }
+static uint32_t part_words(const Dims& d) { return d.nh * MAX_ACHUNKS * (d.hd + 2); }
+
+static int ensure_ws(defer_gpu_model* m, uint32_t rows, uint32_t lm) {
+  if (!m->bw) m->bw = new BatchWs();
+  BatchWs& w = *m->bw;
+  if (rows <= w.rows && lm <= w.lm && w.st) return DEFER_GPU_OK;
+  const Dims& d = m->d;
+  const uint32_t R = std::max(rows, w.rows), Lm = std::max(lm, w.lm);
+  batch_ws_release(&w);
+  const uint32_t kmax = std::max({d.h, d.q, d.ff});
+  HIP_TRY(hipMalloc(&w.X, (size_t)R * d.h * sizeof(float)));
+  HIP_TRY(hipMalloc(&w.Y, (size_t)R * batch_ldy(d) * sizeof(float)));
+  HIP_TRY(hipMalloc(&w.G, (size_t)R * d.ff * sizeof(float)));
+  HIP_TRY(hipMalloc(&w.ATT, (size_t)R * d.q * sizeof(float)));
+  HIP_TRY(hipMalloc(&w.INV, (size_t)R * sizeof(float)));
+  HIP_TRY(hipMalloc(&w.XP, panel_floats(R, kmax) * sizeof(float)));
+  HIP_TRY(hipMalloc(&w.QKVT, (size_t)R * d.qkv_rows * sizeof(u64)));
+  HIP_TRY(hipMalloc(&w.PART, (size_t)R * part_words(d) * sizeof(u64)));
+  HIP_TRY(hipMalloc(&w.drows, (size_t)R * sizeof(BRow)));
+  HIP_TRY(hipMalloc(&w.rargs, (size_t)R * sizeof(Args)));
+  const uint32_t L1 = std::max(Lm, 1u);
+  HIP_TRY(hipMalloc(&w.XS, (size_t)L1 * d.h * sizeof(float)));
+  HIP_TRY(hipMalloc(&w.LINV, (size_t)L1 * sizeof(float)));
+  HIP_TRY(hipMalloc(&w.LOGT, (size_t)L1 * d.V * sizeof(u64)));
+  HIP_TRY(hipMalloc(&w.VMAX, (size_t)L1 * d.nvc * sizeof(u64)));
+  HIP_TRY(hipMalloc(&w.VARG, (size_t)L1 * d.nvc * sizeof(u64)));
+  HIP_TRY(hipMalloc(&w.VSUM, (size_t)L1 * d.nvc * sizeof(u64)));
+  HIP_TRY(hipMalloc(&w.largs, (size_t)L1 * sizeof(Args)));
+  HIP_TRY(hipMalloc(&w.sel, (size_t)L1 * sizeof(uint32_t)));
+  HIP_TRY(hipMalloc(&w.lgen, (size_t)L1 * sizeof(uint32_t)));
+  HIP_TRY(hipMalloc(&w.stick, (size_t)L1 * sizeof(uint32_t)));
+  HIP_TRY(hipMalloc(&w.swords, (size_t)L1 * sizeof(uint32_t)));
+  HIP_TRY(hipMalloc(&w.sout, (size_t)L1 * sizeof(uint32_t)));
+  HIP_TRY(hipMalloc(&w.st, sizeof(DevState)));
+  HIP_TRY(hipMemset(w.st, 0, sizeof(DevState)));
+  w.rows = R;
+  w.lm = Lm;
+  return DEFER_GPU_OK;
+}
+
+static void launch_panel(hipStream_t s, const float* src0, const float* src1, uint32_t R0,
+                         uint32_t R, uint32_t K, uint32_t ld, float* dst) {
+  const size_t n = panel_floats(R, K);
+  const uint32_t blocks = (uint32_t)std::min<size_t>((n + 255) / 256, 16384);
+  k_to_panel<<<blocks, 256, 0, s>>>(src0, src1, R0, R, K, ld, dst);
+}
+
+// The weight panels of every matrix, built once per model.
+static int ensure_panels(defer_gpu_model* m) {
+  if (m->panels) return DEFER_GPU_OK;
+  const Dims& d = m->d;
+  const size_t pq = panel_floats(d.qkv_rows, d.h), po = panel_floats(d.h, d.q),
+               pg = panel_floats(2 * d.ff, d.h), pd = panel_floats(d.h, d.ff),
+               pl = panel_floats(d.V, d.h);
+  const size_t total = (pq + po + pg + pd) * d.L + pl;
+  HIP_TRY(hipMalloc(&m->panels, total * sizeof(float)));
+  const hipStream_t s = m->stream;
+  float* p = m->panels;
+  m->p_qkv.assign(d.L, nullptr);
+  m->p_o.assign(d.L, nullptr);
+  m->p_gu.assign(d.L, nullptr);
+  m->p_d.assign(d.L, nullptr);
+  for (uint32_t l = 0; l < d.L; ++l) {
+    const LayerW& W = m->layers[l];
+    launch_panel(s, W.wqkv, W.wqkv, d.qkv_rows, d.qkv_rows, d.h, d.h, p);
+    m->p_qkv[l] = p;
+    p += pq;
+    launch_panel(s, W.wo, W.wo, d.h, d.h, d.q, d.q, p);
+    m->p_o[l] = p;
+    p += po;
+    launch_panel(s, W.wg, W.wu, d.ff, 2 * d.ff, d.h, d.h, p);
+    m->p_gu[l] = p;
+    p += pg;
+    launch_panel(s, W.wd, W.wd, d.h, d.h, d.ff, d.ff, p);
+    m->p_d[l] = p;
+    p += pd;
+  }
+  launch_panel(s, m->head, m->head, d.V, d.V, d.h, d.h, p);
+  m->p_lm = p;
+  HIP_TRY(hipGetLastError());
+  HIP_TRY(hipStreamSynchronize(s));
+  return DEFER_GPU_OK;
+}
+
+template <uint32_t OUT>
+static void launch_gemm_out(hipStream_t s, const float* Wp, uint32_t M, uint32_t K, const float* Xp,
+                            uint32_t B, float* Y, uint32_t ldy, const float* scale,
+                            const uint32_t* gen) {
+  const uint32_t nct = (B + 15) / 16;
+  if (nct <= 1) {
+    k_gemm<1, OUT><<<dim3((M + 15) / 16, nct), 256, 0, s>>>(Wp, M, K, Xp, B, Y, ldy, scale, gen);
+  } else if (nct <= 2) {
+    k_gemm<2, OUT><<<dim3((M + 15) / 16, 1), 256, 0, s>>>(Wp, M, K, Xp, B, Y, ldy, scale, gen);
+  } else {
+    k_gemm<4, OUT><<<dim3((M + 15) / 16, (nct + 3) / 4), 256, 0, s>>>(Wp, M, K, Xp, B, Y, ldy,
+                                                                      scale, gen);
+  }
+}
+static void launch_gemm(hipStream_t s, uint32_t out, const float* Wp, uint32_t M, uint32_t K,
+                        const float* Xp, uint32_t B, float* Y, uint32_t ldy,
+                        const float* scale = nullptr, const uint32_t* gen = nullptr) {
+  if (out == GO_PLAIN) launch_gemm_out<GO_PLAIN>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen);
+  else if (out == GO_RESID) launch_gemm_out<GO_RESID>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen);
+  else launch_gemm_out<GO_TAG>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen);
+}
+
+// The one-token kernels' view of a batch row (attention, combine): the
+// row cache's arguments with the batch's tagged buffers and no staging.
+static Args row_args(const defer_gpu_cache* c, const BatchWs& w, uint32_t b) {
+  Args a = c->args;
+  a.d.lds_stg = 0;
+  a.mb_qkv = w.QKVT + (size_t)b * a.d.qkv_rows;
+  a.mb_part = w.PART + (size_t)b * part_words(a.d);
+  a.st = w.st;
+  a.mask = nullptr;
+  return a;
+}
+
+// Runs n rows (n <= BATCH_MAX_ROWS) through every layer; logits rows
+// sel[0..nl) (batch row indices) get tagged logits and chunk maxima in the
+// workspace. Rows must already be validated (tokens, capacity).
+static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* const* rcache,
+                     uint32_t n, const uint32_t* sel, uint32_t nl) {
+  const Dims& d = m->d;
+  const hipStream_t s = m->stream;
+  int rc = ensure_panels(m);
+  if (rc) return rc;
+  rc = ensure_ws(m, n, nl);
+  if (rc) return rc;
+  BatchWs& w = *m->bw;
+  std::vector<Args> ra(n);
+  uint32_t max_items = 1;
+  for (uint32_t b = 0; b < n; ++b) {
+    ra[b] = row_args(rcache[b], w, b);
+    max_items = std::max(max_items, d.nkv * attn_nchunks(rows[b].pos));
+  }
+  std::vector<uint32_t> lgen(nl);
+  for (uint32_t i = 0; i < nl; ++i) lgen[i] = gen_lm(d, rows[sel[i]].tick);
+  HIP_TRY(hipMemcpyAsync(w.drows, rows, n * sizeof(BRow), hipMemcpyHostToDevice, s));
+  HIP_TRY(hipMemcpyAsync(w.rargs, ra.data(), n * sizeof(Args), hipMemcpyHostToDevice, s));
+  if (nl) {
+    HIP_TRY(hipMemcpyAsync(w.sel, sel, nl * sizeof(uint32_t), hipMemcpyHostToDevice, s));
+    HIP_TRY(hipMemcpyAsync(w.lgen, lgen.data(), nl * sizeof(uint32_t), hipMemcpyHostToDevice, s));
+  }
+  k_begin<<<1, 1, 0, s>>>(w.st);
+  const uint32_t ldy = batch_ldy(d);
+  k_b_embed<<<n, 256, 0, s>>>(w.drows, m->embed, d.h, w.X);
+  for (uint32_t l = 0; l < d.L; ++l) {
+    k_b_rms<<<(n + 3) / 4, 256, 0, s>>>(w.X, n, d.h, d.eps, w.INV);
+    launch_panel(s, w.X, w.X, n, n, d.h, d.h, w.XP);
+    launch_gemm(s, GO_PLAIN, m->p_qkv[l], d.qkv_rows, d.h, w.XP, n, w.Y, ldy);
+    k_b_qkv_epi<<<dim3((d.qkv_rows / 2 + 255) / 256, n), 256, 0, s>>>(w.rargs, w.drows, l, w.Y, ldy,
+                                                                      w.INV, w.QKVT, d.qkv_rows);
+    k_b_attn<<<dim3(max_items, n), BLOCK, m->lds_rows, s>>>(w.rargs, w.drows, l);
+    k_b_comb<<<dim3(d.nh, n), BLOCK, m->lds_rows, s>>>(w.rargs, w.drows, l, w.ATT, d.q);
+    launch_panel(s, w.ATT, w.ATT, n, n, d.q, d.q, w.XP);
+    launch_gemm(s, GO_RESID, m->p_o[l], d.h, d.q, w.XP, n, w.X, d.h);
+    k_b_rms<<<(n + 3) / 4, 256, 0, s>>>(w.X, n, d.h, d.eps, w.INV);
+    launch_panel(s, w.X, w.X, n, n, d.h, d.h, w.XP);
+    launch_gemm(s, GO_PLAIN, m->p_gu[l], 2 * d.ff, d.h, w.XP, n, w.Y, ldy);
+    k_b_act<<<dim3((d.ff + 255) / 256, n), 256, 0, s>>>(w.Y, ldy, w.INV, d.ff, d.act, w.G, d.ff);
+    launch_panel(s, w.G, w.G, n, n, d.ff, d.ff, w.XP);
+    launch_gemm(s, GO_RESID, m->p_d[l], d.h, d.ff, w.XP, n, w.X, d.h);
+  }
+  if (nl) {
+    k_b_final<<<nl, 64, 0, s>>>(w.X, w.sel, d.h, m->norm, d.eps, w.XS, w.LINV);
+    launch_panel(s, w.XS, w.XS, nl, nl, d.h, d.h, w.XP);
+    launch_gemm(s, GO_TAG, m->p_lm, d.V, d.h, w.XP, nl, reinterpret_cast<float*>(w.LOGT), d.V,
+                w.LINV, w.lgen);
+    k_b_chunkmax<<<dim3((d.nvc + 3) / 4, nl), 256, 0, s>>>(d, w.LOGT, w.lgen, w.VMAX, w.VARG, nl);
+  }
+  HIP_TRY(hipGetLastError());
+  HIP_TRY(hipStreamSynchronize(s));
+  DevState h;
+  HIP_TRY(hipMemcpy(&h, w.st, sizeof(h), hipMemcpyDeviceToHost));
+  if (h.abort) return fail(DEFER_GPU_E_TIMEOUT, "a device-side wait exceeded its bound");
+  return DEFER_GPU_OK;
+}
+
+// Sampling ops on logits rows of the workspace: op j samples logits row
+// lrow[j] of cache c for generation base tick[j] (the tick of the forward
+// that follows the sample) with word words[j].
+static int batch_sample(defer_gpu_model* m, defer_gpu_cache* const* ocache, const uint32_t* lrow,
+                        const uint32_t* tick, const uint32_t* words, uint32_t nops, float T,
+                        uint32_t* out, bool own_logits) {
+  const Dims& d = m->d;
+  const hipStream_t s = m->stream;
+  // Sampling a batch's logits rows: batch_run sized the workspace for them,
+  // so this does not reallocate (which would drop them).
+  int rc = ensure_ws(m, 1, nops);
+  if (rc) return rc;
+  BatchWs& w = *m->bw;
+  std::vector<Args> la(nops);
+  for (uint32_t j = 0; j < nops; ++j) {
+    Args a = ocache[j]->args;
+    a.d.lds_stg = 0;
+    if (!own_logits) {
+      a.mb_logit = w.LOGT + (size_t)lrow[j] * d.V;
+      a.mb_vmax = w.VMAX + (size_t)lrow[j] * d.nvc;
+      a.mb_varg = w.VARG + (size_t)lrow[j] * d.nvc;
+    }
+    a.mb_vsum = w.VSUM + (size_t)j * d.nvc;
+    a.st = w.st;
+    a.mask = nullptr;
+    la[j] = a;
+  }
+  HIP_TRY(hipMemcpyAsync(w.largs, la.data(), nops * sizeof(Args), hipMemcpyHostToDevice, s));
+  HIP_TRY(hipMemcpyAsync(w.stick, tick, nops * sizeof(uint32_t), hipMemcpyHostToDevice, s));
+  if (T != 0.0f)
+    HIP_TRY(hipMemcpyAsync(w.swords, words, nops * sizeof(uint32_t), hipMemcpyHostToDevice, s));
+  k_begin<<<1, 1, 0, s>>>(w.st);
+  k_b_sample<<<nops, BLOCK, m->lds_rows, s>>>(w.largs, w.stick, w.swords, T, w.sout);
+  HIP_TRY(hipGetLastError());
+  HIP_TRY(hipMemcpyAsync(out, w.sout, nops * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  DevState h;
+  HIP_TRY(hipMemcpy(&h, w.st, sizeof(h), hipMemcpyDeviceToHost));
+  if (h.abort) return fail(DEFER_GPU_E_TIMEOUT, "a device-side wait exceeded its bound");
+  return DEFER_GPU_OK;
+}
+
+// A cache after its batch rows: length, generation base and, from logits
+// row li of the workspace, the tagged logits and chunk maxima a following
+// sample reads.
+static int batch_commit(defer_gpu_model* m, defer_gpu_cache* c, uint32_t li, uint32_t pos,
+                        uint32_t tick) {
+  const Dims& d = m->d;
+  const hipStream_t s = m->stream;
+  const BatchWs& w = *m->bw;
+  HIP_TRY(hipMemcpyAsync(c->args.mb_logit, w.LOGT + (size_t)li * d.V, (size_t)d.V * sizeof(u64),
+                         hipMemcpyDeviceToDevice, s));
+  HIP_TRY(hipMemcpyAsync(c->args.mb_vmax, w.VMAX + (size_t)li * d.nvc, (size_t)d.nvc * sizeof(u64),
+                         hipMemcpyDeviceToDevice, s));
+  HIP_TRY(hipMemcpyAsync(c->args.mb_varg, w.VARG + (size_t)li * d.nvc, (size_t)d.nvc * sizeof(u64),
+                         hipMemcpyDeviceToDevice, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  c->pos = pos;
+  c->tick = tick;
+  c->has_logits = true;
+  return push_state(c);
+}
+
+static BRow make_row(const defer_gpu_cache* c, uint32_t pos, uint32_t tick, uint32_t token) {
+  BRow r;
+  r.kc = c->kc;
+  r.vc = c->vc;
+  r.cap = c->cap;
+  r.pos = pos;
+  r.tick = tick;
+  r.token = token;
+  return r;
+}
+
+static bool use_batch(const defer_gpu_model* m, size_t n) { return m->batch_min && n >= m->batch_min; }
+
+extern "C" int defer_gpu_model_set_batching(defer_gpu_model* m, uint32_t min_rows) {
+  if (!m) return fail(DEFER_GPU_E_INVALID, "null model");
+  m->batch_min = min_rows;
+  return DEFER_GPU_OK;
+}
+
+// Feeds tokens[0..n) to one cache in slices; the last slice's last row
+// keeps its logits. Range checks are done by the caller.
+static int feed_batched(defer_gpu_model* m, defer_gpu_cache* c, const uint32_t* tokens, size_t n) {
+  for (size_t o = 0; o < n; o += BATCH_MAX_ROWS) {
+    const uint32_t k = (uint32_t)std::min<size_t>(BATCH_MAX_ROWS, n - o);
+    std::vector<BRow> rows(k);
+    std::vector<defer_gpu_cache*> rc(k, c);
+    for (uint32_t j = 0; j < k; ++j) rows[j] = make_row(c, c->pos + j, c->tick + j, tokens[o + j]);
+    const bool last = o + k == n;
+    const uint32_t sel = k - 1;
+    int e = batch_run(m, rows.data(), rc.data(), k, &sel, last ? 1 : 0);
+    if (e) return e;
+    if (last) {
+      e = batch_commit(m, c, 0, c->pos + k, c->tick + k);
+      if (e) return e;
+    } else {
+      c->pos += k;
+      c->tick += k;
+      c->has_logits = false;
+      e = push_state(c);
+      if (e) return e;
+    }
+  }
+  return DEFER_GPU_OK;
+}
+
+extern "C" int defer_gpu_forward_batch(const defer_gpu_model* mc, defer_gpu_cache* const* caches,
+                                       const uint32_t* tokens, uint32_t n, float* logits_out) {
+  defer_gpu_model* m = const_cast<defer_gpu_model*>(mc);
+  if (!m) return fail(DEFER_GPU_E_INVALID, "null model");
+  if (n == 0) return DEFER_GPU_OK;
+  if (!caches || !tokens) return fail(DEFER_GPU_E_INVALID, "null argument");
+  if (n > BATCH_MAX_ROWS) return fail(DEFER_GPU_E_INVALID, "at most %u rows per batch", BATCH_MAX_ROWS);
+  const Dims& d = m->d;
+  // positions: a cache listed k times gets k consecutive positions
+  std::vector<uint32_t> add(n, 0);
+  std::vector<int> last_of(n, -1);  // per row: is it its cache's last row
+  for (uint32_t b = 0; b < n; ++b) {
+    int rc = check_pair(m, caches[b]);
+    if (rc) return rc;
+    if (tokens[b] >= d.V) return fail(DEFER_GPU_E_TOKEN, "token id %u out of range", tokens[b]);
+    for (uint32_t e = 0; e < b; ++e)
+      if (caches[e] == caches[b]) ++add[b];
+  }
+  for (uint32_t b = 0; b < n; ++b) {
+    bool later = false;
+    for (uint32_t e = b + 1; e < n && !later; ++e) later = caches[e] == caches[b];
+    last_of[b] = later ? 0 : 1;
+    if (last_of[b] && caches[b]->pos + add[b] + 1 > caches[b]->cap)
+      return fail(DEFER_GPU_E_CONTEXT, "context length %u exceeded", m->cfg.max_seq_len);
+  }
+  std::vector<BRow> rows(n);
+  for (uint32_t b = 0; b < n; ++b)
+    rows[b] = make_row(caches[b], caches[b]->pos + add[b], caches[b]->tick + add[b], tokens[b]);
+  std::vector<uint32_t> sel;
+  std::vector<uint32_t> li_of(n, 0);
+  for (uint32_t b = 0; b < n; ++b)
+    if (logits_out || last_of[b]) {
+      li_of[b] = (uint32_t)sel.size();
+      sel.push_back(b);
+    }
+  HIP_TRY(hipEventRecord(m->ev0, m->stream));
+  int rc = batch_run(m, rows.data(), caches, n, sel.data(), (uint32_t)sel.size());
+  if (rc) return rc;
+  HIP_TRY(hipEventRecord(m->ev1, m->stream));
+  HIP_TRY(hipEventSynchronize(m->ev1));
+  float ms = 0.0f;
+  HIP_TRY(hipEventElapsedTime(&ms, m->ev0, m->ev1));
+  m->last_ms = ms;
+  if (logits_out) {
+    const BatchWs& w = *m->bw;
+    for (uint32_t b = 0; b < n; ++b) {
+      float* dst = caches[b]->d_logits;  // [V] staging of the untagged row
+      k_untag<<<(d.V + 255) / 256, 256, 0, m->stream>>>(w.LOGT + (size_t)li_of[b] * d.V, dst, d.V);
+      HIP_TRY(hipMemcpyAsync(logits_out + (size_t)b * d.V, dst, (size_t)d.V * sizeof(float),
+                             hipMemcpyDeviceToHost, m->stream));
+      HIP_TRY(hipStreamSynchronize(m->stream));
+    }
+  }
+  for (uint32_t b = 0; b < n; ++b)
+    if (last_of[b]) {
+      rc = batch_commit(m, caches[b], li_of[b], rows[b].pos + 1, rows[b].tick + 1);
+      if (rc) return rc;
+    }
+  return DEFER_GPU_OK;
+}
+
+extern "C" int defer_gpu_step_batch(const defer_gpu_model* mc, defer_gpu_cache* const* caches,
+                                    uint32_t n, float temperature, const uint32_t* rng_words,
+                                    uint32_t* tokens_out) {
+  defer_gpu_model* m = const_cast<defer_gpu_model*>(mc);
+  if (!m) return fail(DEFER_GPU_E_INVALID, "null model");
+  int rc = check_temperature(temperature);
+  if (rc) return rc;
+  if (n == 0) return DEFER_GPU_OK;
+  if (!caches || !tokens_out) return fail(DEFER_GPU_E_INVALID, "null argument");
+  if (temperature != 0.0f && !rng_words) return fail(DEFER_GPU_E_INVALID, "null rng words");
+  if (n > BATCH_MAX_ROWS) return fail(DEFER_GPU_E_INVALID, "at most %u rows per batch", BATCH_MAX_ROWS);
+  std::vector<uint32_t> tick(n);
+  for (uint32_t b = 0; b < n; ++b) {
+    rc = check_pair(m, caches[b]);
+    if (rc) return rc;
+    for (uint32_t e = 0; e < b; ++e)
+      if (caches[e] == caches[b]) return fail(DEFER_GPU_E_INVALID, "step_batch needs distinct caches");
+    if (!caches[b]->has_logits)
+      return fail(DEFER_GPU_E_NO_LOGITS, "no context: provide a non-empty prompt");
+    if (caches[b]->pos >= caches[b]->cap)
+      return fail(DEFER_GPU_E_CONTEXT, "context length %u exceeded", m->cfg.max_seq_len);
+    tick[b] = caches[b]->tick;
+  }
+  rc = batch_sample(m, caches, nullptr, tick.data(), rng_words, n, temperature, tokens_out, true);
+  if (rc) return rc;
+  return defer_gpu_forward_batch(m, caches, tokens_out, n, nullptr);
+}
+
+// Checkout's replay through batches: every history token is fed (teacher
+// forcing, as the loop feeds the recorded token after comparing), each
+// sampled position re-sampled from its predecessor's logits and compared.
+// The first mismatch ends the replay with the cache holding the positions
+// before it, as the token-by-token loop leaves it.
+static int replay_batched(defer_gpu_model* m, defer_gpu_cache* c, const uint32_t* history,
+                          size_t n, size_t plen, float T, const uint32_t* words,
+                          int64_t* first_div, uint32_t* sampled_at_div) {
+  const uint32_t tick0 = c->tick;
+  for (size_t o = 0; o < n; o += BATCH_MAX_ROWS) {
+    const uint32_t k = (uint32_t)std::min<size_t>(BATCH_MAX_ROWS, n - o);
+    std::vector<BRow> rows(k);
+    std::vector<defer_gpu_cache*> rc(k, c);
+    for (uint32_t j = 0; j < k; ++j)
+      rows[j] = make_row(c, (uint32_t)(o + j), tick0 + (uint32_t)(o + j), history[o + j]);
+    // rows whose logits are sampled (positions >= plen - 1) or kept (the last)
+    std::vector<uint32_t> sel;
+    for (uint32_t j = 0; j < k; ++j)
+      if (o + j + 1 >= plen) sel.push_back(j);
+    int e = batch_run(m, rows.data(), rc.data(), k, sel.data(), (uint32_t)sel.size());
+    if (e) return e;
+    // op i = row + 1 samples logits row `row` (the ops inside the history)
+    std::vector<uint32_t> lrow, tk, wd, out;
+    std::vector<defer_gpu_cache*> oc;
+    for (uint32_t li = 0; li < sel.size(); ++li) {
+      const size_t i = o + sel[li] + 1;
+      if (i >= n || i < plen) continue;
+      lrow.push_back(li);
+      tk.push_back(tick0 + (uint32_t)i);
+      wd.push_back(T != 0.0f ? words[i - plen] : 0u);
+      oc.push_back(c);
+    }
+    const uint32_t nops = (uint32_t)lrow.size();
+    out.resize(nops);
+    if (nops) {
+      e = batch_sample(m, oc.data(), lrow.data(), tk.data(), wd.data(), nops, T, out.data(), false);
+      if (e) return e;
+    }
+    for (uint32_t j = 0; j < nops; ++j) {
+      const size_t i = o + sel[lrow[j]] + 1;
+      if (out[j] != history[i]) {
+        if (first_div) *first_div = (int64_t)i;
+        if (sampled_at_div) *sampled_at_div = out[j];
+        return batch_commit(m, c, lrow[j], (uint32_t)i, tick0 + (uint32_t)i);
+      }
+    }
+    if (o + k == n) return batch_commit(m, c, (uint32_t)sel.size() - 1, (uint32_t)n, tick0 + (uint32_t)n);
+    c->pos = (uint32_t)(o + k);
+    c->tick = tick0 + (uint32_t)(o + k);
+    c->has_logits = false;
+    e = push_state(c);
+    if (e) return e;
   }
   return DEFER_GPU_OK;
 }

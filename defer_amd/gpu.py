@@ -121,6 +121,12 @@ def lib() -> ctypes.CDLL:
     L.defer_gpu_last_error.restype = ctypes.c_char_p
     L.defer_gpu_last_device_ms.argtypes = [vp]
     L.defer_gpu_last_device_ms.restype = ctypes.c_double
+    L.defer_gpu_model_set_batching.argtypes = [vp, u32]
+    L.defer_gpu_model_set_batching.restype = ctypes.c_int
+    L.defer_gpu_forward_batch.argtypes = [vp, P(vp), vp, u32, vp]
+    L.defer_gpu_forward_batch.restype = ctypes.c_int
+    L.defer_gpu_step_batch.argtypes = [vp, P(vp), u32, f32, vp, vp]
+    L.defer_gpu_step_batch.restype = ctypes.c_int
     _lib = L
     return L
 
@@ -227,6 +233,33 @@ class GpuModel:
 
     def last_device_ms(self) -> float:
         return float(lib().defer_gpu_last_device_ms(self._h))
+
+    def set_batching(self, min_rows: int) -> None:
+        """Prompts and replays of at least min_rows tokens take the batched
+        (MFMA GEMM) path; 0 feeds token by token. Same bits either way."""
+        _check(lib().defer_gpu_model_set_batching(self._h, int(min_rows)))
+
+    def forward_batch(self, caches: Sequence["GpuCache"], tokens: Sequence[int],
+                      logits: bool = False) -> Optional[np.ndarray]:
+        """Feeds tokens[b] to caches[b] as one batch (a cache listed k times
+        gets k consecutive positions); [n, V] logits if asked."""
+        t = _u32(tokens)
+        hs = (ctypes.c_void_p * len(caches))(*[c._h for c in caches])
+        out = np.empty((len(t), self.vocab_size), dtype=np.float32) if logits else None
+        _check(lib().defer_gpu_forward_batch(self._h, hs, _ptr(t), len(t), _ptr(out)))
+        return out
+
+    def step_batch(self, caches: Sequence["GpuCache"], temperature: float,
+                   words: Optional[Sequence[int]] = None) -> list:
+        """Session::step on distinct caches in lockstep."""
+        w = _u32(words) if words is not None else None
+        if temperature != 0.0 and (w is None or len(w) < len(caches)):
+            raise ValueError("need one rng word per cache when temperature > 0")
+        hs = (ctypes.c_void_p * len(caches))(*[c._h for c in caches])
+        out = np.zeros(max(len(caches), 1), dtype=np.uint32)
+        _check(lib().defer_gpu_step_batch(self._h, hs, len(caches), float(temperature), _ptr(w),
+                                          _ptr(out)))
+        return [int(x) for x in out[: len(caches)]]
 
 
 class GpuCache:

@@ -17,6 +17,8 @@
  *   defer_gpu_step           Session::step                     engine.rs:113-117
  *   defer_gpu_generate       Session::generate                 engine.rs:121-137
  *   defer_gpu_replay         Session::checkout replay loop     engine.rs:261-271
+ *   defer_gpu_forward_batch, defer_gpu_step_batch, defer_gpu_model_set_batching:
+ *                            no counterpart (the reference is batch-1 only)
  */
 #ifndef DEFER_GPU_H
 #define DEFER_GPU_H
@@ -127,6 +129,33 @@ int defer_gpu_prompt(const defer_gpu_model* m, defer_gpu_cache* c, const uint32_
 int defer_gpu_replay(const defer_gpu_model* m, defer_gpu_cache* c, const uint32_t* history,
                      size_t n_history, size_t prompt_len, float temperature,
                      const uint32_t* rng_words, int64_t* first_div, uint32_t* sampled_at_div);
+
+/* ---------------------------------------------------------------- batches
+ *
+ * Rows run together (no counterpart in the reference, which steps one
+ * session at a time, engine.rs:90-137). Every matrix product of a batch is an
+ * MFMA GEMM that computes each output in the one-token order, and everything
+ * else a row goes through is the one-token arithmetic, so a row's cache
+ * entries, logits and tokens are bit-identical to feeding it on its own. */
+
+/* defer_gpu_prompt and defer_gpu_replay run the batched path for at least
+ * `min_rows` tokens and feed token by token below that; 0 turns batching
+ * off. Results are identical either way. The default is 16. */
+int defer_gpu_model_set_batching(defer_gpu_model* m, uint32_t min_rows);
+
+/* Feeds tokens[b] to caches[b] for b < n as if in the order b = 0, 1, ...: a
+ * cache listed k times receives k consecutive positions. Each cache keeps the
+ * logits of its last row for a following sample/step. logits_out (nullable)
+ * receives [n, V]: row b's logits. Range and capacity errors are reported
+ * before any cache is touched. */
+int defer_gpu_forward_batch(const defer_gpu_model* m, defer_gpu_cache* const* caches,
+                            const uint32_t* tokens, uint32_t n, float* logits_out);
+
+/* Session::step (engine.rs:113-117) on n distinct caches in lockstep: each
+ * samples its last logits (consuming rng_words[b] when temperature > 0),
+ * then the n sampled tokens are fed as one batch. tokens_out [n]. */
+int defer_gpu_step_batch(const defer_gpu_model* m, defer_gpu_cache* const* caches, uint32_t n,
+                         float temperature, const uint32_t* rng_words, uint32_t* tokens_out);
 
 /* Thread-local description of the last failing call. */
 const char* defer_gpu_last_error(void);
