@@ -246,15 +246,18 @@ __device__ __forceinline__ Lds lds_init_rows(const Dims& d) {
   return s;
 }
 
-// Attention items of every row: workgroup (x, b) runs item x of row b with
-// the one-token path's phase_attn (reading the row's tagged q/k/v, writing
-// its tagged partials).
+// Attention items of every row, one per workgroup: entry x of `items` is
+// (row, item) packed as row << 16 | item, and the workgroup runs that item
+// with the one-token path's phase_attn (reading the row's tagged q/k/v,
+// writing its tagged partials).
 __global__ __launch_bounds__(BLOCK) void k_b_attn(const Args* __restrict__ rargs,
-                                                  const BRow* __restrict__ rows, uint32_t l) {
-  const Args& a = rargs[blockIdx.y];
+                                                  const BRow* __restrict__ rows,
+                                                  const uint32_t* __restrict__ items, uint32_t l) {
+  const uint32_t e = items[blockIdx.x], b = e >> 16, x = e & 0xffffu;
+  const Args& a = rargs[b];
   const Lds s = lds_init_rows(a.d);
-  const BRow r = rows[blockIdx.y];
-  phase_attn(a, l, r.tick, r.pos, blockIdx.x, gridDim.x, s);
+  const BRow r = rows[b];
+  phase_attn(a, l, r.tick, r.pos, x, 0x10000u, s);  // stride past every item: just item x
 }
 
 // Combine of the chunk partials (combine_one, as the O phase does), per

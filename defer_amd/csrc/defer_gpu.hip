@@ -1081,6 +1081,7 @@ struct BatchWs {
   Args* rargs = nullptr;
   Args* largs = nullptr;
   uint32_t *sel = nullptr, *lgen = nullptr, *stick = nullptr, *swords = nullptr, *sout = nullptr;
+  uint32_t* items = nullptr;  // attention (row, item) list
   DevState* st = nullptr;
 };
 
@@ -1088,7 +1089,7 @@ static void batch_ws_release(BatchWs* w) {
   if (!w) return;
   void* ps[] = {w->X, w->Y, w->G, w->ATT, w->INV, w->XP, w->XS, w->LINV, w->QKVT, w->PART,
                 w->LOGT, w->VMAX, w->VARG, w->VSUM, w->drows, w->rargs, w->largs, w->sel,
-                w->lgen, w->stick, w->swords, w->sout, w->st};
+                w->lgen, w->stick, w->swords, w->sout, w->items, w->st};
   for (void* p : ps) (void)hipFree(p);
   *w = BatchWs();
 }
@@ -1121,6 +1122,7 @@ static int ensure_ws(defer_gpu_model* m, uint32_t rows, uint32_t lm) {
   HIP_TRY(hipMalloc(&w.PART, (size_t)R * part_words(d) * sizeof(u64)));
   HIP_TRY(hipMalloc(&w.drows, (size_t)R * sizeof(BRow)));
   HIP_TRY(hipMalloc(&w.rargs, (size_t)R * sizeof(Args)));
+  HIP_TRY(hipMalloc(&w.items, (size_t)R * d.nkv * MAX_ACHUNKS * sizeof(uint32_t)));
   const uint32_t L1 = std::max(Lm, 1u);
   HIP_TRY(hipMalloc(&w.XS, (size_t)L1 * d.h * sizeof(float)));
   HIP_TRY(hipMalloc(&w.LINV, (size_t)L1 * sizeof(float)));
@@ -1232,15 +1234,19 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
   if (rc) return rc;
   BatchWs& w = *m->bw;
   std::vector<Args> ra(n);
-  uint32_t max_items = 1;
+  std::vector<uint32_t> items;  // row << 16 | item (rows <= BATCH_MAX_ROWS, items < 2^16)
+  items.reserve((size_t)n * d.nkv);
   for (uint32_t b = 0; b < n; ++b) {
     ra[b] = row_args(rcache[b], w, b);
-    max_items = std::max(max_items, d.nkv * attn_nchunks(rows[b].pos));
+    const uint32_t ni = d.nkv * attn_nchunks(rows[b].pos);
+    for (uint32_t x = 0; x < ni; ++x) items.push_back(b << 16 | x);
   }
   std::vector<uint32_t> lgen(nl);
   for (uint32_t i = 0; i < nl; ++i) lgen[i] = gen_lm(d, rows[sel[i]].tick);
   HIP_TRY(hipMemcpyAsync(w.drows, rows, n * sizeof(BRow), hipMemcpyHostToDevice, s));
   HIP_TRY(hipMemcpyAsync(w.rargs, ra.data(), n * sizeof(Args), hipMemcpyHostToDevice, s));
+  HIP_TRY(hipMemcpyAsync(w.items, items.data(), items.size() * sizeof(uint32_t),
+                         hipMemcpyHostToDevice, s));
   if (nl) {
     HIP_TRY(hipMemcpyAsync(w.sel, sel, nl * sizeof(uint32_t), hipMemcpyHostToDevice, s));
     HIP_TRY(hipMemcpyAsync(w.lgen, lgen.data(), nl * sizeof(uint32_t), hipMemcpyHostToDevice, s));
@@ -1254,7 +1260,7 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
     launch_gemm(s, GO_PLAIN, m->p_qkv[l], d.qkv_rows, d.h, w.XP, n, w.Y, ldy);
     k_b_qkv_epi<<<dim3((d.qkv_rows / 2 + 255) / 256, n), 256, 0, s>>>(w.rargs, w.drows, l, w.Y, ldy,
                                                                       w.INV, w.QKVT, d.qkv_rows);
-    k_b_attn<<<dim3(max_items, n), BLOCK, m->lds_rows, s>>>(w.rargs, w.drows, l);
+    k_b_attn<<<(uint32_t)items.size(), BLOCK, m->lds_rows, s>>>(w.rargs, w.drows, w.items, l);
     k_b_comb<<<dim3(d.nh, n), BLOCK, m->lds_rows, s>>>(w.rargs, w.drows, l, w.ATT, d.q);
     launch_panel(s, w.ATT, w.ATT, n, n, d.q, d.q, w.XP);
     launch_gemm(s, GO_RESID, m->p_o[l], d.h, d.q, w.XP, n, w.X, d.h);
