@@ -194,6 +194,13 @@ struct defer_gpu_model {
   std::vector<const float*> p_qkv, p_o, p_gu, p_d;
   const float* p_lm = nullptr;
   struct BatchWs* bw = nullptr;
+  // Optional timing of the batched path's GEMM and attention launches.
+  bool prof = false;
+  std::vector<hipEvent_t> pev;   // event pool; pairs (start, end) per timed launch
+  std::vector<int> pcls;         // class of each pair: 0 GEMM, 1 attention
+  std::vector<double> pflop;     // algorithmic flop of each pair
+  size_t pused = 0;
+  double pstat[6] = {0, 0, 0, 0, 0, 0};
 };
 
 // A persistent kernel compiled for this exact shape, if there is one.
@@ -514,6 +521,7 @@ extern "C" void defer_gpu_model_destroy(defer_gpu_model* m) {
   if (!m) return;
   if (m->stream) (void)hipStreamSynchronize(m->stream);
   batch_ws_free(m);
+  for (hipEvent_t e : m->pev) (void)hipEventDestroy(e);
   (void)hipFree(m->panels);
   (void)hipFree(m->wbuf);
   (void)hipFree(m->d_layers);
@@ -1209,6 +1217,63 @@ static void launch_gemm(hipStream_t s, uint32_t out, const float* Wp, uint32_t M
   else launch_gemm_out<GO_TAG>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen);
 }
 
+// Timing of one launch (profiling on): events recorded around it on the
+// model's stream, read back after the batch's final synchronisation.
+struct ProfSpan {
+  defer_gpu_model* m;
+  int cls;
+  double flop;
+  size_t at = 0;
+  bool on = false;
+  ProfSpan(defer_gpu_model* m_, int cls_, double flop_) : m(m_), cls(cls_), flop(flop_) {
+    if (!m->prof) return;
+    while (m->pev.size() < m->pused + 2) {
+      hipEvent_t e;
+      if (hipEventCreate(&e) != hipSuccess) return;
+      m->pev.push_back(e);
+    }
+    at = m->pused;
+    m->pused += 2;
+    on = hipEventRecord(m->pev[at], m->stream) == hipSuccess;
+  }
+  ~ProfSpan() {
+    if (!on) return;
+    (void)hipEventRecord(m->pev[at + 1], m->stream);
+    m->pcls.push_back(cls);
+    m->pflop.push_back(flop);
+  }
+};
+
+// After a synchronisation: fold the recorded spans into the totals.
+static void prof_collect(defer_gpu_model* m) {
+  for (size_t i = 0; i < m->pcls.size(); ++i) {
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, m->pev[2 * i], m->pev[2 * i + 1]) != hipSuccess) continue;
+    const int c = m->pcls[i];
+    m->pstat[3 * c] += ms;
+    m->pstat[3 * c + 1] += m->pflop[i];
+    m->pstat[3 * c + 2] += 1.0;
+  }
+  m->pcls.clear();
+  m->pflop.clear();
+  m->pused = 0;
+}
+
+extern "C" int defer_gpu_model_set_profiling(defer_gpu_model* m, uint32_t on) {
+  if (!m) return fail(DEFER_GPU_E_INVALID, "null model");
+  m->prof = on != 0;
+  return DEFER_GPU_OK;
+}
+
+extern "C" int defer_gpu_batch_stats(const defer_gpu_model* mc, double* stats, uint32_t reset) {
+  defer_gpu_model* m = const_cast<defer_gpu_model*>(mc);
+  if (!m || !stats) return fail(DEFER_GPU_E_INVALID, "null argument");
+  for (int i = 0; i < 6; ++i) stats[i] = m->pstat[i];
+  if (reset)
+    for (int i = 0; i < 6; ++i) m->pstat[i] = 0.0;
+  return DEFER_GPU_OK;
+}
+
 // The one-token kernels' view of a batch row (attention, combine): the
 // row cache's arguments with the batch's tagged buffers and no staging.
 static Args row_args(const defer_gpu_cache* c, const BatchWs& w, uint32_t b) {
@@ -1241,6 +1306,10 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
     const uint32_t ni = d.nkv * attn_nchunks(rows[b].pos);
     for (uint32_t x = 0; x < ni; ++x) items.push_back(b << 16 | x);
   }
+  // attention flop per layer: scores and weighted values, 2 * hd each per
+  // (query head, position)
+  double attn_flop = 0.0;
+  for (uint32_t b = 0; b < n; ++b) attn_flop += 4.0 * d.nh * d.hd * (rows[b].pos + 1.0);
   std::vector<uint32_t> lgen(nl);
   for (uint32_t i = 0; i < nl; ++i) lgen[i] = gen_lm(d, rows[sel[i]].tick);
   HIP_TRY(hipMemcpyAsync(w.drows, rows, n * sizeof(BRow), hipMemcpyHostToDevice, s));
@@ -1257,29 +1326,48 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
   for (uint32_t l = 0; l < d.L; ++l) {
     k_b_rms<<<(n + 3) / 4, 256, 0, s>>>(w.X, n, d.h, d.eps, w.INV);
     launch_panel(s, w.X, w.X, n, n, d.h, d.h, w.XP);
-    launch_gemm(s, GO_PLAIN, m->p_qkv[l], d.qkv_rows, d.h, w.XP, n, w.Y, ldy);
+    {
+      ProfSpan ps(m, 0, 2.0 * d.qkv_rows * d.h * n);
+      launch_gemm(s, GO_PLAIN, m->p_qkv[l], d.qkv_rows, d.h, w.XP, n, w.Y, ldy);
+    }
     k_b_qkv_epi<<<dim3((d.qkv_rows / 2 + 255) / 256, n), 256, 0, s>>>(w.rargs, w.drows, l, w.Y, ldy,
                                                                       w.INV, w.QKVT, d.qkv_rows);
-    k_b_attn<<<(uint32_t)items.size(), BLOCK, m->lds_rows, s>>>(w.rargs, w.drows, w.items, l);
+    {
+      ProfSpan ps(m, 1, attn_flop);
+      k_b_attn<<<(uint32_t)items.size(), BLOCK, m->lds_rows, s>>>(w.rargs, w.drows, w.items, l);
+    }
     k_b_comb<<<dim3(d.nh, n), BLOCK, m->lds_rows, s>>>(w.rargs, w.drows, l, w.ATT, d.q);
     launch_panel(s, w.ATT, w.ATT, n, n, d.q, d.q, w.XP);
-    launch_gemm(s, GO_RESID, m->p_o[l], d.h, d.q, w.XP, n, w.X, d.h);
+    {
+      ProfSpan ps(m, 0, 2.0 * d.h * d.q * n);
+      launch_gemm(s, GO_RESID, m->p_o[l], d.h, d.q, w.XP, n, w.X, d.h);
+    }
     k_b_rms<<<(n + 3) / 4, 256, 0, s>>>(w.X, n, d.h, d.eps, w.INV);
     launch_panel(s, w.X, w.X, n, n, d.h, d.h, w.XP);
-    launch_gemm(s, GO_PLAIN, m->p_gu[l], 2 * d.ff, d.h, w.XP, n, w.Y, ldy);
+    {
+      ProfSpan ps(m, 0, 2.0 * 2 * d.ff * d.h * n);
+      launch_gemm(s, GO_PLAIN, m->p_gu[l], 2 * d.ff, d.h, w.XP, n, w.Y, ldy);
+    }
     k_b_act<<<dim3((d.ff + 255) / 256, n), 256, 0, s>>>(w.Y, ldy, w.INV, d.ff, d.act, w.G, d.ff);
     launch_panel(s, w.G, w.G, n, n, d.ff, d.ff, w.XP);
-    launch_gemm(s, GO_RESID, m->p_d[l], d.h, d.ff, w.XP, n, w.X, d.h);
+    {
+      ProfSpan ps(m, 0, 2.0 * d.h * d.ff * n);
+      launch_gemm(s, GO_RESID, m->p_d[l], d.h, d.ff, w.XP, n, w.X, d.h);
+    }
   }
   if (nl) {
     k_b_final<<<nl, 64, 0, s>>>(w.X, w.sel, d.h, m->norm, d.eps, w.XS, w.LINV);
     launch_panel(s, w.XS, w.XS, nl, nl, d.h, d.h, w.XP);
-    launch_gemm(s, GO_TAG, m->p_lm, d.V, d.h, w.XP, nl, reinterpret_cast<float*>(w.LOGT), d.V,
-                w.LINV, w.lgen);
+    {
+      ProfSpan ps(m, 0, 2.0 * d.V * d.h * nl);
+      launch_gemm(s, GO_TAG, m->p_lm, d.V, d.h, w.XP, nl, reinterpret_cast<float*>(w.LOGT), d.V,
+                  w.LINV, w.lgen);
+    }
     k_b_chunkmax<<<dim3((d.nvc + 3) / 4, nl), 256, 0, s>>>(d, w.LOGT, w.lgen, w.VMAX, w.VARG, nl);
   }
   HIP_TRY(hipGetLastError());
   HIP_TRY(hipStreamSynchronize(s));
+  if (m->prof) prof_collect(m);
   DevState h;
   HIP_TRY(hipMemcpy(&h, w.st, sizeof(h), hipMemcpyDeviceToHost));
   if (h.abort) return fail(DEFER_GPU_E_TIMEOUT, "a device-side wait exceeded its bound");

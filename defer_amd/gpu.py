@@ -127,6 +127,10 @@ def lib() -> ctypes.CDLL:
     L.defer_gpu_forward_batch.restype = ctypes.c_int
     L.defer_gpu_step_batch.argtypes = [vp, P(vp), u32, f32, vp, vp]
     L.defer_gpu_step_batch.restype = ctypes.c_int
+    L.defer_gpu_model_set_profiling.argtypes = [vp, u32]
+    L.defer_gpu_model_set_profiling.restype = ctypes.c_int
+    L.defer_gpu_batch_stats.argtypes = [vp, P(ctypes.c_double), u32]
+    L.defer_gpu_batch_stats.restype = ctypes.c_int
     _lib = L
     return L
 
@@ -248,6 +252,16 @@ class GpuModel:
         out = np.empty((len(t), self.vocab_size), dtype=np.float32) if logits else None
         _check(lib().defer_gpu_forward_batch(self._h, hs, _ptr(t), len(t), _ptr(out)))
         return out
+
+    def set_profiling(self, on: bool) -> None:
+        _check(lib().defer_gpu_model_set_profiling(self._h, 1 if on else 0))
+
+    def batch_stats(self, reset: bool = True) -> dict:
+        """Event-timed GEMM / attention totals of batched calls since the last reset."""
+        st = (ctypes.c_double * 6)()
+        _check(lib().defer_gpu_batch_stats(self._h, st, 1 if reset else 0))
+        return {"gemm_ms": st[0], "gemm_flop": st[1], "gemm_launches": int(st[2]),
+                "attn_ms": st[3], "attn_flop": st[4], "attn_launches": int(st[5])}
 
     def step_batch(self, caches: Sequence["GpuCache"], temperature: float,
                    words: Optional[Sequence[int]] = None) -> list:

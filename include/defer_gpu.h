@@ -17,7 +17,8 @@
  *   defer_gpu_step           Session::step                     engine.rs:113-117
  *   defer_gpu_generate       Session::generate                 engine.rs:121-137
  *   defer_gpu_replay         Session::checkout replay loop     engine.rs:261-271
- *   defer_gpu_forward_batch, defer_gpu_step_batch, defer_gpu_model_set_batching:
+ *   defer_gpu_forward_batch, defer_gpu_step_batch, defer_gpu_model_set_batching,
+ *   defer_gpu_model_set_profiling, defer_gpu_batch_stats:
  *                            no counterpart (the reference is batch-1 only)
  */
 #ifndef DEFER_GPU_H
@@ -156,6 +157,14 @@ int defer_gpu_forward_batch(const defer_gpu_model* m, defer_gpu_cache* const* ca
  * then the n sampled tokens are fed as one batch. tokens_out [n]. */
 int defer_gpu_step_batch(const defer_gpu_model* m, defer_gpu_cache* const* caches, uint32_t n,
                          float temperature, const uint32_t* rng_words, uint32_t* tokens_out);
+
+/* Instrumentation of the batched path: when on, every batched call times its
+ * GEMM and attention launches with HIP events on the library's stream.
+ * stats[0..5] = GEMM ms, GEMM flop, GEMM launches, attention ms, attention
+ * flop, attention launches, summed since the last reset (reset != 0 clears
+ * them after reading). */
+int defer_gpu_model_set_profiling(defer_gpu_model* m, uint32_t on);
+int defer_gpu_batch_stats(const defer_gpu_model* m, double* stats, uint32_t reset);
 
 /* Thread-local description of the last failing call. */
 const char* defer_gpu_last_error(void);
