@@ -260,6 +260,164 @@ __global__ __launch_bounds__(BLOCK) void k_b_attn(const Args* __restrict__ rargs
   phase_attn(a, l, r.tick, r.pos, x, 0x10000u, s);  // stride past every item: just item x
 }
 
+// ----------------------------------------------------- tiled attention
+//
+// Rows of one cache at consecutive positions (a prefill or a replay) share
+// their K/V rows, so their attention runs as tiles: a workgroup takes 16
+// consecutive query positions (aligned to 16), one chunk of 128 key
+// positions and one kv head, stages the chunk's K and V rows in LDS once, and
+// computes every query's chunk partials (m, l, acc) in the order phase_attn
+// uses (head_dim 64, chunk 128, positions < 2048), with MFMA chains where
+// phase_attn has fma chains:
+//  * score(q, t): 4 chains over 16 elements each (the lanes of a position),
+//    then ((c0 + c1) + (c2 + c3)) * scale;
+//  * softmax: phase_attn's wave code per (query, head);
+//  * value[d]: 24 position groups (wave w, group pl: positions
+//    4w + pl + 24k, k ascending), each a chain, then per w the tree over its
+//    four groups and the sum w = 0..5 in order, from +0.
+// Positions past a query's own (t > pos) carry probability +0 and zero V
+// rows, which leave an accumulator unchanged (a chain started at +0 never
+// holds -0).
+
+constexpr uint32_t AT_HD = 64, AT_CH = 128, AT_VROWS = 192;  // 24 groups x 8 positions
+constexpr uint32_t AT_KP = 68, AT_VP = 66, AT_QP = 68, AT_SP = 196;  // LDS row pitches
+
+__host__ __device__ inline size_t attn_tile_lds(uint32_t grp) {
+  return sizeof(float) * ((size_t)AT_CH * AT_KP + (size_t)AT_VROWS * AT_VP +
+                          (size_t)grp * 16 * AT_QP + (size_t)grp * 16 * AT_SP + grp * 32);
+}
+
+// tasks[x] = tile << 16 | chunk << 8 | kv head; tiles[m] .. tiles[m + 1] are
+// the batch rows of tile m. rows: the batch (one cache, consecutive
+// positions); qkvt: tagged q/k/v words per row; part: tagged partials.
+__global__ __launch_bounds__(256) void k_b_attn_tile(const Dims d, const BRow* __restrict__ rows,
+                                                     const uint32_t* __restrict__ tasks,
+                                                     const uint32_t* __restrict__ tiles, uint32_t l,
+                                                     const u64* __restrict__ qkvt,
+                                                     u64* __restrict__ part, uint32_t part_w) {
+  extern __shared__ float at_lds[];
+  const uint32_t grp = d.group, hs = AT_HD + 2;
+  float* Ks = at_lds;                       // [AT_CH][AT_KP]
+  float* Vs = Ks + AT_CH * AT_KP;           // [AT_VROWS][AT_VP]
+  float* Qs = Vs + AT_VROWS * AT_VP;        // [grp][16][AT_QP]
+  float* Ss = Qs + grp * 16 * AT_QP;        // [grp][16][AT_SP]: scores, then probabilities
+  float* ML = Ss + grp * 16 * AT_SP;        // [grp][16][2]: m, l
+  const uint32_t task = tasks[blockIdx.x];
+  const uint32_t m = task >> 16, c = (task >> 8) & 0xffu, g = task & 0xffu;
+  const uint32_t rb0 = tiles[m], nq = tiles[m + 1] - rb0;
+  const BRow r0 = rows[rb0];
+  const uint32_t p_last = r0.pos + nq - 1;
+  const uint32_t t0 = c * AT_CH;
+  const uint32_t nk = min(AT_CH, p_last + 1 - t0);
+  const uint32_t tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+  const float* kb = r0.kc + ((size_t)l * d.nkv + g) * r0.cap * d.kvs;
+  const float* vb = r0.vc + ((size_t)l * d.nkv + g) * r0.cap * d.kvs;
+  // 1. K and V rows of the chunk, Q of the tile's queries (16 threads per row).
+  for (uint32_t e = tid; e < AT_VROWS * 16; e += 256) {
+    const uint32_t t = e / 16, q4 = (e % 16) * 4;
+    float4 kv4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), vv4 = kv4;
+    if (t < nk) {
+      kv4 = *reinterpret_cast<const float4*>(kb + (size_t)(t0 + t) * d.kvs + q4);
+      vv4 = *reinterpret_cast<const float4*>(vb + (size_t)(t0 + t) * d.kvs + q4);
+    }
+    if (t < AT_CH) *reinterpret_cast<float4*>(Ks + t * AT_KP + q4) = kv4;
+    float* vd = Vs + t * AT_VP + q4;
+    vd[0] = vv4.x;
+    vd[1] = vv4.y;
+    vd[2] = vv4.z;
+    vd[3] = vv4.w;
+  }
+  for (uint32_t e = tid; e < grp * 16 * AT_HD; e += 256) {
+    const uint32_t j = e / (16 * AT_HD), q = (e / AT_HD) % 16, dd = e % AT_HD;
+    float v = 0.0f;
+    if (q < nq)
+      v = __uint_as_float((uint32_t)qkvt[(size_t)(rb0 + q) * d.qkv_rows + (g * grp + j) * AT_HD + dd]);
+    Qs[(j * 16 + q) * AT_QP + dd] = v;
+  }
+  __syncthreads();
+  // 2. scores: wave w takes key tiles w and w + 4.
+  const uint32_t lr = lane % 16, lc = lane / 16;
+  for (uint32_t kt = wave; kt < (nk + 15) / 16; kt += 4) {
+    for (uint32_t j = 0; j < grp; ++j) {
+      f4v a4[4];
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub) {
+        f4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t el = 16 * sub + 4 * i + lc;
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Qs[(j * 16 + lr) * AT_QP + el],
+                                                     Ks[(kt * 16 + lr) * AT_KP + el], acc, 0, 0, 0);
+        }
+        a4[sub] = acc;
+      }
+      const f4v sc = ((a4[0] + a4[1]) + (a4[2] + a4[3]));
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)  // query 4*lc + rr, key kt*16 + lr
+        Ss[(j * 16 + 4 * lc + rr) * AT_SP + kt * 16 + lr] = sc[rr] * d.scale;
+    }
+  }
+  __syncthreads();
+  // 3. softmax statistics and probabilities, one wave per (query, head).
+  for (uint32_t u = wave; u < grp * 16; u += 4) {
+    const uint32_t j = u / 16, q = u % 16;
+    float* sh = Ss + (j * 16 + q) * AT_SP;
+    const uint32_t n = q < nq ? min(AT_CH, r0.pos + q + 1 - t0) : 0;
+    float mx = -INFINITY;
+    for (uint32_t i = lane; i < n; i += WAVE) mx = fmaxf(mx, sh[i]);
+    mx = wave_max(mx);
+    float ls = 0.0f;
+    for (uint32_t i = lane; i < n; i += WAVE) {
+      const float e = (mx == -INFINITY) ? 0.0f : expf(sh[i] - mx);
+      sh[i] = e;
+      ls += e;
+    }
+    ls = wave_sum(ls);
+    for (uint32_t i = n + lane; i < AT_VROWS; i += WAVE) sh[i] = 0.0f;
+    if (lane == 0) {
+      ML[(j * 16 + q) * 2] = mx;
+      ML[(j * 16 + q) * 2 + 1] = ls;
+    }
+  }
+  __syncthreads();
+  // 4. values: wave w computes dims 16w..16w+15 of every head.
+  for (uint32_t j = 0; j < grp; ++j) {
+    f4v acc[24];
+#pragma unroll
+    for (int gi = 0; gi < 24; ++gi) acc[gi] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int gi = 0; gi < 24; ++gi) {
+#pragma unroll
+      for (int mm = 0; mm < 2; ++mm) {
+        const uint32_t pos = gi + 24 * (4 * mm + lc);  // group gi = 4*w' + pl
+        acc[gi] = __builtin_amdgcn_mfma_f32_16x16x4f32(Ss[(j * 16 + lr) * AT_SP + pos],
+                                                       Vs[pos * AT_VP + 16 * wave + lr], acc[gi],
+                                                       0, 0, 0);
+      }
+    }
+    f4v A = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int w6 = 0; w6 < 6; ++w6) {
+      const f4v W = (acc[4 * w6] + acc[4 * w6 + 1]) + (acc[4 * w6 + 2] + acc[4 * w6 + 3]);
+      A = A + W;
+    }
+    const uint32_t hh = g * grp + j;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {  // query 4*lc + rr, dim 16*wave + lr
+      const uint32_t q = 4 * lc + rr;
+      if (q >= nq) continue;
+      const BRow rq = rows[rb0 + q];
+      const u64 gtag = (u64)gen_of(d, rq.tick, l, PH_ATTN) << 32;
+      u64* out = part + (size_t)(rb0 + q) * part_w + ((size_t)hh * MAX_ACHUNKS + c) * hs;
+      out[2 + 16 * wave + lr] = gtag | __float_as_uint(A[rr]);
+      if (wave == 0 && lr == 0) {
+        out[0] = gtag | __float_as_uint(ML[(j * 16 + q) * 2]);
+        out[1] = gtag | __float_as_uint(ML[(j * 16 + q) * 2 + 1]);
+      }
+    }
+  }
+}
+
 // Combine of the chunk partials (combine_one, as the O phase does), per
 // (head, row), into plain att[b][q].
 __global__ __launch_bounds__(BLOCK) void k_b_comb(const Args* __restrict__ rargs,

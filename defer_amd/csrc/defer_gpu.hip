@@ -497,6 +497,10 @@ extern "C" int defer_gpu_model_create(const defer_gpu_config* cfg, const float* 
       return cleanup(fail(DEFER_GPU_E_HIP, "LDS attribute (%zu bytes): %s", m->lds_bytes,
                           hipGetErrorString(e)));
   }
+  e = hipFuncSetAttribute((const void*)k_b_attn_tile, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)attn_tile_lds(MAX_GROUP));
+  if (e != hipSuccess)
+    return cleanup(fail(DEFER_GPU_E_HIP, "LDS attribute (tiled attention): %s", hipGetErrorString(e)));
   const void* row_kernels[] = {(const void*)k_b_attn, (const void*)k_b_comb,
                                (const void*)k_b_sample};
   for (const void* kf : row_kernels) {
@@ -1089,7 +1093,8 @@ struct BatchWs {
   Args* rargs = nullptr;
   Args* largs = nullptr;
   uint32_t *sel = nullptr, *lgen = nullptr, *stick = nullptr, *swords = nullptr, *sout = nullptr;
-  uint32_t* items = nullptr;  // attention (row, item) list
+  uint32_t* items = nullptr;  // attention (row, item) list, or tiled attention tasks
+  uint32_t* tiles = nullptr;  // tiled attention: first batch row of each tile
   DevState* st = nullptr;
 };
 
@@ -1097,7 +1102,7 @@ static void batch_ws_release(BatchWs* w) {
   if (!w) return;
   void* ps[] = {w->X, w->Y, w->G, w->ATT, w->INV, w->XP, w->XS, w->LINV, w->QKVT, w->PART,
                 w->LOGT, w->VMAX, w->VARG, w->VSUM, w->drows, w->rargs, w->largs, w->sel,
-                w->lgen, w->stick, w->swords, w->sout, w->items, w->st};
+                w->lgen, w->stick, w->swords, w->sout, w->items, w->tiles, w->st};
   for (void* p : ps) (void)hipFree(p);
   *w = BatchWs();
 }
@@ -1131,6 +1136,7 @@ static int ensure_ws(defer_gpu_model* m, uint32_t rows, uint32_t lm) {
   HIP_TRY(hipMalloc(&w.drows, (size_t)R * sizeof(BRow)));
   HIP_TRY(hipMalloc(&w.rargs, (size_t)R * sizeof(Args)));
   HIP_TRY(hipMalloc(&w.items, (size_t)R * d.nkv * MAX_ACHUNKS * sizeof(uint32_t)));
+  HIP_TRY(hipMalloc(&w.tiles, ((size_t)R / 16 + 2) * sizeof(uint32_t)));
   const uint32_t L1 = std::max(Lm, 1u);
   HIP_TRY(hipMalloc(&w.XS, (size_t)L1 * d.h * sizeof(float)));
   HIP_TRY(hipMalloc(&w.LINV, (size_t)L1 * sizeof(float)));
@@ -1299,12 +1305,30 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
   if (rc) return rc;
   BatchWs& w = *m->bw;
   std::vector<Args> ra(n);
-  std::vector<uint32_t> items;  // row << 16 | item (rows <= BATCH_MAX_ROWS, items < 2^16)
-  items.reserve((size_t)n * d.nkv);
-  for (uint32_t b = 0; b < n; ++b) {
-    ra[b] = row_args(rcache[b], w, b);
-    const uint32_t ni = d.nkv * attn_nchunks(rows[b].pos);
-    for (uint32_t x = 0; x < ni; ++x) items.push_back(b << 16 | x);
+  for (uint32_t b = 0; b < n; ++b) ra[b] = row_args(rcache[b], w, b);
+  // Attention: tiles of 16 aligned positions when the rows are one cache's
+  // consecutive positions (a prefill or a replay) and the shape is the tiled
+  // kernel's; otherwise one workgroup per (row, item).
+  bool tiled = d.hd == AT_HD && d.kvs == AT_HD && rows[n - 1].pos < ACHUNK * MAX_ACHUNKS;
+  for (uint32_t b = 1; b < n && tiled; ++b)
+    tiled = rcache[b] == rcache[0] && rows[b].pos == rows[0].pos + b;
+  std::vector<uint32_t> items, tiles;
+  if (tiled) {
+    tiles.push_back(0);
+    for (uint32_t b = 1; b < n; ++b)
+      if (rows[b].pos % 16 == 0) tiles.push_back(b);
+    tiles.push_back(n);
+    for (uint32_t t = 0; t + 1 < tiles.size(); ++t) {
+      const uint32_t nch = attn_nchunks(rows[tiles[t]].pos);
+      for (uint32_t c = 0; c < nch; ++c)
+        for (uint32_t g = 0; g < d.nkv; ++g) items.push_back(t << 16 | c << 8 | g);
+    }
+  } else {
+    items.reserve((size_t)n * d.nkv);
+    for (uint32_t b = 0; b < n; ++b) {
+      const uint32_t ni = d.nkv * attn_nchunks(rows[b].pos);
+      for (uint32_t x = 0; x < ni; ++x) items.push_back(b << 16 | x);  // rows <= 2048, items < 2^16
+    }
   }
   // attention flop per layer: scores and weighted values, 2 * hd each per
   // (query head, position)
@@ -1316,6 +1340,9 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
   HIP_TRY(hipMemcpyAsync(w.rargs, ra.data(), n * sizeof(Args), hipMemcpyHostToDevice, s));
   HIP_TRY(hipMemcpyAsync(w.items, items.data(), items.size() * sizeof(uint32_t),
                          hipMemcpyHostToDevice, s));
+  if (tiled)
+    HIP_TRY(hipMemcpyAsync(w.tiles, tiles.data(), tiles.size() * sizeof(uint32_t),
+                           hipMemcpyHostToDevice, s));
   if (nl) {
     HIP_TRY(hipMemcpyAsync(w.sel, sel, nl * sizeof(uint32_t), hipMemcpyHostToDevice, s));
     HIP_TRY(hipMemcpyAsync(w.lgen, lgen.data(), nl * sizeof(uint32_t), hipMemcpyHostToDevice, s));
@@ -1334,7 +1361,11 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
                                                                       w.INV, w.QKVT, d.qkv_rows);
     {
       ProfSpan ps(m, 1, attn_flop);
-      k_b_attn<<<(uint32_t)items.size(), BLOCK, m->lds_rows, s>>>(w.rargs, w.drows, w.items, l);
+      if (tiled)
+        k_b_attn_tile<<<(uint32_t)items.size(), 256, attn_tile_lds(d.group), s>>>(
+            d, w.drows, w.items, w.tiles, l, w.QKVT, w.PART, part_words(d));
+      else
+        k_b_attn<<<(uint32_t)items.size(), BLOCK, m->lds_rows, s>>>(w.rargs, w.drows, w.items, l);
     }
     k_b_comb<<<dim3(d.nh, n), BLOCK, m->lds_rows, s>>>(w.rargs, w.drows, l, w.ATT, d.q);
     launch_panel(s, w.ATT, w.ATT, n, n, d.q, d.q, w.XP);

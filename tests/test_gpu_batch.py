@@ -186,3 +186,23 @@ def test_135m_batched_replay_matches_sequential(m135):
     for l in (0, 29):
         for x, y in zip(r.read(l), live.read(l)):
             assert np.array_equal(bits(x), bits(y))
+
+
+def test_135m_batched_prefill_from_unaligned_position(m135):
+    """A batched prompt continuing a cache at position 37: the first attention
+    tile holds positions 37..47 only."""
+    cfg, gm, om = m135
+    say("135m: 37 tokens one by one, then 100 batched vs 137 one by one")
+    p = synthetic.make_prompt(cfg["vocab_size"], 137, seed=33)
+    gm.set_batching(0)
+    a = gm.new_cache(256)
+    gm.prompt(a, p)
+    b = gm.new_cache(256)
+    gm.prompt(b, p[:37])
+    gm.set_batching(16)
+    gm.prompt(b, p[37:])
+    assert len(b) == 137
+    assert np.array_equal(bits(a.last_logits()), bits(b.last_logits()))
+    for l in (0, 17, 29):
+        for x, y in zip(a.read(l), b.read(l)):
+            assert np.array_equal(bits(x), bits(y))
