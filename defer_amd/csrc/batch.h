@@ -280,7 +280,7 @@ __global__ __launch_bounds__(BLOCK) void k_b_attn(const Args* __restrict__ rargs
 // holds -0).
 
 constexpr uint32_t AT_HD = 64, AT_CH = 128, AT_VROWS = 192;  // 24 groups x 8 positions
-constexpr uint32_t AT_KP = 68, AT_VP = 66, AT_QP = 68, AT_SP = 196;  // LDS row pitches
+constexpr uint32_t AT_KP = 68, AT_VP = 66, AT_QP = 68, AT_SP = 193;  // LDS row pitches (floats)
 
 __host__ __device__ inline size_t attn_tile_lds(uint32_t grp) {
   return sizeof(float) * ((size_t)AT_CH * AT_KP + (size_t)AT_VROWS * AT_VP +
@@ -312,27 +312,50 @@ __global__ __launch_bounds__(256) void k_b_attn_tile(const Dims d, const BRow* _
   const uint32_t tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
   const float* kb = r0.kc + ((size_t)l * d.nkv + g) * r0.cap * d.kvs;
   const float* vb = r0.vc + ((size_t)l * d.nkv + g) * r0.cap * d.kvs;
-  // 1. K and V rows of the chunk, Q of the tile's queries (16 threads per row).
-  for (uint32_t e = tid; e < AT_VROWS * 16; e += 256) {
-    const uint32_t t = e / 16, q4 = (e % 16) * 4;
-    float4 kv4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), vv4 = kv4;
-    if (t < nk) {
-      kv4 = *reinterpret_cast<const float4*>(kb + (size_t)(t0 + t) * d.kvs + q4);
-      vv4 = *reinterpret_cast<const float4*>(vb + (size_t)(t0 + t) * d.kvs + q4);
+  // 1. K rows, then V rows, then Q words of the chunk: each thread issues a
+  // batch's eight loads before its first LDS store (16 threads per row).
+  constexpr int NR = AT_CH * 16 / 256;  // rows per thread and batch: 8
+#pragma unroll
+  for (int kv = 0; kv < 2; ++kv) {
+    const float* src = kv ? vb : kb;
+    float4 r4[NR];
+#pragma unroll
+    for (int k = 0; k < NR; ++k) {
+      const uint32_t e = tid + 256 * k, t = e / 16, q4 = (e % 16) * 4;
+      r4[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (t < nk) r4[k] = *reinterpret_cast<const float4*>(src + (size_t)(t0 + t) * d.kvs + q4);
     }
-    if (t < AT_CH) *reinterpret_cast<float4*>(Ks + t * AT_KP + q4) = kv4;
-    float* vd = Vs + t * AT_VP + q4;
-    vd[0] = vv4.x;
-    vd[1] = vv4.y;
-    vd[2] = vv4.z;
-    vd[3] = vv4.w;
+#pragma unroll
+    for (int k = 0; k < NR; ++k) {
+      const uint32_t e = tid + 256 * k, t = e / 16, q4 = (e % 16) * 4;
+      if (kv == 0) {
+        *reinterpret_cast<float4*>(Ks + t * AT_KP + q4) = r4[k];
+      } else {
+        float* vd = Vs + t * AT_VP + q4;
+        vd[0] = r4[k].x;
+        vd[1] = r4[k].y;
+        vd[2] = r4[k].z;
+        vd[3] = r4[k].w;
+      }
+    }
   }
-  for (uint32_t e = tid; e < grp * 16 * AT_HD; e += 256) {
-    const uint32_t j = e / (16 * AT_HD), q = (e / AT_HD) % 16, dd = e % AT_HD;
-    float v = 0.0f;
-    if (q < nq)
-      v = __uint_as_float((uint32_t)qkvt[(size_t)(rb0 + q) * d.qkv_rows + (g * grp + j) * AT_HD + dd]);
-    Qs[(j * 16 + q) * AT_QP + dd] = v;
+  for (uint32_t e = AT_CH * AT_VP + tid; e < AT_VROWS * AT_VP; e += 256) Vs[e] = 0.0f;
+  for (uint32_t e0 = 0; e0 < grp * 16 * AT_HD; e0 += 256 * 8) {
+    u64 qw[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t e = e0 + tid + 256 * k, j = e / (16 * AT_HD), q = (e / AT_HD) % 16,
+                     dd = e % AT_HD;
+      qw[k] = 0;
+      if (j < grp && q < nq)
+        qw[k] = qkvt[(size_t)(rb0 + q) * d.qkv_rows + (g * grp + j) * AT_HD + dd];
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t e = e0 + tid + 256 * k, j = e / (16 * AT_HD), q = (e / AT_HD) % 16,
+                     dd = e % AT_HD;
+      if (j < grp) Qs[(j * 16 + q) * AT_QP + dd] = __uint_as_float((uint32_t)qw[k]);
+    }
   }
   __syncthreads();
   // 2. scores: wave w takes key tiles w and w + 4.
