@@ -104,10 +104,9 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ Wp, uint
     const uint32_t ct = min(C0 + t, nct - 1);  // past the last tile: read a real one, never used
     xp[t] = Xp + ((size_t)ct * nch * 4 + wave) * 1024 + lane * 16;
   }
-  for (uint32_t i = 0; i < nch; ++i) {
-    const uint32_t kb = 256 * i + 64 * wave;
-    if (kb >= K) break;
-    float4 a[4], b[TN][4];
+  // Operands of chunk i for this wave, loaded one chunk ahead of their use.
+  const uint32_t nmine = K > 64 * wave ? (K - 64 * wave + 255) / 256 : 0;  // chunks with a slice here
+  auto load = [&](uint32_t i, float4 (&a)[4], float4 (&b)[TN][4]) {
     const float4* wa = reinterpret_cast<const float4*>(wp + (size_t)i * PANEL_TILE);
 #pragma unroll
     for (int q = 0; q < 4; ++q) a[q] = wa[q];
@@ -117,6 +116,9 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ Wp, uint
 #pragma unroll
       for (int q = 0; q < 4; ++q) b[t][q] = xb[q];
     }
+  };
+  auto mfmas = [&](uint32_t i, const float4 (&a)[4], const float4 (&b)[TN][4]) {
+    const uint32_t kb = 256 * i + 64 * wave;
     const uint32_t ns = min(16u, (K - kb + 3) / 4);  // segments with an element in this slice
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
@@ -128,6 +130,15 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ Wp, uint
                                                            0, 0, 0);
       }
     }
+  };
+  float4 a0[4], b0[TN][4], a1[4], b1[TN][4];
+  if (nmine > 0) load(0, a0, b0);
+  for (uint32_t i = 0; i < nmine; i += 2) {
+    if (i + 1 < nmine) load(i + 1, a1, b1);
+    mfmas(i, a0, b0);
+    if (i + 1 >= nmine) break;
+    if (i + 2 < nmine) load(i + 2, a0, b0);
+    mfmas(i + 1, a1, b1);
   }
 #pragma unroll
   for (int t = 0; t < TN; ++t) red[wave][t][lane] = tree16(acc[t]);
