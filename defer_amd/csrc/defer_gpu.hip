@@ -151,6 +151,61 @@ __global__ void k_commit(const Args* __restrict__ ap, const RunDesc* __restrict_
   if (run->mode == RUN_GENERATE && is_stop(*run, st->token)) st->halt = 1;
 }
 
+// The attention probabilities of one layer for the forward in flight (the
+// trace of forward_ext, model.rs:486-488), written as [nh][pos + 1]: scores
+// in phase_attn's order (16-element fma chains per lane group, the group's
+// tree, then the scale; masked positions -inf), then p_t = exp(s_t - M) / S
+// with M the context's max and S the sum of exp(s_t - M) (thread-strided
+// partials in position order, then a fixed tree). One workgroup per head;
+// runs after the layer's attention and before the next layer's q/k/v.
+__global__ __launch_bounds__(256) void k_trace(const Args* __restrict__ ap, uint32_t l,
+                                               float* __restrict__ out) {
+  const Args& a = *ap;
+  const Dims& d = a.d;
+  const uint32_t hh = blockIdx.x, g = hh / d.group, pos = a.st->pos, n = pos + 1;
+  const uint32_t hd = d.hd, lps = hd / 16;
+  float* o = out + (size_t)hh * n;
+  __shared__ float red[256 / WAVE];
+  const float* kb = a.kc + ((size_t)l * d.nkv + g) * d.cap * d.kvs;
+  float mx = -INFINITY;
+  for (uint32_t t = threadIdx.x; t < n; t += blockDim.x) {
+    float part[16];
+    for (uint32_t sb = 0; sb < lps; ++sb) {
+      float acc = 0.0f;
+      for (uint32_t e = 0; e < 16; ++e) {
+        const uint32_t i = sb * 16 + e;
+        const float q = __uint_as_float((uint32_t)a.mb_qkv[hh * hd + i]);
+        acc = fmaf(q, kb[(size_t)t * d.kvs + i], acc);
+      }
+      part[sb] = acc;
+    }
+    for (uint32_t w = 1; w < lps; w <<= 1)
+      for (uint32_t sb = 0; sb + w < lps; sb += 2 * w) part[sb] = part[sb] + part[sb + w];
+    const bool masked = a.mask && t < pos && ((a.mask[t >> 5] >> (t & 31)) & 1u);
+    const float sc = masked ? -INFINITY : part[0] * d.scale;
+    o[t] = sc;
+    mx = fmaxf(mx, sc);
+  }
+  mx = wave_max(mx);
+  if (threadIdx.x % WAVE == 0) red[threadIdx.x / WAVE] = mx;
+  __syncthreads();
+  mx = red[0];
+  for (uint32_t w = 1; w < blockDim.x / WAVE; ++w) mx = fmaxf(mx, red[w]);
+  __syncthreads();
+  float sum = 0.0f;
+  for (uint32_t t = threadIdx.x; t < n; t += blockDim.x) {
+    const float e = (mx == -INFINITY) ? 0.0f : expf(o[t] - mx);
+    o[t] = e;
+    sum += e;
+  }
+  sum = wave_sum(sum);
+  if (threadIdx.x % WAVE == 0) red[threadIdx.x / WAVE] = sum;
+  __syncthreads();
+  float S = 0.0f;
+  for (uint32_t w = 0; w < blockDim.x / WAVE; ++w) S += red[w];
+  for (uint32_t t = threadIdx.x; t < n; t += blockDim.x) o[t] = o[t] / S;
+}
+
 // Strip the tags of logits (or any tagged vector) into plain floats.
 __global__ void k_untag(const u64* src, float* dst, uint32_t n) {
   const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -230,6 +285,8 @@ struct defer_gpu_cache {
   size_t stop_cap = 0;
   float* d_logits = nullptr;
   float* d_tmp = nullptr;  // kv gather staging
+  float* d_trace = nullptr;   // [L][nh][cap] staging of a traced forward
+  float* trace_to = nullptr;  // set during a traced forward: where k_trace writes
   uint32_t pos = 0;        // host mirror of st->pos
   uint32_t tick = 0;
   bool has_logits = false;
@@ -613,6 +670,7 @@ static void cache_free(defer_gpu_cache* c) {
   (void)hipFree(c->d_out);
   (void)hipFree(c->d_logits);
   (void)hipFree(c->d_tmp);
+  (void)hipFree(c->d_trace);
   (void)hipFree(c->d_args);
 }
 
@@ -745,8 +803,13 @@ static int launch_op_kernels(defer_gpu_cache* c, hipStream_t s) {
   const size_t lds = m->lds_bytes;
   k_samp_a<<<G, BLOCK, lds, s>>>(a, c->d_run);
   k_op<<<1, BLOCK, lds, s>>>(a, c->d_run);
-  for (uint32_t l = 0; l < d.L; ++l)
-    for (uint32_t ph = 0; ph < PH_PER_LAYER; ++ph) k_phase<<<G, BLOCK, lds, s>>>(a, ph, l);
+  for (uint32_t l = 0; l < d.L; ++l) {
+    for (uint32_t ph = 0; ph < PH_PER_LAYER; ++ph) {
+      k_phase<<<G, BLOCK, lds, s>>>(a, ph, l);
+      if (ph == PH_COMB && c->trace_to)
+        k_trace<<<d.nh, 256, 0, s>>>(a, l, c->trace_to + (size_t)l * d.nh * (c->pos + 1));
+    }
+  }
   k_phase<<<G, BLOCK, lds, s>>>(a, PH_LM_KERNEL, 0);
   k_commit<<<1, 1, 0, s>>>(a, c->d_run);
   HIP_TRY(hipGetLastError());
@@ -866,7 +929,6 @@ extern "C" int defer_gpu_forward(const defer_gpu_model* m, defer_gpu_cache* c, u
   if (token >= m->d.V) return fail(DEFER_GPU_E_TOKEN, "token id %u out of range", token);
   if (c->pos >= c->cap)
     return fail(DEFER_GPU_E_CONTEXT, "context length %u exceeded", m->cfg.max_seq_len);
-  if (trace_out) return fail(DEFER_GPU_E_INVALID, "attention trace export is not built yet");
   bool use_mask = false;
   if (n_masked) {
     std::vector<uint32_t> bits((c->cap + 31) / 32, 0u);
@@ -884,7 +946,19 @@ extern "C" int defer_gpu_forward(const defer_gpu_model* m, defer_gpu_cache* c, u
     rc = sync_args(c);
     if (rc) return rc;
   }
-  rc = feed_tokens(m, c, &token, 1, use_mask);
+  const uint32_t pos0 = c->pos;
+  if (trace_out) {
+    if (!c->d_trace)
+      HIP_TRY(hipMalloc(&c->d_trace, (size_t)m->d.L * m->d.nh * c->cap * sizeof(float)));
+    c->trace_to = c->d_trace;
+  }
+  rc = feed_tokens(m, c, &token, 1, use_mask || trace_out);
+  c->trace_to = nullptr;
+  if (!rc && trace_out)
+    rc = hipMemcpy(trace_out, c->d_trace, (size_t)m->d.L * m->d.nh * (pos0 + 1) * sizeof(float),
+                   hipMemcpyDeviceToHost) == hipSuccess
+             ? DEFER_GPU_OK
+             : fail(DEFER_GPU_E_HIP, "trace copy failed");
   if (use_mask) {
     c->args.mask = nullptr;
     const int rc2 = sync_args(c);

@@ -186,13 +186,17 @@ class GpuModel:
         return GpuCache(self, capacity)
 
     def forward(self, token: int, cache: "GpuCache", masked: Sequence[int] = (),
-                logits: bool = True) -> Optional[np.ndarray]:
-        """Model::forward_ext (model.rs:394-520); logits copied out if asked."""
+                logits: bool = True, trace: bool = False):
+        """Model::forward_ext (model.rs:394-520); logits copied out if asked.
+        With trace=True returns (logits, probabilities [L, num_heads, pos + 1])."""
         out = np.empty(self.vocab_size, dtype=np.float32) if logits else None
         m = _u32(masked) if len(masked) else None
+        tr = None
+        if trace:
+            tr = np.empty((self.cfg.num_layers, self.cfg.num_heads, len(cache) + 1), dtype=np.float32)
         _check(lib().defer_gpu_forward(self._h, cache._h, int(token), _ptr(m),
-                                       0 if m is None else len(m), _ptr(out), None))
-        return out
+                                       0 if m is None else len(m), _ptr(out), _ptr(tr)))
+        return (out, tr) if trace else out
 
     def prompt(self, cache: "GpuCache", tokens: Sequence[int]) -> None:
         t = _u32(tokens)

@@ -164,3 +164,26 @@ def test_135m_greedy_parity(small135):
     say(f"135m max|dlogit| after 48 positions = {d:.3e}; top-2 gap {top2[1] - top2[0]:.3e}")
     assert toks == otoks
     assert d <= LOGIT_TOL
+
+
+def test_attention_trace_matches_oracle():
+    """forward_ext's trace (model.rs:486-488): per layer and head, the
+    attention probabilities over positions 0..pos, masked ones zero."""
+    cfg = synthetic.CONFIGS["tiny"]
+    w = synthetic.make_weights(cfg, 12)
+    gm, om = G.GpuModel(G.Config.from_dict(cfg), w), O.OracleModel(cfg, w)
+    gc, oc = gm.new_cache(64), om.new_cache()
+    for t in [5, 9, 200, 31, 7, 77, 3]:
+        gm.forward(t, gc, logits=False)
+        om.forward(t, oc)
+    for masked in ((), (1, 4)):
+        lg, tr = gm.forward(11, gc, masked=masked, trace=True)
+        lo, to = om.forward(11, oc, masked=masked, trace=True)
+        assert tr.shape == (cfg["num_layers"], cfg["num_heads"], 8)
+        assert float(np.max(np.abs(tr - to))) <= 1e-5
+        assert np.allclose(tr.sum(axis=2), 1.0, atol=1e-5)
+        for p in masked:
+            assert np.all(tr[:, :, p] == 0.0)
+        assert float(np.max(np.abs(lg - lo))) <= LOGIT_TOL
+        gc.truncate(7)
+        oc.truncate(7)
