@@ -206,3 +206,45 @@ def test_135m_batched_prefill_from_unaligned_position(m135):
     for l in (0, 17, 29):
         for x, y in zip(a.read(l), b.read(l)):
             assert np.array_equal(bits(x), bits(y))
+
+
+def test_1b_shape_lockstep_sessions_bit_identical_and_oracle():
+    """The many-session configuration's shape (Llama-3.2-1B: h 2048, 32/8
+    heads, ff 8192, vocab 128256, tied), cut to 2 layers: 8 sessions stepped
+    together equal their own batch-1 steps bit for bit, and session 0's
+    greedy tokens equal the oracle's."""
+    cfg = dict(synthetic.CONFIGS["llama-3.2-1b"])
+    cfg["num_layers"] = 2
+    say("1b shape x 2 layers: weights")
+    w = synthetic.make_weights(cfg, 0)
+    gm = G.GpuModel(G.Config.from_dict(cfg), w)
+    V = cfg["vocab_size"]
+    lens = [12, 5, 17, 30, 9, 16, 22, 40]
+    A, B = [], []
+    for k, n in enumerate(lens):
+        p = synthetic.make_prompt(V, n, seed=100 + k)
+        a, b = gm.new_cache(128), gm.new_cache(128)
+        gm.set_batching(16)
+        gm.prompt(a, p)
+        gm.set_batching(0)
+        gm.prompt(b, p)
+        assert np.array_equal(bits(a.last_logits()), bits(b.last_logits())), k
+        A.append(a)
+        B.append(b)
+    say("1b shape: 4 lockstep greedy steps of 8 sessions vs per-session steps")
+    steps = []
+    for step in range(4):
+        got = gm.step_batch(A, 0.0)
+        want = [gm.step(b, 0.0) for b in B]
+        assert got == want, step
+        steps.append(got)
+    for a, b in zip(A, B):
+        assert np.array_equal(bits(a.last_logits()), bits(b.last_logits()))
+    say("1b shape: session 0 vs the oracle (12 + 4 forwards on the CPU)")
+    om = O.OracleModel(cfg, w)
+    otoks, _, olog = om.generate(om.new_cache(), bytes(32), 0.0,
+                                 synthetic.make_prompt(V, 12, seed=100), 4)
+    assert [s[0] for s in steps] == otoks
+    d = float(np.max(np.abs(A[0].last_logits() - olog)))
+    say(f"1b shape: max|dlogit| vs oracle = {d:.3e}")
+    assert d <= 1e-3
