@@ -206,6 +206,18 @@ __global__ __launch_bounds__(256) void k_trace(const Args* __restrict__ ap, uint
   for (uint32_t t = threadIdx.x; t < n; t += blockDim.x) o[t] = o[t] / S;
 }
 
+// Length and generation base of many caches at once (batched calls).
+struct StateSet {
+  DevState* st;
+  uint32_t pos, tick;
+};
+__global__ void k_set_state(const StateSet* __restrict__ set, uint32_t n) {
+  const uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= n) return;
+  set[k].st->pos = set[k].pos;
+  set[k].st->tick = set[k].tick;
+}
+
 // Strip the tags of logits (or any tagged vector) into plain floats.
 __global__ void k_untag(const u64* src, float* dst, uint32_t n) {
   const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -1169,6 +1181,7 @@ struct BatchWs {
   uint32_t *sel = nullptr, *lgen = nullptr, *stick = nullptr, *swords = nullptr, *sout = nullptr;
   uint32_t* items = nullptr;  // attention (row, item) list, or tiled attention tasks
   uint32_t* tiles = nullptr;  // tiled attention: first batch row of each tile
+  StateSet* sets = nullptr;   // [rows] cache states to set after a batch
   DevState* st = nullptr;
 };
 
@@ -1176,7 +1189,7 @@ static void batch_ws_release(BatchWs* w) {
   if (!w) return;
   void* ps[] = {w->X, w->Y, w->G, w->ATT, w->INV, w->XP, w->XS, w->LINV, w->QKVT, w->PART,
                 w->LOGT, w->VMAX, w->VARG, w->VSUM, w->drows, w->rargs, w->largs, w->sel,
-                w->lgen, w->stick, w->swords, w->sout, w->items, w->tiles, w->st};
+                w->lgen, w->stick, w->swords, w->sout, w->items, w->tiles, w->sets, w->st};
   for (void* p : ps) (void)hipFree(p);
   *w = BatchWs();
 }
@@ -1211,6 +1224,7 @@ static int ensure_ws(defer_gpu_model* m, uint32_t rows, uint32_t lm) {
   HIP_TRY(hipMalloc(&w.rargs, (size_t)R * sizeof(Args)));
   HIP_TRY(hipMalloc(&w.items, (size_t)R * d.nkv * MAX_ACHUNKS * sizeof(uint32_t)));
   HIP_TRY(hipMalloc(&w.tiles, ((size_t)R / 16 + 2) * sizeof(uint32_t)));
+  HIP_TRY(hipMalloc(&w.sets, (size_t)R * sizeof(StateSet)));
   const uint32_t L1 = std::max(Lm, 1u);
   HIP_TRY(hipMalloc(&w.XS, (size_t)L1 * d.h * sizeof(float)));
   HIP_TRY(hipMalloc(&w.LINV, (size_t)L1 * sizeof(float)));
@@ -1521,25 +1535,42 @@ static int batch_sample(defer_gpu_model* m, defer_gpu_cache* const* ocache, cons
   return DEFER_GPU_OK;
 }
 
-// A cache after its batch rows: length, generation base and, from logits
-// row li of the workspace, the tagged logits and chunk maxima a following
-// sample reads.
-static int batch_commit(defer_gpu_model* m, defer_gpu_cache* c, uint32_t li, uint32_t pos,
-                        uint32_t tick) {
+// Caches after their batch rows: length, generation base and, from logits
+// row li[k] of the workspace, the tagged logits and chunk maxima a following
+// sample reads. All copies are queued, then one kernel sets the device
+// states, then one synchronisation.
+static int batch_commit_many(defer_gpu_model* m, defer_gpu_cache* const* cs, const uint32_t* li,
+                             const uint32_t* pos, const uint32_t* tick, uint32_t n) {
   const Dims& d = m->d;
   const hipStream_t s = m->stream;
   const BatchWs& w = *m->bw;
-  HIP_TRY(hipMemcpyAsync(c->args.mb_logit, w.LOGT + (size_t)li * d.V, (size_t)d.V * sizeof(u64),
-                         hipMemcpyDeviceToDevice, s));
-  HIP_TRY(hipMemcpyAsync(c->args.mb_vmax, w.VMAX + (size_t)li * d.nvc, (size_t)d.nvc * sizeof(u64),
-                         hipMemcpyDeviceToDevice, s));
-  HIP_TRY(hipMemcpyAsync(c->args.mb_varg, w.VARG + (size_t)li * d.nvc, (size_t)d.nvc * sizeof(u64),
-                         hipMemcpyDeviceToDevice, s));
+  std::vector<StateSet> set(n);
+  for (uint32_t k = 0; k < n; ++k) {
+    defer_gpu_cache* c = cs[k];
+    HIP_TRY(hipMemcpyAsync(c->args.mb_logit, w.LOGT + (size_t)li[k] * d.V,
+                           (size_t)d.V * sizeof(u64), hipMemcpyDeviceToDevice, s));
+    HIP_TRY(hipMemcpyAsync(c->args.mb_vmax, w.VMAX + (size_t)li[k] * d.nvc,
+                           (size_t)d.nvc * sizeof(u64), hipMemcpyDeviceToDevice, s));
+    HIP_TRY(hipMemcpyAsync(c->args.mb_varg, w.VARG + (size_t)li[k] * d.nvc,
+                           (size_t)d.nvc * sizeof(u64), hipMemcpyDeviceToDevice, s));
+    set[k].st = c->st;
+    set[k].pos = pos[k];
+    set[k].tick = tick[k];
+  }
+  HIP_TRY(hipMemcpyAsync(w.sets, set.data(), n * sizeof(StateSet), hipMemcpyHostToDevice, s));
+  k_set_state<<<(n + 63) / 64, 64, 0, s>>>(w.sets, n);
+  HIP_TRY(hipGetLastError());
   HIP_TRY(hipStreamSynchronize(s));
-  c->pos = pos;
-  c->tick = tick;
-  c->has_logits = true;
-  return push_state(c);
+  for (uint32_t k = 0; k < n; ++k) {
+    cs[k]->pos = pos[k];
+    cs[k]->tick = tick[k];
+    cs[k]->has_logits = true;
+  }
+  return DEFER_GPU_OK;
+}
+static int batch_commit(defer_gpu_model* m, defer_gpu_cache* c, uint32_t li, uint32_t pos,
+                        uint32_t tick) {
+  return batch_commit_many(m, &c, &li, &pos, &tick, 1);
 }
 
 static BRow make_row(const defer_gpu_cache* c, uint32_t pos, uint32_t tick, uint32_t token) {
@@ -1640,12 +1671,17 @@ extern "C" int defer_gpu_forward_batch(const defer_gpu_model* mc, defer_gpu_cach
       HIP_TRY(hipStreamSynchronize(m->stream));
     }
   }
+  std::vector<defer_gpu_cache*> cc;
+  std::vector<uint32_t> cli, cpos, ctick;
   for (uint32_t b = 0; b < n; ++b)
     if (last_of[b]) {
-      rc = batch_commit(m, caches[b], li_of[b], rows[b].pos + 1, rows[b].tick + 1);
-      if (rc) return rc;
+      cc.push_back(caches[b]);
+      cli.push_back(li_of[b]);
+      cpos.push_back(rows[b].pos + 1);
+      ctick.push_back(rows[b].tick + 1);
     }
-  return DEFER_GPU_OK;
+  return batch_commit_many(m, cc.data(), cli.data(), cpos.data(), ctick.data(),
+                           (uint32_t)cc.size());
 }
 
 extern "C" int defer_gpu_step_batch(const defer_gpu_model* mc, defer_gpu_cache* const* caches,
