@@ -159,3 +159,60 @@ def test_360m_rows_loaded_directly_greedy_parity():
     assert d <= LOGIT_TOL
     c.close()
     gm.close()
+
+
+def test_tiny_past_2048_positions_chunk_256_vs_oracle():
+    """Past 2048 positions the attention chunk is 256 positions: decode and
+    batched prefill there, against the oracle and each other."""
+    cfg = dict(synthetic.CONFIGS["tiny"])
+    cfg["max_seq_len"] = 4096
+    w = synthetic.make_weights(cfg, 3)
+    gm, om = G.GpuModel(G.Config.from_dict(cfg), w), O.OracleModel(cfg, w)
+    say("tiny: prompt 2300 (batched) + 8 greedy vs oracle; and vs token by token")
+    prompt = synthetic.make_prompt(cfg["vocab_size"], 2300, seed=5)
+    a = gm.new_cache(2400)
+    gm.prompt(a, prompt)
+    toks = gm.generate(a, 8, 0.0)
+    otoks, _, olog = om.generate(om.new_cache(), bytes(32), 0.0, prompt, 8)
+    d = float(np.max(np.abs(a.last_logits() - olog)))
+    say(f"tiny at 2308 positions: max|dlogit| = {d:.3e}")
+    assert toks == otoks
+    assert d <= LOGIT_TOL
+    gm.set_batching(0)
+    b = gm.new_cache(2400)
+    gm.prompt(b, prompt)
+    gm.set_batching(16)
+    assert gm.generate(b, 8, 0.0) == toks
+    assert np.array_equal(a.last_logits().view(np.uint32), b.last_logits().view(np.uint32))
+
+
+def test_8b_shape_head_dim_128_untied_vs_oracle():
+    """The 8B shape (h 4096, 32/8 heads, head_dim 128, ff 14336, vocab 128256,
+    untied lm_head) cut to 2 layers: greedy tokens and logits vs the oracle,
+    batched prefill bit-identical to token by token."""
+    cfg = dict(synthetic.CONFIGS["llama-3-8b"])
+    cfg["num_layers"] = 2
+    say("8b shape x 2 layers: weights (about 6 GB)")
+    w = synthetic.make_weights(cfg, 0)
+    gm = G.GpuModel(G.Config.from_dict(cfg), w)
+    prompt = synthetic.make_prompt(cfg["vocab_size"], 20, seed=8)
+    a = gm.new_cache(64)
+    gm.prompt(a, prompt)
+    toks = gm.generate(a, 3, 0.0)
+    gm.set_batching(0)
+    b = gm.new_cache(64)
+    gm.prompt(b, prompt)
+    gm.set_batching(16)
+    assert gm.generate(b, 3, 0.0) == toks
+    assert np.array_equal(a.last_logits().view(np.uint32), b.last_logits().view(np.uint32))
+    say("8b shape: oracle (20 + 3 forwards on the CPU)")
+    om = O.OracleModel(cfg, w)
+    otoks, _, olog = om.generate(om.new_cache(), bytes(32), 0.0, prompt, 3)
+    d = float(np.max(np.abs(a.last_logits() - olog)))
+    say(f"8b shape: max|dlogit| vs oracle = {d:.3e}")
+    assert toks == otoks
+    assert d <= LOGIT_TOL
+    del om
+    a.close()
+    b.close()
+    gm.close()
