@@ -195,12 +195,76 @@ def sessions_workload(args) -> int:
     return 0
 
 
+def decode_workload(args, name: str) -> int:
+    """Batch-1 decode of the long-context (SmolLM2-360M shape: 128-token prompt,
+    4096 tokens at T=0.8, seed 1) or the large-model configuration
+    (Llama-3-8B shape, 32 GB of weights: 64-token prompt, 512 greedy tokens).
+    value = decoded tokens per second (device time of the generate call);
+    roofline = the persistent kernel's algorithmic bytes over that time."""
+    from defer_amd import gpu as G
+    from defer_amd import host as H
+    from defer_amd import synthetic
+
+    if name == "long":
+        cfg_name, n_prompt, n_gen, T, seed = "smollm2-360m", 128, 4096, 0.8, 1
+    else:
+        cfg_name, n_prompt, n_gen, T, seed = "llama-3-8b", 64, 512, 0.0, 0
+    cfg = synthetic.CONFIGS[cfg_name]
+    t0 = time.perf_counter()
+    model = G.GpuModel(G.Config.from_dict(cfg), synthetic.make_weights(cfg, 0))
+    setup_s = time.perf_counter() - t0
+    s = H.Session(model, H.seed_from_u64(seed), T, capacity=n_prompt + n_gen)
+    s.prompt(synthetic.make_prompt(cfg["vocab_size"], n_prompt, seed=seed))
+    toks = s.generate(n_gen)
+    ms = model.last_device_ms()
+    assert len(toks) == n_gen
+    wbytes = synthetic.weight_bytes_streamed(cfg)
+    algo = algorithmic_bytes(cfg, wbytes, n_prompt, n_gen)
+    achieved = algo / (ms / 1e3) / 1e9
+    line = {
+        "metric": "batch-1 decode tok/s (f32) + achieved HBM GB/s as % of peak",
+        "value": round(n_gen / (ms / 1e3), 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": n_gen,
+        "warmup": 0,
+        "ms_per_step": round(ms / n_gen, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (N(0,0.02) weights from seed 0, uniform-random prompt ids)",
+        "config": {
+            "workload": f"{cfg_name}-shaped decode: {n_prompt}-token prompt + {n_gen} tokens at "
+                        f"T={T}, seed {seed}, one token at a time",
+            "weight_bytes_per_token": wbytes,
+            "weight_roofline_tok_s": round(PEAK_GBS * 1e9 / wbytes, 1),
+            "weight_roofline_frac": round(n_gen / (ms / 1e3) * wbytes / (PEAK_GBS * 1e9), 4),
+            "setup_s": round(setup_s, 1),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "k_persistent",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_GBS, 4),
+            "traffic": None,
+        },
+    }
+    s.close()
+    model.close()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--workload", choices=["replay", "sessions"], default="replay",
+    ap.add_argument("--workload", choices=["replay", "sessions", "long", "8b"], default="replay",
                     help="replay: the 2048-position checkout (default, the headline); "
-                         "sessions: 64 Llama-3.2-1B-shaped sessions in lockstep")
+                         "sessions: 64 Llama-3.2-1B-shaped sessions in lockstep; "
+                         "long: 360M-shaped decode of 4096 tokens; 8b: 8B-shaped decode")
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -226,6 +290,8 @@ def main() -> int:
 
     if args.workload == "sessions":
         return sessions_workload(args)
+    if args.workload in ("long", "8b"):
+        return decode_workload(args, args.workload)
 
     from defer_amd import gpu as G
     from defer_amd import host as H
