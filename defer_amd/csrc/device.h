@@ -400,6 +400,39 @@ __device__ __forceinline__ float dot_tail(RowT<NF>& r, const float* __restrict__
   return acc;
 }
 
+// Lane partials of two rows w0 . x and w1 . x (same K), the loads of each
+// next segment issued before the fmas of the current one, so a wave keeps two
+// segments of both rows in flight. Same element order as dot_tail.
+template <int NF>
+__device__ __forceinline__ float2 dot2_stream(const float* __restrict__ w0,
+                                              const float* __restrict__ w1,
+                                              const float* __restrict__ x, uint32_t K,
+                                              uint32_t lane) {
+  constexpr uint32_t SEG = 256u * NF;
+  RowT<NF> a0, a1, b0, b1;
+  row_load(a0, w0, K, lane);
+  row_load(a1, w1, K, lane);
+  float acc0 = 0.0f, acc1 = 0.0f;
+  for (uint32_t base = 0; base < K; base += 2 * SEG) {
+    const uint32_t nb = base + SEG;
+    if (nb < K) {
+      row_load(b0, w0 + nb, K - nb, lane);
+      row_load(b1, w1 + nb, K - nb, lane);
+    }
+    acc0 = row_fma(a0, x + base, K - base, lane, acc0);
+    acc1 = row_fma(a1, x + base, K - base, lane, acc1);
+    if (nb >= K) break;
+    const uint32_t na = nb + SEG;
+    if (na < K) {
+      row_load(a0, w0 + na, K - na, lane);
+      row_load(a1, w1 + na, K - na, lane);
+    }
+    acc0 = row_fma(b0, x + nb, K - nb, lane, acc0);
+    acc1 = row_fma(b1, x + nb, K - nb, lane, acc1);
+  }
+  return make_float2(acc0, acc1);
+}
+
 __device__ __forceinline__ float dot_partial(const float* __restrict__ w,
                                              const float* __restrict__ x, uint32_t K,
                                              uint32_t lane) {

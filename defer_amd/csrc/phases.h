@@ -706,21 +706,24 @@ __device__ __forceinline__ void items_dot(const Args& a, uint32_t kind, uint32_t
     }
     return;
   }
-  for (uint32_t k = cw; k < cnt; k += NCW) {
-    float p0, p1 = 0.0f;
+  // Rows from HBM: two rows streamed together (a pair's rows, or two
+  // single-row items of this wave).
+  for (uint32_t k = cw; k < cnt; k += pair ? NCW : 2 * NCW) {
     const ItemRows r = item_rows(a, kind, l, k, wg, G);
-    if (r.w1) {
-      Row A, B;
-      row_load(A, r.w0, r.K, lane);
-      row_load(B, r.w1, r.K, lane);
-      p0 = dot_tail(A, r.w0, x, r.K, lane);
-      p1 = dot_tail(B, r.w1, x, r.K, lane);
+    if (pair) {
+      const float2 p = dot2_stream<KF>(r.w0, r.w1, x, r.K, lane);
+      float y[2] = {p.x, p.y};
+      wave_sum_n<2>(y);
+      body(k, y[0], y[1]);
     } else {
-      p0 = dot_partial(r.w0, x, r.K, lane);
+      const uint32_t k2 = k + NCW < cnt ? k + NCW : k;
+      const ItemRows r2 = item_rows(a, kind, l, k2, wg, G);
+      const float2 p = dot2_stream<KF>(r.w0, r2.w0, x, r.K, lane);
+      float y[2] = {p.x, p.y};
+      wave_sum_n<2>(y);
+      body(k, y[0], 0.0f);
+      if (k2 != k) body(k2, y[1], 0.0f);
     }
-    const float y0 = wave_sum(p0);
-    const float y1 = r.w1 ? wave_sum(p1) : 0.0f;
-    body(k, y0, y1);
   }
 }
 
