@@ -1222,7 +1222,7 @@ static int ensure_ws(defer_gpu_model* m, uint32_t rows, uint32_t lm) {
   HIP_TRY(hipMalloc(&w.PART, (size_t)R * part_words(d) * sizeof(u64)));
   HIP_TRY(hipMalloc(&w.drows, (size_t)R * sizeof(BRow)));
   HIP_TRY(hipMalloc(&w.rargs, (size_t)R * sizeof(Args)));
-  HIP_TRY(hipMalloc(&w.items, (size_t)R * d.nkv * MAX_ACHUNKS * sizeof(uint32_t)));
+  HIP_TRY(hipMalloc(&w.items, (size_t)R * d.nkv * MAX_ACHUNKS * d.group * sizeof(uint32_t)));
   HIP_TRY(hipMalloc(&w.tiles, ((size_t)R / 16 + 2) * sizeof(uint32_t)));
   HIP_TRY(hipMalloc(&w.sets, (size_t)R * sizeof(StateSet)));
   const uint32_t L1 = std::max(Lm, 1u);
@@ -1414,7 +1414,7 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
   } else {
     items.reserve((size_t)n * d.nkv);
     for (uint32_t b = 0; b < n; ++b) {
-      const uint32_t ni = d.nkv * attn_nchunks(rows[b].pos);
+      const uint32_t ni = attn_items(d, rows[b].pos);
       for (uint32_t x = 0; x < ni; ++x) items.push_back(b << 16 | x);  // rows <= 2048, items < 2^16
     }
   }

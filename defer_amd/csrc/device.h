@@ -177,6 +177,10 @@ __host__ __device__ inline uint32_t attn_nchunks(uint32_t pos) {
   const uint32_t ch = attn_chunk(pos);
   return (pos + 1 + ch - 1) / ch;
 }
+// Attention items of the query at pos: one per (kv head, chunk, query head).
+__host__ __device__ inline uint32_t attn_items(const Dims& d, uint32_t pos) {
+  return d.nkv * attn_nchunks(pos) * d.group;
+}
 __host__ __device__ inline bool comb_inline(const Dims& d, uint32_t pos) {
   return d.nh * attn_nchunks(pos) * (d.hd + 2) <= INLINE_COMB_MAX;
 }

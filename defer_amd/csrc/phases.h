@@ -858,24 +858,24 @@ __device__ __forceinline__ AttGeo att_geo(uint32_t hd) {
   return g;
 }
 
-// Split-context attention for one (kv head, chunk) item (model.rs:471-497):
-// for each query head j of the GQA group, the chunk's softmax partials
-// m_j = max score, l_j = sum exp(score - m_j), acc_j = sum exp(score - m_j) v.
-//  1. scores of every position of the chunk into LDS (each K row read once
-//     for the whole group);
-//  2. wave j: m_j, exp in place, l_j (lane-strided partials, wave tree);
-//  3. exp-weighted V rows (each read once for the group), one partial per
-//     (wave, position lane group), summed in that order.
-// Every order above depends on (pos, head_dim) only. Heads beyond the group
-// size are computed on whatever LDS holds and never stored, which keeps
-// every loop's trip count a compile-time constant.
+// Split-context attention for one (kv head, chunk, query head) item
+// (model.rs:471-497): the chunk's softmax partials of query head j,
+// m = max score, l = sum exp(score - m), acc = sum exp(score - m) v.
+//  1. scores of every position of the chunk into LDS;
+//  2. one wave: m, exp in place, l (lane-strided partials, wave tree);
+//  3. exp-weighted V rows, one partial per (wave, position lane group),
+//     summed in that order.
+// Every order above depends on (pos, head_dim) only.
 __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t tick, uint32_t pos,
                                            uint32_t wg, uint32_t G, const Lds& s) {
   const Dims d = shape_dims(a.d);
   const uint32_t nch = attn_nchunks(pos), CH = attn_chunk(pos);
-  const uint32_t n_items = d.nkv * nch;
+  const uint32_t n_items = attn_items(d, pos);
   const uint32_t gen_in = gen_of(d, tick, l, PH_QKV);
   const uint32_t gen_out = gen_of(d, tick, l, PH_ATTN);
+  // One query head per item: the heads of a GQA group share K/V rows but
+  // nothing else, so splitting them gives each head the same arithmetic.
+  constexpr uint32_t NH1 = 1;  // query heads per item
   const uint32_t hd = d.hd, grp = d.group, hs = hd + 2;
   const AttGeo ge = att_geo(hd);
   float* qs = s.scr;                      // [MAX_GROUP*hd] (rows >= grp: don't care)
@@ -892,7 +892,8 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
   const uint32_t tw = wave * ge.pw + ps;  // this lane's position offset in a score pass
   const uint32_t vw = wave * ge.pv + pl;  // ... and in a value step
   for (uint32_t item = wg; item < n_items; item += G) {
-    const uint32_t g = item / nch, c = item - g * nch;
+    const uint32_t gc = item / grp, j0 = item - gc * grp;  // item = (g * nch + c) * grp + j0
+    const uint32_t g = gc / nch, c = gc - g * nch;
     const uint32_t t0 = c * CH;
     const uint32_t t1 = min(t0 + CH, pos + 1);
     const float* kb = a.kc + ((size_t)l * d.nkv + g) * d.cap * d.kvs + sub * 16;
@@ -911,7 +912,7 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
       const uint32_t t = t0 + vw + u * vstep;
       if (att && t < t1 && t < pos) vr[u] = ldg4(vb + (size_t)t * d.kvs);
     }
-    if (!poll_gather<2, 1, 1>(gather_vec(a.mb_qkv + (size_t)g * grp * hd, grp * hd, gen_in, qs),
+    if (!poll_gather<2, 1, 1>(gather_vec(a.mb_qkv + (size_t)(g * grp + j0) * hd, hd, gen_in, qs),
                               gather_vec(a.mb_qkv + d.q + g * hd, hd, gen_in, kn),
                               gather_vec(a.mb_qkv + d.q + d.kv + g * hd, hd, gen_in, vn), NPOLL,
                               a.st, s.ctl))
@@ -928,7 +929,7 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
                           ((ldg_u32(a.mask + (ts >> 5)) >> (ts & 31)) & 1u);
       // One head at a time keeps the live registers to this lane's K piece.
 #pragma unroll 1
-      for (uint32_t j = 0; j < grp; ++j) {
+      for (uint32_t j = 0; j < NH1; ++j) {
         float acc = 0.0f;
 #pragma unroll
         for (uint32_t i = 0; i < 4; ++i) {
@@ -951,7 +952,7 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
     __syncthreads();
     // 2. softmax statistics, one wave per query head
     const uint32_t n = t1 - t0;
-    if (wave < grp) {
+    if (wave < NH1) {
       float* sh = sc + wave * CH;
       float m = -INFINITY;
       for (uint32_t i = lane; i < n; i += WAVE) m = fmaxf(m, lds_ld(sh + i));
@@ -970,9 +971,9 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
     }
     __syncthreads();
     // 3. exp-weighted V rows: positions t0 + vw + k*vstep, k = 0, 1, ...
-    float4 acc[MAX_GROUP];
+    float4 acc[NH1];
 #pragma unroll
-    for (uint32_t j = 0; j < MAX_GROUP; ++j) acc[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (uint32_t j = 0; j < NH1; ++j) acc[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     const uint32_t nk = att && t0 + vw < t1 ? (t1 - t0 - vw + vstep - 1) / vstep : 0;
     for (uint32_t k0 = 0; k0 < nk; k0 += VU) {
 #pragma unroll
@@ -984,7 +985,7 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
           const uint32_t tf = t + VU * vstep;
           if (k + VU < nk && tf < pos) vr[u] = ldg4(vb + (size_t)tf * d.kvs);
 #pragma unroll
-          for (uint32_t j = 0; j < MAX_GROUP; ++j) {
+          for (uint32_t j = 0; j < NH1; ++j) {
             const float p = lds_ld(sc + j * CH + (t - t0));
             acc[j].x = fmaf(p, v.x, acc[j].x);
             acc[j].y = fmaf(p, v.y, acc[j].y);
@@ -998,8 +999,7 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
     // partial per wave.
     for (uint32_t o = ge.lv; o < WAVE; o <<= 1) {
 #pragma unroll
-      for (uint32_t j = 0; j < MAX_GROUP; ++j)
-        if (j < grp) {
+      for (uint32_t j = 0; j < NH1; ++j) {
           acc[j].x += __shfl_xor(acc[j].x, o);
           acc[j].y += __shfl_xor(acc[j].y, o);
           acc[j].z += __shfl_xor(acc[j].z, o);
@@ -1007,24 +1007,24 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
         }
     }
 #pragma unroll
-    for (uint32_t j = 0; j < MAX_GROUP; ++j)
-      if (att && pl == 0 && j < grp) {
-        float* dst = wp + (wave * grp + j) * hd + dl * 4;
+    for (uint32_t j = 0; j < NH1; ++j)
+      if (att && pl == 0) {
+        float* dst = wp + (wave * NH1 + j) * hd + dl * 4;
         lds_st(dst + 0, acc[j].x);
         lds_st(dst + 1, acc[j].y);
         lds_st(dst + 2, acc[j].z);
         lds_st(dst + 3, acc[j].w);
       }
     __syncthreads();
-    for (uint32_t u = threadIdx.x; threadIdx.x < NPOLL * WAVE && u < grp * hd; u += NPOLL * WAVE) {
+    for (uint32_t u = threadIdx.x; threadIdx.x < NPOLL * WAVE && u < NH1 * hd; u += NPOLL * WAVE) {
       const uint32_t j = u / hd, dd = u - j * hd;
       float pw[NWA];
 #pragma unroll
-      for (uint32_t w = 0; w < NWA; ++w) pw[w] = lds_ld(wp + (w * grp + j) * hd + dd);
+      for (uint32_t w = 0; w < NWA; ++w) pw[w] = lds_ld(wp + (w * NH1 + j) * hd + dd);
       float A = 0.0f;
 #pragma unroll
       for (uint32_t w = 0; w < NWA; ++w) A += pw[w];
-      const uint32_t hh = g * grp + j;
+      const uint32_t hh = g * grp + j0 + j;
       u64* out = a.mb_part + ((size_t)hh * MAX_ACHUNKS + c) * hs;
       mb_put(out + 2 + dd, A, gen_out);
       if (dd == 0) {
