@@ -161,3 +161,44 @@ extern "C" int defer_host_session_checkout(const defer_gpu_model* m, const uint8
   *out = s;
   return DEFER_HOST_OK;
 }
+
+extern "C" int defer_host_session_checkpoint(const defer_host_session* s,
+                                             const uint8_t model_signature[32],
+                                             defer_host_checkpoint_header* h) {
+  if (!s || !model_signature || !h) return fail(DEFER_HOST_E_INVALID, "null argument");
+  memcpy(h->model_signature, model_signature, 32);
+  memcpy(h->base_seed, s->seed, 32);
+  h->temperature = s->temperature;
+  h->prompt_len = s->prompt_len;
+  h->rng_word_pos = s->word_pos;
+  return DEFER_HOST_OK;
+}
+
+extern "C" int defer_host_session_checkout_file(const defer_gpu_model* m,
+                                                const uint8_t model_signature[32],
+                                                const char* path, uint32_t capacity,
+                                                defer_host_session** out) {
+  if (!m || !model_signature || !path || !out) return fail(DEFER_HOST_E_INVALID, "null argument");
+  defer_host_checkpoint_header h;
+  size_t n = 0;
+  int rc = defer_host_checkpoint_load(path, &h, nullptr, &n);
+  if (rc) return rc;
+  std::vector<uint32_t> history(n);
+  rc = defer_host_checkpoint_load(path, &h, history.data(), &n);
+  if (rc) return rc;
+  if (memcmp(h.model_signature, model_signature, 32) != 0) {
+    auto hex = [](const uint8_t* b) {
+      std::string s;
+      char t[3];
+      for (int i = 0; i < 32; ++i) {
+        snprintf(t, sizeof(t), "%02x", b[i]);
+        s += t;
+      }
+      return s;
+    };
+    return fail(DEFER_HOST_E_CHECKPOINT, "model signature mismatch: checkpoint %s vs loaded %s",
+                hex(h.model_signature).c_str(), hex(model_signature).c_str());
+  }
+  return defer_host_session_checkout(m, h.base_seed, h.temperature, history.data(), n,
+                                     h.prompt_len, h.rng_word_pos, capacity, out);
+}

@@ -95,6 +95,10 @@ def lib() -> ctypes.CDLL:
     L.defer_host_session_cache.argtypes = [vp]
     L.defer_host_session_cache.restype = vp
     L.defer_host_session_checkout.argtypes = [vp, u8p, f32, vp, sz, u32, u64, u32, P(vp)]
+    L.defer_host_checkpoint_save.argtypes = [ctypes.c_char_p, P(WalHeader), vp, sz]
+    L.defer_host_checkpoint_load.argtypes = [ctypes.c_char_p, P(WalHeader), vp, P(sz)]
+    L.defer_host_session_checkpoint.argtypes = [vp, u8p, P(WalHeader)]
+    L.defer_host_session_checkout_file.argtypes = [vp, u8p, ctypes.c_char_p, u32, P(vp)]
     _lib = L
     return L
 
@@ -210,6 +214,37 @@ class Wal:
         }
 
 
+class Checkpoint:
+    """DeferCheckpoint files (checkpoint.rs:4-136). The header struct has the
+    WAL header's layout (signature, seed, temperature, prompt_len, u64 word
+    position)."""
+
+    @staticmethod
+    def save(path: str, signature: bytes, seed: bytes, temperature: float, prompt_len: int,
+             rng_word_pos: int, history: Sequence[int]) -> None:
+        h = _header(signature, seed, temperature, prompt_len, rng_word_pos)
+        t = np.ascontiguousarray(np.asarray(history, dtype=np.uint32))
+        _check(lib().defer_host_checkpoint_save(path.encode(), ctypes.byref(h),
+                                                t.ctypes.data if len(t) else None, len(t)))
+
+    @staticmethod
+    def load(path: str) -> dict:
+        h = WalHeader()
+        n = ctypes.c_size_t(0)
+        _check(lib().defer_host_checkpoint_load(path.encode(), ctypes.byref(h), None, ctypes.byref(n)))
+        hist = np.zeros(max(n.value, 1), dtype=np.uint32)
+        _check(lib().defer_host_checkpoint_load(path.encode(), ctypes.byref(h), hist.ctypes.data,
+                                                ctypes.byref(n)))
+        return {
+            "model_signature": bytes(h.model_signature),
+            "base_seed": bytes(h.base_seed),
+            "temperature": float(h.temperature),
+            "prompt_len": int(h.prompt_len),
+            "rng_word_pos": int(h.start_rng_word_pos),
+            "history": [int(x) for x in hist[: n.value]],
+        }
+
+
 class Session:
     """Session (engine.rs:23-137) driving the device path."""
 
@@ -275,6 +310,24 @@ class Session:
         c._h = ctypes.c_void_p(lib().defer_host_session_cache(self._h))
         c.close = lambda: None  # the session destroys it
         return c
+
+    def checkpoint(self, signature: bytes, path: str) -> None:
+        """Session::checkpoint (engine.rs:223-232) saved to `path`."""
+        h = WalHeader()
+        _check(lib().defer_host_session_checkpoint(self._h, _buf(signature), ctypes.byref(h)))
+        t = np.ascontiguousarray(np.asarray(self.history, dtype=np.uint32))
+        _check(lib().defer_host_checkpoint_save(path.encode(), ctypes.byref(h),
+                                                t.ctypes.data if len(t) else None, len(t)))
+
+    @classmethod
+    def checkout_file(cls, model: "gpu.GpuModel", signature: bytes, path: str,
+                      capacity: int = 0) -> "Session":
+        """Session::checkout (engine.rs:241-274) of a checkpoint file."""
+        ck = Checkpoint.load(path)
+        out = ctypes.c_void_p()
+        _check(lib().defer_host_session_checkout_file(model._h, _buf(signature), path.encode(),
+                                                      int(capacity), ctypes.byref(out)))
+        return cls(model, ck["base_seed"], ck["temperature"], _handle=out)
 
     @classmethod
     def checkout(cls, model: "gpu.GpuModel", seed: bytes, temperature: float, history: Sequence[int],

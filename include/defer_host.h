@@ -12,6 +12,7 @@
  *   defer_host_chacha8_words    ChaCha8Rng word stream           engine.rs:51, 213-215
  *   defer_host_words_per_sample sampler::words_per_sample        sampler.rs:15-21
  *   defer_host_wal_*            WalHeader / WalWriter / WalLog   wal.rs:8-255
+ *   defer_host_checkpoint_*     DeferCheckpoint                  checkpoint.rs:4-136
  *   defer_host_session_*        Session                          engine.rs:23-137, 241-274
  */
 #ifndef DEFER_HOST_H
@@ -88,6 +89,27 @@ void defer_host_wal_close(defer_host_wal* w);
 int defer_host_wal_read(const char* path, defer_host_wal_header* h, uint32_t* history,
                         size_t* n_history, uint64_t* rng_word_pos, int* torn_tail);
 
+/* ------------------------------------------------------ checkpoint format */
+
+/* DeferCheckpoint (checkpoint.rs:26-37); the history is passed separately. */
+typedef struct defer_host_checkpoint_header {
+  uint8_t model_signature[32];
+  uint8_t base_seed[32];
+  float temperature;
+  uint32_t prompt_len;
+  uint64_t rng_word_pos; /* u128 in the file; the high half is 0 */
+} defer_host_checkpoint_header;
+
+/* DeferCheckpoint::save (checkpoint.rs:86-97): the 112 + 4n bytes of
+ * to_bytes (checkpoint.rs:44-57) written to `path` with its extension
+ * replaced by "ckpt.tmp", synced, then renamed over `path`. */
+int defer_host_checkpoint_save(const char* path, const defer_host_checkpoint_header* h,
+                               const uint32_t* history, size_t n);
+/* DeferCheckpoint::load (checkpoint.rs:59-84, 99-101). Call with history ==
+ * NULL to learn *n_history, then again with a buffer of that size. */
+int defer_host_checkpoint_load(const char* path, defer_host_checkpoint_header* h,
+                               uint32_t* history, size_t* n_history);
+
 /* --------------------------------------------------------------- session */
 
 typedef struct defer_host_session defer_host_session;
@@ -117,6 +139,17 @@ int defer_host_session_checkout(const defer_gpu_model* m, const uint8_t base_see
                                 float temperature, const uint32_t* history, size_t n_history,
                                 uint32_t prompt_len, uint64_t rng_word_pos, uint32_t capacity,
                                 defer_host_session** out);
+
+/* Session::checkpoint (engine.rs:223-232): the session's header fields with
+ * the loaded model's signature (the history: defer_host_session_history). */
+int defer_host_session_checkpoint(const defer_host_session* s, const uint8_t model_signature[32],
+                                  defer_host_checkpoint_header* h);
+/* Session::checkout (engine.rs:241-274) of a checkpoint file: the model
+ * signature must match (the reference's "model signature mismatch" message),
+ * then defer_host_session_checkout. */
+int defer_host_session_checkout_file(const defer_gpu_model* m, const uint8_t model_signature[32],
+                                     const char* path, uint32_t capacity,
+                                     defer_host_session** out);
 
 #ifdef __cplusplus
 }

@@ -216,3 +216,34 @@ def test_8b_shape_head_dim_128_untied_vs_oracle():
     a.close()
     b.close()
     gm.close()
+
+
+def test_checkpoint_file_checkout_rebuilds_session(tiny, tmp_path):
+    """Session::checkpoint -> file -> Session::checkout (engine.rs:223-274):
+    same history, rng position, cache and logits; a wrong model signature and
+    a tampered record are refused with the reference's messages."""
+    cfg, w, gm, om = tiny
+    say("tiny: generate 30 at T=0.9, checkpoint to a file, checkout from it")
+    sig = H.sha256(b"".join(x.tobytes() for x in w))
+    live = H.Session(gm, H.seed_from_u64(77), 0.9)
+    live.prompt([9, 8, 7, 6])
+    live.generate(30)
+    p = str(tmp_path / "s.ckpt")
+    live.checkpoint(sig, p)
+    rep = H.Session.checkout_file(gm, sig, p)
+    assert rep.history == live.history and rep.prompt_len == 4
+    assert rep.rng_word_pos == live.rng_word_pos == 30
+    assert np.array_equal(rep.cache.last_logits().view(np.uint32),
+                          live.cache.last_logits().view(np.uint32))
+    for x, y in zip(rep.cache.read(1), live.cache.read(1)):
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
+    assert rep.step() == live.step()
+    with pytest.raises(H.DeferHostError, match="model signature mismatch"):
+        H.Session.checkout_file(gm, bytes(32), p)
+    ck = H.Checkpoint.load(p)
+    bad = list(ck["history"])
+    bad[15] = (bad[15] + 1) % cfg["vocab_size"]
+    H.Checkpoint.save(p, sig, ck["base_seed"], ck["temperature"], ck["prompt_len"],
+                      ck["rng_word_pos"], bad)
+    with pytest.raises(H.Divergence, match=f"at position 15, checkpoint recorded {bad[15]}"):
+        H.Session.checkout_file(gm, sig, p)

@@ -156,3 +156,57 @@ def test_wal_greedy_records_keep_rng_position(tmp_path):
     w.close()
     log = H.Wal.read(p)
     assert log["history"] == [1, 2, 3, 4, 5] and log["rng_word_pos"] == 0
+
+
+# ------------------------------------------------------------- checkpoints
+
+def test_checkpoint_roundtrip_and_corruption(tmp_path):  # checkpoint.rs:142-156
+    p = str(tmp_path / "c.ckpt")
+    H.Checkpoint.save(p, bytes([7] * 32), bytes([9] * 32), 0.7, 2, 2, [1, 2, 3, 40000])
+    c = H.Checkpoint.load(p)
+    assert c == {"model_signature": bytes([7] * 32), "base_seed": bytes([9] * 32),
+                 "temperature": float(np.float32(0.7)), "prompt_len": 2, "rng_word_pos": 2,
+                 "history": [1, 2, 3, 40000]}
+    b = bytearray(open(p, "rb").read())
+    b[50] ^= 1
+    open(p, "wb").write(bytes(b))
+    with pytest.raises(H.DeferHostError, match="checksum mismatch"):
+        H.Checkpoint.load(p)
+
+
+def test_checkpoint_byte_layout(tmp_path):  # checkpoint.rs:4-16, 44-57
+    p = str(tmp_path / "s.ckpt")
+    hist = [5, 6, 7, 8, 9]
+    H.Checkpoint.save(p, SIG, SEED, 0.8, 3, 2, hist)
+    b = open(p, "rb").read()
+    assert len(b) == 112 + 4 * len(hist)
+    assert b[:8] == b"DEFERCKP" and struct.unpack_from("<I", b, 8)[0] == 1
+    assert b[12:44] == SIG and b[44:76] == SEED
+    assert struct.unpack_from("<f", b, 76)[0] == np.float32(0.8)
+    assert struct.unpack_from("<I", b, 80)[0] == 3
+    assert int.from_bytes(b[84:100], "little") == 2
+    assert struct.unpack_from("<Q", b, 100)[0] == len(hist)
+    assert list(struct.unpack_from("<5I", b, 108)) == hist
+    assert struct.unpack_from("<I", b, len(b) - 4)[0] == zlib.crc32(b[:-4])
+    assert not os.path.exists(str(tmp_path / "s.ckpt.tmp"))  # written, synced, renamed
+
+
+def test_checkpoint_rejects_malformed_files(tmp_path):  # checkpoint.rs:59-84
+    p = str(tmp_path / "m.ckpt")
+    H.Checkpoint.save(p, SIG, SEED, 0.5, 1, 1, [4, 5])
+    good = open(p, "rb").read()
+
+    def with_crc(body):
+        return body + struct.pack("<I", zlib.crc32(body))
+
+    cases = [
+        (b"NOTACKPT" + good[8:], "not a defer checkpoint"),
+        (with_crc(good[:8] + struct.pack("<I", 2) + good[12:-4]), "unsupported checkpoint version"),
+        (with_crc(good[:100] + struct.pack("<Q", 3) + good[108:-4]), "length mismatch"),
+        (with_crc(good[:80] + struct.pack("<I", 3) + good[84:-4]), "prompt_len exceeds history"),
+        (good[:60], "not a defer checkpoint"),
+    ]
+    for data, msg in cases:
+        open(p, "wb").write(data)
+        with pytest.raises(H.DeferHostError, match=msg):
+            H.Checkpoint.load(p)
