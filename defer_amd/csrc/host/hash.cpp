@@ -2,6 +2,7 @@
 // cache fingerprint (crc32.rs:4-28, sha256.rs:15-134 of the reference).
 #include <string.h>
 
+#include "common.h"
 #include "defer_host.h"
 
 namespace {
@@ -66,19 +67,39 @@ extern "C" uint32_t defer_host_crc32(const uint8_t* data, size_t n) {
   return c ^ 0xFFFFFFFFu;
 }
 
-extern "C" void defer_host_sha256(const uint8_t* data, size_t n, uint8_t out[32]) {
+namespace dh {
+
+Sha256::Sha256() : nbuf(0), total(0) {
   // FIPS 180-4 section 5.3.3 initial hash value.
-  uint32_t h[8] = {0x6a09e667, 0xbb67ae85, 0x3c6ef372, 0xa54ff53a,
-                   0x510e527f, 0x9b05688c, 0x1f83d9ab, 0x5be0cd19};
-  size_t i = 0;
-  for (; i + 64 <= n; i += 64) sha_block(h, data + i);
+  static const uint32_t h0[8] = {0x6a09e667, 0xbb67ae85, 0x3c6ef372, 0xa54ff53a,
+                                 0x510e527f, 0x9b05688c, 0x1f83d9ab, 0x5be0cd19};
+  memcpy(h, h0, sizeof(h));
+}
+
+void Sha256::update(const uint8_t* data, size_t n) {
+  total += n;
+  if (nbuf) {
+    const size_t k = n < 64 - nbuf ? n : 64 - nbuf;
+    memcpy(buf + nbuf, data, k);
+    nbuf += k;
+    data += k;
+    n -= k;
+    if (nbuf < 64) return;
+    sha_block(h, buf);
+    nbuf = 0;
+  }
+  for (; n >= 64; n -= 64, data += 64) sha_block(h, data);
+  memcpy(buf, data, n);
+  nbuf = n;
+}
+
+void Sha256::finish(uint8_t out[32]) {
+  const uint64_t bits = total * 8u;
   uint8_t tail[128];
-  const size_t rem = n - i;
-  memcpy(tail, data + i, rem);
-  tail[rem] = 0x80;
-  const size_t tl = rem + 9 <= 64 ? 64 : 128;
-  memset(tail + rem + 1, 0, tl - rem - 1);
-  const uint64_t bits = (uint64_t)n * 8u;
+  memcpy(tail, buf, nbuf);
+  tail[nbuf] = 0x80;
+  const size_t tl = nbuf + 9 <= 64 ? 64 : 128;
+  memset(tail + nbuf + 1, 0, tl - nbuf - 1);
   for (int k = 0; k < 8; ++k) tail[tl - 1 - k] = (uint8_t)(bits >> (8 * k));
   for (size_t o = 0; o < tl; o += 64) sha_block(h, tail + o);
   for (int k = 0; k < 8; ++k) {
@@ -87,4 +108,12 @@ extern "C" void defer_host_sha256(const uint8_t* data, size_t n, uint8_t out[32]
     out[4 * k + 2] = (uint8_t)(h[k] >> 8);
     out[4 * k + 3] = (uint8_t)h[k];
   }
+}
+
+}  // namespace dh
+
+extern "C" void defer_host_sha256(const uint8_t* data, size_t n, uint8_t out[32]) {
+  dh::Sha256 s;
+  s.update(data, n);
+  s.finish(out);
 }

@@ -25,6 +25,7 @@ E_WAL = 3
 E_CHECKPOINT = 4
 E_DIVERGENCE = 5
 E_GPU = 6
+E_MODEL = 7
 
 
 class DeferHostError(RuntimeError):
@@ -99,6 +100,22 @@ def lib() -> ctypes.CDLL:
     L.defer_host_checkpoint_load.argtypes = [ctypes.c_char_p, P(WalHeader), vp, P(sz)]
     L.defer_host_session_checkpoint.argtypes = [vp, u8p, P(WalHeader)]
     L.defer_host_session_checkout_file.argtypes = [vp, u8p, ctypes.c_char_p, u32, P(vp)]
+    L.defer_host_st_open.argtypes = [ctypes.c_char_p, P(vp)]
+    L.defer_host_st_close.argtypes = [vp]
+    L.defer_host_st_close.restype = None
+    L.defer_host_st_count.argtypes = [vp]
+    L.defer_host_st_count.restype = sz
+    L.defer_host_st_name.argtypes = [vp, sz]
+    L.defer_host_st_name.restype = ctypes.c_char_p
+    L.defer_host_st_shape.argtypes = [vp, sz, P(u64), sz]
+    L.defer_host_st_shape.restype = sz
+    L.defer_host_st_data.argtypes = [vp, sz, P(sz)]
+    L.defer_host_st_data.restype = ctypes.POINTER(ctypes.c_float)
+    L.defer_host_st_meta.argtypes = [vp, ctypes.c_char_p]
+    L.defer_host_st_meta.restype = ctypes.c_char_p
+    L.defer_host_st_signature.argtypes = [vp, u8p]
+    L.defer_host_st_signature.restype = None
+    L.defer_host_model_load.argtypes = [ctypes.c_char_p, u32, P(vp), vp, u8p]
     _lib = L
     return L
 
@@ -212,6 +229,47 @@ class Wal:
             "rng_word_pos": int(rng.value),
             "torn_tail": bool(torn.value),
         }
+
+
+def read_safetensors(path: str) -> dict:
+    """SafeTensors::load (safetensors.rs:142-237) through the C++ reader:
+    {"names": [...on-disk order], "tensors": {name: f32 array}, "metadata":
+    {...} for the keys asked, "signature": SHA-256 of the file}."""
+    h = ctypes.c_void_p()
+    _check(lib().defer_host_st_open(path.encode(), ctypes.byref(h)))
+    try:
+        names, tensors = [], {}
+        for i in range(lib().defer_host_st_count(h)):
+            name = lib().defer_host_st_name(h, i).decode()
+            dims = (ctypes.c_uint64 * 8)()
+            rank = lib().defer_host_st_shape(h, i, dims, 8)
+            n = ctypes.c_size_t()
+            ptr = lib().defer_host_st_data(h, i, ctypes.byref(n))
+            arr = np.ctypeslib.as_array(ptr, shape=(n.value,)).copy() if n.value else np.zeros(0, np.float32)
+            tensors[name] = arr.reshape([int(dims[k]) for k in range(rank)])
+            names.append(name)
+        sig = (ctypes.c_uint8 * 32)()
+        lib().defer_host_st_signature(h, sig)
+        meta = lib().defer_host_st_meta(h, b"defer.config")
+        return {"names": names, "tensors": tensors, "signature": bytes(sig),
+                "defer.config": meta.decode() if meta else None}
+    finally:
+        lib().defer_host_st_close(h)
+
+
+def load_model(path: str, max_seq_len: int = 0):
+    """Model::load (model.rs:285-298): (GpuModel, config dict, signature)."""
+    from . import gpu
+
+    h = ctypes.c_void_p()
+    cfg = gpu.Config()
+    sig = (ctypes.c_uint8 * 32)()
+    _check(lib().defer_host_model_load(path.encode(), int(max_seq_len), ctypes.byref(h),
+                                       ctypes.byref(cfg), sig))
+    m = gpu.GpuModel.__new__(gpu.GpuModel)
+    m.cfg = cfg
+    m._h = h
+    return m, cfg.to_dict(), bytes(sig)
 
 
 class Checkpoint:

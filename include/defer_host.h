@@ -13,6 +13,8 @@
  *   defer_host_words_per_sample sampler::words_per_sample        sampler.rs:15-21
  *   defer_host_wal_*            WalHeader / WalWriter / WalLog   wal.rs:8-255
  *   defer_host_checkpoint_*     DeferCheckpoint                  checkpoint.rs:4-136
+ *   defer_host_st_*             SafeTensors::load                safetensors.rs:142-237
+ *   defer_host_model_load       Model::load / Config::from_json  model.rs:41-118, 285-347
  *   defer_host_session_*        Session                          engine.rs:23-137, 241-274
  */
 #ifndef DEFER_HOST_H
@@ -34,6 +36,7 @@ extern "C" {
 #define DEFER_HOST_E_CHECKPOINT 4  /* checkpoint does not fit the model (DeferError::Checkpoint) */
 #define DEFER_HOST_E_DIVERGENCE 5  /* replay re-sampled another token (DeferError::Divergence) */
 #define DEFER_HOST_E_GPU 6         /* a libdefer_gpu call failed (its message is kept) */
+#define DEFER_HOST_E_MODEL 7       /* malformed model file or config (DeferError::Model) */
 
 /* Thread-local description of the last failing call. */
 const char* defer_host_last_error(void);
@@ -109,6 +112,34 @@ int defer_host_checkpoint_save(const char* path, const defer_host_checkpoint_hea
  * NULL to learn *n_history, then again with a buffer of that size. */
 int defer_host_checkpoint_load(const char* path, defer_host_checkpoint_header* h,
                                uint32_t* history, size_t* n_history);
+
+/* ------------------------------------------------------------ model file */
+
+typedef struct defer_host_st defer_host_st;
+
+/* SafeTensors::load (safetensors.rs:142-237): one front-to-back pass, every
+ * byte hashed (SHA-256 = the model signature), F32 / F16 / BF16 / F64
+ * tensors converted exactly to f32. The accessors index tensors in on-disk
+ * order; the pointers live until defer_host_st_close. */
+int defer_host_st_open(const char* path, defer_host_st** out);
+void defer_host_st_close(defer_host_st* st);
+size_t defer_host_st_count(const defer_host_st* st);
+const char* defer_host_st_name(const defer_host_st* st, size_t i);
+/* Writes up to max_dims dimensions; returns the rank. */
+size_t defer_host_st_shape(const defer_host_st* st, size_t i, uint64_t* dims, size_t max_dims);
+const float* defer_host_st_data(const defer_host_st* st, size_t i, size_t* n);
+/* The __metadata__ string for `key`, or NULL. */
+const char* defer_host_st_meta(const defer_host_st* st, const char* key);
+void defer_host_st_signature(const defer_host_st* st, uint8_t out[32]);
+
+/* Model::load (model.rs:285-298): the file's tensors, the config from its
+ * "defer.config" metadata or config.json beside it (Config::from_json,
+ * model.rs:41-118, with the reference's defaults and inferences), the
+ * tensors in the order of model.rs:301-347, then defer_gpu_model_create.
+ * max_seq_len != 0 overrides max_position_embeddings. cfg_out and
+ * signature (the file's SHA-256) may be NULL. */
+int defer_host_model_load(const char* path, uint32_t max_seq_len, defer_gpu_model** out,
+                          defer_gpu_config* cfg_out, uint8_t signature[32]);
 
 /* --------------------------------------------------------------- session */
 

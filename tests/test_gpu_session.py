@@ -247,3 +247,43 @@ def test_checkpoint_file_checkout_rebuilds_session(tiny, tmp_path):
                       ck["rng_word_pos"], bad)
     with pytest.raises(H.Divergence, match=f"at position 15, checkpoint recorded {bad[15]}"):
         H.Session.checkout_file(gm, sig, p)
+
+
+def test_model_load_from_safetensors(tmp_path):
+    """Model::load (model.rs:285-347): the file's tensors by name, the config
+    from its defer.config metadata (or config.json), the signature = SHA-256
+    of the file; logits bit-identical to the model built from the arrays."""
+    import hashlib
+    import json
+    import safetensors.numpy as stn
+    cfg = synthetic.CONFIGS["tiny"]
+    w = synthetic.make_weights(cfg, 31)
+    names = [n for n, _, _ in synthetic.tensor_specs(cfg)]
+    hf = {"vocab_size": cfg["vocab_size"], "hidden_size": cfg["hidden_size"],
+          "intermediate_size": cfg["intermediate_size"], "num_hidden_layers": cfg["num_layers"],
+          "num_attention_heads": cfg["num_heads"], "num_key_value_heads": cfg["num_kv_heads"],
+          "head_dim": cfg["head_dim"], "rms_norm_eps": cfg["rms_norm_eps"],
+          "rope_theta": cfg["rope_theta"], "max_position_embeddings": cfg["max_seq_len"],
+          "tie_word_embeddings": bool(cfg["tie_word_embeddings"]), "hidden_act": "silu"}
+    p = str(tmp_path / "model.safetensors")
+    stn.save_file(dict(zip(names, w)), p, metadata={"defer.config": json.dumps(hf)})
+    say("tiny: load from a safetensors file vs the arrays")
+    gm, lcfg, sig = H.load_model(p)
+    assert sig == hashlib.sha256(open(p, "rb").read()).digest()
+    ref = G.GpuModel(G.Config.from_dict(cfg), w)
+    a, b = gm.new_cache(64), ref.new_cache(64)
+    for t in (4, 40, 200):
+        la, lb = gm.forward(t, a), ref.forward(t, b)
+        assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+    # F16 tensors with the config in config.json beside the file
+    d = tmp_path / "half"
+    d.mkdir()
+    p2 = str(d / "model.safetensors")
+    stn.save_file({n: x.astype(np.float16) for n, x in zip(names, w)}, p2)
+    (d / "config.json").write_text(json.dumps(hf))
+    gm2, lcfg2, _ = H.load_model(p2)
+    assert lcfg2 == lcfg
+    ref2 = G.GpuModel(G.Config.from_dict(cfg), [x.astype(np.float16).astype(np.float32) for x in w])
+    c2, d2 = gm2.new_cache(64), ref2.new_cache(64)
+    la, lb = gm2.forward(9, c2), ref2.forward(9, d2)
+    assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))

@@ -210,3 +210,78 @@ def test_checkpoint_rejects_malformed_files(tmp_path):  # checkpoint.rs:59-84
         open(p, "wb").write(data)
         with pytest.raises(H.DeferHostError, match=msg):
             H.Checkpoint.load(p)
+
+
+# ------------------------------------------------------------- model files
+
+def _st_file(path, entries, metadata=None):
+    """A safetensors file from (name, dtype, shape, raw bytes), in order."""
+    import json
+    hdr, off = {}, 0
+    if metadata:
+        hdr["__metadata__"] = metadata
+    for name, dt, shape, raw in entries:
+        hdr[name] = {"dtype": dt, "shape": list(shape), "data_offsets": [off, off + len(raw)]}
+        off += len(raw)
+    h = json.dumps(hdr).encode()
+    h += b" " * (-len(h) % 8)
+    blob = struct.pack("<Q", len(h)) + h + b"".join(e[3] for e in entries)
+    open(path, "wb").write(blob)
+    return blob
+
+
+def test_safetensors_half_conversions(tmp_path):  # safetensors.rs:305-313
+    p = str(tmp_path / "h.safetensors")
+    f16 = struct.pack("<5H", 0x3C00, 0xC000, 0x7BFF, 0x0001, 0x7C00)
+    bf16 = struct.pack("<2H", 0x3F80, 0xC2F7)
+    f64 = struct.pack("<2d", 0.1, -3.5)
+    _st_file(p, [("a", "F16", (5,), f16), ("b", "BF16", (2,), bf16), ("c", "F64", (2,), f64)])
+    r = H.read_safetensors(p)
+    a = r["tensors"]["a"]
+    assert a[0] == 1.0 and a[1] == -2.0 and a[2] == 65504.0 and a[3] == np.float32(5.9604645e-8)
+    assert np.isinf(a[4])
+    assert r["tensors"]["b"][0] == 1.0 and r["tensors"]["b"][1] == np.float32(-123.5)
+    assert list(r["tensors"]["c"]) == [np.float32(0.1), -3.5]
+    # every f16 value against numpy's exact widening
+    allh = np.arange(0, 65536, dtype=np.uint32).astype(np.uint16)
+    _st_file(p, [("h", "F16", (65536,), allh.tobytes())])
+    got = H.read_safetensors(p)["tensors"]["h"]
+    want = allh.view(np.float16).astype(np.float32)
+    same = (got.view(np.uint32) == want.view(np.uint32)) | (np.isnan(got) & np.isnan(want))
+    assert same.all()
+
+
+def test_safetensors_order_metadata_signature(tmp_path):  # safetensors.rs:142-237
+    import safetensors.numpy as stn
+    p = str(tmp_path / "m.safetensors")
+    rng = np.random.default_rng(0)
+    t = {"z.weight": rng.standard_normal((3, 4), dtype=np.float32),
+         "a.weight": rng.standard_normal((5,), dtype=np.float32),
+         "m.weight": rng.standard_normal((2, 2, 2), dtype=np.float32).astype(np.float16)}
+    stn.save_file(t, p, metadata={"defer.config": '{"hidden_size": 4}'})
+    r = H.read_safetensors(p)
+    assert r["signature"] == hashlib.sha256(open(p, "rb").read()).digest()
+    assert r["defer.config"] == '{"hidden_size": 4}'
+    for k, v in t.items():
+        assert np.array_equal(r["tensors"][k], v.astype(np.float32))
+    assert sorted(r["names"]) == sorted(t)
+
+
+def test_safetensors_rejects_malformed(tmp_path):
+    p = str(tmp_path / "bad.safetensors")
+    raw = np.zeros(4, np.float32).tobytes()
+    cases = [
+        ([("a", "F32", (5,), raw)], "size mismatch for tensor a"),
+        ([("a", "I8", (4,), raw[:4])], "unsupported safetensors dtype I8"),
+    ]
+    for entries, msg in cases:
+        _st_file(p, entries)
+        with pytest.raises(H.DeferHostError, match=msg):
+            H.read_safetensors(p)
+    open(p, "wb").write(struct.pack("<Q", 1 << 40) + b"{}")
+    with pytest.raises(H.DeferHostError, match="invalid safetensors header length"):
+        H.read_safetensors(p)
+    blob = _st_file(p, [("a", "F32", (4,), raw)])
+    open(p, "wb").write(blob[:-3])  # data shorter than the offsets claim
+    with pytest.raises(H.DeferHostError, match="out of range tensor a"):
+        H.read_safetensors(p)
