@@ -3,13 +3,13 @@
 //
 // Batch invariance. Every output element of every matrix product is computed
 // in the one order the one-token path uses (device.h, "Row dot products"):
-// 64 lane-strided segments s, segment s holding the elements
-// 256*i + 4*s + c (i ascending, c = 0..3), each segment a chain of fused
-// multiply-adds from +0, then the complete binary tree over the 64 segment
-// sums. v_mfma_f32_16x16x4_f32 computes, for each output, exactly
+// 16 segments s, segment s holding the elements 64*i + 4*s + c (i
+// ascending, c = 0..3), each segment a chain of fused multiply-adds from +0,
+// then the complete binary tree over the 16 segment sums.
+// v_mfma_f32_16x16x4_f32 computes, for each output, exactly
 // fma(a3,b3,fma(a2,b2,fma(a1,b1,fma(a0,b0,c)))) -- four links of such a
-// chain -- so chaining MFMAs over a segment's chunks reproduces its sum bit
-// for bit, and the tree is then formed from the 64 segment accumulators. The
+// chain -- so chaining one MFMA per chunk reproduces a segment's sum bit for
+// bit, and the tree is then formed from the 16 segment accumulators. The
 // result of a row depends on that row's inputs only: not on B, not on the
 // other rows, not on the tiling. Everything else a row goes through
 // (RMSNorm, RoPE, attention, combine, residuals, activation, sampling) runs
@@ -25,15 +25,17 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 // ------------------------------------------------------------ panel layout
 //
 // GEMM operands are stored as panels: a matrix of R rows and K columns
-// becomes [ceil(R/16)][nch = ceil(K/256)][4 slices][64 lanes][16 floats],
-// lane l = r + 16c of slice w of chunk i holding element
-// (16*T + r, 256*i + 64*w + 4*s + c) for s = 0..15, zero outside the
-// matrix. That is the MFMA operand (A for weights, B for activations) of
-// segment 16w + s: one wave reads its slice of a chunk as 4 KB contiguous.
+// becomes [ceil(R/16)][nch = ceil(K/64)][4 quarters][64 lanes][4 floats],
+// float u of quarter q of lane l = r + 16c in chunk i of tile T holding
+// element (16*T + r, 64*i + 4*(4q + u) + c), zero outside the matrix. Lane l's
+// float u of quarter q is its MFMA operand (A for weights, B for activations)
+// of segment 4q + u; a (tile, chunk) is 4 KB, each quarter 1 KB contiguous,
+// so one 16-byte-per-lane load moves a quarter, and lanes read LDS copies of
+// it at consecutive addresses.
 
-constexpr uint32_t PANEL_TILE = 4096;  // floats per (16-row tile, chunk)
+constexpr uint32_t PANEL_TILE = 1024;  // floats per (16-row tile, chunk)
 
-__host__ __device__ inline uint32_t panel_chunks(uint32_t K) { return (K + 255) / 256; }
+__host__ __device__ inline uint32_t panel_chunks(uint32_t K) { return (K + 63) / 64; }
 __host__ __device__ inline size_t panel_floats(uint32_t R, uint32_t K) {
   return (size_t)((R + 15) / 16) * panel_chunks(K) * PANEL_TILE;
 }
@@ -47,12 +49,12 @@ __global__ void k_to_panel(const float* __restrict__ src0, const float* __restri
   const uint32_t nch = panel_chunks(K);
   for (size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x; e < n;
        e += (size_t)gridDim.x * blockDim.x) {
-    const uint32_t s = (uint32_t)(e % 16), l = (uint32_t)((e / 16) % 64),
-                   w = (uint32_t)((e / 1024) % 4);
+    const uint32_t u = (uint32_t)(e % 4), l = (uint32_t)((e / 4) % 64),
+                   q = (uint32_t)((e / 256) % 4);
     const size_t rest = e / PANEL_TILE;
     const uint32_t i = (uint32_t)(rest % nch);
     const size_t r = (rest / nch) * 16 + l % 16;
-    const uint32_t k = 256 * i + 64 * w + 4 * s + l / 16;
+    const uint32_t k = 64 * i + 4 * (4 * q + u) + l / 16;
     float v = 0.0f;
     if (r < R && k < K) v = r < R0 ? src0[r * ld + k] : src1[(r - R0) * ld + k];
     dst[e] = v;
@@ -77,49 +79,92 @@ __device__ __forceinline__ f4v tree16(const f4v* a) {
   return (q[0] + q[1]) + (q[2] + q[3]);
 }
 
-// Y[b][o] = W[o] . X[b] for o < M, b < B, K columns. Workgroup (T, g): rows
-// 16T.., column tiles g*TN..; wave w chains segments 16w..16w+15 of every
-// output of the block (its slice of each chunk), reduces them with tree16
-// (the first four levels of the 64-leaf tree), and the four waves' sums
-// are added as (w0 + w1) + (w2 + w3) -- the remaining two levels.
+// Chunks of operands in flight through LDS, and the LDS a launch needs.
+constexpr uint32_t GEMM_STAGES = 4;
+__host__ __device__ constexpr uint32_t gemm_lds_bytes(uint32_t tn) {
+  return GEMM_STAGES * (4 + tn) * PANEL_TILE * 4;
+}
+
+// Y[b][o] = W[o] . X[b] for o < M, b < B, K columns. Workgroup (x, y): wave
+// w owns row tile 4x + w and every wave the column tiles y*TN .. y*TN+TN-1,
+// all 16 segments of each of its outputs in its own accumulators, reduced
+// with tree16 at the end. A chunk's operands (the four row tiles and the TN
+// column tiles, 4 KB each) are copied into LDS by all four waves together
+// (16 bytes per lane straight from memory into LDS), GEMM_STAGES - 1
+// chunks ahead of their use, so each activation tile is read from memory
+// once per workgroup and shared by the four waves.
 template <int TN, uint32_t OUT>
 __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ Wp, uint32_t M, uint32_t K,
                                               const float* __restrict__ Xp, uint32_t B,
                                               float* __restrict__ Y, uint32_t ldy,
                                               const float* __restrict__ scale,
                                               const uint32_t* __restrict__ gen) {
-  __shared__ f4v red[4][TN][64];
+  extern __shared__ float4 gsm[];  // [GEMM_STAGES][4 + TN tiles][4 quarters][64 lanes]
+  constexpr uint32_t NT = 4 + TN, NLD = 4 + TN;  // tiles per stage; loads per wave per stage
   const uint32_t wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-  const uint32_t T = blockIdx.x, C0 = blockIdx.y * TN;
-  const uint32_t nch = panel_chunks(K), nct = (B + 15) / 16;
+  const uint32_t nch = panel_chunks(K), nrt = (M + 15) / 16, nct = (B + 15) / 16;
+  const uint32_t T = blockIdx.x * 4 + wave, C0 = blockIdx.y * TN;
+  // Tiles past the last one load a real tile (never used), so every wave
+  // issues the same number of loads per stage.
+  const float* wsrc = Wp + (size_t)min(T, nrt - 1) * nch * PANEL_TILE + lane * 4;
+  const float* xsrc[TN];
+#pragma unroll
+  for (int t = 0; t < TN; ++t) xsrc[t] = Xp + (size_t)min(C0 + t, nct - 1) * nch * PANEL_TILE + lane * 4;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)gsm;
+  // Chunk i into stage st: this wave's row tile (4 quarters) and quarters
+  // wave, wave + 4, ... of the column tiles.
+  auto issue = [&](uint32_t i, uint32_t st) {
+    const uint32_t sb = lds0 + st * NT * PANEL_TILE * 4;
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q)
+      dma16(wsrc + (size_t)i * PANEL_TILE + q * 256, sb + (wave * 4 + q) * 1024);
+#pragma unroll
+    for (uint32_t u = 0; u < TN; ++u) {
+      const uint32_t idx = wave + 4 * u, t = idx / 4, q = idx % 4;
+      dma16(xsrc[t] + (size_t)i * PANEL_TILE + q * 256, sb + ((4 + t) * 4 + q) * 1024);
+    }
+  };
   f4v acc[TN][16];
 #pragma unroll
   for (int t = 0; t < TN; ++t)
 #pragma unroll
     for (int s = 0; s < 16; ++s) acc[t][s] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
-  const float* wp = Wp + ((size_t)T * nch * 4 + wave) * 1024 + lane * 16;
-  const float* xp[TN];
+  for (uint32_t i = 0; i + 1 < GEMM_STAGES && i < nch; ++i) issue(i, i);
+  // Chunk i's operands from its stage, once it has landed in every wave.
+  auto operands = [&](uint32_t i, float4 (&a)[4], float4 (&b)[TN][4]) {
+    // Chunk i has landed once at most the later chunks' loads are in flight;
+    // the barrier makes that true of every wave, and every wave is then done
+    // with chunk i - 1's stage, which the next request overwrites.
+    stage_wait(min(GEMM_STAGES - 2, nch - 1 - i) * NLD);
+    __syncthreads();
+    if (i + GEMM_STAGES - 1 < nch) issue(i + GEMM_STAGES - 1, (i + GEMM_STAGES - 1) % GEMM_STAGES);
+    const float4* sa = gsm + (i % GEMM_STAGES) * NT * 256;
 #pragma unroll
-  for (int t = 0; t < TN; ++t) {
-    const uint32_t ct = min(C0 + t, nct - 1);  // past the last tile: read a real one, never used
-    xp[t] = Xp + ((size_t)ct * nch * 4 + wave) * 1024 + lane * 16;
-  }
-  // Operands of chunk i for this wave, loaded one chunk ahead of their use.
-  const uint32_t nmine = K > 64 * wave ? (K - 64 * wave + 255) / 256 : 0;  // chunks with a slice here
-  auto load = [&](uint32_t i, float4 (&a)[4], float4 (&b)[TN][4]) {
-    const float4* wa = reinterpret_cast<const float4*>(wp + (size_t)i * PANEL_TILE);
+    for (int q = 0; q < 4; ++q) a[q] = sa[(wave * 4 + q) * 64 + lane];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) a[q] = wa[q];
+    for (int t = 0; t < TN; ++t)
 #pragma unroll
-    for (int t = 0; t < TN; ++t) {
-      const float4* xb = reinterpret_cast<const float4*>(xp[t] + (size_t)i * PANEL_TILE);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) b[t][q] = xb[q];
-    }
+      for (int q = 0; q < 4; ++q) b[t][q] = sa[((4 + t) * 4 + q) * 64 + lane];
   };
-  auto mfmas = [&](uint32_t i, const float4 (&a)[4], const float4 (&b)[TN][4]) {
-    const uint32_t kb = 256 * i + 64 * wave;
-    const uint32_t ns = min(16u, (K - kb + 3) / 4);  // segments with an element in this slice
+  const uint32_t nfull = K / 64;
+  for (uint32_t i = 0; i < nfull; ++i) {
+    float4 a[4], b[TN][4];
+    operands(i, a, b);
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      const float av = (&a[s / 4].x)[s % 4];
+#pragma unroll
+      for (int t = 0; t < TN; ++t)
+        acc[t][s] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, (&b[t][s / 4].x)[s % 4], acc[t][s], 0,
+                                                         0, 0);
+    }
+  }
+  if (nfull < nch) {
+    // A last, partial chunk: the segments past K are left alone (their zero
+    // padding would still turn a -0 sum into +0).
+    float4 a[4], b[TN][4];
+    operands(nfull, a, b);
+    const uint32_t ns = (K - 64 * nfull) / 4;
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
       if ((uint32_t)s < ns) {
@@ -130,24 +175,13 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ Wp, uint
                                                            0, 0, 0);
       }
     }
-  };
-  float4 a0[4], b0[TN][4], a1[4], b1[TN][4];
-  if (nmine > 0) load(0, a0, b0);
-  for (uint32_t i = 0; i < nmine; i += 2) {
-    if (i + 1 < nmine) load(i + 1, a1, b1);
-    mfmas(i, a0, b0);
-    if (i + 1 >= nmine) break;
-    if (i + 2 < nmine) load(i + 2, a0, b0);
-    mfmas(i + 1, a1, b1);
   }
+  if (T >= nrt) return;
 #pragma unroll
-  for (int t = 0; t < TN; ++t) red[wave][t][lane] = tree16(acc[t]);
-  __syncthreads();
-  for (uint32_t idx = threadIdx.x; idx < TN * 64u; idx += 256) {
-    const uint32_t t = idx / 64, l = idx % 64;
-    const f4v r = (red[0][t][l] + red[1][t][l]) + (red[2][t][l] + red[3][t][l]);
-    const uint32_t b = (C0 + t) * 16 + l % 16;
-    const uint32_t o = T * 16 + 4 * (l / 16);
+  for (int t = 0; t < TN; ++t) {
+    const f4v r = tree16(acc[t]);
+    const uint32_t b = (C0 + t) * 16 + lane % 16;
+    const uint32_t o = T * 16 + 4 * (lane / 16);
     if (b >= B) continue;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {

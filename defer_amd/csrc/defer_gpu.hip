@@ -566,6 +566,20 @@ extern "C" int defer_gpu_model_create(const defer_gpu_config* cfg, const float* 
       return cleanup(fail(DEFER_GPU_E_HIP, "LDS attribute (%zu bytes): %s", m->lds_bytes,
                           hipGetErrorString(e)));
   }
+  {
+    const void* gk[] = {(const void*)k_gemm<1, GO_PLAIN>, (const void*)k_gemm<1, GO_RESID>,
+                        (const void*)k_gemm<1, GO_TAG>,   (const void*)k_gemm<2, GO_PLAIN>,
+                        (const void*)k_gemm<2, GO_RESID>, (const void*)k_gemm<2, GO_TAG>,
+                        (const void*)k_gemm<4, GO_PLAIN>, (const void*)k_gemm<4, GO_RESID>,
+                        (const void*)k_gemm<4, GO_TAG>};
+    const int tn[] = {1, 1, 1, 2, 2, 2, 4, 4, 4};
+    for (int i = 0; i < 9; ++i) {
+      e = hipFuncSetAttribute(gk[i], hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)gemm_lds_bytes(tn[i]));
+      if (e != hipSuccess)
+        return cleanup(fail(DEFER_GPU_E_HIP, "LDS attribute (GEMM): %s", hipGetErrorString(e)));
+    }
+  }
   e = hipFuncSetAttribute((const void*)k_b_attn_tile, hipFuncAttributeMaxDynamicSharedMemorySize,
                           (int)attn_tile_lds(MAX_GROUP));
   if (e != hipSuccess)
@@ -1289,19 +1303,25 @@ static int ensure_panels(defer_gpu_model* m) {
   return DEFER_GPU_OK;
 }
 
+template <int TN, uint32_t OUT>
+static void launch_gemm_tn(hipStream_t s, const float* Wp, uint32_t M, uint32_t K, const float* Xp,
+                           uint32_t B, float* Y, uint32_t ldy, const float* scale,
+                           const uint32_t* gen) {
+  const uint32_t nrt = (M + 15) / 16, nct = (B + 15) / 16;
+  k_gemm<TN, OUT><<<dim3((nrt + 3) / 4, (nct + TN - 1) / TN), 256, gemm_lds_bytes(TN), s>>>(
+      Wp, M, K, Xp, B, Y, ldy, scale, gen);
+}
 template <uint32_t OUT>
 static void launch_gemm_out(hipStream_t s, const float* Wp, uint32_t M, uint32_t K, const float* Xp,
                             uint32_t B, float* Y, uint32_t ldy, const float* scale,
                             const uint32_t* gen) {
   const uint32_t nct = (B + 15) / 16;
-  if (nct <= 1) {
-    k_gemm<1, OUT><<<dim3((M + 15) / 16, nct), 256, 0, s>>>(Wp, M, K, Xp, B, Y, ldy, scale, gen);
-  } else if (nct <= 2) {
-    k_gemm<2, OUT><<<dim3((M + 15) / 16, 1), 256, 0, s>>>(Wp, M, K, Xp, B, Y, ldy, scale, gen);
-  } else {
-    k_gemm<4, OUT><<<dim3((M + 15) / 16, (nct + 3) / 4), 256, 0, s>>>(Wp, M, K, Xp, B, Y, ldy,
-                                                                      scale, gen);
-  }
+  if (nct <= 1)
+    launch_gemm_tn<1, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen);
+  else if (nct <= 2)
+    launch_gemm_tn<2, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen);
+  else
+    launch_gemm_tn<4, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen);
 }
 static void launch_gemm(hipStream_t s, uint32_t out, const float* Wp, uint32_t M, uint32_t K,
                         const float* Xp, uint32_t B, float* Y, uint32_t ldy,

@@ -8,8 +8,9 @@
 // the value and its readiness arrive in one access.
 //
 // Determinism. Every reduction below has a fixed shape that depends only on
-// the problem size: lane-strided partials in index order, an xor butterfly
-// across the 64 lanes of a wave, then wave partials summed in wave order.
+// the problem size: chains of fused multiply-adds over fixed element sets in
+// index order, then a fixed tree (an xor butterfly over lanes, wave partials
+// in wave order).
 // Which workgroup computes an output never changes how it is computed, so
 // the persistent kernel and the per-phase kernels give identical bits.
 #pragma once
@@ -235,6 +236,14 @@ __device__ __forceinline__ float4 lds4(const float* p) {
 __device__ __forceinline__ float lds_ld(const float* p) { return *lptr(p); }
 __device__ __forceinline__ void lds_st(float* p, float v) { *lptr(p) = v; }
 
+// p, hidden from the optimiser where it is used: addresses formed from it
+// there (p + constant) are not hoisted into registers kept across the
+// kernel, and their constant parts fold into the LDS instruction's offset.
+__device__ __forceinline__ const float* pin(const float* p) {
+  asm volatile("" : "+v"(p));
+  return p;
+}
+
 __device__ __forceinline__ void mb_put(u64* slot, float v, uint32_t gen) {
   const u64 w = ((u64)gen << 32) | (u64)__float_as_uint(v);
   __hip_atomic_store(gptr(slot), w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -348,38 +357,43 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   return s;
 }
 
-// Row dot products. Lane `lane` owns the float4s at j = 4*lane + 256*k of a
-// row; its partial sum runs over them in ascending j with one fused
-// multiply-add per element, then wave_sum() adds the 64 partials. That order
-// is the same however the loads are scheduled, so the helpers below (all
-// loads of a row issued at once, optionally before the row's input vector is
-// available) all give identical bits.
-constexpr int KF = 6;  // float4 per lane held in registers: rows of up to 1536 floats
+// Row dot products: the one order every matvec of the model uses, whoever
+// computes it (a decode workgroup from LDS or from HBM, or the batched
+// GEMM). A row of K elements is 16 segments, segment s holding the elements
+// 64*i + 4*s + c (i ascending, c = 0..3); each segment is a chain of fused
+// multiply-adds from +0, and the row's value is the complete binary tree over
+// the 16 segment sums. In a wave, lane 16*r + s computes segment s of row r
+// of a quad pass (four rows at once), and group_sum over 16 lanes is the tree.
+__device__ __forceinline__ uint32_t qrow(uint32_t lane) { return lane >> 4; }
+__device__ __forceinline__ uint32_t qseg(uint32_t lane) { return lane & 15u; }
 
+// NF consecutive chunks of one segment held in registers.
 template <int NF>
-struct RowT {
+struct SegT {
   float4 v[NF];
 };
-typedef RowT<KF> Row;
 
+// Chunks i0 .. i0+NF-1 of segment s of the global row w.
 template <int NF>
-__device__ __forceinline__ void row_load(RowT<NF>& r, const float* __restrict__ w, uint32_t K,
-                                         uint32_t lane) {
+__device__ __forceinline__ void seg_load(SegT<NF>& r, const float* __restrict__ w, uint32_t K,
+                                         uint32_t s, uint32_t i0) {
 #pragma unroll
   for (int k = 0; k < NF; ++k) {
-    const uint32_t j = lane * 4 + 256u * k;
+    const uint32_t j = 64u * (i0 + k) + 4u * s;
     if (j < K) r.v[k] = ldg4(w + j);
   }
 }
 
+// The fmas of chunks i0 .. i0+NF-1 (held in r) against the LDS vector x.
 template <int NF>
-__device__ __forceinline__ float row_fma(const RowT<NF>& r, const float* __restrict__ x,
-                                         uint32_t K, uint32_t lane, float acc) {
+__device__ __forceinline__ float seg_fma(const SegT<NF>& r, const float* x, uint32_t K, uint32_t s,
+                                         uint32_t i0, float acc) {
+  const float* xb = pin(x + 64u * i0 + 4u * s);
 #pragma unroll
   for (int k = 0; k < NF; ++k) {
-    const uint32_t j = lane * 4 + 256u * k;
+    const uint32_t j = 64u * (i0 + k) + 4u * s;
     if (j < K) {
-      const float4 xv = lds4(x + j);
+      const float4 xv = lds4(xb + 64 * k);
       acc = fmaf(r.v[k].x, xv.x, acc);
       acc = fmaf(r.v[k].y, xv.y, acc);
       acc = fmaf(r.v[k].z, xv.z, acc);
@@ -389,66 +403,102 @@ __device__ __forceinline__ float row_fma(const RowT<NF>& r, const float* __restr
   return acc;
 }
 
-// Lane partial of w . x given the row's first 256*NF floats already loaded
-// into `r`; longer rows stream the rest segment by segment through the same
-// registers (so `r` is consumed).
+// Segment s of the global row w from chunk i0 on, NF chunks at a time with
+// the next NF in flight, added to acc.
 template <int NF>
-__device__ __forceinline__ float dot_tail(RowT<NF>& r, const float* __restrict__ w,
-                                          const float* __restrict__ x, uint32_t K,
-                                          uint32_t lane) {
-  float acc = row_fma(r, x, K, lane, 0.0f);
-  for (uint32_t base = 256u * NF; base < K; base += 256u * NF) {
-    row_load(r, w + base, K - base, lane);
-    acc = row_fma(r, x + base, K - base, lane, acc);
+__device__ __forceinline__ float seg_stream(const float* __restrict__ w, const float* x, uint32_t K,
+                                            uint32_t s, uint32_t i0, float acc) {
+  const uint32_t nch = (K + 63) / 64;
+  if (i0 >= nch) return acc;
+  SegT<NF> a, b;
+  seg_load(a, w, K, s, i0);
+  for (uint32_t i = i0; i < nch; i += 2 * NF) {
+    if (i + NF < nch) seg_load(b, w, K, s, i + NF);
+    acc = seg_fma(a, x, K, s, i, acc);
+    if (i + NF >= nch) break;
+    if (i + 2 * NF < nch) seg_load(a, w, K, s, i + 2 * NF);
+    acc = seg_fma(b, x, K, s, i + NF, acc);
   }
   return acc;
 }
 
-// Lane partials of two rows w0 . x and w1 . x (same K), the loads of each
-// next segment issued before the fmas of the current one, so a wave keeps two
-// segments of both rows in flight. Same element order as dot_tail.
-template <int NF>
-__device__ __forceinline__ float2 dot2_stream(const float* __restrict__ w0,
-                                              const float* __restrict__ w1,
-                                              const float* __restrict__ x, uint32_t K,
-                                              uint32_t lane) {
-  constexpr uint32_t SEG = 256u * NF;
-  RowT<NF> a0, a1, b0, b1;
-  row_load(a0, w0, K, lane);
-  row_load(a1, w1, K, lane);
-  float acc0 = 0.0f, acc1 = 0.0f;
-  for (uint32_t base = 0; base < K; base += 2 * SEG) {
-    const uint32_t nb = base + SEG;
-    if (nb < K) {
-      row_load(b0, w0 + nb, K - nb, lane);
-      row_load(b1, w1 + nb, K - nb, lane);
+// LDS segment reads four chunks at a time: group g holds the chunks at
+// elements j, j + 64, j + 128, j + 192 (those below K).
+struct SegGroup {
+  float4 w[4], x[4];
+};
+__device__ __forceinline__ void seg_group_load(SegGroup& g, const float* w, const float* x,
+                                               uint32_t K, uint32_t j) {
+  const float* wb = pin(w + j);
+  const float* xb = pin(x + j);
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    if (j + 64 * k < K) {
+      g.w[k] = lds4(wb + 64 * k);
+      g.x[k] = lds4(xb + 64 * k);
     }
-    acc0 = row_fma(a0, x + base, K - base, lane, acc0);
-    acc1 = row_fma(a1, x + base, K - base, lane, acc1);
-    if (nb >= K) break;
-    const uint32_t na = nb + SEG;
-    if (na < K) {
-      row_load(a0, w0 + na, K - na, lane);
-      row_load(a1, w1 + na, K - na, lane);
+}
+__device__ __forceinline__ float seg_group_fma(const SegGroup& g, uint32_t K, uint32_t j, float acc) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    if (j + 64 * k < K) {
+      acc = fmaf(g.w[k].x, g.x[k].x, acc);
+      acc = fmaf(g.w[k].y, g.x[k].y, acc);
+      acc = fmaf(g.w[k].z, g.x[k].z, acc);
+      acc = fmaf(g.w[k].w, g.x[k].w, acc);
     }
-    acc0 = row_fma(b0, x + nb, K - nb, lane, acc0);
-    acc1 = row_fma(b1, x + nb, K - nb, lane, acc1);
+  return acc;
+}
+
+// Segment s of the LDS row w from element j on (j = 64*i0 + 4*s), given
+// the group at j already loaded into a; each next group's reads are issued
+// before the current group's fmas.
+__device__ __forceinline__ float seg_lds_from(SegGroup& a, const float* w, const float* x,
+                                              uint32_t K, uint32_t j, float acc) {
+  SegGroup b;
+#pragma unroll 1
+  for (; j < K; j += 512) {
+    if (j + 256 < K) seg_group_load(b, w, x, K, j + 256);
+    acc = seg_group_fma(a, K, j, acc);
+    if (j + 256 >= K) break;
+    if (j + 512 < K) seg_group_load(a, w, x, K, j + 512);
+    acc = seg_group_fma(b, K, j + 256, acc);
   }
-  return make_float2(acc0, acc1);
+  return acc;
 }
 
-__device__ __forceinline__ float dot_partial(const float* __restrict__ w,
-                                             const float* __restrict__ x, uint32_t K,
-                                             uint32_t lane) {
-  Row r;
-  row_load(r, w, K, lane);
-  return dot_tail(r, w, x, K, lane);
+// Segment s of the LDS row w from chunk i0 on, added to acc.
+__device__ __forceinline__ float seg_lds(const float* w, const float* x, uint32_t K, uint32_t s,
+                                         uint32_t i0, float acc) {
+  const uint32_t j = 64u * i0 + 4u * s;
+  if (j >= K) return acc;
+  SegGroup a;
+  seg_group_load(a, w, x, K, j);
+  return seg_lds_from(a, w, x, K, j, acc);
 }
 
-__device__ __forceinline__ float dot_row(const float* __restrict__ w, const float* __restrict__ x,
-                                         uint32_t K, uint32_t lane) {
-  return wave_sum(dot_partial(w, x, K, lane));
+// Segment s of the global row w given its first NF chunks already in r;
+// longer rows stream the rest NF chunks at a time through r (consumed).
+template <int NF>
+__device__ __forceinline__ float seg_tail(SegT<NF>& r, const float* __restrict__ w, const float* x,
+                                          uint32_t K, uint32_t s) {
+  float acc = seg_fma(r, x, K, s, 0, 0.0f);
+  for (uint32_t i0 = NF; 64u * i0 < K; i0 += NF) {
+    seg_load(r, w, K, s, i0);
+    acc = seg_fma(r, x, K, s, i0, acc);
+  }
+  return acc;
 }
+
+// The four row values of a quad pass from the lanes' segment sums: y[r] is
+// row r's, the same in every lane.
+__device__ __forceinline__ void quad_sums(float p, float (&y)[4]) {
+  const float v = group_sum(p, 16);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) y[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16 * r));
+}
+
+constexpr int KF = 8;  // chunks a streamed segment keeps in flight per buffer (two buffers)
 
 // Norm weights of one vector, the thread's elements i = tid + BLOCK*k.
 constexpr int NWK = 8;  // vectors of up to 8 * BLOCK floats

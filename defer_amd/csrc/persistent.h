@@ -20,6 +20,13 @@ __device__ __forceinline__ bool forward_all(const Args& a, uint32_t tok, uint32_
                                             const Stager& sg) {
   const uint32_t L = shape_dims(a.d).L;
   for (uint32_t l = 0; l < L; ++l) {
+    // Hidden from the optimiser per layer, so values derived from the
+    // workgroup index (item numbers, mailbox and cache addresses) are
+    // recomputed where they are used instead of being hoisted out of the
+    // layer loop and spilled.
+    uint32_t wgl = wg;
+    asm volatile("" : "+s"(wgl));
+    const uint32_t wg = wgl;
     if (!phase_qkv(a, l, tick, pos, tok, wg, G, s, sg)) return false;
     if (!phase_attn(a, l, tick, pos, wg, G, s)) return false;
     if (!phase_comb(a, l, tick, pos, wg, G, s)) return false;

@@ -434,24 +434,8 @@ __device__ __forceinline__ const float* staged_item(const Stager& sg, uint32_t k
   return sg.stg + d.stg_off[kind] + k * kind_rows(kind) * kind_k(d, kind);
 }
 
-// Lane partial of w . x with both in LDS: ascending j, one fma per element
-// (the order row_fma / dot_partial use, so staged and direct rows give the
-// same bits).
-__device__ __forceinline__ float dot_lds(const float* w, const float* x, uint32_t K,
-                                         uint32_t lane) {
-  float acc = 0.0f;
-  for (uint32_t j = lane * 4; j < K; j += 256) {
-    const float4 wv = lds4(w + j), xv = lds4(x + j);
-    acc = fmaf(wv.x, xv.x, acc);
-    acc = fmaf(wv.y, xv.y, acc);
-    acc = fmaf(wv.z, xv.z, acc);
-    acc = fmaf(wv.w, xv.w, acc);
-  }
-  return acc;
-}
-
-// Lane partial of x . x over the lane's elements of a length-K vector, in
-// the order the dot products visit them.
+// Lane partial of x . x over the elements 4*lane + 256*i of a length-K
+// vector (i ascending).
 __device__ __forceinline__ float sumsq_lane(const float* x, uint32_t K, uint32_t lane) {
   float ss = 0.0f;
   uint32_t j = lane * 4;
@@ -482,127 +466,81 @@ __device__ __forceinline__ float rms_inv(const float* x, uint32_t n, float eps, 
   return 1.0f / sqrtf(ss / (float)n + eps);
 }
 
-// Dot products of NR LDS rows w[r] with the LDS vector x, all loads issued
-// before the first multiply (NF = float4 per lane covering K <= 256*NF).
-// Per row: ascending j, one fma per element -- the order dot_lds / row_fma
-// use -- then the wave tree.
-template <int NF, int NR>
-__device__ __forceinline__ void dot_rows_lds(const float* const* w, const float* x, uint32_t K,
-                                             uint32_t lane, float* out) {
-  float4 xv[NF];
-#pragma unroll
-  for (int i = 0; i < NF; ++i) {
-    const uint32_t j = lane * 4 + 256u * i;
-    if (j < K) xv[i] = lds4(x + j);
-  }
-  float4 wv[NR][NF];
-#pragma unroll
-  for (int r = 0; r < NR; ++r)
-#pragma unroll
-    for (int i = 0; i < NF; ++i) {
-      const uint32_t j = lane * 4 + 256u * i;
-      if (j < K) wv[r][i] = lds4(w[r] + j);
-    }
-#pragma unroll
-  for (int r = 0; r < NR; ++r) {
-    float acc = 0.0f;
-#pragma unroll
-    for (int i = 0; i < NF; ++i) {
-      const uint32_t j = lane * 4 + 256u * i;
-      if (j < K) {
-        acc = fmaf(wv[r][i].x, xv[i].x, acc);
-        acc = fmaf(wv[r][i].y, xv[i].y, acc);
-        acc = fmaf(wv[r][i].z, xv[i].z, acc);
-        acc = fmaf(wv[r][i].w, xv[i].w, acc);
-      }
-    }
-    out[r] = acc;
-  }
-  wave_sum_n<NR>(out);
+// Matvec passes. A compute wave takes the rows of its items four at a time
+// (a quad pass, device.h): lane 16*r + s computes segment s of row slot r.
+// Pair kinds put items k and k + NCW in the slots (gate/up or the two RoPE
+// rows of each), single-row kinds items k, k + NCW, k + 2*NCW, k + 3*NCW; a
+// wave's passes start at items cw, cw + PSTEP, ...
+__host__ __device__ constexpr uint32_t pass_items(bool pair) { return pair ? 2u : 4u; }
+__device__ __forceinline__ uint32_t slot_item(bool pair, uint32_t k, uint32_t r) {
+  return k + NCW * (pair ? r / 2 : r);
 }
 
-// The same for any K (rows longer than 8 float4 per lane go through the
-// serial loop).
-template <int NR>
-__device__ __forceinline__ void dot_rows_any(const float* const* w, const float* x, uint32_t K,
-                                             uint32_t lane, float* out) {
-  switch ((K + 255) / 256) {
-    case 1: dot_rows_lds<1, NR>(w, x, K, lane, out); return;
-    case 2: dot_rows_lds<2, NR>(w, x, K, lane, out); return;
-    case 3: dot_rows_lds<3, NR>(w, x, K, lane, out); return;
-    case 4: dot_rows_lds<4, NR>(w, x, K, lane, out); return;
-    case 5: dot_rows_lds<5, NR>(w, x, K, lane, out); return;
-    case 6: dot_rows_lds<6, NR>(w, x, K, lane, out); return;
-    default:
-#pragma unroll
-      for (int r = 0; r < NR; ++r) out[r] = wave_sum(dot_lds(w[r], x, K, lane));
-  }
-}
-
-// A compute wave's first pass of a staged matvec phase: up to two items
-// (four rows for pair kinds), whose rows it reads from LDS into registers
-// while the pollers wait for the phase's input, so only the input vector is
-// read after the barrier. 8 float4 per lane: 2 per row for pairs (K <= 512),
-// 4 per row otherwise (K <= 1024); longer rows read the rest from LDS later.
-constexpr int PRE_F4 = 8;
-__host__ __device__ constexpr int pre_nr(bool pair) { return pair ? 4 : 2; }
-__host__ __device__ constexpr int pre_nf(bool pair) { return pair ? 2 : 4; }
+// A compute wave's first pass of a staged matvec phase: the lane's
+// PRE_F4 first chunks of its segment, read from LDS into registers while the
+// pollers wait for the phase's input, so only the input vector is read after
+// the barrier; longer rows read the rest from LDS later.
+constexpr int PRE_F4 = 9;
 struct Preload {
   float4 w[PRE_F4];
-  uint32_t k, k2;  // items of the pass (k2 == k: no second item)
-  bool any;        // the wave has an item
+  bool any;  // the wave has an item
 };
 
-template <bool PAIR>
-__device__ __forceinline__ void preload_rows(Preload& P, const Stager& sg, uint32_t kind,
-                                             uint32_t cw, uint32_t lane) {
-  constexpr int NR = pre_nr(PAIR), NF = pre_nf(PAIR);
-  const Dims d = shape_dims(sg.a->d);
-  const uint32_t cnt = rows_owned(kind_items(d, kind), sg.wg, sg.G);
-  const uint32_t K = kind_k(d, kind);
-  P.any = cw < cnt;
-  if (!P.any) return;
-  P.k = cw;
-  P.k2 = cw + NCW < cnt ? cw + NCW : cw;
-  const float* w1 = staged_item(sg, kind, P.k);
-  const float* w2 = staged_item(sg, kind, P.k2);
-  const float* rows[4] = {w1, PAIR ? w1 + K : w2, w2, w2 + K};
-#pragma unroll
-  for (int r = 0; r < NR; ++r)
-#pragma unroll
-    for (int i = 0; i < NF; ++i) {
-      const uint32_t j = lane * 4 + 256u * i;
-      if (j < K) P.w[r * NF + i] = lds4(rows[r] + j);
-    }
+// Staged row of slot r of the pass starting at item k (nullptr: no item).
+__device__ __forceinline__ const float* staged_slot(const Stager& sg, uint32_t kind, uint32_t k,
+                                                    uint32_t r, uint32_t cnt) {
+  const bool pair = kind_rows(kind) == 2;
+  const uint32_t it = slot_item(pair, k, r);
+  if (it >= cnt) return nullptr;
+  const float* w = staged_item(sg, kind, it);
+  return pair && (r & 1u) ? w + kind_k(shape_dims(sg.a->d), kind) : w;
 }
 
-// Row r of the pass dotted with x: the preloaded float4s, then (longer
-// rows) the rest from LDS, in ascending j.
-template <bool PAIR>
-__device__ __forceinline__ float pass_dot(const Preload& P, int r, const float* row,
-                                          const float4* xv, const float* x, uint32_t K,
-                                          uint32_t lane) {
-  constexpr int NF = pre_nf(PAIR);
+__device__ __forceinline__ void preload_rows(Preload& P, const Stager& sg, uint32_t kind,
+                                             uint32_t cw, uint32_t lane) {
+  const Dims d = shape_dims(sg.a->d);
+  const uint32_t cnt = rows_owned(kind_items(d, kind), sg.wg, sg.G);
+  const uint32_t K = kind_k(d, kind), s = qseg(lane);
+  P.any = cw < cnt;
+  if (!P.any) return;
+  const float* w = staged_slot(sg, kind, cw, qrow(lane), cnt);
+  if (!w) return;
+  const float* wb = pin(w + 4u * s);
+#pragma unroll
+  for (int i = 0; i < PRE_F4; ++i) {
+    const uint32_t j = 64u * i + 4u * s;
+    if (j < K) P.w[i] = lds4(wb + 64 * i);
+  }
+}
+
+// The lane's segment of the first pass: the preloaded chunks, then (longer
+// rows) the rest from LDS. Every read of x, and the first group of the rest,
+// is issued before the first fma.
+__device__ __forceinline__ float pass_pre(const Preload& P, const float* w, const float* x,
+                                          uint32_t K, uint32_t s) {
+  if (!w) return 0.0f;
+  const float* xb = pin(x + 4u * s);
+  float4 xv[PRE_F4];
+#pragma unroll
+  for (int i = 0; i < PRE_F4; ++i) {
+    const uint32_t j = 64u * i + 4u * s;
+    if (j < K) xv[i] = lds4(xb + 64 * i);
+  }
+  const uint32_t jr = 64u * PRE_F4 + 4u * s;
+  SegGroup g;
+  if (jr < K) seg_group_load(g, w, x, K, jr);
   float acc = 0.0f;
 #pragma unroll
-  for (int i = 0; i < NF; ++i) {
-    const uint32_t j = lane * 4 + 256u * i;
+  for (int i = 0; i < PRE_F4; ++i) {
+    const uint32_t j = 64u * i + 4u * s;
     if (j < K) {
-      const float4 w = P.w[r * NF + i];
-      acc = fmaf(w.x, xv[i].x, acc);
-      acc = fmaf(w.y, xv[i].y, acc);
-      acc = fmaf(w.z, xv[i].z, acc);
-      acc = fmaf(w.w, xv[i].w, acc);
+      acc = fmaf(P.w[i].x, xv[i].x, acc);
+      acc = fmaf(P.w[i].y, xv[i].y, acc);
+      acc = fmaf(P.w[i].z, xv[i].z, acc);
+      acc = fmaf(P.w[i].w, xv[i].w, acc);
     }
   }
-  for (uint32_t j = lane * 4 + 256u * NF; j < K; j += 256) {
-    const float4 wv = lds4(row + j), xx = lds4(x + j);
-    acc = fmaf(wv.x, xx.x, acc);
-    acc = fmaf(wv.y, xx.y, acc);
-    acc = fmaf(wv.z, xx.z, acc);
-    acc = fmaf(wv.w, xx.w, acc);
-  }
-  return acc;
+  return jr < K ? seg_lds_from(g, w, x, K, jr, acc) : acc;
 }
 
 // Barrier work of a staged matvec phase: loaders wait for this kind's rows
@@ -622,10 +560,7 @@ struct MvHook {
     if (sg->loader) {
       if (op.issue < 4) stage_issue(*sg, op.issue, op.layer);
     } else if (wave >= NPOLL) {
-      if (kind_rows(kind) == 2)
-        preload_rows<true>(*pre, *sg, kind, wave - NPOLL, threadIdx.x % WAVE);
-      else
-        preload_rows<false>(*pre, *sg, kind, wave - NPOLL, threadIdx.x % WAVE);
+      preload_rows(*pre, *sg, kind, wave - NPOLL, threadIdx.x % WAVE);
     }
   }
 };
@@ -640,9 +575,9 @@ __device__ __forceinline__ MvHook mv_hook(const Stager& sg, LoadOp op, Preload& 
 }
 
 // body(k, y0, y1) for every item k of `kind` dealt to compute wave cw, with
-// its dot products against the LDS vector x (y1 = 0 for single-row kinds).
-// Staged: the preloaded first pass, then further passes of two items read
-// from LDS. Otherwise the rows are loaded from memory now.
+// its dot products against the LDS vector x (y1 = 0 for single-row kinds),
+// wave-uniform. Staged: the preloaded first pass, then further passes read
+// from LDS. Otherwise each lane streams its segment of its row from memory.
 template <class F>
 __device__ __forceinline__ void items_dot(const Args& a, uint32_t kind, uint32_t cw, uint32_t l,
                                           const Stager& sg, const Preload& P, const float* x,
@@ -651,79 +586,37 @@ __device__ __forceinline__ void items_dot(const Args& a, uint32_t kind, uint32_t
   const uint32_t cnt = rows_owned(kind_items(dd, kind), wg, G);
   const uint32_t K = kind_k(dd, kind);
   const bool pair = kind_rows(kind) == 2;
+  const uint32_t r = qrow(lane), s = qseg(lane);
+  const uint32_t step = NCW * pass_items(pair);
+  auto emit = [&](uint32_t k, float acc) {
+    float y[4];
+    quad_sums(acc, y);
+    if (pair) {
+      body(k, y[0], y[1]);
+      if (k + NCW < cnt) body(k + NCW, y[2], y[3]);
+    } else {
+#pragma unroll
+      for (uint32_t u = 0; u < 4; ++u)
+        if (k + NCW * u < cnt) body(k + NCW * u, y[u], 0.0f);
+    }
+  };
   if (sg.on) {
     if (!P.any) return;
-    const float* w1 = staged_item(sg, kind, P.k);
-    const float* w2 = staged_item(sg, kind, P.k2);
-    if (pair) {
-      constexpr int NF = pre_nf(true);
-      float4 xv[NF];
-#pragma unroll
-      for (int i = 0; i < NF; ++i) {
-        const uint32_t j = lane * 4 + 256u * i;
-        if (j < K) xv[i] = lds4(x + j);
-      }
-      float y[4];
-      y[0] = pass_dot<true>(P, 0, w1, xv, x, K, lane);
-      y[1] = pass_dot<true>(P, 1, w1 + K, xv, x, K, lane);
-      y[2] = pass_dot<true>(P, 2, w2, xv, x, K, lane);
-      y[3] = pass_dot<true>(P, 3, w2 + K, xv, x, K, lane);
-      wave_sum_n<4>(y);
-      body(P.k, y[0], y[1]);
-      if (P.k2 != P.k) body(P.k2, y[2], y[3]);
-    } else {
-      constexpr int NF = pre_nf(false);
-      float4 xv[NF];
-#pragma unroll
-      for (int i = 0; i < NF; ++i) {
-        const uint32_t j = lane * 4 + 256u * i;
-        if (j < K) xv[i] = lds4(x + j);
-      }
-      float y[2];
-      y[0] = pass_dot<false>(P, 0, w1, xv, x, K, lane);
-      y[1] = pass_dot<false>(P, 1, w2, xv, x, K, lane);
-      wave_sum_n<2>(y);
-      body(P.k, y[0], 0.0f);
-      if (P.k2 != P.k) body(P.k2, y[1], 0.0f);
-    }
-    for (uint32_t k = cw + 2 * NCW; k < cnt; k += 2 * NCW) {
-      const uint32_t k2 = k + NCW < cnt ? k + NCW : k;
-      const float* v1 = staged_item(sg, kind, k);
-      const float* v2 = staged_item(sg, kind, k2);
-      if (pair) {
-        const float* rows[4] = {v1, v1 + K, v2, v2 + K};
-        float y[4];
-        dot_rows_any<4>(rows, x, K, lane, y);
-        body(k, y[0], y[1]);
-        if (k2 != k) body(k2, y[2], y[3]);
-      } else {
-        const float* rows[2] = {v1, v2};
-        float y[2];
-        dot_rows_any<2>(rows, x, K, lane, y);
-        body(k, y[0], 0.0f);
-        if (k2 != k) body(k2, y[1], 0.0f);
-      }
+    emit(cw, pass_pre(P, staged_slot(sg, kind, cw, r, cnt), x, K, s));
+    for (uint32_t k = cw + step; k < cnt; k += step) {
+      const float* w = staged_slot(sg, kind, k, r, cnt);
+      emit(k, w ? seg_lds(w, x, K, s, 0, 0.0f) : 0.0f);
     }
     return;
   }
-  // Rows from HBM: two rows streamed together (a pair's rows, or two
-  // single-row items of this wave).
-  for (uint32_t k = cw; k < cnt; k += pair ? NCW : 2 * NCW) {
-    const ItemRows r = item_rows(a, kind, l, k, wg, G);
-    if (pair) {
-      const float2 p = dot2_stream<KF>(r.w0, r.w1, x, r.K, lane);
-      float y[2] = {p.x, p.y};
-      wave_sum_n<2>(y);
-      body(k, y[0], y[1]);
-    } else {
-      const uint32_t k2 = k + NCW < cnt ? k + NCW : k;
-      const ItemRows r2 = item_rows(a, kind, l, k2, wg, G);
-      const float2 p = dot2_stream<KF>(r.w0, r2.w0, x, r.K, lane);
-      float y[2] = {p.x, p.y};
-      wave_sum_n<2>(y);
-      body(k, y[0], 0.0f);
-      if (k2 != k) body(k2, y[1], 0.0f);
+  for (uint32_t k = cw; k < cnt; k += step) {
+    const uint32_t it = slot_item(pair, k, r);
+    float acc = 0.0f;
+    if (it < cnt) {
+      const ItemRows rw = item_rows(a, kind, l, it, wg, G);
+      acc = seg_stream<KF>(pair && (r & 1u) ? rw.w1 : rw.w0, x, K, s, 0, 0.0f);
     }
+    emit(k, acc);
   }
 }
 
@@ -1193,7 +1086,7 @@ __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t b
   return v > bv || (v == bv && i < bi);
 }
 
-constexpr int LMF = 4;  // float4 per lane per lm_head row held in registers (h <= 1024 in one go)
+constexpr int LMF = 9;  // chunks of a lane's lm_head segment held in registers (h <= 576 in one go)
 
 // The final RMSNorm weight, kept in LDS for the kernel's lifetime (the
 // lm_head may be the tied embedding, so it cannot be folded into the rows).
@@ -1206,8 +1099,8 @@ __device__ __forceinline__ void lm_prime(const Args& a, const Lds& s) {
 
 // rmsnorm(final) -> logits = H . x (model.rs:515-519), plus each vocabulary
 // chunk's (max, argmax) for the sampler. The workgroup owns chunks
-// c = wg + G*k; every wave computes rows, two at a time, with the next two
-// rows in flight. logit = inv * (H . (x * w_norm)).
+// c = wg + G*k; every wave computes quad passes of four rows, with the next
+// four rows in flight. logit = inv * (H . (x * w_norm)).
 __device__ __forceinline__ bool phase_lm(const Args& a, uint32_t tick, uint32_t wg, uint32_t G,
                                          const Lds& s, const Stager& sg) {
   const Dims d = shape_dims(a.d);
@@ -1218,16 +1111,16 @@ __device__ __forceinline__ bool phase_lm(const Args& a, uint32_t tick, uint32_t 
   float* xs = s.vec2;                    // x * w_norm
   const float* nrm = s.vec2 + d.h;       // final norm weight (lm_prime)
   auto vocab_row = [&](uint32_t r) { return (wg + G * (r / VCHUNK)) * VCHUNK + r % VCHUNK; };
-  RowT<LMF> A0, A1, B0, B1;
+  const uint32_t sgm = qseg(lane);
+  SegT<LMF> A, B;
   const bool lmw = wave < NWA;  // loader waves only meet the barriers
-  auto load_pair = [&](RowT<LMF>& x0, RowT<LMF>& x1, uint32_t r0) {
-    const uint32_t r1 = r0 + NWA;
-    if (r0 < nrows && vocab_row(r0) < d.V)
-      row_load(x0, a.head + (size_t)vocab_row(r0) * d.h, d.h, lane);
-    if (r1 < nrows && vocab_row(r1) < d.V)
-      row_load(x1, a.head + (size_t)vocab_row(r1) * d.h, d.h, lane);
+  // Quad q: local rows 4q .. 4q+3, this lane's 4q + qrow(lane).
+  auto live = [&](uint32_t q) {
+    const uint32_t rr = 4 * q + qrow(lane);
+    return rr < nrows && vocab_row(rr) < d.V;
   };
-  if (lmw) load_pair(A0, A1, wave);
+  auto row_of = [&](uint32_t q) { return a.head + (size_t)vocab_row(4 * q + qrow(lane)) * d.h; };
+  if (lmw && live(wave)) seg_load(A, row_of(wave), d.h, sgm, 0);
   if (!poll_gather<8>(gather_vec(a.mb_xd, d.h, gen_of(d, tick, d.L - 1, PH_D), s.vec), NPOLL, a.st,
                       s.ctl))
     return false;
@@ -1235,26 +1128,17 @@ __device__ __forceinline__ bool phase_lm(const Args& a, uint32_t tick, uint32_t 
   __syncthreads();
   const float inv = rms_inv(s.vec, d.h, d.eps, lane);
   const uint32_t gen = gen_lm(d, tick);
-  for (uint32_t r0 = wave; lmw && r0 < nrows; r0 += 2 * NWA) {
-    const uint32_t r1 = r0 + NWA;
-    load_pair(B0, B1, r0 + 2 * NWA);
-    const uint32_t v0 = vocab_row(r0), v1 = vocab_row(r1);
-    if (v0 < d.V) {
-      const float y = inv * wave_sum(dot_tail(A0, a.head + (size_t)v0 * d.h, xs, d.h, lane));
-      if (lane == 0) {
-        lds_st(lg + r0, y);
-        mb_put(a.mb_logit + v0, y, gen);
-      }
+  for (uint32_t q = wave; lmw && 4 * q < nrows; q += NWA) {
+    if (live(q + NWA)) seg_load(B, row_of(q + NWA), d.h, sgm, 0);
+    const bool lv = live(q);
+    const float acc = lv ? seg_tail(A, row_of(q), xs, d.h, sgm) : 0.0f;
+    const float y = inv * group_sum(acc, 16);
+    if (lv && sgm == 0) {
+      const uint32_t rr = 4 * q + qrow(lane);
+      lds_st(lg + rr, y);
+      mb_put(a.mb_logit + vocab_row(rr), y, gen);
     }
-    if (r1 < nrows && v1 < d.V) {
-      const float y = inv * wave_sum(dot_tail(A1, a.head + (size_t)v1 * d.h, xs, d.h, lane));
-      if (lane == 0) {
-        lds_st(lg + r1, y);
-        mb_put(a.mb_logit + v1, y, gen);
-      }
-    }
-    A0 = B0;
-    A1 = B1;
+    A = B;
   }
   __syncthreads();
   // Chunk (max, argmax): one wave per chunk, one lane per row.
