@@ -316,26 +316,35 @@ __global__ __launch_bounds__(BLOCK) void k_b_attn(const Args* __restrict__ rargs
 // phase_attn has fma chains:
 //  * score(q, t): 4 chains over 16 elements each (the lanes of a position),
 //    then ((c0 + c1) + (c2 + c3)) * scale;
-//  * softmax: phase_attn's wave code per (query, head);
+//  * softmax: phase_attn's sums -- lane slot L = 0..63 adds positions L,
+//    L + 64 from +0, then the wave tree over the 64 slots -- with 16 lanes
+//    per (query, head), lane s holding slots s + 16v, so a wave takes four
+//    (query, head) rows at once;
 //  * value[d]: 24 position groups (wave w, group pl: positions
 //    4w + pl + 24k, k ascending), each a chain, then per w the tree over its
 //    four groups and the sum w = 0..5 in order, from +0.
 // Positions past a query's own (t > pos) carry probability +0 and zero V
 // rows, which leave an accumulator unchanged (a chain started at +0 never
-// holds -0).
+// holds -0). The scores reuse the LDS of K and Q once every wave is done
+// with them, so with three query heads per kv head two workgroups fit a CU.
 
 constexpr uint32_t AT_HD = 64, AT_CH = 128, AT_VROWS = 192;  // 24 groups x 8 positions
-constexpr uint32_t AT_KP = 68, AT_VP = 66, AT_QP = 68, AT_SP = 193;  // LDS row pitches (floats)
+constexpr uint32_t AT_KP = 65, AT_VP = 66, AT_QP = 65, AT_SP = 193;  // LDS row pitches (floats)
 
+// Floats of the K + Q region, which the scores then take.
+__host__ __device__ inline size_t attn_tile_kq(uint32_t grp) {
+  const size_t kq = (size_t)AT_CH * AT_KP + (size_t)grp * 16 * AT_QP;
+  const size_t sc = (size_t)grp * 16 * AT_SP;
+  return kq > sc ? kq : sc;
+}
 __host__ __device__ inline size_t attn_tile_lds(uint32_t grp) {
-  return sizeof(float) * ((size_t)AT_CH * AT_KP + (size_t)AT_VROWS * AT_VP +
-                          (size_t)grp * 16 * AT_QP + (size_t)grp * 16 * AT_SP + grp * 32);
+  return sizeof(float) * (attn_tile_kq(grp) + (size_t)AT_CH * AT_VP + grp * 32);
 }
 
 // tasks[x] = tile << 16 | chunk << 8 | kv head; tiles[m] .. tiles[m + 1] are
 // the batch rows of tile m. rows: the batch (one cache, consecutive
 // positions); qkvt: tagged q/k/v words per row; part: tagged partials.
-__global__ __launch_bounds__(256) void k_b_attn_tile(const Dims d, const BRow* __restrict__ rows,
+__global__ __launch_bounds__(256, 2) void k_b_attn_tile(const Dims d, const BRow* __restrict__ rows,
                                                      const uint32_t* __restrict__ tasks,
                                                      const uint32_t* __restrict__ tiles, uint32_t l,
                                                      const u64* __restrict__ qkvt,
@@ -343,10 +352,10 @@ __global__ __launch_bounds__(256) void k_b_attn_tile(const Dims d, const BRow* _
   extern __shared__ float at_lds[];
   const uint32_t grp = d.group, hs = AT_HD + 2;
   float* Ks = at_lds;                       // [AT_CH][AT_KP]
-  float* Vs = Ks + AT_CH * AT_KP;           // [AT_VROWS][AT_VP]
-  float* Qs = Vs + AT_VROWS * AT_VP;        // [grp][16][AT_QP]
-  float* Ss = Qs + grp * 16 * AT_QP;        // [grp][16][AT_SP]: scores, then probabilities
-  float* ML = Ss + grp * 16 * AT_SP;        // [grp][16][2]: m, l
+  float* Qs = Ks + AT_CH * AT_KP;           // [grp][16][AT_QP]
+  float* Ss = at_lds;                       // [grp][16][AT_SP]: scores, then probabilities
+  float* Vs = at_lds + attn_tile_kq(grp);   // [AT_CH][AT_VP]
+  float* ML = Vs + AT_CH * AT_VP;           // [grp][16][2]: m, l
   const uint32_t task = tasks[blockIdx.x];
   const uint32_t m = task >> 16, c = (task >> 8) & 0xffu, g = task & 0xffu;
   const uint32_t rb0 = tiles[m], nq = tiles[m + 1] - rb0;
@@ -373,18 +382,13 @@ __global__ __launch_bounds__(256) void k_b_attn_tile(const Dims d, const BRow* _
 #pragma unroll
     for (int k = 0; k < NR; ++k) {
       const uint32_t e = tid + 256 * k, t = e / 16, q4 = (e % 16) * 4;
-      if (kv == 0) {
-        *reinterpret_cast<float4*>(Ks + t * AT_KP + q4) = r4[k];
-      } else {
-        float* vd = Vs + t * AT_VP + q4;
-        vd[0] = r4[k].x;
-        vd[1] = r4[k].y;
-        vd[2] = r4[k].z;
-        vd[3] = r4[k].w;
-      }
+      float* dst = kv ? Vs + t * AT_VP + q4 : Ks + t * AT_KP + q4;
+      dst[0] = r4[k].x;
+      dst[1] = r4[k].y;
+      dst[2] = r4[k].z;
+      dst[3] = r4[k].w;
     }
   }
-  for (uint32_t e = AT_CH * AT_VP + tid; e < AT_VROWS * AT_VP; e += 256) Vs[e] = 0.0f;
   for (uint32_t e0 = 0; e0 < grp * 16 * AT_HD; e0 += 256 * 8) {
     u64 qw[8];
 #pragma unroll
@@ -403,10 +407,17 @@ __global__ __launch_bounds__(256) void k_b_attn_tile(const Dims d, const BRow* _
     }
   }
   __syncthreads();
-  // 2. scores: wave w takes key tiles w and w + 4.
+  // 2. scores: wave w takes key tiles w and w + 4, kept in registers until
+  // every wave is done with K and Q, whose LDS the scores then take.
   const uint32_t lr = lane % 16, lc = lane / 16;
-  for (uint32_t kt = wave; kt < (nk + 15) / 16; kt += 4) {
-    for (uint32_t j = 0; j < grp; ++j) {
+  const uint32_t nkt = (nk + 15) / 16;
+  f4v sreg[2][MAX_GROUP];
+#pragma unroll
+  for (uint32_t u = 0; u < 2; ++u) {
+    const uint32_t kt = wave + 4 * u;
+#pragma unroll
+    for (uint32_t j = 0; j < MAX_GROUP; ++j) {
+      if (kt >= nkt || j >= grp) continue;
       f4v a4[4];
 #pragma unroll
       for (int sub = 0; sub < 4; ++sub) {
@@ -419,32 +430,58 @@ __global__ __launch_bounds__(256) void k_b_attn_tile(const Dims d, const BRow* _
         }
         a4[sub] = acc;
       }
-      const f4v sc = ((a4[0] + a4[1]) + (a4[2] + a4[3]));
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr)  // query 4*lc + rr, key kt*16 + lr
-        Ss[(j * 16 + 4 * lc + rr) * AT_SP + kt * 16 + lr] = sc[rr] * d.scale;
+      sreg[u][j] = ((a4[0] + a4[1]) + (a4[2] + a4[3]));
     }
   }
   __syncthreads();
-  // 3. softmax statistics and probabilities, one wave per (query, head).
-  for (uint32_t u = wave; u < grp * 16; u += 4) {
-    const uint32_t j = u / 16, q = u % 16;
-    float* sh = Ss + (j * 16 + q) * AT_SP;
-    const uint32_t n = q < nq ? min(AT_CH, r0.pos + q + 1 - t0) : 0;
-    float mx = -INFINITY;
-    for (uint32_t i = lane; i < n; i += WAVE) mx = fmaxf(mx, sh[i]);
-    mx = wave_max(mx);
-    float ls = 0.0f;
-    for (uint32_t i = lane; i < n; i += WAVE) {
-      const float e = (mx == -INFINITY) ? 0.0f : expf(sh[i] - mx);
-      sh[i] = e;
-      ls += e;
+#pragma unroll
+  for (uint32_t u = 0; u < 2; ++u) {
+    const uint32_t kt = wave + 4 * u;
+#pragma unroll
+    for (uint32_t j = 0; j < MAX_GROUP; ++j) {
+      if (kt >= nkt || j >= grp) continue;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)  // query 4*lc + rr, key kt*16 + lr
+        Ss[(j * 16 + 4 * lc + rr) * AT_SP + kt * 16 + lr] = sreg[u][j][rr] * d.scale;
     }
-    ls = wave_sum(ls);
-    for (uint32_t i = n + lane; i < AT_VROWS; i += WAVE) sh[i] = 0.0f;
-    if (lane == 0) {
-      ML[(j * 16 + q) * 2] = mx;
-      ML[(j * 16 + q) * 2 + 1] = ls;
+  }
+  __syncthreads();
+  // 3. softmax statistics and probabilities, 16 lanes per (query, head):
+  // lane sub holds phase_attn's lane slots L = sub + 16v (v = 0..3), each
+  // the sum of positions L, L + 64 from +0; the slots' tree is group_sum
+  // over the 16 lanes of each v, then (R3 + R2) + (R1 + R0) as wave_sum.
+  {
+    const uint32_t sub = lane % 16;
+    for (uint32_t u0 = 4 * wave; u0 < grp * 16; u0 += 16) {
+      const uint32_t u = u0 + lane / 16;
+      const bool live = u < grp * 16;
+      const uint32_t j = u / 16, q = u % 16;
+      float* sh = Ss + (live ? u : 0) * AT_SP;
+      const uint32_t n = live && q < nq ? min(AT_CH, r0.pos + q + 1 - t0) : 0;
+      float mx = -INFINITY;
+      for (uint32_t i = sub; i < n; i += 16) mx = fmaxf(mx, sh[i]);
+      mx = row_max(mx);
+      float R[4];
+#pragma unroll
+      for (uint32_t v = 0; v < 4; ++v) {
+        float ls = 0.0f;
+        for (uint32_t i = sub + 16 * v; i < n; i += WAVE) {
+          const float e = (mx == -INFINITY) ? 0.0f : expf(sh[i] - mx);
+          sh[i] = e;
+          ls += e;
+        }
+        R[v] = ls;
+      }
+#pragma unroll
+      for (uint32_t v = 0; v < 4; ++v) R[v] = group_sum(R[v], 16);
+      const float lsum = (R[3] + R[2]) + (R[1] + R[0]);
+      if (live) {
+        for (uint32_t i = n + sub; i < AT_VROWS; i += 16) sh[i] = 0.0f;
+        if (sub == 0) {
+          ML[(j * 16 + q) * 2] = mx;
+          ML[(j * 16 + q) * 2 + 1] = lsum;
+        }
+      }
     }
   }
   __syncthreads();
@@ -458,8 +495,8 @@ __global__ __launch_bounds__(256) void k_b_attn_tile(const Dims d, const BRow* _
 #pragma unroll
       for (int mm = 0; mm < 2; ++mm) {
         const uint32_t pos = gi + 24 * (4 * mm + lc);  // group gi = 4*w' + pl
-        acc[gi] = __builtin_amdgcn_mfma_f32_16x16x4f32(Ss[(j * 16 + lr) * AT_SP + pos],
-                                                       Vs[pos * AT_VP + 16 * wave + lr], acc[gi],
+        const float vv = pos < AT_CH ? Vs[pos * AT_VP + 16 * wave + lr] : 0.0f;
+        acc[gi] = __builtin_amdgcn_mfma_f32_16x16x4f32(Ss[(j * 16 + lr) * AT_SP + pos], vv, acc[gi],
                                                        0, 0, 0);
       }
     }
