@@ -86,7 +86,8 @@ __host__ __device__ constexpr uint32_t gemm_lds_bytes(uint32_t tn) {
 }
 
 // Y[b][o] = W[o] . X[b] for o < M, b < B, K columns. Workgroup (x, y): wave
-// w owns row tile 4x + w and every wave the column tiles y*TN .. y*TN+TN-1,
+// w owns row tile 4x + w and every wave the column tiles cbase + y*TN ..
+// cbase + y*TN + TN-1,
 // all 16 segments of each of its outputs in its own accumulators, reduced
 // with tree16 at the end. A chunk's operands (the four row tiles and the TN
 // column tiles, 4 KB each) are copied into LDS by all four waves together
@@ -98,12 +99,12 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ Wp, uint
                                               const float* __restrict__ Xp, uint32_t B,
                                               float* __restrict__ Y, uint32_t ldy,
                                               const float* __restrict__ scale,
-                                              const uint32_t* __restrict__ gen) {
+                                              const uint32_t* __restrict__ gen, uint32_t cbase) {
   extern __shared__ float4 gsm[];  // [GEMM_STAGES][4 + TN tiles][4 quarters][64 lanes]
   constexpr uint32_t NT = 4 + TN, NLD = 4 + TN;  // tiles per stage; loads per wave per stage
   const uint32_t wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
   const uint32_t nch = panel_chunks(K), nrt = (M + 15) / 16, nct = (B + 15) / 16;
-  const uint32_t T = blockIdx.x * 4 + wave, C0 = blockIdx.y * TN;
+  const uint32_t T = blockIdx.x * 4 + wave, C0 = cbase + blockIdx.y * TN;
   // Tiles past the last one load a real tile (never used), so every wave
   // issues the same number of loads per stage.
   const float* wsrc = Wp + (size_t)min(T, nrt - 1) * nch * PANEL_TILE + lane * 4;
@@ -523,22 +524,21 @@ __global__ __launch_bounds__(256, 2) void k_b_attn_tile(const Dims d, const BRow
   }
 }
 
-// Combine of the chunk partials (combine_one, as the O phase does), per
-// (head, row), into plain att[b][q].
-__global__ __launch_bounds__(BLOCK) void k_b_comb(const Args* __restrict__ rargs,
-                                                  const BRow* __restrict__ rows, uint32_t l,
-                                                  float* __restrict__ att, uint32_t lda) {
-  const Args& a = rargs[blockIdx.y];
-  const Lds s = lds_init_rows(a.d);
-  const BRow r = rows[blockIdx.y];
-  const Dims& d = a.d;
-  const uint32_t hh = blockIdx.x, nch = attn_nchunks(r.pos), hs = d.hd + 2;
-  if (!poll_gather<4>(gather_vec(a.mb_part + (size_t)hh * MAX_ACHUNKS * hs, nch * hs,
-                                 gen_of(d, r.tick, l, PH_ATTN), s.scr),
-                      NPOLL, a.st, s.ctl))
-    return;
-  for (uint32_t dd = threadIdx.x; dd < d.hd; dd += BLOCK)
-    att[(size_t)blockIdx.y * lda + hh * d.hd + dd] = combine_one(s.scr, nch, hs, dd);
+// Combine of the chunk partials (combine_with, as the O phase does) into
+// plain att[b][q]: one workgroup per row, a thread per (head, dim). The
+// partials were written by earlier launches on the same stream, so their
+// values are read directly (the low half of each tagged word).
+__global__ __launch_bounds__(256) void k_b_comb(const Dims d, const BRow* __restrict__ rows,
+                                                const u64* __restrict__ part, uint32_t part_w,
+                                                float* __restrict__ att, uint32_t lda) {
+  const uint32_t b = blockIdx.x;
+  const uint32_t nch = attn_nchunks(rows[b].pos), hs = d.hd + 2;
+  for (uint32_t u = threadIdx.x; u < d.q; u += blockDim.x) {
+    const uint32_t hh = u / d.hd, dd = u - hh * d.hd;
+    const u64* p = part + (size_t)b * part_w + (size_t)hh * MAX_ACHUNKS * hs;
+    att[(size_t)b * lda + u] =
+        combine_with([&](uint32_t i) { return __uint_as_float((uint32_t)p[i]); }, nch, hs, dd);
+  }
 }
 
 // g = act(gate * inv) * (up * inv) (phase_gu); Y holds gate rows then up rows.

@@ -241,6 +241,7 @@ struct defer_gpu_model {
   Dims d;
   int device = 0;
   uint32_t G = 0;  // workgroups per phase (= CUs, capped by the smallest phase)
+  uint32_t ncu = 0;  // compute units of the device
   size_t lds_bytes = 0;
   hipStream_t stream = nullptr;
   float* wbuf = nullptr;
@@ -394,6 +395,7 @@ extern "C" int defer_gpu_model_create(const defer_gpu_config* cfg, const float* 
   // by the smallest phase.
   const uint32_t min_items = std::min({d.qkv_rows / 2, d.h, d.ff, d.nvc});
   m->G = std::min<uint32_t>((uint32_t)prop.multiProcessorCount, min_items);
+  m->ncu = (uint32_t)prop.multiProcessorCount;
 
   d.lds_vec = (std::max({d.h, d.q, d.ff}) + 3) & ~3u;
   d.lds_vec2 = (2 * d.h + 3) & ~3u;
@@ -584,7 +586,7 @@ extern "C" int defer_gpu_model_create(const defer_gpu_config* cfg, const float* 
                           (int)attn_tile_lds(MAX_GROUP));
   if (e != hipSuccess)
     return cleanup(fail(DEFER_GPU_E_HIP, "LDS attribute (tiled attention): %s", hipGetErrorString(e)));
-  const void* row_kernels[] = {(const void*)k_b_attn, (const void*)k_b_comb,
+  const void* row_kernels[] = {(const void*)k_b_attn,
                                (const void*)k_b_sample};
   for (const void* kf : row_kernels) {
     e = hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)m->lds_rows);
@@ -1306,29 +1308,46 @@ static int ensure_panels(defer_gpu_model* m) {
 template <int TN, uint32_t OUT>
 static void launch_gemm_tn(hipStream_t s, const float* Wp, uint32_t M, uint32_t K, const float* Xp,
                            uint32_t B, float* Y, uint32_t ldy, const float* scale,
-                           const uint32_t* gen) {
-  const uint32_t nrt = (M + 15) / 16, nct = (B + 15) / 16;
-  k_gemm<TN, OUT><<<dim3((nrt + 3) / 4, (nct + TN - 1) / TN), 256, gemm_lds_bytes(TN), s>>>(
-      Wp, M, K, Xp, B, Y, ldy, scale, gen);
+                           const uint32_t* gen, uint32_t cbase, uint32_t ncols) {
+  const uint32_t nrt = (M + 15) / 16;
+  k_gemm<TN, OUT><<<dim3((nrt + 3) / 4, (ncols + TN - 1) / TN), 256, gemm_lds_bytes(TN), s>>>(
+      Wp, M, K, Xp, B, Y, ldy, scale, gen, cbase);
 }
+// One workgroup per CU runs at a time (registers and LDS), so a grid whose
+// last round would hold only a few workgroups is split: whole rounds of
+// four-column-tile workgroups, then the remaining column tiles one per
+// workgroup (a quarter of the work each), which finish in a fraction of a
+// round. Every output is computed the same way either way.
 template <uint32_t OUT>
 static void launch_gemm_out(hipStream_t s, const float* Wp, uint32_t M, uint32_t K, const float* Xp,
                             uint32_t B, float* Y, uint32_t ldy, const float* scale,
-                            const uint32_t* gen) {
-  const uint32_t nct = (B + 15) / 16;
-  if (nct <= 1)
-    launch_gemm_tn<1, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen);
-  else if (nct <= 2)
-    launch_gemm_tn<2, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen);
-  else
-    launch_gemm_tn<4, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen);
+                            const uint32_t* gen, uint32_t ncu) {
+  const uint32_t nct = (B + 15) / 16, nrg = (M + 63) / 64;
+  if (nct <= 1) {
+    launch_gemm_tn<1, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 0, nct);
+    return;
+  }
+  if (nct <= 2) {
+    launch_gemm_tn<2, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 0, nct);
+    return;
+  }
+  const uint32_t w4 = nrg * ((nct + 3) / 4), rounds = w4 / ncu, rest = w4 % ncu;
+  if (rounds >= 1 && rest > 0 && rest * 4 <= ncu) {
+    const uint32_t y4 = rounds * ncu / nrg;  // column groups of 4 in the whole rounds
+    if (y4 >= 1 && 4 * y4 < nct) {
+      launch_gemm_tn<4, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 0, 4 * y4);
+      launch_gemm_tn<1, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 4 * y4, nct - 4 * y4);
+      return;
+    }
+  }
+  launch_gemm_tn<4, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 0, nct);
 }
-static void launch_gemm(hipStream_t s, uint32_t out, const float* Wp, uint32_t M, uint32_t K,
-                        const float* Xp, uint32_t B, float* Y, uint32_t ldy,
+static void launch_gemm(hipStream_t s, uint32_t ncu, uint32_t out, const float* Wp, uint32_t M,
+                        uint32_t K, const float* Xp, uint32_t B, float* Y, uint32_t ldy,
                         const float* scale = nullptr, const uint32_t* gen = nullptr) {
-  if (out == GO_PLAIN) launch_gemm_out<GO_PLAIN>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen);
-  else if (out == GO_RESID) launch_gemm_out<GO_RESID>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen);
-  else launch_gemm_out<GO_TAG>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen);
+  if (out == GO_PLAIN) launch_gemm_out<GO_PLAIN>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, ncu);
+  else if (out == GO_RESID) launch_gemm_out<GO_RESID>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, ncu);
+  else launch_gemm_out<GO_TAG>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, ncu);
 }
 
 // Timing of one launch (profiling on): events recorded around it on the
@@ -1463,7 +1482,7 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
     launch_panel(s, w.X, w.X, n, n, d.h, d.h, w.XP);
     {
       ProfSpan ps(m, 0, 2.0 * d.qkv_rows * d.h * n);
-      launch_gemm(s, GO_PLAIN, m->p_qkv[l], d.qkv_rows, d.h, w.XP, n, w.Y, ldy);
+      launch_gemm(s, m->ncu, GO_PLAIN, m->p_qkv[l], d.qkv_rows, d.h, w.XP, n, w.Y, ldy);
     }
     k_b_qkv_epi<<<dim3((d.qkv_rows / 2 + 255) / 256, n), 256, 0, s>>>(w.rargs, w.drows, l, w.Y, ldy,
                                                                       w.INV, w.QKVT, d.qkv_rows);
@@ -1475,23 +1494,23 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
       else
         k_b_attn<<<(uint32_t)items.size(), BLOCK, m->lds_rows, s>>>(w.rargs, w.drows, w.items, l);
     }
-    k_b_comb<<<dim3(d.nh, n), BLOCK, m->lds_rows, s>>>(w.rargs, w.drows, l, w.ATT, d.q);
+    k_b_comb<<<n, 256, 0, s>>>(d, w.drows, w.PART, part_words(d), w.ATT, d.q);
     launch_panel(s, w.ATT, w.ATT, n, n, d.q, d.q, w.XP);
     {
       ProfSpan ps(m, 0, 2.0 * d.h * d.q * n);
-      launch_gemm(s, GO_RESID, m->p_o[l], d.h, d.q, w.XP, n, w.X, d.h);
+      launch_gemm(s, m->ncu, GO_RESID, m->p_o[l], d.h, d.q, w.XP, n, w.X, d.h);
     }
     k_b_rms<<<(n + 3) / 4, 256, 0, s>>>(w.X, n, d.h, d.eps, w.INV);
     launch_panel(s, w.X, w.X, n, n, d.h, d.h, w.XP);
     {
       ProfSpan ps(m, 0, 2.0 * 2 * d.ff * d.h * n);
-      launch_gemm(s, GO_PLAIN, m->p_gu[l], 2 * d.ff, d.h, w.XP, n, w.Y, ldy);
+      launch_gemm(s, m->ncu, GO_PLAIN, m->p_gu[l], 2 * d.ff, d.h, w.XP, n, w.Y, ldy);
     }
     k_b_act<<<dim3((d.ff + 255) / 256, n), 256, 0, s>>>(w.Y, ldy, w.INV, d.ff, d.act, w.G, d.ff);
     launch_panel(s, w.G, w.G, n, n, d.ff, d.ff, w.XP);
     {
       ProfSpan ps(m, 0, 2.0 * d.h * d.ff * n);
-      launch_gemm(s, GO_RESID, m->p_d[l], d.h, d.ff, w.XP, n, w.X, d.h);
+      launch_gemm(s, m->ncu, GO_RESID, m->p_d[l], d.h, d.ff, w.XP, n, w.X, d.h);
     }
   }
   if (nl) {
@@ -1499,7 +1518,7 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
     launch_panel(s, w.XS, w.XS, nl, nl, d.h, d.h, w.XP);
     {
       ProfSpan ps(m, 0, 2.0 * d.V * d.h * nl);
-      launch_gemm(s, GO_TAG, m->p_lm, d.V, d.h, w.XP, nl, reinterpret_cast<float*>(w.LOGT), d.V,
+      launch_gemm(s, m->ncu, GO_TAG, m->p_lm, d.V, d.h, w.XP, nl, reinterpret_cast<float*>(w.LOGT), d.V,
                   w.LINV, w.lgen);
     }
     k_b_chunkmax<<<dim3((d.nvc + 3) / 4, nl), 256, 0, s>>>(d, w.LOGT, w.lgen, w.VMAX, w.VARG, nl);

@@ -931,23 +931,27 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
 
 // Combine the chunk partials of one head (in chunk order) into its output:
 // att[d] = sum_c acc_c[d] e^(m_c - M) / sum_c l_c e^(m_c - M).
-__device__ __forceinline__ float combine_one(const float* part, uint32_t nch, uint32_t hs,
-                                             uint32_t dd) {
+// ld(i): float i of the head's partials [nch][hs] (m, l, acc[hd]).
+template <class LD>
+__device__ __forceinline__ float combine_with(LD ld, uint32_t nch, uint32_t hs, uint32_t dd) {
   if (nch == 1) {  // one chunk: its own max, weight exp(0) = 1
-    const float Ls = lds_ld(part + 1) * 1.0f, A = lds_ld(part + 2 + dd) * 1.0f;
+    const float Ls = ld(1) * 1.0f, A = ld(2 + dd) * 1.0f;
     return A / Ls;
   }
   float M = -INFINITY;
-  for (uint32_t c = 0; c < nch; ++c) M = fmaxf(M, lds_ld(part + c * hs));
+  for (uint32_t c = 0; c < nch; ++c) M = fmaxf(M, ld(c * hs));
   float Ls = 0.0f, A = 0.0f;
   for (uint32_t c = 0; c < nch; ++c) {
-    const float* p = part + c * hs;
-    const float mc = lds_ld(p);
+    const float mc = ld(c * hs);
     const float sc = (mc == -INFINITY) ? 0.0f : expf(mc - M);
-    Ls = Ls + lds_ld(p + 1) * sc;
-    A = A + lds_ld(p + 2 + dd) * sc;
+    Ls = Ls + ld(c * hs + 1) * sc;
+    A = A + ld(c * hs + 2 + dd) * sc;
   }
   return A / Ls;
+}
+__device__ __forceinline__ float combine_one(const float* part, uint32_t nch, uint32_t hs,
+                                             uint32_t dd) {
+  return combine_with([&](uint32_t i) { return lds_ld(part + i); }, nch, hs, dd);
 }
 
 // Separate combine (used when the partials of all heads do not fit the O
