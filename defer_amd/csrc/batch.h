@@ -524,20 +524,30 @@ __global__ __launch_bounds__(256, 2) void k_b_attn_tile(const Dims d, const BRow
   }
 }
 
-// Combine of the chunk partials (combine_with, as the O phase does) into
-// plain att[b][q]: one workgroup per row, a thread per (head, dim). The
+// Combine of the chunk partials (combine_scales / combine_value, as the O
+// phase does) into plain att[b][q]: one workgroup per row; the weights of a
+// head's chunks are formed once in LDS, then a thread per (head, dim). The
 // partials were written by earlier launches on the same stream, so their
 // values are read directly (the low half of each tagged word).
+constexpr uint32_t COMB_MAX_HEADS = 64;
 __global__ __launch_bounds__(256) void k_b_comb(const Dims d, const BRow* __restrict__ rows,
                                                 const u64* __restrict__ part, uint32_t part_w,
                                                 float* __restrict__ att, uint32_t lda) {
+  __shared__ float sc[COMB_MAX_HEADS][MAX_ACHUNKS];
+  __shared__ float ls[COMB_MAX_HEADS];
   const uint32_t b = blockIdx.x;
   const uint32_t nch = attn_nchunks(rows[b].pos), hs = d.hd + 2;
+  const u64* pb = part + (size_t)b * part_w;
+  auto ld_head = [&](uint32_t hh) {
+    const u64* p = pb + (size_t)hh * MAX_ACHUNKS * hs;
+    return [p](uint32_t i) { return __uint_as_float((uint32_t)p[i]); };
+  };
+  for (uint32_t hh = threadIdx.x; hh < d.nh; hh += blockDim.x)
+    ls[hh] = combine_scales(ld_head(hh), nch, hs, sc[hh]);
+  __syncthreads();
   for (uint32_t u = threadIdx.x; u < d.q; u += blockDim.x) {
     const uint32_t hh = u / d.hd, dd = u - hh * d.hd;
-    const u64* p = part + (size_t)b * part_w + (size_t)hh * MAX_ACHUNKS * hs;
-    att[(size_t)b * lda + u] =
-        combine_with([&](uint32_t i) { return __uint_as_float((uint32_t)p[i]); }, nch, hs, dd);
+    att[(size_t)b * lda + u] = combine_value(ld_head(hh), nch, hs, dd, sc[hh], ls[hh]);
   }
 }
 

@@ -332,6 +332,8 @@ static int validate(const defer_gpu_config* c) {
     return fail(DEFER_GPU_E_INVALID, "head_dim %u unsupported (need 16 * 2^k, at most 256)", hd);
   if (c->num_heads / c->num_kv_heads > MAX_GROUP)
     return fail(DEFER_GPU_E_INVALID, "GQA group larger than %u", MAX_GROUP);
+  if (c->num_heads > COMB_MAX_HEADS)
+    return fail(DEFER_GPU_E_INVALID, "num_attention_heads above %u", COMB_MAX_HEADS);
   if (c->hidden_size % 4 || c->intermediate_size % 4)
     return fail(DEFER_GPU_E_INVALID, "hidden and intermediate sizes must be multiples of 4");
   const uint64_t q = (uint64_t)c->num_heads * hd;

@@ -932,22 +932,35 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
 // Combine the chunk partials of one head (in chunk order) into its output:
 // att[d] = sum_c acc_c[d] e^(m_c - M) / sum_c l_c e^(m_c - M).
 // ld(i): float i of the head's partials [nch][hs] (m, l, acc[hd]).
+// combine_scales: the chunks' weights sc[c] = exp(m_c - M) and their
+// weighted total l; combine_value: one output dim. Together they are
+// combine_with.
 template <class LD>
-__device__ __forceinline__ float combine_with(LD ld, uint32_t nch, uint32_t hs, uint32_t dd) {
-  if (nch == 1) {  // one chunk: its own max, weight exp(0) = 1
-    const float Ls = ld(1) * 1.0f, A = ld(2 + dd) * 1.0f;
-    return A / Ls;
-  }
+__device__ __forceinline__ float combine_scales(LD ld, uint32_t nch, uint32_t hs, float* sc) {
+  if (nch == 1) return ld(1) * 1.0f;  // one chunk: its own max, weight exp(0) = 1
   float M = -INFINITY;
   for (uint32_t c = 0; c < nch; ++c) M = fmaxf(M, ld(c * hs));
-  float Ls = 0.0f, A = 0.0f;
+  float Ls = 0.0f;
   for (uint32_t c = 0; c < nch; ++c) {
     const float mc = ld(c * hs);
-    const float sc = (mc == -INFINITY) ? 0.0f : expf(mc - M);
-    Ls = Ls + ld(c * hs + 1) * sc;
-    A = A + ld(c * hs + 2 + dd) * sc;
+    sc[c] = (mc == -INFINITY) ? 0.0f : expf(mc - M);
+    Ls = Ls + ld(c * hs + 1) * sc[c];
   }
+  return Ls;
+}
+template <class LD>
+__device__ __forceinline__ float combine_value(LD ld, uint32_t nch, uint32_t hs, uint32_t dd,
+                                               const float* sc, float Ls) {
+  if (nch == 1) return (ld(2 + dd) * 1.0f) / Ls;
+  float A = 0.0f;
+  for (uint32_t c = 0; c < nch; ++c) A = A + ld(c * hs + 2 + dd) * sc[c];
   return A / Ls;
+}
+template <class LD>
+__device__ __forceinline__ float combine_with(LD ld, uint32_t nch, uint32_t hs, uint32_t dd) {
+  float sc[MAX_ACHUNKS];
+  const float Ls = combine_scales(ld, nch, hs, sc);
+  return combine_value(ld, nch, hs, dd, sc, Ls);
 }
 __device__ __forceinline__ float combine_one(const float* part, uint32_t nch, uint32_t hs,
                                              uint32_t dd) {
