@@ -367,72 +367,96 @@ __global__ __launch_bounds__(256, 2) void k_b_attn_tile(const Dims d, const BRow
   const uint32_t tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
   const float* kb = r0.kc + ((size_t)l * d.nkv + g) * r0.cap * d.kvs;
   const float* vb = r0.vc + ((size_t)l * d.nkv + g) * r0.cap * d.kvs;
-  // 1. K rows, then V rows, then Q words of the chunk: each thread issues a
-  // batch's eight loads before its first LDS store (16 threads per row).
-  constexpr int NR = AT_CH * 16 / 256;  // rows per thread and batch: 8
+  // 1. K rows, V rows and Q words of the chunk: each thread issues all its
+  // loads before its first LDS store (16 threads per K/V row).
+  constexpr int NR = AT_CH * 16 / 256;                 // K/V float4 per thread: 8
+  constexpr int NQ = MAX_GROUP * 16 * AT_HD / 256;     // Q words per thread: 16
+  float4 kr[NR], vr[NR];
+  u64 qw[NQ];
+  // Generation tags of this lane's output queries 4*lc + rr (values stage).
+  const uint32_t lr = lane % 16, lc = lane / 16;
+  u64 gtag[4];
 #pragma unroll
-  for (int kv = 0; kv < 2; ++kv) {
-    const float* src = kv ? vb : kb;
-    float4 r4[NR];
+  for (int rr = 0; rr < 4; ++rr) {
+    const uint32_t q = 4 * lc + rr;
+    gtag[rr] = q < nq ? (u64)gen_of(d, rows[rb0 + q].tick, l, PH_ATTN) << 32 : 0;
+  }
 #pragma unroll
-    for (int k = 0; k < NR; ++k) {
-      const uint32_t e = tid + 256 * k, t = e / 16, q4 = (e % 16) * 4;
-      r4[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      if (t < nk) r4[k] = *reinterpret_cast<const float4*>(src + (size_t)(t0 + t) * d.kvs + q4);
-    }
-#pragma unroll
-    for (int k = 0; k < NR; ++k) {
-      const uint32_t e = tid + 256 * k, t = e / 16, q4 = (e % 16) * 4;
-      float* dst = kv ? Vs + t * AT_VP + q4 : Ks + t * AT_KP + q4;
-      dst[0] = r4[k].x;
-      dst[1] = r4[k].y;
-      dst[2] = r4[k].z;
-      dst[3] = r4[k].w;
+  for (int k = 0; k < NR; ++k) {
+    const uint32_t e = tid + 256 * k, t = e / 16, q4 = (e % 16) * 4;
+    kr[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    vr[k] = kr[k];
+    if (t < nk) {
+      kr[k] = *reinterpret_cast<const float4*>(kb + (size_t)(t0 + t) * d.kvs + q4);
+      vr[k] = *reinterpret_cast<const float4*>(vb + (size_t)(t0 + t) * d.kvs + q4);
     }
   }
-  for (uint32_t e0 = 0; e0 < grp * 16 * AT_HD; e0 += 256 * 8) {
-    u64 qw[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const uint32_t e = e0 + tid + 256 * k, j = e / (16 * AT_HD), q = (e / AT_HD) % 16,
-                     dd = e % AT_HD;
-      qw[k] = 0;
-      if (j < grp && q < nq)
-        qw[k] = qkvt[(size_t)(rb0 + q) * d.qkv_rows + (g * grp + j) * AT_HD + dd];
-    }
+  for (int k = 0; k < NQ; ++k) {
+    const uint32_t e = tid + 256 * k, j = e / (16 * AT_HD), q = (e / AT_HD) % 16, dd = e % AT_HD;
+    qw[k] = 0;
+    if (j < grp && q < nq) qw[k] = qkvt[(size_t)(rb0 + q) * d.qkv_rows + (g * grp + j) * AT_HD + dd];
+  }
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const uint32_t e = e0 + tid + 256 * k, j = e / (16 * AT_HD), q = (e / AT_HD) % 16,
-                     dd = e % AT_HD;
-      if (j < grp) Qs[(j * 16 + q) * AT_QP + dd] = __uint_as_float((uint32_t)qw[k]);
-    }
+  for (int k = 0; k < NR; ++k) {
+    const uint32_t e = tid + 256 * k, t = e / 16, q4 = (e % 16) * 4;
+    float* kd = Ks + t * AT_KP + q4;
+    float* vd = Vs + t * AT_VP + q4;
+    kd[0] = kr[k].x;
+    kd[1] = kr[k].y;
+    kd[2] = kr[k].z;
+    kd[3] = kr[k].w;
+    vd[0] = vr[k].x;
+    vd[1] = vr[k].y;
+    vd[2] = vr[k].z;
+    vd[3] = vr[k].w;
+  }
+#pragma unroll
+  for (int k = 0; k < NQ; ++k) {
+    const uint32_t e = tid + 256 * k, j = e / (16 * AT_HD), q = (e / AT_HD) % 16, dd = e % AT_HD;
+    if (j < grp) Qs[(j * 16 + q) * AT_QP + dd] = __uint_as_float((uint32_t)qw[k]);
   }
   __syncthreads();
   // 2. scores: wave w takes key tiles w and w + 4, kept in registers until
-  // every wave is done with K and Q, whose LDS the scores then take.
-  const uint32_t lr = lane % 16, lc = lane / 16;
+  // every wave is done with K and Q, whose LDS the scores then take. The
+  // (head, sub) chains of a key tile run interleaved.
   const uint32_t nkt = (nk + 15) / 16;
+  float qa[MAX_GROUP][4][4];  // element 16*sub + 4*i + lc of query lr, head j
+#pragma unroll
+  for (uint32_t j = 0; j < MAX_GROUP; ++j)
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        qa[j][sub][i] = j < grp ? Qs[(j * 16 + lr) * AT_QP + 16 * sub + 4 * i + lc] : 0.0f;
   f4v sreg[2][MAX_GROUP];
 #pragma unroll
   for (uint32_t u = 0; u < 2; ++u) {
     const uint32_t kt = wave + 4 * u;
+    if (kt >= nkt) continue;
+    float ka[4][4];
 #pragma unroll
-    for (uint32_t j = 0; j < MAX_GROUP; ++j) {
-      if (kt >= nkt || j >= grp) continue;
-      f4v a4[4];
+    for (int sub = 0; sub < 4; ++sub)
 #pragma unroll
-      for (int sub = 0; sub < 4; ++sub) {
-        f4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int i = 0; i < 4; ++i) ka[sub][i] = Ks[(kt * 16 + lr) * AT_KP + 16 * sub + 4 * i + lc];
+    f4v acc[MAX_GROUP][4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint32_t el = 16 * sub + 4 * i + lc;
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Qs[(j * 16 + lr) * AT_QP + el],
-                                                     Ks[(kt * 16 + lr) * AT_KP + el], acc, 0, 0, 0);
-        }
-        a4[sub] = acc;
+    for (uint32_t j = 0; j < MAX_GROUP; ++j)
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub) acc[j][sub] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (uint32_t j = 0; j < MAX_GROUP; ++j) {
+        if (j >= grp) continue;
+#pragma unroll
+        for (int sub = 0; sub < 4; ++sub)
+          acc[j][sub] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[j][sub][i], ka[sub][i], acc[j][sub],
+                                                             0, 0, 0);
       }
-      sreg[u][j] = ((a4[0] + a4[1]) + (a4[2] + a4[3]));
-    }
+#pragma unroll
+    for (uint32_t j = 0; j < MAX_GROUP; ++j)
+      sreg[u][j] = (acc[j][0] + acc[j][1]) + (acc[j][2] + acc[j][3]);
   }
   __syncthreads();
 #pragma unroll
@@ -451,56 +475,69 @@ __global__ __launch_bounds__(256, 2) void k_b_attn_tile(const Dims d, const BRow
   // lane sub holds phase_attn's lane slots L = sub + 16v (v = 0..3), each
   // the sum of positions L, L + 64 from +0; the slots' tree is group_sum
   // over the 16 lanes of each v, then (R3 + R2) + (R1 + R0) as wave_sum.
+  // A lane's eight positions sub + 16k are read at once; positions from n
+  // on (up to AT_VROWS) get probability +0.
   {
     const uint32_t sub = lane % 16;
     for (uint32_t u0 = 4 * wave; u0 < grp * 16; u0 += 16) {
       const uint32_t u = u0 + lane / 16;
-      const bool live = u < grp * 16;
       const uint32_t j = u / 16, q = u % 16;
-      float* sh = Ss + (live ? u : 0) * AT_SP;
-      const uint32_t n = live && q < nq ? min(AT_CH, r0.pos + q + 1 - t0) : 0;
-      float mx = -INFINITY;
-      for (uint32_t i = sub; i < n; i += 16) mx = fmaxf(mx, sh[i]);
-      mx = row_max(mx);
-      float R[4];
+      float* sh = Ss + u * AT_SP;
+      const uint32_t n = q < nq ? min(AT_CH, r0.pos + q + 1 - t0) : 0;
+      float sv[8];
 #pragma unroll
-      for (uint32_t v = 0; v < 4; ++v) {
-        float ls = 0.0f;
-        for (uint32_t i = sub + 16 * v; i < n; i += WAVE) {
-          const float e = (mx == -INFINITY) ? 0.0f : expf(sh[i] - mx);
-          sh[i] = e;
-          ls += e;
-        }
-        R[v] = ls;
+      for (uint32_t k = 0; k < 8; ++k) {
+        const uint32_t i = sub + 16 * k;
+        sv[k] = i < n ? sh[i] : -INFINITY;
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (uint32_t k = 0; k < 8; ++k) mx = fmaxf(mx, sv[k]);
+      mx = row_max(mx);
+      float e[8];
+#pragma unroll
+      for (uint32_t k = 0; k < 8; ++k) {
+        const uint32_t i = sub + 16 * k;
+        e[k] = (i < n && mx != -INFINITY) ? expf(sv[k] - mx) : 0.0f;
+        sh[i] = e[k];
       }
 #pragma unroll
-      for (uint32_t v = 0; v < 4; ++v) R[v] = group_sum(R[v], 16);
+      for (uint32_t k = 8; k < AT_VROWS / 16; ++k) sh[sub + 16 * k] = 0.0f;
+      float R[4];
+#pragma unroll
+      for (uint32_t v = 0; v < 4; ++v) R[v] = group_sum((0.0f + e[v]) + e[v + 4], 16);
       const float lsum = (R[3] + R[2]) + (R[1] + R[0]);
-      if (live) {
-        for (uint32_t i = n + sub; i < AT_VROWS; i += 16) sh[i] = 0.0f;
-        if (sub == 0) {
-          ML[(j * 16 + q) * 2] = mx;
-          ML[(j * 16 + q) * 2 + 1] = lsum;
-        }
+      if (sub == 0) {
+        ML[(j * 16 + q) * 2] = mx;
+        ML[(j * 16 + q) * 2 + 1] = lsum;
       }
     }
   }
   __syncthreads();
-  // 4. values: wave w computes dims 16w..16w+15 of every head.
+  // 4. values: wave w computes dims 16w..16w+15 of every head; the V
+  // operands are read once for all heads.
+  float vop[24][2];
+#pragma unroll
+  for (int gi = 0; gi < 24; ++gi)
+#pragma unroll
+    for (int mm = 0; mm < 2; ++mm) {
+      const uint32_t pos = gi + 24 * (4 * mm + lc);  // group gi = 4*w' + pl
+      vop[gi][mm] = pos < AT_CH ? Vs[pos * AT_VP + 16 * wave + lr] : 0.0f;
+    }
   for (uint32_t j = 0; j < grp; ++j) {
+    float pop[24][2];
+#pragma unroll
+    for (int gi = 0; gi < 24; ++gi)
+#pragma unroll
+      for (int mm = 0; mm < 2; ++mm) pop[gi][mm] = Ss[(j * 16 + lr) * AT_SP + gi + 24 * (4 * mm + lc)];
     f4v acc[24];
 #pragma unroll
     for (int gi = 0; gi < 24; ++gi) acc[gi] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int gi = 0; gi < 24; ++gi) {
+    for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
-      for (int mm = 0; mm < 2; ++mm) {
-        const uint32_t pos = gi + 24 * (4 * mm + lc);  // group gi = 4*w' + pl
-        const float vv = pos < AT_CH ? Vs[pos * AT_VP + 16 * wave + lr] : 0.0f;
-        acc[gi] = __builtin_amdgcn_mfma_f32_16x16x4f32(Ss[(j * 16 + lr) * AT_SP + pos], vv, acc[gi],
-                                                       0, 0, 0);
-      }
-    }
+      for (int gi = 0; gi < 24; ++gi)
+        acc[gi] = __builtin_amdgcn_mfma_f32_16x16x4f32(pop[gi][mm], vop[gi][mm], acc[gi], 0, 0, 0);
     f4v A = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int w6 = 0; w6 < 6; ++w6) {
@@ -512,13 +549,11 @@ __global__ __launch_bounds__(256, 2) void k_b_attn_tile(const Dims d, const BRow
     for (int rr = 0; rr < 4; ++rr) {  // query 4*lc + rr, dim 16*wave + lr
       const uint32_t q = 4 * lc + rr;
       if (q >= nq) continue;
-      const BRow rq = rows[rb0 + q];
-      const u64 gtag = (u64)gen_of(d, rq.tick, l, PH_ATTN) << 32;
       u64* out = part + (size_t)(rb0 + q) * part_w + ((size_t)hh * MAX_ACHUNKS + c) * hs;
-      out[2 + 16 * wave + lr] = gtag | __float_as_uint(A[rr]);
+      out[2 + 16 * wave + lr] = gtag[rr] | __float_as_uint(A[rr]);
       if (wave == 0 && lr == 0) {
-        out[0] = gtag | __float_as_uint(ML[(j * 16 + q) * 2]);
-        out[1] = gtag | __float_as_uint(ML[(j * 16 + q) * 2 + 1]);
+        out[0] = gtag[rr] | __float_as_uint(ML[(j * 16 + q) * 2]);
+        out[1] = gtag[rr] | __float_as_uint(ML[(j * 16 + q) * 2 + 1]);
       }
     }
   }
