@@ -80,121 +80,151 @@ __device__ __forceinline__ f4v tree16(const f4v* a) {
 }
 
 // Chunks of operands in flight through LDS, and the LDS a launch needs.
-constexpr uint32_t GEMM_STAGES = 4;
+// Four-tile tasks take a CU's LDS alone; smaller ones fit two workgroups
+// per CU with three stages.
+__host__ __device__ constexpr uint32_t gemm_stages(uint32_t tn) { return tn == 4 ? 4 : 3; }
 __host__ __device__ constexpr uint32_t gemm_lds_bytes(uint32_t tn) {
-  return GEMM_STAGES * (4 + tn) * PANEL_TILE * 4;
+  return gemm_stages(tn) * (4 + tn) * PANEL_TILE * 4;
 }
+constexpr uint32_t GEMM_WAVES = 8;
 
-// Y[b][o] = W[o] . X[b] for o < M, b < B, K columns. Workgroup (x, y): wave
-// w owns row tile 4x + w and every wave the column tiles cbase + y*TN ..
-// cbase + y*TN + TN-1,
-// all 16 segments of each of its outputs in its own accumulators, reduced
-// with tree16 at the end. A chunk's operands (the four row tiles and the TN
-// column tiles, 4 KB each) are copied into LDS by all four waves together
-// (16 bytes per lane straight from memory into LDS), GEMM_STAGES - 1
-// chunks ahead of their use, so each activation tile is read from memory
-// once per workgroup and shared by the four waves.
-template <int TN, uint32_t OUT>
-__global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ Wp, uint32_t M, uint32_t K,
+// Y[b][o] = W[o] . X[b] for o < M, b < B, K columns. A task (x, y) covers
+// row tiles 4x .. 4x+3 and column tiles cbase + y*TN .. cbase + y*TN+TN-1.
+// Eight waves, two per SIMD, so one wave's MFMAs run while the other waits
+// for its operands: wave w owns row tile 4x + w%4 and column tiles
+// (w/4)*TN/2 .. of the task (TN = 1: the waves w < 4 only), all 16
+// segments of each of its outputs in its own accumulators, reduced with
+// tree16 at the end. A chunk's operands (the four row tiles and the TN
+// column tiles, 4 KB each) are copied into LDS by the waves together (16
+// bytes per lane straight from memory into LDS), gemm_stages(TN) - 1 chunks
+// ahead of their use, so each tile is read from memory once per workgroup.
+// The kernel is persistent: workgroup k takes tasks k, k + gridDim.x, ...,
+// and the copies run ahead across task boundaries. PARTIAL: K may end
+// inside a chunk.
+template <int TN, uint32_t OUT, bool PARTIAL>
+__global__ __launch_bounds__(512) void k_gemm(const float* __restrict__ Wp, uint32_t M, uint32_t K,
                                               const float* __restrict__ Xp, uint32_t B,
                                               float* __restrict__ Y, uint32_t ldy,
                                               const float* __restrict__ scale,
-                                              const uint32_t* __restrict__ gen, uint32_t cbase) {
-  extern __shared__ float4 gsm[];  // [GEMM_STAGES][4 + TN tiles][4 quarters][64 lanes]
-  constexpr uint32_t NT = 4 + TN, NLD = 4 + TN;  // tiles per stage; loads per wave per stage
+                                              const uint32_t* __restrict__ gen, uint32_t cbase,
+                                              uint32_t ncols) {
+  extern __shared__ float4 gsm[];  // [stages][4 + TN tiles][4 quarters][64 lanes]
+  constexpr uint32_t GEMM_STAGES = gemm_stages(TN);
+  constexpr uint32_t NT = 4 + TN;                    // tiles per stage
+  constexpr uint32_t WN = TN >= 2 ? TN / 2 : 1;      // column tiles per wave
+  constexpr uint32_t NQ = 4 * NT;                    // 1 KB copies per stage
   const uint32_t wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+  const uint32_t rt = wave % 4, half = wave / 4;
+  const bool mfma_wave = TN >= 2 || half == 0;
+  const uint32_t nld = (NQ - wave + GEMM_WAVES - 1) / GEMM_WAVES;  // this wave's copies per stage
   const uint32_t nch = panel_chunks(K), nrt = (M + 15) / 16, nct = (B + 15) / 16;
-  const uint32_t T = blockIdx.x * 4 + wave, C0 = cbase + blockIdx.y * TN;
-  // Tiles past the last one load a real tile (never used), so every wave
-  // issues the same number of loads per stage.
-  const float* wsrc = Wp + (size_t)min(T, nrt - 1) * nch * PANEL_TILE + lane * 4;
-  const float* xsrc[TN];
-#pragma unroll
-  for (int t = 0; t < TN; ++t) xsrc[t] = Xp + (size_t)min(C0 + t, nct - 1) * nch * PANEL_TILE + lane * 4;
+  const uint32_t nrg = (nrt + 3) / 4, ngy = (ncols + TN - 1) / TN, ntask = nrg * ngy;
+  const uint32_t mine = blockIdx.x < ntask ? (ntask - blockIdx.x + gridDim.x - 1) / gridDim.x : 0;
+  const uint32_t total = mine * nch;  // chunks of this workgroup's tasks, in order
   const uint32_t lds0 = (uint32_t)(uintptr_t)gsm;
-  // Chunk i into stage st: this wave's row tile (4 quarters) and quarters
-  // wave, wave + 4, ... of the column tiles.
-  auto issue = [&](uint32_t i, uint32_t st) {
+  // Chunk g into stage st: copies wave, wave + 8, ... of the stage's
+  // (tile, quarter) list. Tiles past the last one load a real tile (never
+  // used), so a wave issues the same number of copies for every chunk.
+  auto issue = [&](uint32_t g, uint32_t st) {
+    const uint32_t t = blockIdx.x + gridDim.x * (g / nch), i = g % nch;
+    const uint32_t x = t % nrg, y = t / nrg, C0 = cbase + y * TN;
     const uint32_t sb = lds0 + st * NT * PANEL_TILE * 4;
 #pragma unroll
-    for (uint32_t q = 0; q < 4; ++q)
-      dma16(wsrc + (size_t)i * PANEL_TILE + q * 256, sb + (wave * 4 + q) * 1024);
-#pragma unroll
-    for (uint32_t u = 0; u < TN; ++u) {
-      const uint32_t idx = wave + 4 * u, t = idx / 4, q = idx % 4;
-      dma16(xsrc[t] + (size_t)i * PANEL_TILE + q * 256, sb + ((4 + t) * 4 + q) * 1024);
+    for (uint32_t f = wave; f < NQ; f += GEMM_WAVES) {
+      const uint32_t tile = f / 4, q = f % 4;
+      const float* src = tile < 4 ? Wp + ((size_t)min(4 * x + tile, nrt - 1) * nch + i) * PANEL_TILE
+                                  : Xp + ((size_t)min(C0 + tile - 4, nct - 1) * nch + i) * PANEL_TILE;
+      dma16(src + q * 256 + lane * 4, sb + f * 1024);
     }
   };
-  f4v acc[TN][16];
+  for (uint32_t g = 0; g + 1 < GEMM_STAGES && g < total; ++g) issue(g, g);
+  for (uint32_t k = 0; k < mine; ++k) {
+    f4v acc[WN][16];
 #pragma unroll
-  for (int t = 0; t < TN; ++t)
+    for (int t = 0; t < (int)WN; ++t)
 #pragma unroll
-    for (int s = 0; s < 16; ++s) acc[t][s] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
-  for (uint32_t i = 0; i + 1 < GEMM_STAGES && i < nch; ++i) issue(i, i);
-  // Chunk i's operands from its stage, once it has landed in every wave.
-  auto operands = [&](uint32_t i, float4 (&a)[4], float4 (&b)[TN][4]) {
-    // Chunk i has landed once at most the later chunks' loads are in flight;
-    // the barrier makes that true of every wave, and every wave is then done
-    // with chunk i - 1's stage, which the next request overwrites.
-    stage_wait(min(GEMM_STAGES - 2, nch - 1 - i) * NLD);
-    __syncthreads();
-    if (i + GEMM_STAGES - 1 < nch) issue(i + GEMM_STAGES - 1, (i + GEMM_STAGES - 1) % GEMM_STAGES);
-    const float4* sa = gsm + (i % GEMM_STAGES) * NT * 256;
+      for (int s = 0; s < 16; ++s) acc[t][s] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+    // Chunk i of this task from its stage, once it has landed: chunk g has
+    // landed once at most the later chunks' copies are in flight; the
+    // barrier makes that true of every wave, and every wave is then done
+    // with chunk g - 1's stage, which the next request overwrites.
+    auto operands = [&](uint32_t i, float4 (&a)[4], float4 (&b)[WN][4]) {
+      const uint32_t g = k * nch + i;
+      stage_wait(min(GEMM_STAGES - 2, total - 1 - g) * nld);
+      __syncthreads();
+      if (g + GEMM_STAGES - 1 < total)
+        issue(g + GEMM_STAGES - 1, (g + GEMM_STAGES - 1) % GEMM_STAGES);
+      const float4* sa = gsm + (g % GEMM_STAGES) * NT * 256;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) a[q] = sa[(wave * 4 + q) * 64 + lane];
+      for (int q = 0; q < 4; ++q) a[q] = sa[(rt * 4 + q) * 64 + lane];
 #pragma unroll
-    for (int t = 0; t < TN; ++t)
+      for (int t = 0; t < (int)WN; ++t)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) b[t][q] = sa[((4 + t) * 4 + q) * 64 + lane];
-  };
-  const uint32_t nfull = K / 64;
-  for (uint32_t i = 0; i < nfull; ++i) {
-    float4 a[4], b[TN][4];
-    operands(i, a, b);
+        for (int q = 0; q < 4; ++q) b[t][q] = sa[((4 + half * WN + t) * 4 + q) * 64 + lane];
+    };
+    const uint32_t nfull = K / 64;
+    for (uint32_t i = 0; i < nfull; ++i) {
+      float4 a[4], b[WN][4];
+      operands(i, a, b);
+      if (!mfma_wave) continue;
 #pragma unroll
-    for (int s = 0; s < 16; ++s) {
-      const float av = (&a[s / 4].x)[s % 4];
-#pragma unroll
-      for (int t = 0; t < TN; ++t)
-        acc[t][s] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, (&b[t][s / 4].x)[s % 4], acc[t][s], 0,
-                                                         0, 0);
-    }
-  }
-  if (nfull < nch) {
-    // A last, partial chunk: the segments past K are left alone (their zero
-    // padding would still turn a -0 sum into +0).
-    float4 a[4], b[TN][4];
-    operands(nfull, a, b);
-    const uint32_t ns = (K - 64 * nfull) / 4;
-#pragma unroll
-    for (int s = 0; s < 16; ++s) {
-      if ((uint32_t)s < ns) {
+      for (int s = 0; s < 16; ++s) {
         const float av = (&a[s / 4].x)[s % 4];
 #pragma unroll
-        for (int t = 0; t < TN; ++t)
+        for (int t = 0; t < (int)WN; ++t)
           acc[t][s] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, (&b[t][s / 4].x)[s % 4], acc[t][s],
                                                            0, 0, 0);
       }
     }
-  }
-  if (T >= nrt) return;
+    if (PARTIAL && nfull < nch) {
+      // A last, partial chunk: the segments past K are left alone (their
+      // zero padding would still turn a -0 sum into +0).
+      float4 a[4], b[WN][4];
+      operands(nfull, a, b);
+      const uint32_t ns = (K - 64 * nfull) / 4;
 #pragma unroll
-  for (int t = 0; t < TN; ++t) {
-    const f4v r = tree16(acc[t]);
-    const uint32_t b = (C0 + t) * 16 + lane % 16;
-    const uint32_t o = T * 16 + 4 * (lane / 16);
-    if (b >= B) continue;
+      for (int s = 0; s < 16; ++s) {
+        if ((uint32_t)s < ns && mfma_wave) {
+          const float av = (&a[s / 4].x)[s % 4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (o + j >= M) continue;
-      const size_t at = (size_t)b * ldy + o + j;
-      if (OUT == GO_PLAIN) {
-        Y[at] = r[j];
-      } else if (OUT == GO_RESID) {
-        Y[at] = Y[at] + r[j];
-      } else {
-        const float v = scale[b] * r[j];
-        reinterpret_cast<u64*>(Y)[at] = ((u64)gen[b] << 32) | (u64)__float_as_uint(v);
+          for (int t = 0; t < (int)WN; ++t)
+            acc[t][s] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, (&b[t][s / 4].x)[s % 4],
+                                                             acc[t][s], 0, 0, 0);
+        }
+      }
+    }
+    // The task's outputs, one tile at a time.
+    const uint32_t tk = blockIdx.x + gridDim.x * k;
+    const uint32_t T = 4 * (tk % nrg) + rt, C0 = cbase + (tk / nrg) * TN + half * WN;
+#pragma unroll
+    for (int t = 0; t < (int)WN; ++t) {
+      __builtin_amdgcn_sched_barrier(0);
+      const f4v r = tree16(acc[t]);
+      const uint32_t b = (C0 + t) * 16 + lane % 16;
+      const uint32_t o = T * 16 + 4 * (lane / 16);
+      if (!mfma_wave || T >= nrt || C0 + t >= cbase + ncols || b >= B) continue;
+      const size_t at = (size_t)b * ldy + o;
+      if (OUT != GO_TAG && o + 4 <= M && (at & 3) == 0) {
+        float4* y4 = reinterpret_cast<float4*>(Y + at);
+        float4 v = make_float4(r[0], r[1], r[2], r[3]);
+        if (OUT == GO_RESID) {
+          const float4 old = *y4;
+          v = make_float4(old.x + r[0], old.y + r[1], old.z + r[2], old.w + r[3]);
+        }
+        *y4 = v;
+        continue;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (o + j >= M) continue;
+        if (OUT == GO_PLAIN) {
+          Y[at + j] = r[j];
+        } else if (OUT == GO_RESID) {
+          Y[at + j] = Y[at + j] + r[j];
+        } else {
+          const float v = scale[b] * r[j];
+          reinterpret_cast<u64*>(Y)[at + j] = ((u64)gen[b] << 32) | (u64)__float_as_uint(v);
+        }
       }
     }
   }

@@ -571,13 +571,18 @@ extern "C" int defer_gpu_model_create(const defer_gpu_config* cfg, const float* 
                           hipGetErrorString(e)));
   }
   {
-    const void* gk[] = {(const void*)k_gemm<1, GO_PLAIN>, (const void*)k_gemm<1, GO_RESID>,
-                        (const void*)k_gemm<1, GO_TAG>,   (const void*)k_gemm<2, GO_PLAIN>,
-                        (const void*)k_gemm<2, GO_RESID>, (const void*)k_gemm<2, GO_TAG>,
-                        (const void*)k_gemm<4, GO_PLAIN>, (const void*)k_gemm<4, GO_RESID>,
-                        (const void*)k_gemm<4, GO_TAG>};
-    const int tn[] = {1, 1, 1, 2, 2, 2, 4, 4, 4};
-    for (int i = 0; i < 9; ++i) {
+    const void* gk[] = {
+        (const void*)k_gemm<1, GO_PLAIN, false>, (const void*)k_gemm<1, GO_RESID, false>,
+        (const void*)k_gemm<1, GO_TAG, false>,   (const void*)k_gemm<2, GO_PLAIN, false>,
+        (const void*)k_gemm<2, GO_RESID, false>, (const void*)k_gemm<2, GO_TAG, false>,
+        (const void*)k_gemm<4, GO_PLAIN, false>, (const void*)k_gemm<4, GO_RESID, false>,
+        (const void*)k_gemm<4, GO_TAG, false>,   (const void*)k_gemm<1, GO_PLAIN, true>,
+        (const void*)k_gemm<1, GO_RESID, true>,  (const void*)k_gemm<1, GO_TAG, true>,
+        (const void*)k_gemm<2, GO_PLAIN, true>,  (const void*)k_gemm<2, GO_RESID, true>,
+        (const void*)k_gemm<2, GO_TAG, true>,    (const void*)k_gemm<4, GO_PLAIN, true>,
+        (const void*)k_gemm<4, GO_RESID, true>,  (const void*)k_gemm<4, GO_TAG, true>};
+    const int tn[] = {1, 1, 1, 2, 2, 2, 4, 4, 4, 1, 1, 1, 2, 2, 2, 4, 4, 4};
+    for (int i = 0; i < 18; ++i) {
       e = hipFuncSetAttribute(gk[i], hipFuncAttributeMaxDynamicSharedMemorySize,
                               (int)gemm_lds_bytes(tn[i]));
       if (e != hipSuccess)
@@ -1310,10 +1315,17 @@ static int ensure_panels(defer_gpu_model* m) {
 template <int TN, uint32_t OUT>
 static void launch_gemm_tn(hipStream_t s, const float* Wp, uint32_t M, uint32_t K, const float* Xp,
                            uint32_t B, float* Y, uint32_t ldy, const float* scale,
-                           const uint32_t* gen, uint32_t cbase, uint32_t ncols) {
-  const uint32_t nrt = (M + 15) / 16;
-  k_gemm<TN, OUT><<<dim3((nrt + 3) / 4, (ncols + TN - 1) / TN), 256, gemm_lds_bytes(TN), s>>>(
-      Wp, M, K, Xp, B, Y, ldy, scale, gen, cbase);
+                           const uint32_t* gen, uint32_t cbase, uint32_t ncols, uint32_t ncu) {
+  const uint32_t nrg = (M + 63) / 64, ntask = nrg * ((ncols + TN - 1) / TN);
+  // One workgroup per CU (two for smaller tasks, whose LDS and registers allow it).
+  const uint32_t grid = std::min(ntask, (TN == 4 ? 1 : 2) * ncu);
+  const uint32_t threads = GEMM_WAVES * WAVE;
+  if (K % 64 == 0)
+    k_gemm<TN, OUT, false><<<grid, threads, gemm_lds_bytes(TN), s>>>(Wp, M, K, Xp, B, Y, ldy, scale,
+                                                                      gen, cbase, ncols);
+  else
+    k_gemm<TN, OUT, true><<<grid, threads, gemm_lds_bytes(TN), s>>>(Wp, M, K, Xp, B, Y, ldy, scale,
+                                                                     gen, cbase, ncols);
 }
 // One workgroup per CU runs at a time (registers and LDS), so a grid whose
 // last round would hold only a few workgroups is split: whole rounds of
@@ -1326,23 +1338,23 @@ static void launch_gemm_out(hipStream_t s, const float* Wp, uint32_t M, uint32_t
                             const uint32_t* gen, uint32_t ncu) {
   const uint32_t nct = (B + 15) / 16, nrg = (M + 63) / 64;
   if (nct <= 1) {
-    launch_gemm_tn<1, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 0, nct);
+    launch_gemm_tn<1, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 0, nct, ncu);
     return;
   }
   if (nct <= 2) {
-    launch_gemm_tn<2, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 0, nct);
+    launch_gemm_tn<2, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 0, nct, ncu);
     return;
   }
   const uint32_t w4 = nrg * ((nct + 3) / 4), rounds = w4 / ncu, rest = w4 % ncu;
   if (rounds >= 1 && rest > 0 && rest * 4 <= ncu) {
     const uint32_t y4 = rounds * ncu / nrg;  // column groups of 4 in the whole rounds
     if (y4 >= 1 && 4 * y4 < nct) {
-      launch_gemm_tn<4, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 0, 4 * y4);
-      launch_gemm_tn<1, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 4 * y4, nct - 4 * y4);
+      launch_gemm_tn<4, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 0, 4 * y4, ncu);
+      launch_gemm_tn<1, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 4 * y4, nct - 4 * y4, ncu);
       return;
     }
   }
-  launch_gemm_tn<4, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 0, nct);
+  launch_gemm_tn<4, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 0, nct, ncu);
 }
 static void launch_gemm(hipStream_t s, uint32_t ncu, uint32_t out, const float* Wp, uint32_t M,
                         uint32_t K, const float* Xp, uint32_t B, float* Y, uint32_t ldy,
