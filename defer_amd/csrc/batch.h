@@ -40,6 +40,12 @@ __host__ __device__ inline size_t panel_floats(uint32_t R, uint32_t K) {
   return (size_t)((R + 15) / 16) * panel_chunks(K) * PANEL_TILE;
 }
 
+// Position of element (row r, column k) in a panel of nch chunks.
+__host__ __device__ inline size_t panel_at(uint32_t r, uint32_t k, uint32_t nch) {
+  const uint32_t i = k / 64, s = (k % 64) / 4, c = k % 4;
+  return (((size_t)(r / 16) * nch + i) * 4 + s / 4) * 256 + ((r % 16) + 16 * c) * 4 + s % 4;
+}
+
 // Rows [0, R0) from src0, rows [R0, R) from src1 (row r - R0): a stacked
 // matrix without a stacked copy. ld: row stride of both sources.
 __global__ void k_to_panel(const float* __restrict__ src0, const float* __restrict__ src1,
@@ -65,7 +71,7 @@ __global__ void k_to_panel(const float* __restrict__ src0, const float* __restri
 
 enum GemmOut : uint32_t {
   GO_PLAIN = 0,  // Y[b][o] = y
-  GO_RESID = 1,  // Y[b][o] = Y[b][o] + y   (the residual stream, in place)
+  GO_RESID = 1,  // Y[b][o] = Y[b][o] + y   (the residual stream, in place; also into panel P)
   GO_TAG = 2,    // T[b][o] = tag(gen[b], scale[b] * y)  (tagged logits)
 };
 
@@ -107,7 +113,7 @@ __global__ __launch_bounds__(512) void k_gemm(const float* __restrict__ Wp, uint
                                               float* __restrict__ Y, uint32_t ldy,
                                               const float* __restrict__ scale,
                                               const uint32_t* __restrict__ gen, uint32_t cbase,
-                                              uint32_t ncols) {
+                                              uint32_t ncols, float* __restrict__ P) {
   extern __shared__ float4 gsm[];  // [stages][4 + TN tiles][4 quarters][64 lanes]
   constexpr uint32_t GEMM_STAGES = gemm_stages(TN);
   constexpr uint32_t NT = 4 + TN;                    // tiles per stage
@@ -204,12 +210,17 @@ __global__ __launch_bounds__(512) void k_gemm(const float* __restrict__ Wp, uint
       const uint32_t o = T * 16 + 4 * (lane / 16);
       if (!mfma_wave || T >= nrt || C0 + t >= cbase + ncols || b >= B) continue;
       const size_t at = (size_t)b * ldy + o;
+      const uint32_t nchp = panel_chunks(M);  // the residual's panel: K = M
       if (OUT != GO_TAG && o + 4 <= M && (at & 3) == 0) {
         float4* y4 = reinterpret_cast<float4*>(Y + at);
         float4 v = make_float4(r[0], r[1], r[2], r[3]);
         if (OUT == GO_RESID) {
           const float4 old = *y4;
           v = make_float4(old.x + r[0], old.y + r[1], old.z + r[2], old.w + r[3]);
+          P[panel_at(b, o, nchp)] = v.x;
+          P[panel_at(b, o + 1, nchp)] = v.y;
+          P[panel_at(b, o + 2, nchp)] = v.z;
+          P[panel_at(b, o + 3, nchp)] = v.w;
         }
         *y4 = v;
         continue;
@@ -220,7 +231,9 @@ __global__ __launch_bounds__(512) void k_gemm(const float* __restrict__ Wp, uint
         if (OUT == GO_PLAIN) {
           Y[at + j] = r[j];
         } else if (OUT == GO_RESID) {
-          Y[at + j] = Y[at + j] + r[j];
+          const float v = Y[at + j] + r[j];
+          Y[at + j] = v;
+          P[panel_at(b, o + j, nchp)] = v;
         } else {
           const float v = scale[b] * r[j];
           reinterpret_cast<u64*>(Y)[at + j] = ((u64)gen[b] << 32) | (u64)__float_as_uint(v);
@@ -240,12 +253,16 @@ struct BRow {
   uint32_t cap, pos, tick, token;
 };
 
-// X[b] = E[token_b] (model.rs:428).
+// X[b] = E[token_b] (model.rs:428), and its panel XP.
 __global__ void k_b_embed(const BRow* __restrict__ rows, const float* __restrict__ embed, uint32_t h,
-                          float* __restrict__ X) {
-  const uint32_t b = blockIdx.x;
+                          float* __restrict__ X, float* __restrict__ XP) {
+  const uint32_t b = blockIdx.x, nch = panel_chunks(h);
   const float* e = embed + (size_t)rows[b].token * h;
-  for (uint32_t i = threadIdx.x; i < h; i += blockDim.x) X[(size_t)b * h + i] = e[i];
+  for (uint32_t i = threadIdx.x; i < h; i += blockDim.x) {
+    const float v = e[i];
+    X[(size_t)b * h + i] = v;
+    XP[panel_at(b, i, nch)] = v;
+  }
 }
 
 // inv[b] = 1/rms(X[b]) in the order of rms_inv: each lane's elements
@@ -590,14 +607,14 @@ __global__ __launch_bounds__(256, 2) void k_b_attn_tile(const Dims d, const BRow
 }
 
 // Combine of the chunk partials (combine_scales / combine_value, as the O
-// phase does) into plain att[b][q]: one workgroup per row; the weights of a
+// phase does) into the panel of att[b][q]: one workgroup per row; the weights of a
 // head's chunks are formed once in LDS, then a thread per (head, dim). The
 // partials were written by earlier launches on the same stream, so their
 // values are read directly (the low half of each tagged word).
 constexpr uint32_t COMB_MAX_HEADS = 64;
 __global__ __launch_bounds__(256) void k_b_comb(const Dims d, const BRow* __restrict__ rows,
                                                 const u64* __restrict__ part, uint32_t part_w,
-                                                float* __restrict__ att, uint32_t lda) {
+                                                float* __restrict__ attp) {
   __shared__ float sc[COMB_MAX_HEADS][MAX_ACHUNKS];
   __shared__ float ls[COMB_MAX_HEADS];
   const uint32_t b = blockIdx.x;
@@ -612,31 +629,31 @@ __global__ __launch_bounds__(256) void k_b_comb(const Dims d, const BRow* __rest
   __syncthreads();
   for (uint32_t u = threadIdx.x; u < d.q; u += blockDim.x) {
     const uint32_t hh = u / d.hd, dd = u - hh * d.hd;
-    att[(size_t)b * lda + u] = combine_value(ld_head(hh), nch, hs, dd, sc[hh], ls[hh]);
+    attp[panel_at(b, u, panel_chunks(d.q))] = combine_value(ld_head(hh), nch, hs, dd, sc[hh], ls[hh]);
   }
 }
 
-// g = act(gate * inv) * (up * inv) (phase_gu); Y holds gate rows then up rows.
+// g = act(gate * inv) * (up * inv) (phase_gu), into the panel GP; Y holds
+// gate rows then up rows.
 __global__ void k_b_act(const float* __restrict__ Y, uint32_t ldy, const float* __restrict__ inv,
-                        uint32_t ff, uint32_t act, float* __restrict__ G, uint32_t ldg_) {
+                        uint32_t ff, uint32_t act, float* __restrict__ GP) {
   const uint32_t b = blockIdx.y;
   const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
   if (j >= ff) return;
   const float iv = inv[b];
   const float gate = Y[(size_t)b * ldy + j], up = Y[(size_t)b * ldy + ff + j];
-  G[(size_t)b * ldg_ + j] = act_fn(gate * iv, act) * (up * iv);
+  GP[panel_at(b, j, panel_chunks(ff))] = act_fn(gate * iv, act) * (up * iv);
 }
 
 // Final norm of the rows that need logits (phase_lm): xs = x * w_norm and
-// inv = 1/rms(x) in rms_inv's order. One wave per logits row; sel[i] is its
-// batch row.
+// inv = 1/rms(x) in rms_inv's order; xs goes into the panel XSP. One wave
+// per logits row; sel[i] is its batch row.
 __global__ __launch_bounds__(64) void k_b_final(const float* __restrict__ X,
                                                 const uint32_t* __restrict__ sel, uint32_t h,
                                                 const float* __restrict__ nrm, float eps,
-                                                float* __restrict__ XS, float* __restrict__ linv) {
-  const uint32_t i = blockIdx.x, lane = threadIdx.x;
+                                                float* __restrict__ XSP, float* __restrict__ linv) {
+  const uint32_t i = blockIdx.x, lane = threadIdx.x, nch = panel_chunks(h);
   const float* x = X + (size_t)sel[i] * h;
-  float* xs = XS + (size_t)i * h;
   float ss = 0.0f;
   for (uint32_t j = lane * 4; j < h; j += 256) {
     const float4 v = *reinterpret_cast<const float4*>(x + j);
@@ -644,10 +661,10 @@ __global__ __launch_bounds__(64) void k_b_final(const float* __restrict__ X,
     ss = fmaf(v.y, v.y, ss);
     ss = fmaf(v.z, v.z, ss);
     ss = fmaf(v.w, v.w, ss);
-    xs[j] = v.x * nrm[j];
-    xs[j + 1] = v.y * nrm[j + 1];
-    xs[j + 2] = v.z * nrm[j + 2];
-    xs[j + 3] = v.w * nrm[j + 3];
+    XSP[panel_at(i, j, nch)] = v.x * nrm[j];
+    XSP[panel_at(i, j + 1, nch)] = v.y * nrm[j + 1];
+    XSP[panel_at(i, j + 2, nch)] = v.z * nrm[j + 2];
+    XSP[panel_at(i, j + 3, nch)] = v.w * nrm[j + 3];
   }
   ss = wave_sum(ss);
   if (lane == 0) linv[i] = 1.0f / sqrtf(ss / (float)h + eps);

@@ -1194,8 +1194,10 @@ static constexpr uint32_t BATCH_MAX_ROWS = 2048;
 
 struct BatchWs {
   uint32_t rows = 0, lm = 0;  // capacities
-  float *X = nullptr, *Y = nullptr, *G = nullptr, *ATT = nullptr, *INV = nullptr, *XP = nullptr;
-  float *XS = nullptr, *LINV = nullptr;
+  // X: the residual rows; XP its GEMM panel (written with it); XQ the panel of
+  // the other GEMM inputs (attention output, activation, final-norm rows).
+  float *X = nullptr, *Y = nullptr, *INV = nullptr, *XP = nullptr, *XQ = nullptr;
+  float* LINV = nullptr;
   u64 *QKVT = nullptr, *PART = nullptr, *LOGT = nullptr, *VMAX = nullptr, *VARG = nullptr,
       *VSUM = nullptr;
   BRow* drows = nullptr;
@@ -1210,7 +1212,7 @@ struct BatchWs {
 
 static void batch_ws_release(BatchWs* w) {
   if (!w) return;
-  void* ps[] = {w->X, w->Y, w->G, w->ATT, w->INV, w->XP, w->XS, w->LINV, w->QKVT, w->PART,
+  void* ps[] = {w->X, w->Y, w->INV, w->XP, w->XQ, w->LINV, w->QKVT, w->PART,
                 w->LOGT, w->VMAX, w->VARG, w->VSUM, w->drows, w->rargs, w->largs, w->sel,
                 w->lgen, w->stick, w->swords, w->sout, w->items, w->tiles, w->sets, w->st};
   for (void* p : ps) (void)hipFree(p);
@@ -1237,10 +1239,8 @@ static int ensure_ws(defer_gpu_model* m, uint32_t rows, uint32_t lm) {
   const uint32_t kmax = std::max({d.h, d.q, d.ff});
   HIP_TRY(hipMalloc(&w.X, (size_t)R * d.h * sizeof(float)));
   HIP_TRY(hipMalloc(&w.Y, (size_t)R * batch_ldy(d) * sizeof(float)));
-  HIP_TRY(hipMalloc(&w.G, (size_t)R * d.ff * sizeof(float)));
-  HIP_TRY(hipMalloc(&w.ATT, (size_t)R * d.q * sizeof(float)));
   HIP_TRY(hipMalloc(&w.INV, (size_t)R * sizeof(float)));
-  HIP_TRY(hipMalloc(&w.XP, panel_floats(R, kmax) * sizeof(float)));
+  HIP_TRY(hipMalloc(&w.XP, panel_floats(R, d.h) * sizeof(float)));
   HIP_TRY(hipMalloc(&w.QKVT, (size_t)R * d.qkv_rows * sizeof(u64)));
   HIP_TRY(hipMalloc(&w.PART, (size_t)R * part_words(d) * sizeof(u64)));
   HIP_TRY(hipMalloc(&w.drows, (size_t)R * sizeof(BRow)));
@@ -1249,7 +1249,7 @@ static int ensure_ws(defer_gpu_model* m, uint32_t rows, uint32_t lm) {
   HIP_TRY(hipMalloc(&w.tiles, ((size_t)R / 16 + 2) * sizeof(uint32_t)));
   HIP_TRY(hipMalloc(&w.sets, (size_t)R * sizeof(StateSet)));
   const uint32_t L1 = std::max(Lm, 1u);
-  HIP_TRY(hipMalloc(&w.XS, (size_t)L1 * d.h * sizeof(float)));
+  HIP_TRY(hipMalloc(&w.XQ, panel_floats(std::max(R, L1), kmax) * sizeof(float)));
   HIP_TRY(hipMalloc(&w.LINV, (size_t)L1 * sizeof(float)));
   HIP_TRY(hipMalloc(&w.LOGT, (size_t)L1 * d.V * sizeof(u64)));
   HIP_TRY(hipMalloc(&w.VMAX, (size_t)L1 * d.nvc * sizeof(u64)));
@@ -1315,17 +1315,18 @@ static int ensure_panels(defer_gpu_model* m) {
 template <int TN, uint32_t OUT>
 static void launch_gemm_tn(hipStream_t s, const float* Wp, uint32_t M, uint32_t K, const float* Xp,
                            uint32_t B, float* Y, uint32_t ldy, const float* scale,
-                           const uint32_t* gen, uint32_t cbase, uint32_t ncols, uint32_t ncu) {
+                           const uint32_t* gen, uint32_t cbase, uint32_t ncols, uint32_t ncu,
+                           float* P) {
   const uint32_t nrg = (M + 63) / 64, ntask = nrg * ((ncols + TN - 1) / TN);
   // One workgroup per CU (two for smaller tasks, whose LDS and registers allow it).
   const uint32_t grid = std::min(ntask, (TN == 4 ? 1 : 2) * ncu);
   const uint32_t threads = GEMM_WAVES * WAVE;
   if (K % 64 == 0)
     k_gemm<TN, OUT, false><<<grid, threads, gemm_lds_bytes(TN), s>>>(Wp, M, K, Xp, B, Y, ldy, scale,
-                                                                      gen, cbase, ncols);
+                                                                      gen, cbase, ncols, P);
   else
     k_gemm<TN, OUT, true><<<grid, threads, gemm_lds_bytes(TN), s>>>(Wp, M, K, Xp, B, Y, ldy, scale,
-                                                                     gen, cbase, ncols);
+                                                                     gen, cbase, ncols, P);
 }
 // One workgroup per CU runs at a time (registers and LDS), so a grid whose
 // last round would hold only a few workgroups is split: whole rounds of
@@ -1335,33 +1336,35 @@ static void launch_gemm_tn(hipStream_t s, const float* Wp, uint32_t M, uint32_t 
 template <uint32_t OUT>
 static void launch_gemm_out(hipStream_t s, const float* Wp, uint32_t M, uint32_t K, const float* Xp,
                             uint32_t B, float* Y, uint32_t ldy, const float* scale,
-                            const uint32_t* gen, uint32_t ncu) {
+                            const uint32_t* gen, uint32_t ncu, float* P) {
   const uint32_t nct = (B + 15) / 16, nrg = (M + 63) / 64;
   if (nct <= 1) {
-    launch_gemm_tn<1, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 0, nct, ncu);
+    launch_gemm_tn<1, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 0, nct, ncu, P);
     return;
   }
   if (nct <= 2) {
-    launch_gemm_tn<2, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 0, nct, ncu);
+    launch_gemm_tn<2, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 0, nct, ncu, P);
     return;
   }
   const uint32_t w4 = nrg * ((nct + 3) / 4), rounds = w4 / ncu, rest = w4 % ncu;
   if (rounds >= 1 && rest > 0 && rest * 4 <= ncu) {
     const uint32_t y4 = rounds * ncu / nrg;  // column groups of 4 in the whole rounds
     if (y4 >= 1 && 4 * y4 < nct) {
-      launch_gemm_tn<4, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 0, 4 * y4, ncu);
-      launch_gemm_tn<1, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 4 * y4, nct - 4 * y4, ncu);
+      launch_gemm_tn<4, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 0, 4 * y4, ncu, P);
+      launch_gemm_tn<1, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 4 * y4, nct - 4 * y4, ncu, P);
       return;
     }
   }
-  launch_gemm_tn<4, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 0, nct, ncu);
+  launch_gemm_tn<4, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 0, nct, ncu, P);
 }
+// P: GO_RESID's panel of the updated rows (K = M).
 static void launch_gemm(hipStream_t s, uint32_t ncu, uint32_t out, const float* Wp, uint32_t M,
                         uint32_t K, const float* Xp, uint32_t B, float* Y, uint32_t ldy,
-                        const float* scale = nullptr, const uint32_t* gen = nullptr) {
-  if (out == GO_PLAIN) launch_gemm_out<GO_PLAIN>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, ncu);
-  else if (out == GO_RESID) launch_gemm_out<GO_RESID>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, ncu);
-  else launch_gemm_out<GO_TAG>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, ncu);
+                        const float* scale = nullptr, const uint32_t* gen = nullptr,
+                        float* P = nullptr) {
+  if (out == GO_PLAIN) launch_gemm_out<GO_PLAIN>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, ncu, P);
+  else if (out == GO_RESID) launch_gemm_out<GO_RESID>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, ncu, P);
+  else launch_gemm_out<GO_TAG>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, ncu, P);
 }
 
 // Timing of one launch (profiling on): events recorded around it on the
@@ -1490,10 +1493,9 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
   }
   k_begin<<<1, 1, 0, s>>>(w.st);
   const uint32_t ldy = batch_ldy(d);
-  k_b_embed<<<n, 256, 0, s>>>(w.drows, m->embed, d.h, w.X);
+  k_b_embed<<<n, 256, 0, s>>>(w.drows, m->embed, d.h, w.X, w.XP);
   for (uint32_t l = 0; l < d.L; ++l) {
     k_b_rms<<<(n + 3) / 4, 256, 0, s>>>(w.X, n, d.h, d.eps, w.INV);
-    launch_panel(s, w.X, w.X, n, n, d.h, d.h, w.XP);
     {
       ProfSpan ps(m, 0, 2.0 * d.qkv_rows * d.h * n);
       launch_gemm(s, m->ncu, GO_PLAIN, m->p_qkv[l], d.qkv_rows, d.h, w.XP, n, w.Y, ldy);
@@ -1508,31 +1510,29 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
       else
         k_b_attn<<<(uint32_t)items.size(), BLOCK, m->lds_rows, s>>>(w.rargs, w.drows, w.items, l);
     }
-    k_b_comb<<<n, 256, 0, s>>>(d, w.drows, w.PART, part_words(d), w.ATT, d.q);
-    launch_panel(s, w.ATT, w.ATT, n, n, d.q, d.q, w.XP);
+    k_b_comb<<<n, 256, 0, s>>>(d, w.drows, w.PART, part_words(d), w.XQ);
     {
       ProfSpan ps(m, 0, 2.0 * d.h * d.q * n);
-      launch_gemm(s, m->ncu, GO_RESID, m->p_o[l], d.h, d.q, w.XP, n, w.X, d.h);
+      launch_gemm(s, m->ncu, GO_RESID, m->p_o[l], d.h, d.q, w.XQ, n, w.X, d.h, nullptr, nullptr,
+                  w.XP);
     }
     k_b_rms<<<(n + 3) / 4, 256, 0, s>>>(w.X, n, d.h, d.eps, w.INV);
-    launch_panel(s, w.X, w.X, n, n, d.h, d.h, w.XP);
     {
       ProfSpan ps(m, 0, 2.0 * 2 * d.ff * d.h * n);
       launch_gemm(s, m->ncu, GO_PLAIN, m->p_gu[l], 2 * d.ff, d.h, w.XP, n, w.Y, ldy);
     }
-    k_b_act<<<dim3((d.ff + 255) / 256, n), 256, 0, s>>>(w.Y, ldy, w.INV, d.ff, d.act, w.G, d.ff);
-    launch_panel(s, w.G, w.G, n, n, d.ff, d.ff, w.XP);
+    k_b_act<<<dim3((d.ff + 255) / 256, n), 256, 0, s>>>(w.Y, ldy, w.INV, d.ff, d.act, w.XQ);
     {
       ProfSpan ps(m, 0, 2.0 * d.h * d.ff * n);
-      launch_gemm(s, m->ncu, GO_RESID, m->p_d[l], d.h, d.ff, w.XP, n, w.X, d.h);
+      launch_gemm(s, m->ncu, GO_RESID, m->p_d[l], d.h, d.ff, w.XQ, n, w.X, d.h, nullptr, nullptr,
+                  w.XP);
     }
   }
   if (nl) {
-    k_b_final<<<nl, 64, 0, s>>>(w.X, w.sel, d.h, m->norm, d.eps, w.XS, w.LINV);
-    launch_panel(s, w.XS, w.XS, nl, nl, d.h, d.h, w.XP);
+    k_b_final<<<nl, 64, 0, s>>>(w.X, w.sel, d.h, m->norm, d.eps, w.XQ, w.LINV);
     {
       ProfSpan ps(m, 0, 2.0 * d.V * d.h * nl);
-      launch_gemm(s, m->ncu, GO_TAG, m->p_lm, d.V, d.h, w.XP, nl, reinterpret_cast<float*>(w.LOGT), d.V,
+      launch_gemm(s, m->ncu, GO_TAG, m->p_lm, d.V, d.h, w.XQ, nl, reinterpret_cast<float*>(w.LOGT), d.V,
                   w.LINV, w.lgen);
     }
     k_b_chunkmax<<<dim3((d.nvc + 3) / 4, nl), 256, 0, s>>>(d, w.LOGT, w.lgen, w.VMAX, w.VARG, nl);
