@@ -792,18 +792,17 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
     const float* kb = a.kc + ((size_t)l * d.nkv + g) * d.cap * d.kvs + sub * 16;
     const float* vb = a.vc + ((size_t)l * d.nkv + g) * d.cap * d.kvs + dl * 4;
     // The chunk's first K rows (score pass) and V rows (value pass) of the
-    // history are requested before waiting for this token's q/k/v.
-    float4 kr[4];
-    if (att && t0 + tw < t1 && t0 + tw < pos) {
-      const float* r = kb + (size_t)(t0 + tw) * d.kvs;
+    // history are requested before waiting for this token's q/k/v, all in
+    // one straight run (rows past the chunk are clamped to a row of the
+    // cache and never used), so no load waits for another.
+    float4 kr[4], vr[VU];
+    if (att) {
+      const float* r = kb + (size_t)min(t0 + tw, d.cap - 1) * d.kvs;
 #pragma unroll
       for (uint32_t i = 0; i < 4; ++i) kr[i] = ldg4(r + 4 * i);
-    }
-    float4 vr[VU];
 #pragma unroll
-    for (uint32_t u = 0; u < VU; ++u) {
-      const uint32_t t = t0 + vw + u * vstep;
-      if (att && t < t1 && t < pos) vr[u] = ldg4(vb + (size_t)t * d.kvs);
+      for (uint32_t u = 0; u < VU; ++u)
+        vr[u] = ldg4(vb + (size_t)min(t0 + vw + u * vstep, d.cap - 1) * d.kvs);
     }
     if (!poll_gather<2, 1, 1>(gather_vec(a.mb_qkv + (size_t)(g * grp + j0) * hd, hd, gen_in, qs),
                               gather_vec(a.mb_qkv + d.q + g * hd, hd, gen_in, kn),
