@@ -243,6 +243,106 @@ __global__ __launch_bounds__(512) void k_gemm(const float* __restrict__ Wp, uint
   }
 }
 
+// The same product for narrow batches (at most four column tiles, B <= 64):
+// a task is one row tile with every column tile, so there are enough tasks
+// to stream the weights through every CU. Wave w computes column tile w % 4
+// over segments 8h .. 8h+7 (h = w / 4) and forms their subtree; the two
+// halves meet in LDS as (s0..s7) + (s8..s15) -- the same tree16.
+constexpr uint32_t GEMMN_STAGES = 3;  // two workgroups per CU
+__host__ __device__ constexpr uint32_t gemm_n_lds_bytes() {
+  return GEMMN_STAGES * 5 * PANEL_TILE * 4 + 4 * 64 * 16;
+}
+template <uint32_t OUT, bool PARTIAL>
+__global__ __launch_bounds__(512) void k_gemm_n(const float* __restrict__ Wp, uint32_t M,
+                                                uint32_t K, const float* __restrict__ Xp,
+                                                uint32_t B, float* __restrict__ Y, uint32_t ldy,
+                                                const float* __restrict__ scale,
+                                                const uint32_t* __restrict__ gen,
+                                                float* __restrict__ P) {
+  extern __shared__ float4 gsm[];  // [stages][5 tiles][4 quarters][64 lanes], then [4][64] f4v
+  constexpr uint32_t NT = 5, NQ = 4 * NT;
+  f4v* half_sum = reinterpret_cast<f4v*>(gsm + GEMMN_STAGES * NT * 256);
+  const uint32_t wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+  const uint32_t ct = wave % 4, h = wave / 4;
+  const uint32_t nch = panel_chunks(K), nrt = (M + 15) / 16, nct = (B + 15) / 16;
+  const uint32_t nld = (NQ - wave + GEMM_WAVES - 1) / GEMM_WAVES;
+  const uint32_t mine = blockIdx.x < nrt ? (nrt - blockIdx.x + gridDim.x - 1) / gridDim.x : 0;
+  const uint32_t total = mine * nch;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)gsm;
+  auto issue = [&](uint32_t g, uint32_t st) {
+    const uint32_t T = blockIdx.x + gridDim.x * (g / nch), i = g % nch;
+    const uint32_t sb = lds0 + st * NT * PANEL_TILE * 4;
+#pragma unroll
+    for (uint32_t f = wave; f < NQ; f += GEMM_WAVES) {
+      const uint32_t tile = f / 4, q = f % 4;
+      const float* src = tile == 0 ? Wp + ((size_t)T * nch + i) * PANEL_TILE
+                                   : Xp + ((size_t)min(tile - 1, nct - 1) * nch + i) * PANEL_TILE;
+      dma16(src + q * 256 + lane * 4, sb + f * 1024);
+    }
+  };
+  for (uint32_t g = 0; g + 1 < GEMMN_STAGES && g < total; ++g) issue(g, g);
+  for (uint32_t k = 0; k < mine; ++k) {
+    f4v acc[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) acc[s] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t i = 0; i < nch; ++i) {
+      const uint32_t g = k * nch + i;
+      stage_wait(min(GEMMN_STAGES - 2, total - 1 - g) * nld);
+      __syncthreads();
+      if (g + GEMMN_STAGES - 1 < total)
+        issue(g + GEMMN_STAGES - 1, (g + GEMMN_STAGES - 1) % GEMMN_STAGES);
+      const float4* sa = gsm + (g % GEMMN_STAGES) * NT * 256;
+      float4 a[2], b[2];
+#pragma unroll
+      for (int qq = 0; qq < 2; ++qq) {
+        a[qq] = sa[(2 * h + qq) * 64 + lane];
+        b[qq] = sa[((1 + ct) * 4 + 2 * h + qq) * 64 + lane];
+      }
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        // A last, partial chunk: the segments past K are left alone (their
+        // zero padding would still turn a -0 sum into +0).
+        if (PARTIAL && 64 * i + 4 * (8 * h + s) >= K) continue;
+        acc[s] = __builtin_amdgcn_mfma_f32_16x16x4f32((&a[s / 4].x)[s % 4], (&b[s / 4].x)[s % 4],
+                                                      acc[s], 0, 0, 0);
+      }
+    }
+    // Subtree of this wave's eight segments; the upper half hands its own to
+    // the lower half through LDS.
+    f4v p4[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) p4[u] = acc[2 * u] + acc[2 * u + 1];
+    const f4v t8 = (p4[0] + p4[1]) + (p4[2] + p4[3]);
+    if (h == 1) half_sum[ct * 64 + lane] = t8;
+    __syncthreads();
+    const uint32_t T = blockIdx.x + gridDim.x * k;
+    if (h == 0 && ct < nct) {
+      const f4v r = t8 + half_sum[ct * 64 + lane];
+      const uint32_t b = ct * 16 + lane % 16;
+      const uint32_t o = T * 16 + 4 * (lane / 16);
+      if (b < B) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (o + j >= M) continue;
+          const size_t at = (size_t)b * ldy + o + j;
+          if (OUT == GO_PLAIN) {
+            Y[at] = r[j];
+          } else if (OUT == GO_RESID) {
+            const float v = Y[at] + r[j];
+            Y[at] = v;
+            P[panel_at(b, o + j, panel_chunks(M))] = v;
+          } else {
+            const float v = scale[b] * r[j];
+            reinterpret_cast<u64*>(Y)[at] = ((u64)gen[b] << 32) | (u64)__float_as_uint(v);
+          }
+        }
+      }
+    }
+    // half_sum is rewritten by the next task only after this barrier.
+    __syncthreads();
+  }
+}
+
 // ------------------------------------------------------------- rows
 
 // One row of a batch: the cache it extends, at which position and

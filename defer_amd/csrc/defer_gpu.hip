@@ -588,6 +588,14 @@ extern "C" int defer_gpu_model_create(const defer_gpu_config* cfg, const float* 
       if (e != hipSuccess)
         return cleanup(fail(DEFER_GPU_E_HIP, "LDS attribute (GEMM): %s", hipGetErrorString(e)));
     }
+    const void* gn[] = {(const void*)k_gemm_n<GO_PLAIN, false>, (const void*)k_gemm_n<GO_RESID, false>,
+                        (const void*)k_gemm_n<GO_TAG, false>,   (const void*)k_gemm_n<GO_PLAIN, true>,
+                        (const void*)k_gemm_n<GO_RESID, true>,  (const void*)k_gemm_n<GO_TAG, true>};
+    for (const void* kf : gn) {
+      e = hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)gemm_n_lds_bytes());
+      if (e != hipSuccess)
+        return cleanup(fail(DEFER_GPU_E_HIP, "LDS attribute (narrow GEMM): %s", hipGetErrorString(e)));
+    }
   }
   e = hipFuncSetAttribute((const void*)k_b_attn_tile, hipFuncAttributeMaxDynamicSharedMemorySize,
                           (int)attn_tile_lds(MAX_GROUP));
@@ -1338,12 +1346,14 @@ static void launch_gemm_out(hipStream_t s, const float* Wp, uint32_t M, uint32_t
                             uint32_t B, float* Y, uint32_t ldy, const float* scale,
                             const uint32_t* gen, uint32_t ncu, float* P) {
   const uint32_t nct = (B + 15) / 16, nrg = (M + 63) / 64;
-  if (nct <= 1) {
-    launch_gemm_tn<1, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 0, nct, ncu, P);
-    return;
-  }
-  if (nct <= 2) {
-    launch_gemm_tn<2, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 0, nct, ncu, P);
+  if (nct <= 4) {  // narrow: one row tile per task, enough tasks for every CU
+    const uint32_t grid = std::min((M + 15) / 16, 2 * ncu), threads = GEMM_WAVES * WAVE;
+    if (K % 64 == 0)
+      k_gemm_n<OUT, false><<<grid, threads, gemm_n_lds_bytes(), s>>>(Wp, M, K, Xp, B, Y, ldy, scale,
+                                                                     gen, P);
+    else
+      k_gemm_n<OUT, true><<<grid, threads, gemm_n_lds_bytes(), s>>>(Wp, M, K, Xp, B, Y, ldy, scale,
+                                                                    gen, P);
     return;
   }
   const uint32_t w4 = nrg * ((nct + 3) / 4), rounds = w4 / ncu, rest = w4 % ncu;
