@@ -234,6 +234,39 @@ __global__ void k_kv_gather(const float* src, float* dst, uint32_t len, uint32_t
   dst[i] = src[((size_t)g * cap + t) * kvs + dd];
 }
 
+// ValueNorms::sync (attribution.rs:116-148): ||W_o,h . v_{t,kv(h)}|| for
+// positions t0 + blockIdx.y, query head blockIdx.x, layer blockIdx.z. Thread
+// i forms o_i = sum_d Wo[i][h*hd + d] * v[d] as a sequential sum of rounded
+// products (built without contraction, so no fused multiply-add), the
+// squares go to LDS, and one thread adds them in order i = 0, 1, ... before
+// the square root -- the reference's loop order exactly.
+__global__ __launch_bounds__(256) void k_value_norms(const LayerW* __restrict__ layers,
+                                                     const float* __restrict__ vc, Dims d,
+                                                     uint32_t cap, uint32_t t0, uint32_t nt,
+                                                     float* __restrict__ out) {
+  extern __shared__ float vn_lds[];  // [hd] value row, then [h] squares
+  const uint32_t h = blockIdx.x, t = t0 + blockIdx.y, l = blockIdx.z;
+  const uint32_t kvh = h / d.group, hd = d.hd;
+  float* v = vn_lds;
+  float* sq = vn_lds + hd;
+  const float* vrow = vc + (((size_t)l * d.nkv + kvh) * cap + t) * d.kvs;
+  for (uint32_t x = threadIdx.x; x < hd; x += blockDim.x) v[x] = vrow[x];
+  __syncthreads();
+  const float* wo = layers[l].wo;
+  for (uint32_t i = threadIdx.x; i < d.h; i += blockDim.x) {
+    const float* row = wo + (size_t)i * d.q + h * hd;
+    float o = 0.0f;
+    for (uint32_t x = 0; x < hd; ++x) o = o + row[x] * v[x];
+    sq[i] = o * o;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float s = 0.0f;
+    for (uint32_t i = 0; i < d.h; ++i) s = s + sq[i];
+    out[((size_t)l * nt + blockIdx.y) * d.nh + h] = sqrtf(s);
+  }
+}
+
 // ------------------------------------------------------------------ host side
 
 struct defer_gpu_model {
@@ -811,6 +844,30 @@ extern "C" int defer_gpu_cache_read(const defer_gpu_cache* cc, uint32_t layer, f
     HIP_TRY(hipMemcpyAsync(dst, c->d_tmp, n * sizeof(float), hipMemcpyDeviceToHost, s));
     HIP_TRY(hipStreamSynchronize(s));
   }
+  return DEFER_GPU_OK;
+}
+
+extern "C" int defer_gpu_value_norms(const defer_gpu_cache* cc, uint32_t t0, uint32_t t1,
+                                     float* out) {
+  defer_gpu_cache* c = const_cast<defer_gpu_cache*>(cc);
+  if (!c || !out) return fail(DEFER_GPU_E_INVALID, "null cache or output");
+  if (t0 > t1 || t1 > c->pos)
+    return fail(DEFER_GPU_E_INVALID, "positions [%u, %u) outside the cache's %u", t0, t1, c->pos);
+  const defer_gpu_model* m = c->m;
+  const Dims& d = m->d;
+  const uint32_t nt = t1 - t0;
+  if (nt == 0) return DEFER_GPU_OK;
+  const size_t n = (size_t)d.L * nt * d.nh;
+  float* dout = nullptr;
+  HIP_TRY(hipMalloc(&dout, n * sizeof(float)));
+  const hipStream_t s = m->stream;
+  k_value_norms<<<dim3(d.nh, nt, d.L), 256, (d.hd + d.h) * sizeof(float), s>>>(
+      m->d_layers, c->vc, d, c->cap, t0, nt, dout);
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess) e = hipMemcpyAsync(out, dout, n * sizeof(float), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  (void)hipFree(dout);
+  if (e != hipSuccess) return fail(DEFER_GPU_E_HIP, "value norms: %s", hipGetErrorString(e));
   return DEFER_GPU_OK;
 }
 

@@ -103,6 +103,8 @@ def lib() -> ctypes.CDLL:
     L.defer_gpu_cache_clone.restype = ctypes.c_int
     L.defer_gpu_cache_read.argtypes = [vp, u32, vp, vp]
     L.defer_gpu_cache_read.restype = ctypes.c_int
+    L.defer_gpu_value_norms.argtypes = [vp, u32, u32, vp]
+    L.defer_gpu_value_norms.restype = ctypes.c_int
     L.defer_gpu_forward.argtypes = [vp, vp, u32, vp, sz, vp, vp]
     L.defer_gpu_forward.restype = ctypes.c_int
     L.defer_gpu_last_logits.argtypes = [vp, vp]
@@ -324,7 +326,47 @@ class GpuCache:
         _check(lib().defer_gpu_cache_read(self._h, int(layer), _ptr(k), _ptr(v)))
         return k, v
 
+    def value_norms(self, t0: int, t1: int) -> np.ndarray:
+        """||W_o,h . v_{t,kv(h)}|| for positions [t0, t1): [layers, t1 - t0, heads]
+        (the extension step of ValueNorms::sync, attribution.rs:116-148)."""
+        c = self.model.cfg
+        out = np.empty((c.num_layers, t1 - t0, c.num_heads), dtype=np.float32)
+        _check(lib().defer_gpu_value_norms(self._h, int(t0), int(t1), _ptr(out)))
+        return out
+
     def last_logits(self) -> np.ndarray:
         out = np.empty(self.model.vocab_size, dtype=np.float32)
         _check(lib().defer_gpu_last_logits(self._h, _ptr(out)))
         return out
+
+
+class ValueNorms:
+    """Cache of ||W_o,h . v_{t,kv(h)}|| per (layer, position, query head)
+    (attribution.rs:91-153): values depend only on the cached V rows, so they
+    are computed once per position -- on the device -- and reused."""
+
+    def __init__(self, model: "GpuModel"):
+        self.num_heads = model.cfg.num_heads
+        self._len = 0
+        self.per_layer = [np.zeros((0, self.num_heads), dtype=np.float32)
+                          for _ in range(model.cfg.num_layers)]
+
+    def __len__(self) -> int:
+        return self._len
+
+    def is_empty(self) -> bool:
+        return self._len == 0
+
+    def sync(self, cache: "GpuCache") -> None:
+        """Bring the cache in line with `cache` (extend, or drop stale entries)."""
+        n = len(cache)
+        if n < self._len:
+            self.per_layer = [v[:n] for v in self.per_layer]
+            self._len = n
+        if n > self._len:
+            new = cache.value_norms(self._len, n)
+            self.per_layer = [np.concatenate([v, new[l]]) for l, v in enumerate(self.per_layer)]
+        self._len = n
+
+    def get(self, layer: int, t: int, head: int) -> float:
+        return float(self.per_layer[layer][t, head])

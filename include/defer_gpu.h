@@ -88,6 +88,15 @@ int defer_gpu_cache_clone(const defer_gpu_cache* c, defer_gpu_cache** out); /* d
  * [len, kv_dim] row-major host array. */
 int defer_gpu_cache_read(const defer_gpu_cache* c, uint32_t layer, float* keys, float* values);
 
+/* ValueNorms::sync (attribution.rs:116-148), the extension step: for cached
+ * positions t in [t0, t1), every layer l and query head h,
+ * out[(l * (t1 - t0) + t - t0) * num_heads + h] = ||W_o,h . v_{t,kv(h)}||,
+ * computed on the device in the reference's order (sequential sums of
+ * rounded products, then sqrt), so the values equal the CPU loop's bit for
+ * bit. The caller keeps the per-layer arrays and truncates them as
+ * ValueNorms::sync does when the cache shrinks. */
+int defer_gpu_value_norms(const defer_gpu_cache* c, uint32_t t0, uint32_t t1, float* out);
+
 /* Model::forward_ext (model.rs:394-520). Appends the token's keys/values at
  * position cache_len and keeps the logits on the device. `logits_out` [V]
  * and `trace_out` [L, num_heads, pos+1] may be NULL. `masked` lists earlier

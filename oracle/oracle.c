@@ -605,3 +605,21 @@ int64_t oracle_checkout(const oracle_model* m, oracle_cache* c, const uint8_t se
   free(logits);
   return -1;
 }
+
+/* attribution.rs:116-148 (ValueNorms::sync, the loop body per layer) */
+void oracle_value_norms(const float* wo, const float* vals, uint32_t hidden, uint32_t nh,
+                        uint32_t nkv, uint32_t hd, uint32_t t0, uint32_t t1, float* out) {
+  const uint32_t q_dim = nh * hd, kv_dim = nkv * hd, group = nh / nkv;
+  for (uint32_t t = t0; t < t1; ++t)
+    for (uint32_t h = 0; h < nh; ++h) {
+      const float* v = vals + (size_t)t * kv_dim + (h / group) * hd;
+      float sq = 0.0f;
+      for (uint32_t i = 0; i < hidden; ++i) {
+        const float* row = wo + (size_t)i * q_dim + h * hd;
+        float o = 0.0f;
+        for (uint32_t d = 0; d < hd; ++d) o += row[d] * v[d];
+        sq += o * o;
+      }
+      out[(size_t)(t - t0) * nh + h] = sqrtf(sq);
+    }
+}

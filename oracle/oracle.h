@@ -22,6 +22,9 @@
  *                    8-round zero-key keystream.
  *   seed_from_u64 -- parity unpinned (rand_core 0.6.4 PCG32 expansion; no
  *                    vector exists outside the crate).
+ *   value_norms   -- closed forms: a one-hot value row returns the norm of
+ *                    one column of W_o (float64 within 1e-6), scaling v by
+ *                    2^k scales every norm by exactly 2^k, zero v gives 0.
  */
 #ifndef DEFER_ORACLE_H
 #define DEFER_ORACLE_H
@@ -127,4 +130,12 @@ int64_t oracle_checkout(const oracle_model* m, oracle_cache* c, const uint8_t se
 #ifdef __cplusplus
 }
 #endif
+/* ValueNorms::sync (attribution.rs:116-148) for one layer: for positions
+ * t in [t0, t1) and query heads h, out[(t - t0) * nh + h] =
+ * sqrt(sum_i (sum_d wo[i][h*hd + d] * v[t][kvh*hd + d])^2), kvh = h / group,
+ * each sum sequential with the product rounded before the add. wo is
+ * [hidden][nh*hd]; vals is the layer's cached values [t][nkv*hd]. */
+void oracle_value_norms(const float* wo, const float* vals, uint32_t hidden, uint32_t nh,
+                        uint32_t nkv, uint32_t hd, uint32_t t0, uint32_t t1, float* out);
+
 #endif

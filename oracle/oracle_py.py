@@ -97,6 +97,8 @@ def lib() -> ctypes.CDLL:
     L.oracle_generate.argtypes = [vp, vp, vp, f32, vp, sz, sz, vp, vp]
     L.oracle_generate.restype = ctypes.c_int64
     L.oracle_checkout.argtypes = [vp, vp, vp, f32, vp, sz, sz, P(u32), vp]
+    L.oracle_value_norms.argtypes = [vp, vp, u32, u32, u32, u32, u32, u32, vp]
+    L.oracle_value_norms.restype = None
     L.oracle_checkout.restype = ctypes.c_int64
     _lib = L
     return L
@@ -179,6 +181,15 @@ def mul_inplace(a, b) -> np.ndarray:
 def argmax(logits) -> int:
     l = f32a(logits)
     return int(lib().oracle_argmax(_p(l), l.size))
+
+
+def value_norms(wo, vals, hidden: int, nh: int, nkv: int, hd: int, t0: int, t1: int) -> np.ndarray:
+    """ValueNorms::sync for one layer (attribution.rs:116-148): [t1 - t0, nh]."""
+    w = f32a(wo)
+    v = f32a(vals)
+    out = np.zeros((t1 - t0, nh), dtype=np.float32)
+    lib().oracle_value_norms(_p(w), _p(v), hidden, nh, nkv, hd, t0, t1, _p(out))
+    return out
 
 
 def softmax_with_temperature(logits, t) -> np.ndarray:

@@ -187,3 +187,46 @@ def test_attention_trace_matches_oracle():
         assert float(np.max(np.abs(lg - lo))) <= LOGIT_TOL
         gc.truncate(7)
         oc.truncate(7)
+
+
+def _wo(cfg, w, layer):
+    """W_o of a layer from the canonical tensor list [h, q]."""
+    names = [n for n, _, _ in synthetic.tensor_specs(cfg)]
+    return w[names.index(f"model.layers.{layer}.self_attn.o_proj.weight")]
+
+
+@pytest.mark.parametrize("name", ["tiny", "smollm2-135m"])
+def test_value_norms_match_oracle_bitwise(name):
+    """ValueNorms::sync on the device (attribution.rs:116-148) equals the
+    oracle's sequential loop bit for bit on the same cached V rows, and the
+    ValueNorms mirror extends and truncates as the reference does."""
+    cfg = synthetic.CONFIGS[name]
+    w = synthetic.make_weights(cfg, 4)
+    gm = G.GpuModel(G.Config.from_dict(cfg), w)
+    c = gm.new_cache(256)
+    n = 20 if name == "tiny" else 12
+    say(f"{name}: prompt of {n}, value norms of every position")
+    gm.prompt(c, synthetic.make_prompt(cfg["vocab_size"], n, seed=6))
+    got = c.value_norms(0, n)
+    L, nh, nkv, hd, h = (cfg["num_layers"], cfg["num_heads"], cfg["num_kv_heads"],
+                         cfg["head_dim"], cfg["hidden_size"])
+    assert got.shape == (L, n, nh)
+    for l in range(L):
+        _, vals = c.read(l)
+        ref = O.value_norms(_wo(cfg, w, l), vals, h, nh, nkv, hd, 0, n)
+        assert np.array_equal(got[l].view(np.uint32), ref.view(np.uint32)), f"layer {l}"
+    vn = G.ValueNorms(gm)
+    vn.sync(c)
+    assert len(vn) == n
+    c.truncate(n - 5)
+    vn.sync(c)
+    assert len(vn) == n - 5
+    gm.prompt(c, [1, 2, 3])
+    vn.sync(c)
+    assert len(vn) == n - 2
+    again = c.value_norms(0, n - 2)
+    for l in range(L):
+        assert np.array_equal(vn.per_layer[l].view(np.uint32), again[l].view(np.uint32))
+    assert vn.get(0, 0, 0) == float(again[0, 0, 0])
+    with pytest.raises(G.DeferGpuError):
+        c.value_norms(0, n + 5)

@@ -271,3 +271,41 @@ def test_checkout_replay_of_generated_session_and_divergence():
     bad[10] = (bad[10] + 1) % cfg["vocab_size"]
     fd, sampled, _ = om.checkout(om.new_cache(), seed, 0.8, bad, len(prompt))
     assert fd == 10 and sampled == hist[10]
+
+
+def test_value_norms_closed_forms():  # attribution.rs:116-148
+    """A one-hot value row makes every o_i one entry of W_o exactly, so each
+    norm is a column norm of the head's W_o slice (float64 within 1e-6);
+    scaling v by 2^k scales every norm by exactly 2^k; a zero row gives 0."""
+    rs = np.random.RandomState(3)
+    hidden, nh, nkv, hd, n = 48, 4, 2, 8, 5
+    wo = rs.standard_normal((hidden, nh * hd)).astype(np.float32)
+    vals = np.zeros((n, nkv * hd), dtype=np.float32)
+    vals[1, 3] = 1.0          # kv head 0, dim 3
+    vals[2, hd + 5] = 1.0     # kv head 1, dim 5
+    vals[3] = rs.standard_normal(nkv * hd).astype(np.float32)
+    vals[4] = vals[3] * np.float32(8.0)
+    out = O.value_norms(wo, vals, hidden, nh, nkv, hd, 0, n)
+    assert out.shape == (n, nh)
+    assert np.all(out[0] == 0.0)
+    group = nh // nkv
+    for h in range(nh):
+        kvh = h // group
+        col = {1: 3 if kvh == 0 else None, 2: 5 if kvh == 1 else None}
+        for t, d in col.items():
+            if d is None:
+                assert out[t, h] == 0.0
+            else:
+                ref = math.sqrt(float(np.sum(wo[:, h * hd + d].astype(np.float64) ** 2)))
+                assert abs(out[t, h] - ref) <= 1e-6 * ref
+    assert np.array_equal(out[4].view(np.uint32), (out[3] * np.float32(8.0)).view(np.uint32))
+    # A sub-range is the same computation on those positions.
+    part = O.value_norms(wo, vals, hidden, nh, nkv, hd, 2, 5)
+    assert np.array_equal(part.view(np.uint32), out[2:].view(np.uint32))
+    # Random rows: float64 within a rounding budget.
+    for t in (3, 4):
+        for h in range(nh):
+            kvh = h // group
+            o = wo[:, h * hd:(h + 1) * hd].astype(np.float64) @ vals[t, kvh * hd:(kvh + 1) * hd]
+            ref = math.sqrt(float(np.sum(o * o)))
+            assert abs(out[t, h] - ref) <= 1e-5 * ref
