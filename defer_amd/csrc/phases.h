@@ -120,12 +120,14 @@ __device__ __forceinline__ uint32_t rounds_for(uint32_t n, uint32_t per_round) {
   return per_round ? (n + per_round - 1) / per_round : (n ? 0xffffffffu : 0u);
 }
 
-// Work other waves do around a poll's first barrier (the barrier after which
-// the previous phase's compute is over): pre_b1 runs before it, post_b1
-// after it, while the pollers poll.
+// Work other waves do around a poll's barriers: pre_b1 runs before the first
+// (the barrier after which the previous phase's compute is over), post_b1
+// after it, while the pollers poll, and post_b2 after the last (the input is
+// in LDS).
 struct NoHook {
   __device__ __forceinline__ void pre_b1() const {}
   __device__ __forceinline__ void post_b1() const {}
+  __device__ __forceinline__ void post_b2() const {}
 };
 
 // Wait until every element of up to three gathers carries its generation and
@@ -178,6 +180,7 @@ __device__ __forceinline__ bool poll_gather(const Gather& g0, const Gather& g1, 
     }
   }
   __syncthreads();
+  hook.post_b2();
   return ctl->abort_seen == 0;
 }
 
@@ -544,8 +547,10 @@ __device__ __forceinline__ float pass_pre(const Preload& P, const float* w, cons
 }
 
 // Barrier work of a staged matvec phase: loaders wait for this kind's rows
-// before the first barrier and request the previous kind's after it;
-// compute waves then preload their first pass.
+// before the first barrier and request the previous kind's once the poll is
+// over (requested while the pollers poll, that burst of weight reads competes
+// with the poll's reads); compute waves preload their first pass while the
+// pollers poll.
 struct MvHook {
   const Stager* sg;
   LoadOp op;
@@ -557,11 +562,10 @@ struct MvHook {
   __device__ __forceinline__ void post_b1() const {
     if (!sg->on) return;
     const uint32_t wave = threadIdx.x / WAVE;
-    if (sg->loader) {
-      if (op.issue < 4) stage_issue(*sg, op.issue, op.layer);
-    } else if (wave >= NPOLL) {
-      preload_rows(*pre, *sg, kind, wave - NPOLL, threadIdx.x % WAVE);
-    }
+    if (!sg->loader && wave >= NPOLL) preload_rows(*pre, *sg, kind, wave - NPOLL, threadIdx.x % WAVE);
+  }
+  __device__ __forceinline__ void post_b2() const {
+    if (sg->on && sg->loader && op.issue < 4) stage_issue(*sg, op.issue, op.layer);
   }
 };
 
@@ -682,6 +686,7 @@ __device__ __forceinline__ bool phase_qkv(const Args& a, uint32_t l, uint32_t ti
     for (uint32_t i = threadIdx.x; i < d.h && threadIdx.x < NPOLL * WAVE; i += NPOLL * WAVE)
       lds_st(s.vec + i, ldg(e + i));
     __syncthreads();
+    hk.post_b2();
   } else if (!poll_gather<8>(gather_vec(a.mb_xd, d.h, gen_of(d, tick, l - 1, PH_D), s.vec), NPOLL,
                              a.st, s.ctl, hk)) {
     return false;
