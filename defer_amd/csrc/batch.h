@@ -441,8 +441,10 @@ __device__ __forceinline__ Lds lds_init_rows(const Dims& d) {
 
 // Attention items of every row, one per workgroup: entry x of `items` is
 // (row, item) packed as row << 16 | item, and the workgroup runs that item
-// with the one-token path's phase_attn (reading the row's tagged q/k/v,
-// writing its tagged partials).
+// with the one-token path's phase_attn in its grouped form (item = (kv head,
+// chunk) with all the group's query heads; each head's arithmetic is the
+// one-token path's), reading the row's tagged q/k/v and writing its tagged
+// partials.
 __global__ __launch_bounds__(BLOCK) void k_b_attn(const Args* __restrict__ rargs,
                                                   const BRow* __restrict__ rows,
                                                   const uint32_t* __restrict__ items, uint32_t l) {
@@ -450,7 +452,7 @@ __global__ __launch_bounds__(BLOCK) void k_b_attn(const Args* __restrict__ rargs
   const Args& a = rargs[b];
   const Lds s = lds_init_rows(a.d);
   const BRow r = rows[b];
-  phase_attn(a, l, r.tick, r.pos, x, 0x10000u, s);  // stride past every item: just item x
+  phase_attn<true>(a, l, r.tick, r.pos, x, 0x10000u, s);  // stride past every item: just item x
 }
 
 // ----------------------------------------------------- tiled attention

@@ -1537,7 +1537,8 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
   } else {
     items.reserve((size_t)n * d.nkv);
     for (uint32_t b = 0; b < n; ++b) {
-      const uint32_t ni = attn_items(d, rows[b].pos);
+      // Grouped items (kv head, chunk): every query head of the group in one.
+      const uint32_t ni = d.nkv * attn_nchunks(rows[b].pos);
       for (uint32_t x = 0; x < ni; ++x) items.push_back(b << 16 | x);  // rows <= 2048, items < 2^16
     }
   }

@@ -764,17 +764,23 @@ __device__ __forceinline__ AttGeo att_geo(uint32_t hd) {
 //  3. exp-weighted V rows, one partial per (wave, position lane group),
 //     summed in that order.
 // Every order above depends on (pos, head_dim) only.
+// GROUPED = false: one query head per item (items (kv head, chunk, query
+// head); the decode spreads them over the most workgroups). GROUPED = true:
+// the group's query heads in one item (items (kv head, chunk); the batched
+// path, whose rows bring workgroups enough, reads each K/V row once per item
+// instead of once per head). The heads of a GQA group share K/V rows but
+// nothing else, so both give each head the same arithmetic, bit for bit.
+template <bool GROUPED = false>
 __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t tick, uint32_t pos,
                                            uint32_t wg, uint32_t G, const Lds& s) {
   const Dims d = shape_dims(a.d);
   const uint32_t nch = attn_nchunks(pos), CH = attn_chunk(pos);
-  const uint32_t n_items = attn_items(d, pos);
+  const uint32_t n_items = GROUPED ? d.nkv * nch : attn_items(d, pos);
   const uint32_t gen_in = gen_of(d, tick, l, PH_QKV);
   const uint32_t gen_out = gen_of(d, tick, l, PH_ATTN);
-  // One query head per item: the heads of a GQA group share K/V rows but
-  // nothing else, so splitting them gives each head the same arithmetic.
-  constexpr uint32_t NH1 = 1;  // query heads per item
+  constexpr uint32_t MH = GROUPED ? MAX_GROUP : 1;  // query heads per item, at most
   const uint32_t hd = d.hd, grp = d.group, hs = hd + 2;
+  const uint32_t NH1 = GROUPED ? grp : 1;  // query heads per item
   const AttGeo ge = att_geo(hd);
   float* qs = s.scr;                      // [MAX_GROUP*hd] (rows >= grp: don't care)
   float* kn = qs + MAX_GROUP * hd;        // [hd]
@@ -790,7 +796,8 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
   const uint32_t tw = wave * ge.pw + ps;  // this lane's position offset in a score pass
   const uint32_t vw = wave * ge.pv + pl;  // ... and in a value step
   for (uint32_t item = wg; item < n_items; item += G) {
-    const uint32_t gc = item / grp, j0 = item - gc * grp;  // item = (g * nch + c) * grp + j0
+    // item = (g * nch + c) * grp + j0, or g * nch + c when grouped
+    const uint32_t gc = GROUPED ? item : item / grp, j0 = GROUPED ? 0 : item - gc * grp;
     const uint32_t g = gc / nch, c = gc - g * nch;
     const uint32_t t0 = c * CH;
     const uint32_t t1 = min(t0 + CH, pos + 1);
@@ -809,7 +816,7 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
       for (uint32_t u = 0; u < VU; ++u)
         vr[u] = ldg4(vb + (size_t)min(t0 + vw + u * vstep, d.cap - 1) * d.kvs);
     }
-    if (!poll_gather<2, 1, 1>(gather_vec(a.mb_qkv + (size_t)(g * grp + j0) * hd, hd, gen_in, qs),
+    if (!poll_gather<GROUPED ? 4 : 2, 1, 1>(gather_vec(a.mb_qkv + (size_t)(g * grp + j0) * hd, NH1 * hd, gen_in, qs),
                               gather_vec(a.mb_qkv + d.q + g * hd, hd, gen_in, kn),
                               gather_vec(a.mb_qkv + d.q + d.kv + g * hd, hd, gen_in, vn), NPOLL,
                               a.st, s.ctl))
@@ -868,9 +875,9 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
     }
     __syncthreads();
     // 3. exp-weighted V rows: positions t0 + vw + k*vstep, k = 0, 1, ...
-    float4 acc[NH1];
+    float4 acc[MH];
 #pragma unroll
-    for (uint32_t j = 0; j < NH1; ++j) acc[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (uint32_t j = 0; j < MH; ++j) acc[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     const uint32_t nk = att && t0 + vw < t1 ? (t1 - t0 - vw + vstep - 1) / vstep : 0;
     for (uint32_t k0 = 0; k0 < nk; k0 += VU) {
 #pragma unroll
@@ -882,7 +889,8 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
           const uint32_t tf = t + VU * vstep;
           if (k + VU < nk && tf < pos) vr[u] = ldg4(vb + (size_t)tf * d.kvs);
 #pragma unroll
-          for (uint32_t j = 0; j < NH1; ++j) {
+          for (uint32_t j = 0; j < MH; ++j) {
+            if (j >= NH1) break;
             const float p = lds_ld(sc + j * CH + (t - t0));
             acc[j].x = fmaf(p, v.x, acc[j].x);
             acc[j].y = fmaf(p, v.y, acc[j].y);
@@ -896,16 +904,17 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
     // partial per wave.
     for (uint32_t o = ge.lv; o < WAVE; o <<= 1) {
 #pragma unroll
-      for (uint32_t j = 0; j < NH1; ++j) {
-          acc[j].x += __shfl_xor(acc[j].x, o);
-          acc[j].y += __shfl_xor(acc[j].y, o);
-          acc[j].z += __shfl_xor(acc[j].z, o);
-          acc[j].w += __shfl_xor(acc[j].w, o);
-        }
+      for (uint32_t j = 0; j < MH; ++j) {
+        if (j >= NH1) break;
+        acc[j].x += __shfl_xor(acc[j].x, o);
+        acc[j].y += __shfl_xor(acc[j].y, o);
+        acc[j].z += __shfl_xor(acc[j].z, o);
+        acc[j].w += __shfl_xor(acc[j].w, o);
+      }
     }
 #pragma unroll
-    for (uint32_t j = 0; j < NH1; ++j)
-      if (att && pl == 0) {
+    for (uint32_t j = 0; j < MH; ++j)
+      if (j < NH1 && att && pl == 0) {
         float* dst = wp + (wave * NH1 + j) * hd + dl * 4;
         lds_st(dst + 0, acc[j].x);
         lds_st(dst + 1, acc[j].y);
