@@ -343,6 +343,124 @@ __global__ __launch_bounds__(512) void k_gemm_n(const float* __restrict__ Wp, ui
   }
 }
 
+// Narrow batches (B <= 64) with few row groups: the segments split four
+// ways. Quarter q of tree16 is ((s_4q + s_4q+1) + (s_4q+2 + s_4q+3)), a
+// subtree of its own, and it needs only quarter q of every chunk (one
+// contiguous 1 KB block per tile and chunk in the panel layout), so a task
+// is (row group of four row tiles, quarter q, pair of column tiles): it
+// reads a quarter of the rows' weights and of two column tiles' panel, and
+// writes its subtree to plane q of Q ([4][B][M]); k_gemm_qcomb forms
+// (t_0 + t_1) + (t_2 + t_3), the same tree16, and applies OUT. Eight waves:
+// wave w owns row tile w % 4 and column tile w / 4 of the pair. A chunk's
+// six 1 KB blocks (four row tiles, two column tiles) take one copy each
+// from waves 0..5; a stage holds GEMMQ_CPB chunks (one barrier per stage),
+// GEMMQ_STAGES - 1 stages ahead.
+constexpr uint32_t GEMMQ_CPB = 8, GEMMQ_STAGES = 3;
+__host__ __device__ constexpr uint32_t gemm_q_lds_bytes() {
+  return GEMMQ_STAGES * GEMMQ_CPB * 6 * 1024;
+}
+template <bool PARTIAL>
+__global__ __launch_bounds__(512) void k_gemm_q(const float* __restrict__ Wp, uint32_t M, uint32_t K,
+                                                const float* __restrict__ Xp, uint32_t B,
+                                                float* __restrict__ Q) {
+  extern __shared__ float4 gsm[];  // [stages][GEMMQ_CPB chunks][6 blocks][64 lanes]
+  const uint32_t wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+  const uint32_t rt = wave % 4, ct = wave / 4;
+  const uint32_t nch = panel_chunks(K), nrt = (M + 15) / 16, nct = (B + 15) / 16;
+  const uint32_t nsc = (nch + GEMMQ_CPB - 1) / GEMMQ_CPB;  // stages of chunks per task
+  const uint32_t nrg = (nrt + 3) / 4, ncg = (nct + 1) / 2, ntask = 4 * nrg * ncg;
+  const uint32_t mine = blockIdx.x < ntask ? (ntask - blockIdx.x + gridDim.x - 1) / gridDim.x : 0;
+  const uint32_t total = mine * nsc;
+  const uint32_t nld = wave < 6 ? GEMMQ_CPB : 0u;  // copies per stage
+  const uint32_t lds0 = (uint32_t)(uintptr_t)gsm;
+  // Task t = (x * 4 + q) * ncg + cg. Stage g's chunks into LDS stage st:
+  // block `wave` of each is row tile 4x + wave (waves 0..3) or column tile
+  // 2cg + wave - 4, quarter q. Tiles and chunks past the last load a real
+  // one (never used), so every copying wave issues GEMMQ_CPB per stage.
+  auto issue = [&](uint32_t g, uint32_t st) {
+    const uint32_t t = blockIdx.x + gridDim.x * (g / nsc), i0 = (g % nsc) * GEMMQ_CPB;
+    const uint32_t cg = t % ncg, xq = t / ncg, x = xq / 4, q = xq % 4;
+    if (wave >= 6) return;
+    const float* src = wave < 4 ? Wp + (size_t)min(4 * x + wave, nrt - 1) * nch * PANEL_TILE
+                                : Xp + (size_t)min(2 * cg + wave - 4, nct - 1) * nch * PANEL_TILE;
+#pragma unroll
+    for (uint32_t c = 0; c < GEMMQ_CPB; ++c)
+      dma16(src + (size_t)min(i0 + c, nch - 1) * PANEL_TILE + q * 256 + lane * 4,
+            lds0 + ((st * GEMMQ_CPB + c) * 6 + wave) * 1024);
+  };
+  for (uint32_t g = 0; g + 1 < GEMMQ_STAGES && g < total; ++g) issue(g, g);
+  for (uint32_t k = 0; k < mine; ++k) {
+    const uint32_t t = blockIdx.x + gridDim.x * k;
+    const uint32_t cg = t % ncg, xq = t / ncg, x = xq / 4, q = xq % 4;
+    f4v acc[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[u] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t j = 0; j < nsc; ++j) {
+      const uint32_t g = k * nsc + j;
+      // Stage g has landed once at most the later stages' copies are in
+      // flight; after the barrier every wave is done with stage g - 1's
+      // LDS, which the next request overwrites.
+      stage_wait(min(GEMMQ_STAGES - 2, total - 1 - g) * nld);
+      __syncthreads();
+      if (g + GEMMQ_STAGES - 1 < total) issue(g + GEMMQ_STAGES - 1, (g + GEMMQ_STAGES - 1) % GEMMQ_STAGES);
+      const float4* sa = gsm + (g % GEMMQ_STAGES) * GEMMQ_CPB * 6 * 64;
+      float4 a[GEMMQ_CPB], b[GEMMQ_CPB];
+#pragma unroll
+      for (uint32_t c = 0; c < GEMMQ_CPB; ++c) {
+        a[c] = sa[(c * 6 + rt) * 64 + lane];
+        b[c] = sa[(c * 6 + 4 + ct) * 64 + lane];
+      }
+#pragma unroll
+      for (uint32_t c = 0; c < GEMMQ_CPB; ++c) {
+        const uint32_t i = j * GEMMQ_CPB + c;
+        if (i >= nch) break;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          // A last, partial chunk: the segments past K are left alone.
+          if (PARTIAL && 64 * i + 4 * (4 * q + u) >= K) continue;
+          acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32((&a[c].x)[u], (&b[c].x)[u], acc[u], 0, 0, 0);
+        }
+      }
+    }
+    const uint32_t T = 4 * x + rt, o = T * 16 + 4 * (lane / 16);
+    const f4v r = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    const uint32_t bc = (2 * cg + ct) * 16 + lane % 16;
+    if (T < nrt && bc < B) {
+      float* dst = Q + ((size_t)q * B + bc) * M + o;
+      if (o + 4 <= M && (((size_t)q * B + bc) * M + o) % 4 == 0) {
+        *reinterpret_cast<float4*>(dst) = make_float4(r[0], r[1], r[2], r[3]);
+      } else {
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+          if (o + jj < M) dst[jj] = r[jj];
+      }
+    }
+  }
+}
+
+// The four quarter subtrees of k_gemm_q into tree16 and the output: thread
+// (b, o) for o < M, b < B.
+template <uint32_t OUT>
+__global__ void k_gemm_qcomb(const float* __restrict__ Q, uint32_t M, uint32_t B,
+                             float* __restrict__ Y, uint32_t ldy, const float* __restrict__ scale,
+                             const uint32_t* __restrict__ gen, float* __restrict__ P) {
+  const uint32_t o = blockIdx.x * blockDim.x + threadIdx.x, b = blockIdx.y;
+  if (o >= M || b >= B) return;
+  const size_t plane = (size_t)B * M, e = (size_t)b * M + o;
+  const float r = (Q[e] + Q[plane + e]) + (Q[2 * plane + e] + Q[3 * plane + e]);
+  const size_t at = (size_t)b * ldy + o;
+  if (OUT == GO_PLAIN) {
+    Y[at] = r;
+  } else if (OUT == GO_RESID) {
+    const float v = Y[at] + r;
+    Y[at] = v;
+    P[panel_at(b, o, panel_chunks(M))] = v;
+  } else {
+    const float v = scale[b] * r;
+    reinterpret_cast<u64*>(Y)[at] = ((u64)gen[b] << 32) | (u64)__float_as_uint(v);
+  }
+}
+
 // ------------------------------------------------------------- rows
 
 // One row of a batch: the cache it extends, at which position and

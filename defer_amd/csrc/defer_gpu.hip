@@ -629,6 +629,11 @@ extern "C" int defer_gpu_model_create(const defer_gpu_config* cfg, const float* 
       if (e != hipSuccess)
         return cleanup(fail(DEFER_GPU_E_HIP, "LDS attribute (narrow GEMM): %s", hipGetErrorString(e)));
     }
+    for (const void* kf : {(const void*)k_gemm_q<false>, (const void*)k_gemm_q<true>}) {
+      e = hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)gemm_q_lds_bytes());
+      if (e != hipSuccess)
+        return cleanup(fail(DEFER_GPU_E_HIP, "LDS attribute (quarter GEMM): %s", hipGetErrorString(e)));
+    }
   }
   e = hipFuncSetAttribute((const void*)k_b_attn_tile, hipFuncAttributeMaxDynamicSharedMemorySize,
                           (int)attn_tile_lds(MAX_GROUP));
@@ -1263,6 +1268,7 @@ struct BatchWs {
   // the other GEMM inputs (attention output, activation, final-norm rows).
   float *X = nullptr, *Y = nullptr, *INV = nullptr, *XP = nullptr, *XQ = nullptr;
   float* LINV = nullptr;
+  float* QS = nullptr;  // quarter-split GEMM subtrees [4][B][M], B <= 64, M <= batch_ldy
   u64 *QKVT = nullptr, *PART = nullptr, *LOGT = nullptr, *VMAX = nullptr, *VARG = nullptr,
       *VSUM = nullptr;
   BRow* drows = nullptr;
@@ -1277,7 +1283,7 @@ struct BatchWs {
 
 static void batch_ws_release(BatchWs* w) {
   if (!w) return;
-  void* ps[] = {w->X, w->Y, w->INV, w->XP, w->XQ, w->LINV, w->QKVT, w->PART,
+  void* ps[] = {w->X, w->Y, w->INV, w->XP, w->XQ, w->LINV, w->QS, w->QKVT, w->PART,
                 w->LOGT, w->VMAX, w->VARG, w->VSUM, w->drows, w->rargs, w->largs, w->sel,
                 w->lgen, w->stick, w->swords, w->sout, w->items, w->tiles, w->sets, w->st};
   for (void* p : ps) (void)hipFree(p);
@@ -1304,6 +1310,7 @@ static int ensure_ws(defer_gpu_model* m, uint32_t rows, uint32_t lm) {
   const uint32_t kmax = std::max({d.h, d.q, d.ff});
   HIP_TRY(hipMalloc(&w.X, (size_t)R * d.h * sizeof(float)));
   HIP_TRY(hipMalloc(&w.Y, (size_t)R * batch_ldy(d) * sizeof(float)));
+  HIP_TRY(hipMalloc(&w.QS, (size_t)4 * std::min(R, 64u) * batch_ldy(d) * sizeof(float)));
   HIP_TRY(hipMalloc(&w.INV, (size_t)R * sizeof(float)));
   HIP_TRY(hipMalloc(&w.XP, panel_floats(R, d.h) * sizeof(float)));
   HIP_TRY(hipMalloc(&w.QKVT, (size_t)R * d.qkv_rows * sizeof(u64)));
@@ -1401,9 +1408,22 @@ static void launch_gemm_tn(hipStream_t s, const float* Wp, uint32_t M, uint32_t 
 template <uint32_t OUT>
 static void launch_gemm_out(hipStream_t s, const float* Wp, uint32_t M, uint32_t K, const float* Xp,
                             uint32_t B, float* Y, uint32_t ldy, const float* scale,
-                            const uint32_t* gen, uint32_t ncu, float* P) {
+                            const uint32_t* gen, uint32_t ncu, float* P, float* QS, size_t qs_floats) {
   const uint32_t nct = (B + 15) / 16, nrg = (M + 63) / 64;
-  if (nct <= 4) {  // narrow: one row tile per task, enough tasks for every CU
+  // Narrow batches: four full column tiles and a row group per CU take the
+  // four-tile tasks below; fewer row groups split the segments four ways
+  // (the subtrees in QS, then combined); otherwise one row tile per task.
+  if (nct <= 4 && !(nct == 4 && nrg >= ncu) && QS && nrg < ncu && (size_t)4 * B * M <= qs_floats) {
+    const uint32_t per_cu = gemm_q_lds_bytes() <= 80 * 1024 ? 2 : 1;
+    const uint32_t grid = std::min(4 * nrg * ((nct + 1) / 2), per_cu * ncu);
+    if (K % 64 == 0)
+      k_gemm_q<false><<<grid, GEMM_WAVES * WAVE, gemm_q_lds_bytes(), s>>>(Wp, M, K, Xp, B, QS);
+    else
+      k_gemm_q<true><<<grid, GEMM_WAVES * WAVE, gemm_q_lds_bytes(), s>>>(Wp, M, K, Xp, B, QS);
+    k_gemm_qcomb<OUT><<<dim3((M + 255) / 256, B), 256, 0, s>>>(QS, M, B, Y, ldy, scale, gen, P);
+    return;
+  }
+  if (nct <= 4 && !(nct == 4 && nrg >= ncu)) {  // narrow: one row tile per task
     const uint32_t grid = std::min((M + 15) / 16, 2 * ncu), threads = GEMM_WAVES * WAVE;
     if (K % 64 == 0)
       k_gemm_n<OUT, false><<<grid, threads, gemm_n_lds_bytes(), s>>>(Wp, M, K, Xp, B, Y, ldy, scale,
@@ -1425,13 +1445,17 @@ static void launch_gemm_out(hipStream_t s, const float* Wp, uint32_t M, uint32_t
   launch_gemm_tn<4, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 0, nct, ncu, P);
 }
 // P: GO_RESID's panel of the updated rows (K = M).
+// QS / qs_floats: scratch for the quarter-split narrow GEMM (null: not used).
 static void launch_gemm(hipStream_t s, uint32_t ncu, uint32_t out, const float* Wp, uint32_t M,
                         uint32_t K, const float* Xp, uint32_t B, float* Y, uint32_t ldy,
                         const float* scale = nullptr, const uint32_t* gen = nullptr,
-                        float* P = nullptr) {
-  if (out == GO_PLAIN) launch_gemm_out<GO_PLAIN>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, ncu, P);
-  else if (out == GO_RESID) launch_gemm_out<GO_RESID>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, ncu, P);
-  else launch_gemm_out<GO_TAG>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, ncu, P);
+                        float* P = nullptr, float* QS = nullptr, size_t qs_floats = 0) {
+  if (out == GO_PLAIN)
+    launch_gemm_out<GO_PLAIN>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, ncu, P, QS, qs_floats);
+  else if (out == GO_RESID)
+    launch_gemm_out<GO_RESID>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, ncu, P, QS, qs_floats);
+  else
+    launch_gemm_out<GO_TAG>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, ncu, P, QS, qs_floats);
 }
 
 // Timing of one launch (profiling on): events recorded around it on the
@@ -1561,12 +1585,14 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
   }
   k_begin<<<1, 1, 0, s>>>(w.st);
   const uint32_t ldy = batch_ldy(d);
+  const size_t qs_n = (size_t)4 * std::min(w.rows, 64u) * ldy;
   k_b_embed<<<n, 256, 0, s>>>(w.drows, m->embed, d.h, w.X, w.XP);
   for (uint32_t l = 0; l < d.L; ++l) {
     k_b_rms<<<(n + 3) / 4, 256, 0, s>>>(w.X, n, d.h, d.eps, w.INV);
     {
       ProfSpan ps(m, 0, 2.0 * d.qkv_rows * d.h * n);
-      launch_gemm(s, m->ncu, GO_PLAIN, m->p_qkv[l], d.qkv_rows, d.h, w.XP, n, w.Y, ldy);
+      launch_gemm(s, m->ncu, GO_PLAIN, m->p_qkv[l], d.qkv_rows, d.h, w.XP, n, w.Y, ldy, nullptr,
+                  nullptr, nullptr, w.QS, qs_n);
     }
     k_b_qkv_epi<<<dim3((d.qkv_rows / 2 + 255) / 256, n), 256, 0, s>>>(w.rargs, w.drows, l, w.Y, ldy,
                                                                       w.INV, w.QKVT, d.qkv_rows);
@@ -1582,18 +1608,19 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
     {
       ProfSpan ps(m, 0, 2.0 * d.h * d.q * n);
       launch_gemm(s, m->ncu, GO_RESID, m->p_o[l], d.h, d.q, w.XQ, n, w.X, d.h, nullptr, nullptr,
-                  w.XP);
+                  w.XP, w.QS, qs_n);
     }
     k_b_rms<<<(n + 3) / 4, 256, 0, s>>>(w.X, n, d.h, d.eps, w.INV);
     {
       ProfSpan ps(m, 0, 2.0 * 2 * d.ff * d.h * n);
-      launch_gemm(s, m->ncu, GO_PLAIN, m->p_gu[l], 2 * d.ff, d.h, w.XP, n, w.Y, ldy);
+      launch_gemm(s, m->ncu, GO_PLAIN, m->p_gu[l], 2 * d.ff, d.h, w.XP, n, w.Y, ldy, nullptr,
+                  nullptr, nullptr, w.QS, qs_n);
     }
     k_b_act<<<dim3((d.ff + 255) / 256, n), 256, 0, s>>>(w.Y, ldy, w.INV, d.ff, d.act, w.XQ);
     {
       ProfSpan ps(m, 0, 2.0 * d.h * d.ff * n);
       launch_gemm(s, m->ncu, GO_RESID, m->p_d[l], d.h, d.ff, w.XQ, n, w.X, d.h, nullptr, nullptr,
-                  w.XP);
+                  w.XP, w.QS, qs_n);
     }
   }
   if (nl) {
@@ -1601,7 +1628,7 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
     {
       ProfSpan ps(m, 0, 2.0 * d.V * d.h * nl);
       launch_gemm(s, m->ncu, GO_TAG, m->p_lm, d.V, d.h, w.XQ, nl, reinterpret_cast<float*>(w.LOGT), d.V,
-                  w.LINV, w.lgen);
+                  w.LINV, w.lgen, nullptr, w.QS, qs_n);
     }
     k_b_chunkmax<<<dim3((d.nvc + 3) / 4, nl), 256, 0, s>>>(d, w.LOGT, w.lgen, w.VMAX, w.VARG, nl);
   }
