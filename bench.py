@@ -59,14 +59,15 @@ def algorithmic_bytes(cfg: dict, weight_bytes: int, first_pos: int, n_pos: int) 
     return total
 
 
-def measured_traffic() -> int | None:
-    """HBM bytes per replay launch from the committed rocprofv3 PMC summary
-    (FETCH_SIZE and WRITE_SIZE, each scaled by a 1 GiB copy's reading)."""
-    p = os.path.join(ROOT, "profiles", "k_persistent_replay_135m.md")
+def measured_traffic(profile: str = "k_persistent_replay_135m.md",
+                     key: str = "traffic_bytes_per_launch") -> int | None:
+    """HBM bytes from a committed rocprofv3 PMC summary (FETCH_SIZE and
+    WRITE_SIZE, each scaled by a 1 GiB copy's reading)."""
+    p = os.path.join(ROOT, "profiles", profile)
     if not os.path.exists(p):
         return None
     for line in open(p):
-        if line.startswith("traffic_bytes_per_launch:"):
+        if line.startswith(key + ":"):
             return int(line.split(":")[1])
     return None
 
@@ -195,6 +196,56 @@ def sessions_workload(args) -> int:
     return 0
 
 
+def c1_workload(args) -> int:
+    """Batch-1 decode of the CPU-runnable configuration alone (c1_decode: a
+    32-token prompt, 128 greedy tokens, then 128 at T = 0.7; positions 32..288
+    timed); roofline = the persistent kernel's algorithmic bytes over the
+    device time of the two timed generate calls."""
+    from defer_amd import gpu as G
+    from defer_amd import host as H
+    from defer_amd import synthetic
+
+    cfg = synthetic.CONFIGS[CFG_NAME]
+    model = G.GpuModel(G.Config.from_dict(cfg), synthetic.make_weights(cfg, 0))
+    c1 = c1_decode(model, cfg, H)
+    ms = 256 / c1["tok_s"] * 1e3
+    wbytes = synthetic.weight_bytes_streamed(cfg)
+    achieved = algorithmic_bytes(cfg, wbytes, 32, 256) / (ms / 1e3) / 1e9
+    line = {
+        "metric": "batch-1 decode tok/s (f32) + achieved HBM GB/s as % of peak",
+        "value": c1["tok_s"],
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": 256,
+        "warmup": 0,
+        "ms_per_step": round(ms / 256, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (N(0,0.02) weights from seed 0, uniform-random prompt ids)",
+        "config": {
+            "workload": "SmolLM2-135M-shaped decode: 32-token prompt, 128 greedy tokens, then "
+                        "128 at T=0.7 (seed 42), one token at a time",
+            "weight_bytes_per_token": wbytes,
+            "weight_roofline_tok_s": round(PEAK_GBS * 1e9 / wbytes, 1),
+            "weight_roofline_frac": round(c1["tok_s"] * wbytes / (PEAK_GBS * 1e9), 4),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "k_persistent",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_GBS, 4),
+            "traffic": None,
+        },
+    }
+    model.close()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def decode_workload(args, name: str) -> int:
     """Batch-1 decode of the long-context (SmolLM2-360M shape: 128-token prompt,
     4096 tokens at T=0.8, seed 1) or the large-model configuration
@@ -261,9 +312,11 @@ def decode_workload(args, name: str) -> int:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--workload", choices=["replay", "sessions", "long", "8b"], default="replay",
+    ap.add_argument("--workload", choices=["replay", "sessions", "c1", "long", "8b"],
+                    default="replay",
                     help="replay: the 2048-position checkout (default, the headline); "
                          "sessions: 64 Llama-3.2-1B-shaped sessions in lockstep; "
+                         "c1: 135M-shaped batch-1 decode of 256 tokens; "
                          "long: 360M-shaped decode of 4096 tokens; 8b: 8B-shaped decode")
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=1)
@@ -290,6 +343,8 @@ def main() -> int:
 
     if args.workload == "sessions":
         return sessions_workload(args)
+    if args.workload == "c1":
+        return c1_workload(args)
     if args.workload in ("long", "8b"):
         return decode_workload(args, args.workload)
 
@@ -419,7 +474,9 @@ def main() -> int:
             "peak": PEAK_F32_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_F32_TFLOPS, 4),
-            "traffic": None,
+            # HBM bytes of one replay's k_gemm launches (PMC, committed profile)
+            "traffic": (measured_traffic("k_gemm_replay_135m.md", "gemm_traffic_bytes_per_replay")
+                        if cls == "gemm" else None),
         },
     }
     # Device objects are released here, not during interpreter shutdown.
