@@ -210,12 +210,34 @@ __global__ __launch_bounds__(256) void k_trace(const Args* __restrict__ ap, uint
 struct StateSet {
   DevState* st;
   uint32_t pos, tick;
+  // batch commits: the cache's tagged logits and chunk maxima, filled from
+  // workspace logits row li
+  u64 *logit, *vmax, *varg;
+  uint32_t li;
 };
 __global__ void k_set_state(const StateSet* __restrict__ set, uint32_t n) {
   const uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
   if (k >= n) return;
   set[k].st->pos = set[k].pos;
   set[k].st->tick = set[k].tick;
+}
+
+// Batch commit: cache k's tagged logits and chunk (max, argmax) words from
+// the workspace's logits row set[k].li, all caches in one launch (grid y = k).
+__global__ void k_commit_rows(const StateSet* __restrict__ set, const u64* __restrict__ logt,
+                              const u64* __restrict__ vmax, const u64* __restrict__ varg,
+                              uint32_t V, uint32_t nvc) {
+  const StateSet e = set[blockIdx.y];
+  const size_t li = e.li;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < V + 2 * nvc;
+       i += gridDim.x * blockDim.x) {
+    if (i < V)
+      e.logit[i] = logt[li * V + i];
+    else if (i < V + nvc)
+      e.vmax[i - V] = vmax[li * nvc + (i - V)];
+    else
+      e.varg[i - V - nvc] = varg[li * nvc + (i - V - nvc)];
+  }
 }
 
 // Strip the tags of logits (or any tagged vector) into plain floats.
@@ -1685,7 +1707,7 @@ static int batch_sample(defer_gpu_model* m, defer_gpu_cache* const* ocache, cons
 
 // Caches after their batch rows: length, generation base and, from logits
 // row li[k] of the workspace, the tagged logits and chunk maxima a following
-// sample reads. All copies are queued, then one kernel sets the device
+// sample reads. One kernel copies every cache's words, one sets the device
 // states, then one synchronisation.
 static int batch_commit_many(defer_gpu_model* m, defer_gpu_cache* const* cs, const uint32_t* li,
                              const uint32_t* pos, const uint32_t* tick, uint32_t n) {
@@ -1695,17 +1717,20 @@ static int batch_commit_many(defer_gpu_model* m, defer_gpu_cache* const* cs, con
   std::vector<StateSet> set(n);
   for (uint32_t k = 0; k < n; ++k) {
     defer_gpu_cache* c = cs[k];
-    HIP_TRY(hipMemcpyAsync(c->args.mb_logit, w.LOGT + (size_t)li[k] * d.V,
-                           (size_t)d.V * sizeof(u64), hipMemcpyDeviceToDevice, s));
-    HIP_TRY(hipMemcpyAsync(c->args.mb_vmax, w.VMAX + (size_t)li[k] * d.nvc,
-                           (size_t)d.nvc * sizeof(u64), hipMemcpyDeviceToDevice, s));
-    HIP_TRY(hipMemcpyAsync(c->args.mb_varg, w.VARG + (size_t)li[k] * d.nvc,
-                           (size_t)d.nvc * sizeof(u64), hipMemcpyDeviceToDevice, s));
     set[k].st = c->st;
     set[k].pos = pos[k];
     set[k].tick = tick[k];
+    set[k].logit = c->args.mb_logit;
+    set[k].vmax = c->args.mb_vmax;
+    set[k].varg = c->args.mb_varg;
+    set[k].li = li[k];
   }
   HIP_TRY(hipMemcpyAsync(w.sets, set.data(), n * sizeof(StateSet), hipMemcpyHostToDevice, s));
+  if (n > 0) {
+    const uint32_t words = d.V + 2 * d.nvc;
+    k_commit_rows<<<dim3(std::min((words + 1023) / 1024, 64u), n), 256, 0, s>>>(
+        w.sets, w.LOGT, w.VMAX, w.VARG, d.V, d.nvc);
+  }
   k_set_state<<<(n + 63) / 64, 64, 0, s>>>(w.sets, n);
   HIP_TRY(hipGetLastError());
   HIP_TRY(hipStreamSynchronize(s));
