@@ -438,6 +438,49 @@ __global__ __launch_bounds__(512) void k_gemm_q(const float* __restrict__ Wp, ui
   }
 }
 
+// 1/rms of one row of n floats, by one wave: lane partials over the float4s
+// at 4*lane + 256*i (i ascending), then the wave tree.
+__device__ __forceinline__ float rms_row_inv(const float* __restrict__ x, uint32_t n, float eps,
+                                             uint32_t lane) {
+  float ss = 0.0f;
+  for (uint32_t j = lane * 4; j < n; j += 256) {
+    const float4 v = *reinterpret_cast<const float4*>(x + j);
+    ss = fmaf(v.x, v.x, ss);
+    ss = fmaf(v.y, v.y, ss);
+    ss = fmaf(v.z, v.z, ss);
+    ss = fmaf(v.w, v.w, ss);
+  }
+  ss = wave_sum(ss);
+  return 1.0f / sqrtf(ss / (float)n + eps);
+}
+
+// The residual output of k_gemm_q (x += tree16 of the four subtrees, and
+// its panel) for one row per workgroup, then the row's 1/rms (k_b_rms's
+// order) for the next matrix product's normalisation: one launch instead of
+// two.
+__global__ __launch_bounds__(256) void k_gemm_qcomb_rms(const float* __restrict__ Q, uint32_t M,
+                                                        uint32_t B, float* __restrict__ Y,
+                                                        uint32_t ldy, float* __restrict__ P,
+                                                        float eps, float* __restrict__ inv) {
+  const uint32_t b = blockIdx.x;
+  const size_t plane = (size_t)B * M;
+  for (uint32_t o = threadIdx.x; o < M; o += blockDim.x) {
+    const size_t e = (size_t)b * M + o;
+    const float r = (Q[e] + Q[plane + e]) + (Q[2 * plane + e] + Q[3 * plane + e]);
+    const size_t at = (size_t)b * ldy + o;
+    const float v = Y[at] + r;
+    Y[at] = v;
+    P[panel_at(b, o, panel_chunks(M))] = v;
+  }
+  // The row's new values, written by the whole workgroup, are visible to it
+  // after the barrier.
+  __syncthreads();
+  if (threadIdx.x < WAVE) {
+    const float r = rms_row_inv(Y + (size_t)b * ldy, M, eps, threadIdx.x);
+    if (threadIdx.x == 0) inv[b] = r;
+  }
+}
+
 // The four quarter subtrees of k_gemm_q into tree16 and the output: thread
 // (b, o) for o < M, b < B.
 template <uint32_t OUT>
@@ -489,17 +532,8 @@ __global__ __launch_bounds__(256) void k_b_rms(const float* __restrict__ X, uint
                                                float eps, float* __restrict__ inv) {
   const uint32_t b = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
   if (b >= B) return;
-  const float* x = X + (size_t)b * n;
-  float ss = 0.0f;
-  for (uint32_t j = lane * 4; j < n; j += 256) {
-    const float4 v = *reinterpret_cast<const float4*>(x + j);
-    ss = fmaf(v.x, v.x, ss);
-    ss = fmaf(v.y, v.y, ss);
-    ss = fmaf(v.z, v.z, ss);
-    ss = fmaf(v.w, v.w, ss);
-  }
-  ss = wave_sum(ss);
-  if (lane == 0) inv[b] = 1.0f / sqrtf(ss / (float)n + eps);
+  const float r = rms_row_inv(X + (size_t)b * n, n, eps, lane);
+  if (lane == 0) inv[b] = r;
 }
 
 // QKV epilogue of the one-token path (phase_qkv), per (row, pair): scale,
@@ -832,24 +866,27 @@ __global__ __launch_bounds__(256, 2) void k_b_attn_tile(const Dims d, const BRow
 // partials were written by earlier launches on the same stream, so their
 // values are read directly (the low half of each tagged word).
 constexpr uint32_t COMB_MAX_HEADS = 64;
+constexpr uint32_t COMB_HEADS_PER_BLOCK = 4;  // grid y: groups of heads
 __global__ __launch_bounds__(256) void k_b_comb(const Dims d, const BRow* __restrict__ rows,
                                                 const u64* __restrict__ part, uint32_t part_w,
                                                 float* __restrict__ attp) {
-  __shared__ float sc[COMB_MAX_HEADS][MAX_ACHUNKS];
-  __shared__ float ls[COMB_MAX_HEADS];
-  const uint32_t b = blockIdx.x;
+  __shared__ float sc[COMB_HEADS_PER_BLOCK][MAX_ACHUNKS];
+  __shared__ float ls[COMB_HEADS_PER_BLOCK];
+  const uint32_t b = blockIdx.x, h0 = blockIdx.y * COMB_HEADS_PER_BLOCK;
+  const uint32_t nh = min(COMB_HEADS_PER_BLOCK, d.nh - h0);
   const uint32_t nch = attn_nchunks(rows[b].pos), hs = d.hd + 2;
   const u64* pb = part + (size_t)b * part_w;
   auto ld_head = [&](uint32_t hh) {
     const u64* p = pb + (size_t)hh * MAX_ACHUNKS * hs;
     return [p](uint32_t i) { return __uint_as_float((uint32_t)p[i]); };
   };
-  for (uint32_t hh = threadIdx.x; hh < d.nh; hh += blockDim.x)
-    ls[hh] = combine_scales(ld_head(hh), nch, hs, sc[hh]);
+  for (uint32_t k = threadIdx.x; k < nh; k += blockDim.x)
+    ls[k] = combine_scales(ld_head(h0 + k), nch, hs, sc[k]);
   __syncthreads();
-  for (uint32_t u = threadIdx.x; u < d.q; u += blockDim.x) {
-    const uint32_t hh = u / d.hd, dd = u - hh * d.hd;
-    attp[panel_at(b, u, panel_chunks(d.q))] = combine_value(ld_head(hh), nch, hs, dd, sc[hh], ls[hh]);
+  for (uint32_t v = threadIdx.x; v < nh * d.hd; v += blockDim.x) {
+    const uint32_t k = v / d.hd, dd = v - k * d.hd, u = (h0 + k) * d.hd + dd;
+    attp[panel_at(b, u, panel_chunks(d.q))] =
+        combine_value(ld_head(h0 + k), nch, hs, dd, sc[k], ls[k]);
   }
 }
 

@@ -1428,9 +1428,11 @@ static void launch_gemm_tn(hipStream_t s, const float* Wp, uint32_t M, uint32_t 
 // workgroup (a quarter of the work each), which finish in a fraction of a
 // round. Every output is computed the same way either way.
 template <uint32_t OUT>
-static void launch_gemm_out(hipStream_t s, const float* Wp, uint32_t M, uint32_t K, const float* Xp,
+static bool launch_gemm_out(hipStream_t s, const float* Wp, uint32_t M, uint32_t K, const float* Xp,
                             uint32_t B, float* Y, uint32_t ldy, const float* scale,
-                            const uint32_t* gen, uint32_t ncu, float* P, float* QS, size_t qs_floats) {
+                            const uint32_t* gen, uint32_t ncu, float* P, float* QS, size_t qs_floats,
+                            float* inv_out, float eps) {
+  // Returns whether the rows' 1/rms (inv_out) was written as well.
   const uint32_t nct = (B + 15) / 16, nrg = (M + 63) / 64;
   // Narrow batches: four full column tiles and a row group per CU take the
   // four-tile tasks below; fewer row groups split the segments four ways
@@ -1442,9 +1444,14 @@ static void launch_gemm_out(hipStream_t s, const float* Wp, uint32_t M, uint32_t
       k_gemm_q<false><<<grid, GEMM_WAVES * WAVE, gemm_q_lds_bytes(), s>>>(Wp, M, K, Xp, B, QS);
     else
       k_gemm_q<true><<<grid, GEMM_WAVES * WAVE, gemm_q_lds_bytes(), s>>>(Wp, M, K, Xp, B, QS);
+    if (OUT == GO_RESID && inv_out) {
+      k_gemm_qcomb_rms<<<B, 256, 0, s>>>(QS, M, B, Y, ldy, P, eps, inv_out);
+      return true;
+    }
     k_gemm_qcomb<OUT><<<dim3((M + 255) / 256, B), 256, 0, s>>>(QS, M, B, Y, ldy, scale, gen, P);
-    return;
+    return false;
   }
+
   if (nct <= 4 && !(nct == 4 && nrg >= ncu)) {  // narrow: one row tile per task
     const uint32_t grid = std::min((M + 15) / 16, 2 * ncu), threads = GEMM_WAVES * WAVE;
     if (K % 64 == 0)
@@ -1453,7 +1460,7 @@ static void launch_gemm_out(hipStream_t s, const float* Wp, uint32_t M, uint32_t
     else
       k_gemm_n<OUT, true><<<grid, threads, gemm_n_lds_bytes(), s>>>(Wp, M, K, Xp, B, Y, ldy, scale,
                                                                     gen, P);
-    return;
+    return false;
   }
   const uint32_t w4 = nrg * ((nct + 3) / 4), rounds = w4 / ncu, rest = w4 % ncu;
   if (rounds >= 1 && rest > 0 && rest * 4 <= ncu) {
@@ -1461,23 +1468,29 @@ static void launch_gemm_out(hipStream_t s, const float* Wp, uint32_t M, uint32_t
     if (y4 >= 1 && 4 * y4 < nct) {
       launch_gemm_tn<4, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 0, 4 * y4, ncu, P);
       launch_gemm_tn<1, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 4 * y4, nct - 4 * y4, ncu, P);
-      return;
+      return false;
     }
   }
   launch_gemm_tn<4, OUT>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, 0, nct, ncu, P);
+  return false;
 }
 // P: GO_RESID's panel of the updated rows (K = M).
 // QS / qs_floats: scratch for the quarter-split narrow GEMM (null: not used).
-static void launch_gemm(hipStream_t s, uint32_t ncu, uint32_t out, const float* Wp, uint32_t M,
+// inv_out (GO_RESID, ldy = M): the updated rows' 1/rms (k_b_rms's order) as
+// well; returns whether this launch wrote it (else the caller runs k_b_rms).
+static bool launch_gemm(hipStream_t s, uint32_t ncu, uint32_t out, const float* Wp, uint32_t M,
                         uint32_t K, const float* Xp, uint32_t B, float* Y, uint32_t ldy,
                         const float* scale = nullptr, const uint32_t* gen = nullptr,
-                        float* P = nullptr, float* QS = nullptr, size_t qs_floats = 0) {
+                        float* P = nullptr, float* QS = nullptr, size_t qs_floats = 0,
+                        float* inv_out = nullptr, float eps = 0.0f) {
   if (out == GO_PLAIN)
-    launch_gemm_out<GO_PLAIN>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, ncu, P, QS, qs_floats);
-  else if (out == GO_RESID)
-    launch_gemm_out<GO_RESID>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, ncu, P, QS, qs_floats);
-  else
-    launch_gemm_out<GO_TAG>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, ncu, P, QS, qs_floats);
+    return launch_gemm_out<GO_PLAIN>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, ncu, P, QS,
+                                     qs_floats, nullptr, eps);
+  if (out == GO_RESID)
+    return launch_gemm_out<GO_RESID>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, ncu, P, QS,
+                                     qs_floats, inv_out, eps);
+  return launch_gemm_out<GO_TAG>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, ncu, P, QS, qs_floats,
+                                 nullptr, eps);
 }
 
 // Timing of one launch (profiling on): events recorded around it on the
@@ -1609,8 +1622,10 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
   const uint32_t ldy = batch_ldy(d);
   const size_t qs_n = (size_t)4 * std::min(w.rows, 64u) * ldy;
   k_b_embed<<<n, 256, 0, s>>>(w.drows, m->embed, d.h, w.X, w.XP);
+  // Each layer's residual products also leave the rows' 1/rms for the next
+  // product (GO_RESID with inv_out); the embedding rows need their own.
+  k_b_rms<<<(n + 3) / 4, 256, 0, s>>>(w.X, n, d.h, d.eps, w.INV);
   for (uint32_t l = 0; l < d.L; ++l) {
-    k_b_rms<<<(n + 3) / 4, 256, 0, s>>>(w.X, n, d.h, d.eps, w.INV);
     {
       ProfSpan ps(m, 0, 2.0 * d.qkv_rows * d.h * n);
       launch_gemm(s, m->ncu, GO_PLAIN, m->p_qkv[l], d.qkv_rows, d.h, w.XP, n, w.Y, ldy, nullptr,
@@ -1626,13 +1641,15 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
       else
         k_b_attn<<<(uint32_t)items.size(), BLOCK, m->lds_rows, s>>>(w.rargs, w.drows, w.items, l);
     }
-    k_b_comb<<<n, 256, 0, s>>>(d, w.drows, w.PART, part_words(d), w.XQ);
+    k_b_comb<<<dim3(n, (d.nh + COMB_HEADS_PER_BLOCK - 1) / COMB_HEADS_PER_BLOCK), 256, 0, s>>>(
+        d, w.drows, w.PART, part_words(d), w.XQ);
+    bool inv_done;
     {
       ProfSpan ps(m, 0, 2.0 * d.h * d.q * n);
-      launch_gemm(s, m->ncu, GO_RESID, m->p_o[l], d.h, d.q, w.XQ, n, w.X, d.h, nullptr, nullptr,
-                  w.XP, w.QS, qs_n);
+      inv_done = launch_gemm(s, m->ncu, GO_RESID, m->p_o[l], d.h, d.q, w.XQ, n, w.X, d.h, nullptr,
+                             nullptr, w.XP, w.QS, qs_n, w.INV, d.eps);
     }
-    k_b_rms<<<(n + 3) / 4, 256, 0, s>>>(w.X, n, d.h, d.eps, w.INV);
+    if (!inv_done) k_b_rms<<<(n + 3) / 4, 256, 0, s>>>(w.X, n, d.h, d.eps, w.INV);
     {
       ProfSpan ps(m, 0, 2.0 * 2 * d.ff * d.h * n);
       launch_gemm(s, m->ncu, GO_PLAIN, m->p_gu[l], 2 * d.ff, d.h, w.XP, n, w.Y, ldy, nullptr,
@@ -1641,9 +1658,10 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
     k_b_act<<<dim3((d.ff + 255) / 256, n), 256, 0, s>>>(w.Y, ldy, w.INV, d.ff, d.act, w.XQ);
     {
       ProfSpan ps(m, 0, 2.0 * d.h * d.ff * n);
-      launch_gemm(s, m->ncu, GO_RESID, m->p_d[l], d.h, d.ff, w.XQ, n, w.X, d.h, nullptr, nullptr,
-                  w.XP, w.QS, qs_n);
+      inv_done = launch_gemm(s, m->ncu, GO_RESID, m->p_d[l], d.h, d.ff, w.XQ, n, w.X, d.h, nullptr,
+                             nullptr, w.XP, w.QS, qs_n, w.INV, d.eps);
     }
+    if (!inv_done && l + 1 < d.L) k_b_rms<<<(n + 3) / 4, 256, 0, s>>>(w.X, n, d.h, d.eps, w.INV);
   }
   if (nl) {
     k_b_final<<<nl, 64, 0, s>>>(w.X, w.sel, d.h, m->norm, d.eps, w.XQ, w.LINV);
