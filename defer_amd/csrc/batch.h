@@ -539,9 +539,12 @@ __global__ __launch_bounds__(256) void k_b_rms(const float* __restrict__ X, uint
 // QKV epilogue of the one-token path (phase_qkv), per (row, pair): scale,
 // bias, RoPE; q/k/v words tagged for the attention item; k, v into the
 // row's cache at its position.
+// QS (if not null): the product is still k_gemm_q's four subtree planes
+// ([4][nb][qkv_rows]), combined here as k_gemm_qcomb would.
 __global__ void k_b_qkv_epi(const Args* __restrict__ ap, const BRow* __restrict__ rows, uint32_t l,
                             const float* __restrict__ Y, uint32_t ldy, const float* __restrict__ inv,
-                            u64* __restrict__ qkvt, uint32_t ldq) {
+                            u64* __restrict__ qkvt, uint32_t ldq, const float* __restrict__ QS,
+                            uint32_t nb) {
   const Dims& d = ap->d;
   const uint32_t b = blockIdx.y;
   const uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
@@ -561,7 +564,15 @@ __global__ void k_b_qkv_epi(const Args* __restrict__ ap, const BRow* __restrict_
     e.w = bias[r0 + d.half];
   }
   const float iv = inv[b];
-  float y0 = Y[(size_t)b * ldy + r0], y1 = Y[(size_t)b * ldy + r1];
+  float y0, y1;
+  if (QS) {
+    const size_t plane = (size_t)nb * d.qkv_rows, e0 = (size_t)b * d.qkv_rows + r0, e1 = e0 + d.half;
+    y0 = (QS[e0] + QS[plane + e0]) + (QS[2 * plane + e0] + QS[3 * plane + e0]);
+    y1 = (QS[e1] + QS[plane + e1]) + (QS[2 * plane + e1] + QS[3 * plane + e1]);
+  } else {
+    y0 = Y[(size_t)b * ldy + r0];
+    y1 = Y[(size_t)b * ldy + r1];
+  }
   y0 = y0 * iv + e.z;
   y1 = y1 * iv + e.w;
   float a0 = y0, a1 = y1;

@@ -1431,8 +1431,10 @@ template <uint32_t OUT>
 static bool launch_gemm_out(hipStream_t s, const float* Wp, uint32_t M, uint32_t K, const float* Xp,
                             uint32_t B, float* Y, uint32_t ldy, const float* scale,
                             const uint32_t* gen, uint32_t ncu, float* P, float* QS, size_t qs_floats,
-                            float* inv_out, float eps) {
-  // Returns whether the rows' 1/rms (inv_out) was written as well.
+                            float* inv_out, float eps, bool leave_planes) {
+  // Returns whether the rows' 1/rms (inv_out) was written as well (GO_RESID),
+  // or whether the product was left as QS's four subtree planes and Y not
+  // written (GO_PLAIN with leave_planes).
   const uint32_t nct = (B + 15) / 16, nrg = (M + 63) / 64;
   // Narrow batches: four full column tiles and a row group per CU take the
   // four-tile tasks below; fewer row groups split the segments four ways
@@ -1448,6 +1450,7 @@ static bool launch_gemm_out(hipStream_t s, const float* Wp, uint32_t M, uint32_t
       k_gemm_qcomb_rms<<<B, 256, 0, s>>>(QS, M, B, Y, ldy, P, eps, inv_out);
       return true;
     }
+    if (OUT == GO_PLAIN && leave_planes) return true;
     k_gemm_qcomb<OUT><<<dim3((M + 255) / 256, B), 256, 0, s>>>(QS, M, B, Y, ldy, scale, gen, P);
     return false;
   }
@@ -1478,19 +1481,21 @@ static bool launch_gemm_out(hipStream_t s, const float* Wp, uint32_t M, uint32_t
 // QS / qs_floats: scratch for the quarter-split narrow GEMM (null: not used).
 // inv_out (GO_RESID, ldy = M): the updated rows' 1/rms (k_b_rms's order) as
 // well; returns whether this launch wrote it (else the caller runs k_b_rms).
+// leave_planes (GO_PLAIN): the quarter-split product may stay as QS's
+// subtree planes for the consumer to combine; returns whether it did.
 static bool launch_gemm(hipStream_t s, uint32_t ncu, uint32_t out, const float* Wp, uint32_t M,
                         uint32_t K, const float* Xp, uint32_t B, float* Y, uint32_t ldy,
                         const float* scale = nullptr, const uint32_t* gen = nullptr,
                         float* P = nullptr, float* QS = nullptr, size_t qs_floats = 0,
-                        float* inv_out = nullptr, float eps = 0.0f) {
+                        float* inv_out = nullptr, float eps = 0.0f, bool leave_planes = false) {
   if (out == GO_PLAIN)
     return launch_gemm_out<GO_PLAIN>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, ncu, P, QS,
-                                     qs_floats, nullptr, eps);
+                                     qs_floats, nullptr, eps, leave_planes);
   if (out == GO_RESID)
     return launch_gemm_out<GO_RESID>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, ncu, P, QS,
-                                     qs_floats, inv_out, eps);
+                                     qs_floats, inv_out, eps, false);
   return launch_gemm_out<GO_TAG>(s, Wp, M, K, Xp, B, Y, ldy, scale, gen, ncu, P, QS, qs_floats,
-                                 nullptr, eps);
+                                 nullptr, eps, false);
 }
 
 // Timing of one launch (profiling on): events recorded around it on the
@@ -1626,13 +1631,14 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
   // product (GO_RESID with inv_out); the embedding rows need their own.
   k_b_rms<<<(n + 3) / 4, 256, 0, s>>>(w.X, n, d.h, d.eps, w.INV);
   for (uint32_t l = 0; l < d.L; ++l) {
+    bool planes;
     {
       ProfSpan ps(m, 0, 2.0 * d.qkv_rows * d.h * n);
-      launch_gemm(s, m->ncu, GO_PLAIN, m->p_qkv[l], d.qkv_rows, d.h, w.XP, n, w.Y, ldy, nullptr,
-                  nullptr, nullptr, w.QS, qs_n);
+      planes = launch_gemm(s, m->ncu, GO_PLAIN, m->p_qkv[l], d.qkv_rows, d.h, w.XP, n, w.Y, ldy,
+                           nullptr, nullptr, nullptr, w.QS, qs_n, nullptr, 0.0f, true);
     }
-    k_b_qkv_epi<<<dim3((d.qkv_rows / 2 + 255) / 256, n), 256, 0, s>>>(w.rargs, w.drows, l, w.Y, ldy,
-                                                                      w.INV, w.QKVT, d.qkv_rows);
+    k_b_qkv_epi<<<dim3((d.qkv_rows / 2 + 255) / 256, n), 256, 0, s>>>(
+        w.rargs, w.drows, l, w.Y, ldy, w.INV, w.QKVT, d.qkv_rows, planes ? w.QS : nullptr, n);
     {
       ProfSpan ps(m, 1, attn_flop);
       if (tiled)
