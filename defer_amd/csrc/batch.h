@@ -514,11 +514,13 @@ struct BRow {
   uint32_t cap, pos, tick, token;
 };
 
-// X[b] = E[token_b] (model.rs:428), and its panel XP.
-__global__ void k_b_embed(const BRow* __restrict__ rows, const float* __restrict__ embed, uint32_t h,
+// X[b] = E[token_b] (model.rs:428), and its panel XP; token_b from dtok
+// (device, e.g. just sampled) when given, else from the row.
+__global__ void k_b_embed(const BRow* __restrict__ rows, const uint32_t* __restrict__ dtok,
+                          const float* __restrict__ embed, uint32_t h,
                           float* __restrict__ X, float* __restrict__ XP) {
   const uint32_t b = blockIdx.x, nch = panel_chunks(h);
-  const float* e = embed + (size_t)rows[b].token * h;
+  const float* e = embed + (size_t)(dtok ? dtok[b] : rows[b].token) * h;
   for (uint32_t i = threadIdx.x; i < h; i += blockDim.x) {
     const float v = e[i];
     X[(size_t)b * h + i] = v;

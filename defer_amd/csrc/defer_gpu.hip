@@ -1570,8 +1570,11 @@ static Args row_args(const defer_gpu_cache* c, const BatchWs& w, uint32_t b) {
 // Runs n rows (n <= BATCH_MAX_ROWS) through every layer; logits rows
 // sel[0..nl) (batch row indices) get tagged logits and chunk maxima in the
 // workspace. Rows must already be validated (tokens, capacity).
+// dtok: the rows' tokens on the device (else rows[b].token). deferred: the
+// caller synchronises and checks the run state later (and has reset it).
 static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* const* rcache,
-                     uint32_t n, const uint32_t* sel, uint32_t nl) {
+                     uint32_t n, const uint32_t* sel, uint32_t nl,
+                     const uint32_t* dtok = nullptr, bool deferred = false) {
   const Dims& d = m->d;
   const hipStream_t s = m->stream;
   int rc = ensure_panels(m);
@@ -1623,10 +1626,10 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
     HIP_TRY(hipMemcpyAsync(w.sel, sel, nl * sizeof(uint32_t), hipMemcpyHostToDevice, s));
     HIP_TRY(hipMemcpyAsync(w.lgen, lgen.data(), nl * sizeof(uint32_t), hipMemcpyHostToDevice, s));
   }
-  k_begin<<<1, 1, 0, s>>>(w.st);
+  if (!deferred) k_begin<<<1, 1, 0, s>>>(w.st);
   const uint32_t ldy = batch_ldy(d);
   const size_t qs_n = (size_t)4 * std::min(w.rows, 64u) * ldy;
-  k_b_embed<<<n, 256, 0, s>>>(w.drows, m->embed, d.h, w.X, w.XP);
+  k_b_embed<<<n, 256, 0, s>>>(w.drows, dtok, m->embed, d.h, w.X, w.XP);
   // Each layer's residual products also leave the rows' 1/rms for the next
   // product (GO_RESID with inv_out); the embedding rows need their own.
   k_b_rms<<<(n + 3) / 4, 256, 0, s>>>(w.X, n, d.h, d.eps, w.INV);
@@ -1679,6 +1682,7 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
     k_b_chunkmax<<<dim3((d.nvc + 3) / 4, nl), 256, 0, s>>>(d, w.LOGT, w.lgen, w.VMAX, w.VARG, nl);
   }
   HIP_TRY(hipGetLastError());
+  if (deferred && !m->prof) return DEFER_GPU_OK;
   HIP_TRY(hipStreamSynchronize(s));
   if (m->prof) prof_collect(m);
   DevState h;
@@ -1690,9 +1694,11 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
 // Sampling ops on logits rows of the workspace: op j samples logits row
 // lrow[j] of cache c for generation base tick[j] (the tick of the forward
 // that follows the sample) with word words[j].
+// deferred: the tokens stay in the workspace (w.sout) and the caller
+// synchronises and checks the run state later.
 static int batch_sample(defer_gpu_model* m, defer_gpu_cache* const* ocache, const uint32_t* lrow,
                         const uint32_t* tick, const uint32_t* words, uint32_t nops, float T,
-                        uint32_t* out, bool own_logits) {
+                        uint32_t* out, bool own_logits, bool deferred = false) {
   const Dims& d = m->d;
   const hipStream_t s = m->stream;
   // Sampling a batch's logits rows: batch_run sized the workspace for them,
@@ -1721,6 +1727,7 @@ static int batch_sample(defer_gpu_model* m, defer_gpu_cache* const* ocache, cons
   k_begin<<<1, 1, 0, s>>>(w.st);
   k_b_sample<<<nops, BLOCK, m->lds_rows, s>>>(w.largs, w.stick, w.swords, T, w.sout);
   HIP_TRY(hipGetLastError());
+  if (deferred) return DEFER_GPU_OK;
   HIP_TRY(hipMemcpyAsync(out, w.sout, nops * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
   HIP_TRY(hipStreamSynchronize(s));
   DevState h;
@@ -1815,21 +1822,22 @@ static int feed_batched(defer_gpu_model* m, defer_gpu_cache* c, const uint32_t* 
   return DEFER_GPU_OK;
 }
 
-extern "C" int defer_gpu_forward_batch(const defer_gpu_model* mc, defer_gpu_cache* const* caches,
-                                       const uint32_t* tokens, uint32_t n, float* logits_out) {
-  defer_gpu_model* m = const_cast<defer_gpu_model*>(mc);
-  if (!m) return fail(DEFER_GPU_E_INVALID, "null model");
-  if (n == 0) return DEFER_GPU_OK;
-  if (!caches || !tokens) return fail(DEFER_GPU_E_INVALID, "null argument");
-  if (n > BATCH_MAX_ROWS) return fail(DEFER_GPU_E_INVALID, "at most %u rows per batch", BATCH_MAX_ROWS);
+// The batch forward. tokens: host token ids (checked), or null with dtok:
+// the tokens on the device (just sampled into the workspace, in range by
+// construction), copied to tok_out in the same pass; the run state was
+// reset by the sampling, and one synchronisation ends the call.
+static int forward_batch_impl(defer_gpu_model* m, defer_gpu_cache* const* caches,
+                              const uint32_t* tokens, const uint32_t* dtok, uint32_t* tok_out,
+                              uint32_t n, float* logits_out) {
   const Dims& d = m->d;
+  const bool deferred = dtok != nullptr;
   // positions: a cache listed k times gets k consecutive positions
   std::vector<uint32_t> add(n, 0);
   std::vector<int> last_of(n, -1);  // per row: is it its cache's last row
   for (uint32_t b = 0; b < n; ++b) {
     int rc = check_pair(m, caches[b]);
     if (rc) return rc;
-    if (tokens[b] >= d.V) return fail(DEFER_GPU_E_TOKEN, "token id %u out of range", tokens[b]);
+    if (tokens && tokens[b] >= d.V) return fail(DEFER_GPU_E_TOKEN, "token id %u out of range", tokens[b]);
     for (uint32_t e = 0; e < b; ++e)
       if (caches[e] == caches[b]) ++add[b];
   }
@@ -1842,7 +1850,8 @@ extern "C" int defer_gpu_forward_batch(const defer_gpu_model* mc, defer_gpu_cach
   }
   std::vector<BRow> rows(n);
   for (uint32_t b = 0; b < n; ++b)
-    rows[b] = make_row(caches[b], caches[b]->pos + add[b], caches[b]->tick + add[b], tokens[b]);
+    rows[b] = make_row(caches[b], caches[b]->pos + add[b], caches[b]->tick + add[b],
+                       tokens ? tokens[b] : 0u);
   std::vector<uint32_t> sel;
   std::vector<uint32_t> li_of(n, 0);
   for (uint32_t b = 0; b < n; ++b)
@@ -1851,9 +1860,11 @@ extern "C" int defer_gpu_forward_batch(const defer_gpu_model* mc, defer_gpu_cach
       sel.push_back(b);
     }
   HIP_TRY(hipEventRecord(m->ev0, m->stream));
-  int rc = batch_run(m, rows.data(), caches, n, sel.data(), (uint32_t)sel.size());
+  int rc = batch_run(m, rows.data(), caches, n, sel.data(), (uint32_t)sel.size(), dtok, deferred);
   if (rc) return rc;
   HIP_TRY(hipEventRecord(m->ev1, m->stream));
+  if (deferred)
+    HIP_TRY(hipMemcpyAsync(tok_out, dtok, n * sizeof(uint32_t), hipMemcpyDeviceToHost, m->stream));
   HIP_TRY(hipEventSynchronize(m->ev1));
   float ms = 0.0f;
   HIP_TRY(hipEventElapsedTime(&ms, m->ev0, m->ev1));
@@ -1877,8 +1888,22 @@ extern "C" int defer_gpu_forward_batch(const defer_gpu_model* mc, defer_gpu_cach
       cpos.push_back(rows[b].pos + 1);
       ctick.push_back(rows[b].tick + 1);
     }
-  return batch_commit_many(m, cc.data(), cli.data(), cpos.data(), ctick.data(),
-                           (uint32_t)cc.size());
+  rc = batch_commit_many(m, cc.data(), cli.data(), cpos.data(), ctick.data(), (uint32_t)cc.size());
+  if (rc || !deferred) return rc;
+  DevState h;
+  HIP_TRY(hipMemcpy(&h, m->bw->st, sizeof(h), hipMemcpyDeviceToHost));
+  if (h.abort) return fail(DEFER_GPU_E_TIMEOUT, "a device-side wait exceeded its bound");
+  return DEFER_GPU_OK;
+}
+
+extern "C" int defer_gpu_forward_batch(const defer_gpu_model* mc, defer_gpu_cache* const* caches,
+                                       const uint32_t* tokens, uint32_t n, float* logits_out) {
+  defer_gpu_model* m = const_cast<defer_gpu_model*>(mc);
+  if (!m) return fail(DEFER_GPU_E_INVALID, "null model");
+  if (n == 0) return DEFER_GPU_OK;
+  if (!caches || !tokens) return fail(DEFER_GPU_E_INVALID, "null argument");
+  if (n > BATCH_MAX_ROWS) return fail(DEFER_GPU_E_INVALID, "at most %u rows per batch", BATCH_MAX_ROWS);
+  return forward_batch_impl(m, caches, tokens, nullptr, nullptr, n, logits_out);
 }
 
 extern "C" int defer_gpu_step_batch(const defer_gpu_model* mc, defer_gpu_cache* const* caches,
@@ -1904,9 +1929,15 @@ extern "C" int defer_gpu_step_batch(const defer_gpu_model* mc, defer_gpu_cache* 
       return fail(DEFER_GPU_E_CONTEXT, "context length %u exceeded", m->cfg.max_seq_len);
     tick[b] = caches[b]->tick;
   }
-  rc = batch_sample(m, caches, nullptr, tick.data(), rng_words, n, temperature, tokens_out, true);
+  // Sample, forward and commit in one pass with one synchronisation: the
+  // sampled tokens stay on the device for the embedding (the workspace is
+  // sized first, so the forward does not reallocate it under them).
+  rc = ensure_ws(m, n, n);
   if (rc) return rc;
-  return defer_gpu_forward_batch(m, caches, tokens_out, n, nullptr);
+  rc = batch_sample(m, caches, nullptr, tick.data(), rng_words, n, temperature, tokens_out, true,
+                    true);
+  if (rc) return rc;
+  return forward_batch_impl(m, caches, nullptr, m->bw->sout, tokens_out, n, nullptr);
 }
 
 // Checkout's replay through batches: every history token is fed (teacher
