@@ -337,7 +337,7 @@ def main() -> int:
         return 0
     if args.gpus != 1:
         print(f"bench.py runs on one GPU; --gpus {args.gpus} is not supported "
-              "(the single-GPU path is the whole product; see DESIGN.md for how it would shard)",
+              "(the single-GPU path is the whole product: one GPU's share at its real shape)",
               file=sys.stderr)
         return 2
 
