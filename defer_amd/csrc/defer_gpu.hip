@@ -714,8 +714,11 @@ static int cache_alloc(const defer_gpu_model* m, uint32_t cap, defer_gpu_cache* 
   HIP_TRY(hipMalloc(&c->kc, kvn * sizeof(float)));
   HIP_TRY(hipMalloc(&c->vc, kvn * sizeof(float)));
   const size_t hs = d.hd + 2;
-  const size_t words = d.qkv_rows + (size_t)d.nh * MAX_ACHUNKS * hs + d.q + d.h + d.h + d.ff +
-                       d.V + 3 * (size_t)d.nvc + 64;
+  // xo, xd, g: MB_REPS replicas of one block, each on its own 32 KB boundary
+  const size_t rep_words = ((size_t)2 * d.h + d.ff + 4095) / 4096 * 4096;
+  const size_t base_words = (d.qkv_rows + (size_t)d.nh * MAX_ACHUNKS * hs + d.q + d.V +
+                             3 * (size_t)d.nvc + 64 + 4095) / 4096 * 4096;
+  const size_t words = base_words + MB_REPS * rep_words;
   c->mb_words = words;
   HIP_TRY(hipMalloc(&c->mb, words * sizeof(u64)));
   HIP_TRY(hipMemset(c->mb, 0, words * sizeof(u64)));
@@ -738,13 +741,15 @@ static int cache_alloc(const defer_gpu_model* m, uint32_t cap, defer_gpu_cache* 
   a.mb_qkv = p; p += d.qkv_rows;
   a.mb_part = p; p += (size_t)d.nh * MAX_ACHUNKS * hs;
   a.mb_att = p; p += d.q;
-  a.mb_xo = p; p += d.h;
-  a.mb_xd = p; p += d.h;
-  a.mb_g = p; p += d.ff;
   a.mb_logit = p; p += d.V;
   a.mb_vmax = p; p += d.nvc;
   a.mb_varg = p; p += d.nvc;
   a.mb_vsum = p; p += d.nvc;
+  p = c->mb + base_words;
+  a.mb_xo = p;
+  a.mb_xd = p + d.h;
+  a.mb_g = p + 2 * d.h;
+  a.rep_words = (uint32_t)rep_words;
   a.st = c->st;
   a.mask = nullptr;
   HIP_TRY(hipMalloc(&c->d_args, sizeof(Args)));

@@ -37,6 +37,9 @@ constexpr uint32_t ACHUNK = 128;       // attention positions per chunk (base si
 constexpr uint32_t MAX_ACHUNKS = 16;   // attention chunks per head at most
 constexpr uint32_t INLINE_COMB_MAX = 1536;  // floats of partials combined inside the O phase
 constexpr uint32_t SPIN_LIMIT = 1u << 21;
+// Replicas of the all-to-all mailboxes (xo, xd, g): one per XCD, so the
+// 32 workgroups of an XCD poll their own copy.
+constexpr uint32_t MB_REPS = 8;
 constexpr uint32_t NO_INDEX = 0xffffffffu;
 
 // ------------------------------------------------------------------ layout
@@ -111,9 +114,12 @@ struct Args {
   u64* mb_qkv;           // [qkv_rows]
   u64* mb_part;          // [nh][MAX_ACHUNKS][hd + 2]  (m, l, acc[hd])
   u64* mb_att;           // [q] combined attention (separate-combine path)
+  // xo, xd and g have MB_REPS replicas, rep_words apart: a word is
+  // published to every replica and a workgroup reads its XCD's (wg % 8)
   u64* mb_xo;            // [h] residual after attention
   u64* mb_xd;            // [h] residual after the MLP
   u64* mb_g;             // [ff]
+  uint32_t rep_words;
   u64* mb_logit;         // [V]
   u64* mb_vmax;          // [nvc] chunk max logit
   u64* mb_varg;          // [nvc] chunk argmax (index bits)

@@ -228,19 +228,38 @@ __device__ __forceinline__ void pub_float(const Lds& s, uint32_t i, float* p, fl
   e[1] = (u64)(uintptr_t)p | 1u;
 }
 __device__ __forceinline__ void pub_none(const Lds& s, uint32_t i) { lptr(s.pub + 2 * i)[1] = 0; }
+// Entry i: a tagged word for every replica of a replicated mailbox (address
+// bit 1 marks it).
+__device__ __forceinline__ void pub_word_rep(const Lds& s, uint32_t i, u64* slot, float v,
+                                             uint32_t gen) {
+  AS_LDS u64* e = lptr(s.pub + 2 * i);
+  e[0] = ((u64)gen << 32) | (u64)__float_as_uint(v);
+  e[1] = (u64)(uintptr_t)slot | 2u;
+}
+// A workgroup's replica of a replicated mailbox.
+__device__ __forceinline__ const u64* rep_of(const Args& a, const u64* base, uint32_t wg) {
+  return base + (size_t)(wg % MB_REPS) * a.rep_words;
+}
 
 // The barrier that ends a matvec phase, then the pollers' stores.
-__device__ __forceinline__ void pub_flush(const Lds& s, uint32_t n) {
+__device__ __forceinline__ void pub_flush(const Lds& s, uint32_t n, uint32_t rep_words = 0) {
   __syncthreads();
   if (threadIdx.x >= NPOLL * WAVE) return;
   for (uint32_t i = threadIdx.x; i < n; i += NPOLL * WAVE) {
     const AS_LDS u64* e = lptr(s.pub + 2 * i);
     const u64 w = e[0], addr = e[1];
-    if (addr & 1u)
+    if (addr & 1u) {
       st_coherent(reinterpret_cast<float*>((uintptr_t)(addr & ~(u64)1)), __uint_as_float((uint32_t)w));
-    else if (addr)
+    } else if (addr & 2u) {
+      u64* p = reinterpret_cast<u64*>((uintptr_t)(addr & ~(u64)2));
+#pragma unroll
+      for (uint32_t r = 0; r < MB_REPS; ++r)
+        __hip_atomic_store(gptr(p + (size_t)r * rep_words), w, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    } else if (addr) {
       __hip_atomic_store(gptr(reinterpret_cast<u64*>((uintptr_t)addr)), w, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
@@ -687,7 +706,7 @@ __device__ __forceinline__ bool phase_qkv(const Args& a, uint32_t l, uint32_t ti
       lds_st(s.vec + i, ldg(e + i));
     __syncthreads();
     hk.post_b2();
-  } else if (!poll_gather<8>(gather_vec(a.mb_xd, d.h, gen_of(d, tick, l - 1, PH_D), s.vec), NPOLL,
+  } else if (!poll_gather<8>(gather_vec(rep_of(a, a.mb_xd, wg), d.h, gen_of(d, tick, l - 1, PH_D), s.vec), NPOLL,
                              a.st, s.ctl, hk)) {
     return false;
   }
@@ -1017,7 +1036,7 @@ __device__ __forceinline__ bool phase_o(const Args& a, uint32_t l, uint32_t tick
                            part)
           : gather_vec(a.mb_att, d.q, gen_of(d, tick, l, PH_COMB), s.vec);
   const Gather gr = (l > 0 && R > 0)
-                        ? gather_vec(a.mb_xd + item_of(d.h, wg, G, 0), R, gen_of(d, tick, l - 1, PH_D), xres)
+                        ? gather_vec(rep_of(a, a.mb_xd, wg) + item_of(d.h, wg, G, 0), R, gen_of(d, tick, l - 1, PH_D), xres)
                         : no_gather();
   // Layer 0's residual is the embedding row: its words are loaded before the
   // wait (pollers, one word per thread).
@@ -1041,10 +1060,10 @@ __device__ __forceinline__ bool phase_o(const Args& a, uint32_t l, uint32_t tick
   if (wave >= NPOLL && wave < NWA) {
     const uint32_t gen = gen_of(d, tick, l, PH_O);
     items_dot(a, IK_O, wave - NPOLL, l, sg, P, s.vec, wg, G, lane, [&](uint32_t k, float y, float) {
-      if (lane == 0) pub_word(s, k, a.mb_xo + item_of(d.h, wg, G, k), lds_ld(xres + k) + y, gen);
+      if (lane == 0) pub_word_rep(s, k, a.mb_xo + item_of(d.h, wg, G, k), lds_ld(xres + k) + y, gen);
     });
   }
-  pub_flush(s, R);
+  pub_flush(s, R, a.rep_words);
   return true;
 }
 
@@ -1062,7 +1081,7 @@ __device__ __forceinline__ bool phase_gu(const Args& a, uint32_t l, uint32_t tic
     op.layer = l + 1 < d.L ? l + 1 : 0;
     op.wait = sg.wait[IK_GU];
   }
-  if (!poll_gather<8>(gather_vec(a.mb_xo, d.h, gen_of(d, tick, l, PH_O), s.vec), NPOLL, a.st, s.ctl,
+  if (!poll_gather<8>(gather_vec(rep_of(a, a.mb_xo, wg), d.h, gen_of(d, tick, l, PH_O), s.vec), NPOLL, a.st, s.ctl,
                       mv_hook(sg, op, P, IK_GU)))
     return false;
   if (wave >= NPOLL && wave < NWA) {
@@ -1071,10 +1090,10 @@ __device__ __forceinline__ bool phase_gu(const Args& a, uint32_t l, uint32_t tic
     items_dot(a, IK_GU, wave - NPOLL, l, sg, P, s.vec, wg, G, lane,
               [&](uint32_t k, float gate, float up) {
                 if (lane == 0)
-                  pub_word(s, k, a.mb_g + item_of(d.ff, wg, G, k), act_fn(gate * inv, d.act) * (up * inv), gen);
+                  pub_word_rep(s, k, a.mb_g + item_of(d.ff, wg, G, k), act_fn(gate * inv, d.act) * (up * inv), gen);
               });
   }
-  pub_flush(s, rows_owned(d.ff, wg, G));
+  pub_flush(s, rows_owned(d.ff, wg, G), a.rep_words);
   return true;
 }
 
@@ -1084,7 +1103,7 @@ __device__ __forceinline__ bool phase_d(const Args& a, uint32_t l, uint32_t tick
   const Dims d = shape_dims(a.d);
   const uint32_t R = rows_owned(d.h, wg, G);
   const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
-  const Gather gr = R > 0 ? gather_vec(a.mb_xo + item_of(d.h, wg, G, 0), R, gen_of(d, tick, l, PH_O), s.scr)
+  const Gather gr = R > 0 ? gather_vec(rep_of(a, a.mb_xo, wg) + item_of(d.h, wg, G, 0), R, gen_of(d, tick, l, PH_O), s.scr)
                           : no_gather();
   Preload P;
   LoadOp op = no_load();
@@ -1093,16 +1112,16 @@ __device__ __forceinline__ bool phase_d(const Args& a, uint32_t l, uint32_t tick
     op.layer = l + 1 < d.L ? l + 1 : 0;
     op.wait = sg.wait[IK_D];
   }
-  if (!poll_gather<12, 1>(gather_vec(a.mb_g, d.ff, gen_of(d, tick, l, PH_GU), s.vec), gr, NPOLL,
+  if (!poll_gather<12, 1>(gather_vec(rep_of(a, a.mb_g, wg), d.ff, gen_of(d, tick, l, PH_GU), s.vec), gr, NPOLL,
                           a.st, s.ctl, mv_hook(sg, op, P, IK_D)))
     return false;
   if (wave >= NPOLL && wave < NWA) {
     const uint32_t gen = gen_of(d, tick, l, PH_D);
     items_dot(a, IK_D, wave - NPOLL, l, sg, P, s.vec, wg, G, lane, [&](uint32_t k, float y, float) {
-      if (lane == 0) pub_word(s, k, a.mb_xd + item_of(d.h, wg, G, k), lds_ld(s.scr + k) + y, gen);
+      if (lane == 0) pub_word_rep(s, k, a.mb_xd + item_of(d.h, wg, G, k), lds_ld(s.scr + k) + y, gen);
     });
   }
-  pub_flush(s, R);
+  pub_flush(s, R, a.rep_words);
   return true;
 }
 
@@ -1151,7 +1170,7 @@ __device__ __forceinline__ bool phase_lm(const Args& a, uint32_t tick, uint32_t 
   };
   auto row_of = [&](uint32_t q) { return a.head + (size_t)vocab_row(4 * q + qrow(lane)) * d.h; };
   if (lmw && live(wave)) seg_load(A, row_of(wave), d.h, sgm, 0);
-  if (!poll_gather<8>(gather_vec(a.mb_xd, d.h, gen_of(d, tick, d.L - 1, PH_D), s.vec), NPOLL, a.st,
+  if (!poll_gather<8>(gather_vec(rep_of(a, a.mb_xd, wg), d.h, gen_of(d, tick, d.L - 1, PH_D), s.vec), NPOLL, a.st,
                       s.ctl))
     return false;
   for (uint32_t i = threadIdx.x; i < d.h; i += BLOCK) lds_st(xs + i, lds_ld(s.vec + i) * lds_ld(nrm + i));
