@@ -1,27 +1,30 @@
 #!/usr/bin/env python3
-"""Benchmark: verified GPU replay of a 2048-token session, SmolLM2-135M shape, f32.
+"""Benchmark: batch-1 f32 decode of a SmolLM2-135M-shaped model on one MI355X.
 
-Workload (the replay/checkout configuration of the headline metric): a
-135M-shaped Llama with N(0, 0.02) weights from seed 0; a 512-token prompt of
-uniform-random ids; 1536 tokens sampled at temperature 0.7 with seed 7,
-generated on the GPU and logged to a write-ahead log. One step is one
-checkout of that log: all 2048 positions are rebuilt on the GPU and every
-sampled position is re-sampled from its predecessor's logits and compared
-with the record. The library runs the checkout through its batched path
-(every position's forward as rows of MFMA GEMMs in the one-token reduction
-order, the one-token attention and sampler per row), whose results are bit
-for bit those of feeding the positions one at a time: the first step's
-rebuilt cache and logits must equal the generating session's.
+The default workload is the north-star configuration: a 135M-shaped Llama
+(hidden 576, 30 layers, 9/3 heads, head_dim 64, ff 1536, vocab 49152, tied)
+with N(0, 0.02) weights from seed 0 and a 32-token uniform-random prompt;
+session A generates 128 greedy tokens, session B 128 tokens at T = 0.7 with
+seed 42, one token at a time. One step of the benchmark is both sessions:
+their prompts are fed untimed (as the reference's `defer run` excludes load
+and prompt from its tok/s, main.rs:261-312) and the two generate calls --
+256 tokens at positions 32..160 -- are timed on the host clock.
 
-Prints one JSON line. `value` is replayed positions per second with the
-weights, the history and the rng words already in HBM / host memory when the
-timed region starts. `roofline` prices the dominant kernel class of a step
-(by event-timed device time: the GEMMs or the attention), whose launches the
-library times with HIP events on its own stream during the first timed step,
-against MI355X's dense f32 peak. `config` also carries the token-by-token replay rate (one
-persistent-kernel launch, priced against HBM bandwidth) and the batch-1
-decode rates. `cpu_baseline` is the single-threaded C restatement of the
-reference (the oracle) timed on a bounded sample of the same workload.
+Prints one JSON line. `value` is decoded tokens per second over the K timed
+steps. `roofline` prices the persistent decode kernel (`k_persistent`, one
+launch per generate call) against the 8 TB/s HBM peak: its algorithmic bytes
+(every weight once per token, the cached K/V once per GQA group, the new K/V
+row and the logits) over its HIP-event-timed duration on the library's
+stream; `traffic` is its HBM bytes per launch from the committed rocprofv3
+PMC profile. `config` also carries the weight-streaming roofline fraction and
+the replay figures (the 2048-position checkout, batched and token by token).
+`cpu_baseline` is the oracle -- the single-threaded C restatement of the
+reference's loops -- timed on the same workload, pinned to one core, before
+the GPU is touched.
+
+Other workloads (--workload): replay (the 2048-position checkout as its own
+line), sessions (64 Llama-3.2-1B-shaped sessions in lockstep), long
+(360M-shaped 4096-token decode), 8b (8B-shaped decode).
 """
 from __future__ import annotations
 
@@ -72,53 +75,76 @@ def measured_traffic(profile: str = "k_persistent_replay_135m.md",
     return None
 
 
-def cpu_baseline(cfg: dict, weights, history, budget_s: float = 12.0) -> dict:
-    """The oracle (C, one thread) replaying the session's first positions
-    until `budget_s` of CPU work is spent."""
+def host_cpu() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline_c1(cfg: dict, weights, prompt, budget_s: float = 15.0) -> dict:
+    """The oracle (C, one thread, pinned to one core) on the decode workload:
+    session A's greedy tokens, then session B's tokens at T = 0.7, prompts
+    untimed, until `budget_s` of timed decoding is spent."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle_py as O
 
     om = O.OracleModel(cfg, weights)
-    cache = om.new_cache()
-    n = 0
-    t0 = time.perf_counter()
-    while n < len(history) and time.perf_counter() - t0 < budget_s:
-        om.forward(int(history[n]), cache)
-        n += 1
-    dt = time.perf_counter() - t0
-    cores = os.cpu_count() or 0
+    saved = os.sched_getaffinity(0)
+    core = min(saved)
+    os.sched_setaffinity(0, {core})
+    n, spent = 0, 0.0
+    try:
+        for T, seed in ((0.0, 42), (TEMPERATURE, 42)):
+            cache = om.new_cache()
+            logits = None
+            for t in prompt:
+                logits = om.forward(int(t), cache)
+            s = O.seed_from_u64(seed)
+            t0 = time.perf_counter()
+            for g in range(128):
+                w = O.chacha8_word(s, g) if T != 0.0 else 0
+                tok = O.sample_token(logits, T, w)
+                logits = om.forward(tok, cache)
+                n += 1
+                if time.perf_counter() - t0 + spent > budget_s:
+                    break
+            spent += time.perf_counter() - t0
+            if spent > budget_s:
+                break
+    finally:
+        os.sched_setaffinity(0, saved)
     return {
-        "value": n / dt,
+        "value": round(n / spent, 2),
         "unit": "tok/s",
         "cores": 1,
         "kind": "port",
-        "sample": f"oracle replay of positions 0..{n - 1} of the same session "
-                  f"(prompt forwards, 1 thread, {dt:.1f} s; host has {cores} cores)",
+        "sample": f"oracle (C restatement of ops.rs/model.rs/sampler.rs, -O2, no FMA contraction) "
+                  f"decoding {n} tokens of the same two sessions from position 32 (greedy, then "
+                  f"T=0.7), prompts untimed, {spent:.1f} s on core {core}; host: {host_cpu()}, "
+                  f"{os.cpu_count()} logical cores",
     }
 
 
-def c1_decode(model, cfg: dict, H) -> dict:
-    """Batch-1 decode of the CPU-runnable configuration: a 32-token prompt,
-    128 greedy tokens then 128 at T = 0.7 (seed 42), device time of the two
-    generate calls."""
-    from defer_amd import synthetic
-
-    prompt = synthetic.make_prompt(cfg["vocab_size"], 32, seed=42)
-    model.set_batching(0)
-    s = H.Session(model, H.seed_from_u64(42), 0.0, capacity=512)
-    s.prompt(prompt)
-    s.generate(128)
-    ms = model.last_device_ms()
-    s.close()
-    s = H.Session(model, H.seed_from_u64(42), TEMPERATURE, capacity=512)
-    s.prompt(prompt)
-    s.generate(128)
-    s.generate(128)
-    ms += model.last_device_ms()
-    s.close()
-    model.set_batching(16)
-    tok_s = 256 / (ms / 1e3)
-    return {"tok_s": round(tok_s, 2), "us": round(1e6 / tok_s, 1)}
+def c1_step(model, prompt, H) -> tuple:
+    """One step of the decode workload: sessions A (greedy) and B (T = 0.7,
+    seed 42), 128 generated tokens each. Returns (host seconds of the two
+    generate calls, device ms of their two launches, tokens of A, tokens of B)."""
+    wall, dev, out = 0.0, 0.0, []
+    for T in (0.0, TEMPERATURE):
+        s = H.Session(model, H.seed_from_u64(42), T, capacity=512)
+        s.prompt(prompt)
+        t0 = time.perf_counter()
+        toks = s.generate(128)
+        wall += time.perf_counter() - t0
+        dev += model.last_device_ms()
+        assert len(toks) == 128
+        out.append(toks)
+        s.close()
+    return wall, dev, out[0], out[1]
 
 
 def sessions_workload(args) -> int:
@@ -196,56 +222,6 @@ def sessions_workload(args) -> int:
     return 0
 
 
-def c1_workload(args) -> int:
-    """Batch-1 decode of the CPU-runnable configuration alone (c1_decode: a
-    32-token prompt, 128 greedy tokens, then 128 at T = 0.7; positions 32..288
-    timed); roofline = the persistent kernel's algorithmic bytes over the
-    device time of the two timed generate calls."""
-    from defer_amd import gpu as G
-    from defer_amd import host as H
-    from defer_amd import synthetic
-
-    cfg = synthetic.CONFIGS[CFG_NAME]
-    model = G.GpuModel(G.Config.from_dict(cfg), synthetic.make_weights(cfg, 0))
-    c1 = c1_decode(model, cfg, H)
-    ms = 256 / c1["tok_s"] * 1e3
-    wbytes = synthetic.weight_bytes_streamed(cfg)
-    achieved = algorithmic_bytes(cfg, wbytes, 32, 256) / (ms / 1e3) / 1e9
-    line = {
-        "metric": "batch-1 decode tok/s (f32) + achieved HBM GB/s as % of peak",
-        "value": c1["tok_s"],
-        "unit": "tok/s",
-        "n_gpus": 1,
-        "steps": 256,
-        "warmup": 0,
-        "ms_per_step": round(ms / 256, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic (N(0,0.02) weights from seed 0, uniform-random prompt ids)",
-        "config": {
-            "workload": "SmolLM2-135M-shaped decode: 32-token prompt, 128 greedy tokens, then "
-                        "128 at T=0.7 (seed 42), one token at a time",
-            "weight_bytes_per_token": wbytes,
-            "weight_roofline_tok_s": round(PEAK_GBS * 1e9 / wbytes, 1),
-            "weight_roofline_frac": round(c1["tok_s"] * wbytes / (PEAK_GBS * 1e9), 4),
-        },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": "k_persistent",
-            "achieved": round(achieved, 2),
-            "peak": PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / PEAK_GBS, 4),
-            "traffic": None,
-        },
-    }
-    model.close()
-    print(json.dumps(line), flush=True)
-    return 0
-
-
 def decode_workload(args, name: str) -> int:
     """Batch-1 decode of the long-context (SmolLM2-360M shape: 128-token prompt,
     4096 tokens at T=0.8, seed 1) or the large-model configuration
@@ -309,61 +285,18 @@ def decode_workload(args, name: str) -> int:
     return 0
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--workload", choices=["replay", "sessions", "c1", "long", "8b"],
-                    default="replay",
-                    help="replay: the 2048-position checkout (default, the headline); "
-                         "sessions: 64 Llama-3.2-1B-shaped sessions in lockstep; "
-                         "c1: 135M-shaped batch-1 decode of 256 tokens; "
-                         "long: 360M-shaped decode of 4096 tokens; 8b: 8B-shaped decode")
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
-                    help="only copy MIB MiB device-to-device once (calibrates HBM byte counters)")
-    args = ap.parse_args()
-    if args.copy_probe:
-        import torch
-
-        n = args.copy_probe * (1 << 20) // 4
-        src = torch.ones(n, dtype=torch.float32, device="cuda")
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"copy_probe_bytes": n * 4}), flush=True)
-        return 0
-    if args.gpus != 1:
-        print(f"bench.py runs on one GPU; --gpus {args.gpus} is not supported "
-              "(the single-GPU path is the whole product: one GPU's share at its real shape)",
-              file=sys.stderr)
-        return 2
-
-    if args.workload == "sessions":
-        return sessions_workload(args)
-    if args.workload == "c1":
-        return c1_workload(args)
-    if args.workload in ("long", "8b"):
-        return decode_workload(args, args.workload)
-
-    from defer_amd import gpu as G
-    from defer_amd import host as H
-    from defer_amd import synthetic
-
-    cfg = synthetic.CONFIGS[CFG_NAME]
-    weights = synthetic.make_weights(cfg, 0)
-    model = G.GpuModel(G.Config.from_dict(cfg), weights)
+def replay_measure(model, cfg: dict, weights, H, steps: int, warmup: int) -> dict:
+    """The replay configuration: a 2048-token session (512 prompt + 1536
+    sampled at T=0.7, seed 7) generated on the GPU and logged to a WAL, then
+    checked out `steps` times through the batched path (every position
+    rebuilt, every sampled position re-sampled and verified; bit-identical to
+    the token-by-token path, which is timed once beside). The first timed
+    checkout's cache and logits are compared bit for bit with the generating
+    session's."""
+    n_pos = PROMPT_LEN + SAMPLED
     signature = H.sha256(b"".join(w.tobytes() for w in weights))
     seed = H.seed_from_u64(SEED)
-    prompt = synthetic.make_prompt(cfg["vocab_size"], PROMPT_LEN, seed=SEED)
-    n_pos = PROMPT_LEN + SAMPLED
-
-    # The session, generated on the GPU and logged (untimed setup; its decode
-    # rate is reported beside the replay rate). Everything outside the timed
-    # replays runs token by token, so every GEMM launch of the run belongs to
-    # a replay and a kernel trace of the run prices exactly those.
+    prompt = synthetic_prompt(cfg, PROMPT_LEN, SEED)
     live = H.Session(model, seed, TEMPERATURE, capacity=n_pos)
     model.set_batching(0)
     live.prompt(prompt)
@@ -383,25 +316,20 @@ def main() -> int:
         return H.Session.checkout(model, log["base_seed"], log["temperature"], log["history"],
                                   log["prompt_len"], log["rng_word_pos"], capacity=n_pos)
 
-    # Token-by-token replay (one persistent launch), timed once beside.
     model.set_batching(0)
     t0 = time.perf_counter()
     replay().close()
     tbt_s = time.perf_counter() - t0
     tbt_dev_s = model.last_device_ms() / 1e3
     model.set_batching(16)
-
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         replay().close()
     # HIP events around every GEMM and attention launch of the first timed
-    # step (the kernels' event-timed durations); the other steps run without
-    # them, since each event pair adds a few microseconds between launches.
+    # checkout only (each event pair adds a few microseconds between launches).
     model.set_profiling(True)
     model.batch_stats(reset=True)
-    times, dev_ms = [], []
-    first = None
-    prof = None
-    for k in range(args.steps):
+    times, dev_ms, first, prof = [], [], None, None
+    for _ in range(steps):
         t0 = time.perf_counter()
         s = replay()
         times.append(time.perf_counter() - t0)
@@ -413,8 +341,6 @@ def main() -> int:
             first = s
         else:
             s.close()
-    prof_steps = 1
-    # Verification of the first timed step (outside the timed region).
     a, b = first.cache, live.cache
     for layer in range(cfg["num_layers"]):
         for x, y in zip(a.read(layer), b.read(layer)):
@@ -423,17 +349,149 @@ def main() -> int:
     if not np.array_equal(a.last_logits().view(np.uint32), b.last_logits().view(np.uint32)):
         raise SystemExit("replayed logits differ from the generated session's")
     first.close()
-
-    total_s = sum(times)
-    value = args.steps * n_pos / total_s
-    wbytes = synthetic.weight_bytes_streamed(cfg)
+    live.close()
+    wbytes = synthetic_weight_bytes(cfg)
     algo = algorithmic_bytes(cfg, wbytes, 0, n_pos)
-    tbt_gbs = algo / tbt_dev_s / 1e9
-    # Dominant kernel class of the batched replay, by event-timed device time.
-    cls = "gemm" if prof["gemm_ms"] >= prof["attn_ms"] else "attn"
-    k_ms, k_flop, k_n = prof[cls + "_ms"], prof[cls + "_flop"], prof[cls + "_launches"]
-    achieved = (k_flop / k_n) / (k_ms / k_n / 1e3) / 1e12
-    c1 = c1_decode(model, cfg, H)
+    gemm_tflops = prof["gemm_flop"] / (prof["gemm_ms"] / 1e3) / 1e12
+    return {
+        "replay_positions": n_pos,
+        "replay_tok_s": round(steps * n_pos / sum(times), 2),
+        "replay_ms": round(sum(times) / steps * 1e3, 3),
+        "replay_device_ms": round(float(np.mean(dev_ms)), 3),
+        "replay_gemm_ms": round(prof["gemm_ms"], 3),
+        "replay_gemm_tflops": round(gemm_tflops, 2),
+        "replay_gemm_mfma_frac": round(gemm_tflops / PEAK_F32_TFLOPS, 4),
+        "replay_attention_ms": round(prof["attn_ms"], 3),
+        "token_by_token_replay_tok_s": round(n_pos / tbt_s, 2),
+        "token_by_token_replay_hbm_gbs": round(algo / tbt_dev_s / 1e9, 2),
+        "token_by_token_replay_hbm_frac": round(algo / tbt_dev_s / 1e9 / PEAK_GBS, 4),
+        "decode_tok_s_ctx_512_2048": round(SAMPLED / (decode_ms / 1e3), 2),
+    }
+
+
+def synthetic_prompt(cfg: dict, n: int, seed: int):
+    from defer_amd import synthetic
+
+    return synthetic.make_prompt(cfg["vocab_size"], n, seed=seed)
+
+
+def synthetic_weight_bytes(cfg: dict) -> int:
+    from defer_amd import synthetic
+
+    return synthetic.weight_bytes_streamed(cfg)
+
+
+def replay_workload(args) -> int:
+    """The replay configuration as its own line (value: replayed positions/s)."""
+    from defer_amd import gpu as G
+    from defer_amd import host as H
+    from defer_amd import synthetic
+
+    cfg = synthetic.CONFIGS[CFG_NAME]
+    weights = synthetic.make_weights(cfg, 0)
+    model = G.GpuModel(G.Config.from_dict(cfg), weights)
+    r = replay_measure(model, cfg, weights, H, args.steps, args.warmup)
+    model.close()
+    line = {
+        "metric": "verified replay positions/s (f32), 2048-position checkout",
+        "value": r["replay_tok_s"],
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": r["replay_ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (N(0,0.02) weights from seed 0, uniform-random prompt ids)",
+        "config": {"workload": "SmolLM2-135M-shaped checkout of a 2048-token session (512 prompt "
+                               "+ 1536 sampled at T=0.7, seed 7), batched path", **r},
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "k_gemm (MFMA f32 GEMMs)",
+            "achieved": r["replay_gemm_tflops"],
+            "peak": PEAK_F32_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": r["replay_gemm_mfma_frac"],
+            "traffic": measured_traffic("k_gemm_replay_135m.md", "gemm_traffic_bytes_per_replay"),
+        },
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--workload", choices=["c1", "replay", "sessions", "long", "8b"],
+                    default="c1",
+                    help="c1: 135M-shaped batch-1 decode (default, the headline); replay: the "
+                         "2048-position checkout; sessions: 64 Llama-3.2-1B-shaped sessions in "
+                         "lockstep; long: 360M-shaped decode of 4096 tokens; 8b: 8B-shaped decode")
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-replay", action="store_true",
+                    help="skip the replay figures in the decode line's config")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only copy MIB MiB device-to-device once (calibrates HBM byte counters)")
+    args = ap.parse_args()
+    if args.copy_probe:
+        import torch
+
+        n = args.copy_probe * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": n * 4}), flush=True)
+        return 0
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the single-GPU path is the whole product: one GPU's share at its real shape)",
+              file=sys.stderr)
+        return 2
+    if args.workload == "sessions":
+        return sessions_workload(args)
+    if args.workload == "replay":
+        return replay_workload(args)
+    if args.workload in ("long", "8b"):
+        return decode_workload(args, args.workload)
+
+    from defer_amd import synthetic
+
+    cfg = synthetic.CONFIGS[CFG_NAME]
+    weights = synthetic.make_weights(cfg, 0)
+    prompt = synthetic.make_prompt(cfg["vocab_size"], 32, seed=42)
+    # The CPU baseline runs first, before anything touches the GPU.
+    cpu = None if args.no_cpu else cpu_baseline_c1(cfg, weights, prompt)
+
+    from defer_amd import gpu as G
+    from defer_amd import host as H
+
+    model = G.GpuModel(G.Config.from_dict(cfg), weights)
+    model.set_batching(0)
+    ref = None
+    for _ in range(args.warmup):
+        ref = c1_step(model, prompt, H)[2:]
+    wall, dev = 0.0, 0.0
+    for _ in range(args.steps):
+        w, d, ta, tb = c1_step(model, prompt, H)
+        wall += w
+        dev += d
+        if ref is not None and (ta, tb) != ref:
+            raise SystemExit("decode is not repeatable: tokens differ between steps")
+        ref = (ta, tb)
+    model.set_batching(16)
+    n_tok = 256 * args.steps
+    wbytes = synthetic.weight_bytes_streamed(cfg)
+    algo = 2 * algorithmic_bytes(cfg, wbytes, 32, 128) * args.steps
+    achieved = algo / (dev / 1e3) / 1e9
+    value = n_tok / wall
+    secondary = {} if args.no_replay else replay_measure(model, cfg, weights, H, 3, 1)
+    model.close()
     line = {
         "metric": "batch-1 decode tok/s (f32) + achieved HBM GB/s as % of peak; replay tok/s",
         "value": round(value, 2),
@@ -441,49 +499,36 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(total_s / args.steps * 1e3, 3),
+        "ms_per_step": round(wall / args.steps * 1e3, 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (N(0,0.02) weights from seed 0, uniform-random prompt ids)",
         "config": {
-            "workload": "SmolLM2-135M-shaped replay: 2048-token session (512 prompt + 1536 sampled "
-                        "at T=0.7, seed 7), every position rebuilt and every sampled position "
-                        "re-sampled and verified on the GPU (batched path, bit-identical to "
-                        "token by token)",
-            "positions_per_step": n_pos,
-            "replay_device_ms": round(float(np.mean(dev_ms)), 3),
-            "gemm_ms_per_step": round(prof["gemm_ms"] / prof_steps, 3),
-            "attention_ms_per_step": round(prof["attn_ms"] / prof_steps, 3),
-            "event_timed_steps": prof_steps,
-            "token_by_token_replay_tok_s": round(n_pos / tbt_s, 2),
-            "token_by_token_replay_hbm_gbs": round(tbt_gbs, 2),
-            "token_by_token_replay_hbm_frac": round(tbt_gbs / PEAK_GBS, 4),
-            "token_by_token_replay_traffic": measured_traffic(),
-            "decode_tok_s_ctx_512_2048": round(SAMPLED / (decode_ms / 1e3), 2),
-            "c1_decode_tok_s": c1["tok_s"],
-            "c1_decode_us_per_token": c1["us"],
-            "c1_weight_roofline_frac": round(c1["tok_s"] * wbytes / (PEAK_GBS * 1e9), 4),
+            "workload": "SmolLM2-135M-shaped batch-1 decode: 32-token prompt; session A 128 "
+                        "greedy tokens, session B 128 tokens at T=0.7 (seed 42); one step = both "
+                        "sessions (256 tokens at positions 32..160, prompts untimed)",
+            "tokens_per_step": 256,
+            "us_per_token": round(wall / n_tok * 1e6, 1),
+            "device_us_per_token": round(dev / n_tok * 1e3, 1),
+            "weight_bytes_per_token": wbytes,
             "weight_roofline_tok_s": round(PEAK_GBS * 1e9 / wbytes, 1),
+            "weight_roofline_frac": round(value * wbytes / (PEAK_GBS * 1e9), 4),
+            **secondary,
         },
         "roofline": {
-            "bound": "mfma",
-            "kernel": "k_gemm (MFMA f32 GEMMs)" if cls == "gemm" else "k_b_attn (attention items)",
-            "achieved": round(achieved, 3),
-            "peak": PEAK_F32_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_F32_TFLOPS, 4),
-            # HBM bytes of one replay's k_gemm launches (PMC, committed profile)
-            "traffic": (measured_traffic("k_gemm_replay_135m.md", "gemm_traffic_bytes_per_replay")
-                        if cls == "gemm" else None),
+            "bound": "hbm",
+            "kernel": "k_persistent (one launch per 128-token generate call)",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_GBS, 4),
+            "traffic": measured_traffic("k_persistent_decode_135m.md", "traffic_bytes_per_launch"),
         },
     }
-    # Device objects are released here, not during interpreter shutdown.
-    live.close()
-    model.close()
-    if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(cfg, weights, log["history"])
+    if cpu is not None:
+        line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)
     return 0
 

@@ -981,13 +981,16 @@ __global__ __launch_bounds__(256) void k_b_chunkmax(const Dims d, const u64* __r
 __global__ __launch_bounds__(BLOCK) void k_b_sample(const Args* __restrict__ largs,
                                                     const uint32_t* __restrict__ tick,
                                                     const uint32_t* __restrict__ words, float T,
-                                                    uint32_t* __restrict__ out) {
+                                                    uint32_t tag0, uint32_t* __restrict__ out) {
   const uint32_t j = blockIdx.x;
   const Args& a = largs[j];
   const Lds s = lds_init_rows(a.d);
-  if (T != 0.0f && !sample_stage_a(a, tick[j], T, 0, 1, s)) return;
+  // A row whose wait runs out still leaves a token in range (0), so a
+  // following batched embedding never reads outside the table.
+  if (threadIdx.x == 0) out[j] = 0u;
+  if (T != 0.0f && !sample_stage_a(a, tick[j], tag0 + j, T, 0, 1, s)) return;
   uint32_t tok = 0;
-  if (!sample_stage_b(a, tick[j], T, T != 0.0f ? words[j] : 0u, s, &tok)) return;
+  if (!sample_stage_b(a, tick[j], tag0 + j, T, T != 0.0f ? words[j] : 0u, s, &tok)) return;
   if (threadIdx.x == 0) out[j] = tok;
 }
 

@@ -104,7 +104,8 @@ __global__ __launch_bounds__(BLOCK) void k_samp_a(const Args* __restrict__ ap,
   if (st->halt) return;
   const uint32_t i = st->op;
   if (i < run->sample_from || run->temperature == 0.0f) return;
-  sample_stage_a(a, st->tick, run->temperature, blockIdx.x, gridDim.x, s);
+  sample_stage_a(a, st->tick, run->samp_tag0 + (i - run->sample_from), run->temperature,
+                 blockIdx.x, gridDim.x, s);
 }
 
 // One workgroup: sampler stage B (if the op samples) and the token to feed.
@@ -119,7 +120,9 @@ __global__ __launch_bounds__(BLOCK) void k_op(const Args* __restrict__ ap,
   uint32_t tok;
   if (i >= r.sample_from) {
     const uint32_t word = r.temperature != 0.0f ? r.words[i - r.sample_from] : 0u;
-    if (!sample_stage_b(a, st->tick, r.temperature, word, s, &tok)) return;
+    if (!sample_stage_b(a, st->tick, r.samp_tag0 + (i - r.sample_from), r.temperature, word, s,
+                        &tok))
+      return;
     if (r.mode == RUN_REPLAY) {
       if (tok != r.tokens[i]) {
         __syncthreads();
@@ -240,6 +243,37 @@ __global__ void k_commit_rows(const StateSet* __restrict__ set, const u64* __res
   }
 }
 
+// Caller-given logits become the cache's last logits: each word tagged as
+// the last forward's lm_head phase tags it, and each vocabulary chunk's
+// (max, argmax) formed as phase_lm forms it. One 64-lane block per chunk.
+__global__ __launch_bounds__(VCHUNK) void k_set_logits(const Args* __restrict__ ap,
+                                                       const float* __restrict__ lg, uint32_t gen) {
+  const Args& a = *ap;
+  const uint32_t c = blockIdx.x, v = c * VCHUNK + threadIdx.x;
+  float bv = -INFINITY;
+  uint32_t bi = NO_INDEX;
+  if (v < a.d.V) {
+    const float y = lg[v];
+    mb_put(a.mb_logit + v, y, gen);
+    if (!isnan(y)) {
+      bv = y;
+      bi = v;
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    const float v2 = __shfl_xor(bv, o);
+    const uint32_t i2 = __shfl_xor(bi, o);
+    if (better(v2, i2, bv, bi)) {
+      bv = v2;
+      bi = i2;
+    }
+  }
+  if (threadIdx.x == 0) {
+    mb_put(a.mb_vmax + c, bv, gen);
+    mb_put(a.mb_varg + c, __uint_as_float(bi), gen);
+  }
+}
+
 // Strip the tags of logits (or any tagged vector) into plain floats.
 __global__ void k_untag(const u64* src, float* dst, uint32_t n) {
   const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -297,6 +331,8 @@ struct defer_gpu_model {
   int device = 0;
   uint32_t G = 0;  // workgroups per phase (= CUs, capped by the smallest phase)
   uint32_t ncu = 0;  // compute units of the device
+  uint32_t gemm_ncu = 0;  // compute units the batched path's GEMM launches are shaped for
+  uint32_t n_caches = 0;  // live caches (their argument blocks copy the layout)
   size_t lds_bytes = 0;
   hipStream_t stream = nullptr;
   float* wbuf = nullptr;
@@ -312,6 +348,7 @@ struct defer_gpu_model {
   double last_ms = 0.0;
   // Batched path (built on first use): weight panels and the workspace.
   uint32_t batch_min = 16;
+  uint32_t samp_next = 1;  // tag of the next batched sampling op's chunk sums (workspace)
   size_t lds_rows = 0;  // LDS of the batched kernels that run one-token functions
   float* panels = nullptr;
   std::vector<const float*> p_qkv, p_o, p_gu, p_d;
@@ -357,6 +394,7 @@ struct defer_gpu_cache {
   float* trace_to = nullptr;  // set during a traced forward: where k_trace writes
   uint32_t pos = 0;        // host mirror of st->pos
   uint32_t tick = 0;
+  uint32_t samp_next = 1;  // tag of the next sampling event's chunk sums (RunDesc)
   bool has_logits = false;
   hipGraphExec_t graph = nullptr;
   Args args;       // host copy
@@ -398,6 +436,80 @@ static int validate(const defer_gpu_config* c) {
   if (c->hidden_size > (uint32_t)NWK * BLOCK)
     return fail(DEFER_GPU_E_INVALID, "hidden_size %u above %u", c->hidden_size, NWK * BLOCK);
   if (c->activation > 1) return fail(DEFER_GPU_E_INVALID, "unsupported activation");
+  return DEFER_GPU_OK;
+}
+
+// The smallest matvec phase: every workgroup must own work in every phase
+// (phases.h), so the persistent grid is at most this many workgroups.
+static uint32_t min_phase_items(const Dims& d) {
+  return std::min({d.qkv_rows / 2, d.h, d.ff, d.nvc});
+}
+
+// Everything that depends on the persistent grid G: the LDS regions (the
+// publish list, the weight staging of the busiest workgroup, the scratch the
+// O phase and lm_head size per workgroup), the kernels' LDS attribute and the
+// co-residency check. Results never depend on G (an item is computed the same
+// way whichever workgroup owns it); only the layout does.
+static int apply_layout(defer_gpu_model* m, uint32_t G) {
+  Dims& d = m->d;
+  d.lds_vec = (std::max({d.h, d.q, d.ff}) + 3) & ~3u;
+  d.lds_vec2 = (2 * d.h + 3) & ~3u;
+  const uint32_t hs = d.hd + 2;
+  const uint32_t rmax = (d.h + G - 1) / G;
+  const uint32_t scr_attn = MAX_GROUP * d.hd + 2 * d.hd + 2 * MAX_GROUP +
+                            MAX_GROUP * attn_chunk(d.cap - 1) + NWA * 256 * d.group;
+  const uint32_t scr_o = INLINE_COMB_MAX + rmax;
+  const uint32_t scr_comb = MAX_ACHUNKS * hs;
+  const uint32_t scr_samp = 3 * d.nvc + VCHUNK + NWAVES + 2 + NWA * VCHUNK;
+  const uint32_t scr_lm = ((d.nvc + G - 1) / G) * VCHUNK;
+  d.lds_scr = (std::max({scr_attn, scr_o, scr_comb, scr_samp, scr_lm, 2 * NWAVES}) + 3) & ~3u;
+  // Publish list: one entry per matvec result of a phase (four per QKV item).
+  {
+    const uint32_t per_wg[4] = {4 * ((d.qkv_rows / 2 + G - 1) / G), (d.h + G - 1) / G,
+                                (d.ff + G - 1) / G, (d.h + G - 1) / G};
+    d.lds_pub = std::max({per_wg[0], per_wg[1], per_wg[2], per_wg[3]});
+  }
+  // Weight staging for the persistent kernel: each kind's rows of one layer
+  // for the workgroup with the most items, if that fits the CU's LDS.
+  {
+    const uint32_t n_items[4] = {d.qkv_rows / 2, d.h, d.ff, d.h};
+    const uint32_t rows[4] = {2, 1, 2, 1};
+    const uint32_t K[4] = {d.h, d.q, d.h, d.ff};
+    uint32_t stg = 0;
+    for (int k = 0; k < 4; ++k) {
+      d.stg_off[k] = stg;
+      stg += (n_items[k] + G - 1) / G * rows[k] * K[k];
+    }
+    const size_t base = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr) * sizeof(float) +
+                        (size_t)d.lds_pub * 2 * sizeof(u64);
+    d.lds_stg = (base + (size_t)stg * sizeof(float) <= LDS_BYTES_MAX) ? stg : 0;
+  }
+  m->lds_bytes = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr + d.lds_stg) * sizeof(float) +
+                 (size_t)d.lds_pub * 2 * sizeof(u64);
+  m->lds_rows = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr) * sizeof(float);
+
+  m->G = G;
+  const void* kernels[] = {m->persistent, (const void*)k_phase, (const void*)k_samp_a,
+                           (const void*)k_op};
+  for (const void* kf : kernels) {
+    const hipError_t e =
+        hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)m->lds_bytes);
+    if (e != hipSuccess)
+      return fail(DEFER_GPU_E_HIP, "LDS attribute (%zu bytes): %s", m->lds_bytes,
+                  hipGetErrorString(e));
+  }
+  for (const void* kf : {(const void*)k_b_attn, (const void*)k_b_sample}) {
+    const hipError_t e =
+        hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)m->lds_rows);
+    if (e != hipSuccess)
+      return fail(DEFER_GPU_E_HIP, "LDS attribute (%zu bytes): %s", m->lds_rows,
+                  hipGetErrorString(e));
+  }
+  int occ = 0;
+  const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, m->persistent, BLOCK,
+                                                                     m->lds_bytes);
+  if (e != hipSuccess || occ < 1)
+    return fail(DEFER_GPU_E_HIP, "persistent kernel does not fit a CU (occupancy %d)", occ);
   return DEFER_GPU_OK;
 }
 
@@ -450,45 +562,9 @@ extern "C" int defer_gpu_model_create(const defer_gpu_config* cfg, const float* 
     return cleanup(fail(DEFER_GPU_E_HIP, "hipGetDeviceProperties: %s", hipGetErrorString(e)));
   // Every workgroup must own work in every matvec phase (see phases.h): cap G
   // by the smallest phase.
-  const uint32_t min_items = std::min({d.qkv_rows / 2, d.h, d.ff, d.nvc});
-  m->G = std::min<uint32_t>((uint32_t)prop.multiProcessorCount, min_items);
+  const uint32_t min_items = min_phase_items(d);
   m->ncu = (uint32_t)prop.multiProcessorCount;
-
-  d.lds_vec = (std::max({d.h, d.q, d.ff}) + 3) & ~3u;
-  d.lds_vec2 = (2 * d.h + 3) & ~3u;
-  const uint32_t hs = d.hd + 2;
-  const uint32_t rmax = (d.h + m->G - 1) / m->G;
-  const uint32_t scr_attn = MAX_GROUP * d.hd + 2 * d.hd + 2 * MAX_GROUP +
-                            MAX_GROUP * attn_chunk(d.cap - 1) + NWA * 256 * d.group;
-  const uint32_t scr_o = INLINE_COMB_MAX + rmax;
-  const uint32_t scr_comb = MAX_ACHUNKS * hs;
-  const uint32_t scr_samp = 3 * d.nvc + VCHUNK + NWAVES + 2 + NWA * VCHUNK;
-  const uint32_t scr_lm = ((d.nvc + m->G - 1) / m->G) * VCHUNK;
-  d.lds_scr = (std::max({scr_attn, scr_o, scr_comb, scr_samp, scr_lm, 2 * NWAVES}) + 3) & ~3u;
-  // Publish list: one entry per matvec result of a phase (four per QKV item).
-  {
-    const uint32_t per_wg[4] = {4 * ((d.qkv_rows / 2 + m->G - 1) / m->G), (d.h + m->G - 1) / m->G,
-                                (d.ff + m->G - 1) / m->G, (d.h + m->G - 1) / m->G};
-    d.lds_pub = std::max({per_wg[0], per_wg[1], per_wg[2], per_wg[3]});
-  }
-  // Weight staging for the persistent kernel: each kind's rows of one layer
-  // for the workgroup with the most items, if that fits the CU's LDS.
-  {
-    const uint32_t n_items[4] = {d.qkv_rows / 2, d.h, d.ff, d.h};
-    const uint32_t rows[4] = {2, 1, 2, 1};
-    const uint32_t K[4] = {d.h, d.q, d.h, d.ff};
-    uint32_t stg = 0;
-    for (int k = 0; k < 4; ++k) {
-      d.stg_off[k] = stg;
-      stg += (n_items[k] + m->G - 1) / m->G * rows[k] * K[k];
-    }
-    const size_t base = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr) * sizeof(float) +
-                        (size_t)d.lds_pub * 2 * sizeof(u64);
-    d.lds_stg = (base + (size_t)stg * sizeof(float) <= LDS_BYTES_MAX) ? stg : 0;
-  }
-  m->lds_bytes = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr + d.lds_stg) * sizeof(float) +
-                 (size_t)d.lds_pub * 2 * sizeof(u64);
-  m->lds_rows = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr) * sizeof(float);
+  m->gemm_ncu = m->ncu;
 
   // Weight layout: one allocation, each tensor 256-byte aligned; q/k/v rows
   // are stored back to back as one [q + 2kv, h] matrix.
@@ -617,14 +693,8 @@ extern "C" int defer_gpu_model_create(const defer_gpu_config* cfg, const float* 
   if (e != hipSuccess) return cleanup(fail(DEFER_GPU_E_HIP, "rope table: %s", hipGetErrorString(e)));
 
   m->persistent = persistent_kernel_for(d);
-  const void* kernels[] = {m->persistent, (const void*)k_phase,
-                           (const void*)k_samp_a, (const void*)k_op};
-  for (const void* kf : kernels) {
-    e = hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)m->lds_bytes);
-    if (e != hipSuccess)
-      return cleanup(fail(DEFER_GPU_E_HIP, "LDS attribute (%zu bytes): %s", m->lds_bytes,
-                          hipGetErrorString(e)));
-  }
+  rc = apply_layout(m, std::min<uint32_t>(m->ncu, min_items));
+  if (rc) return cleanup(rc);
   {
     const void* gk[] = {
         (const void*)k_gemm<1, GO_PLAIN, false>, (const void*)k_gemm<1, GO_RESID, false>,
@@ -661,18 +731,6 @@ extern "C" int defer_gpu_model_create(const defer_gpu_config* cfg, const float* 
                           (int)attn_tile_lds(MAX_GROUP));
   if (e != hipSuccess)
     return cleanup(fail(DEFER_GPU_E_HIP, "LDS attribute (tiled attention): %s", hipGetErrorString(e)));
-  const void* row_kernels[] = {(const void*)k_b_attn,
-                               (const void*)k_b_sample};
-  for (const void* kf : row_kernels) {
-    e = hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)m->lds_rows);
-    if (e != hipSuccess)
-      return cleanup(fail(DEFER_GPU_E_HIP, "LDS attribute (%zu bytes): %s", m->lds_rows,
-                          hipGetErrorString(e)));
-  }
-  int occ = 0;
-  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, m->persistent, BLOCK, m->lds_bytes);
-  if (e != hipSuccess || occ < 1)
-    return cleanup(fail(DEFER_GPU_E_HIP, "persistent kernel does not fit a CU (occupancy %d)", occ));
   if (hipEventCreate(&m->ev0) != hipSuccess || hipEventCreate(&m->ev1) != hipSuccess)
     return cleanup(fail(DEFER_GPU_E_HIP, "event create"));
   *out = m;
@@ -704,11 +762,24 @@ extern "C" int defer_gpu_model_set_exec(defer_gpu_model* m, uint32_t mode) {
 
 extern "C" double defer_gpu_last_device_ms(const defer_gpu_model* m) { return m ? m->last_ms : 0.0; }
 
+extern "C" int defer_gpu_model_set_grid(defer_gpu_model* m, uint32_t workgroups,
+                                        uint32_t gemm_cus) {
+  if (!m) return fail(DEFER_GPU_E_INVALID, "null model");
+  if (m->n_caches) return fail(DEFER_GPU_E_INVALID, "set the grid before creating caches");
+  const uint32_t top = std::min(m->ncu, min_phase_items(m->d));
+  const uint32_t G = workgroups ? std::min(workgroups, top) : top;
+  const int rc = apply_layout(m, G);
+  if (rc) return rc;
+  m->gemm_ncu = gemm_cus ? std::min(gemm_cus, m->ncu) : m->ncu;
+  return DEFER_GPU_OK;
+}
+
 // ------------------------------------------------------------------ caches
 
 static int cache_alloc(const defer_gpu_model* m, uint32_t cap, defer_gpu_cache* c) {
   const Dims& d = m->d;
   c->m = m;
+  ++const_cast<defer_gpu_model*>(m)->n_caches;
   c->cap = cap;
   const size_t kvn = (size_t)d.L * d.nkv * cap * d.kvs;
   HIP_TRY(hipMalloc(&c->kc, kvn * sizeof(float)));
@@ -764,6 +835,7 @@ static int sync_args(defer_gpu_cache* c) {
 
 static void cache_free(defer_gpu_cache* c) {
   if (!c) return;
+  if (c->m) --const_cast<defer_gpu_model*>(c->m)->n_caches;
   if (c->m && c->m->stream) (void)hipStreamSynchronize(c->m->stream);
   if (c->graph) (void)hipGraphExecDestroy(c->graph);
   (void)hipFree(c->kc);
@@ -808,6 +880,7 @@ extern "C" void defer_gpu_cache_destroy(defer_gpu_cache* c) {
 }
 
 extern "C" uint32_t defer_gpu_cache_len(const defer_gpu_cache* c) { return c ? c->pos : 0; }
+extern "C" uint32_t defer_gpu_cache_capacity(const defer_gpu_cache* c) { return c ? c->cap : 0; }
 
 static int push_state(defer_gpu_cache* c) {
   DevState h;
@@ -850,6 +923,7 @@ extern "C" int defer_gpu_cache_clone(const defer_gpu_cache* src, defer_gpu_cache
   }
   c->pos = src->pos;
   c->tick = src->tick;
+  c->samp_next = src->samp_next;
   c->has_logits = src->has_logits;
   *out = c;
   return DEFER_GPU_OK;
@@ -906,11 +980,14 @@ extern "C" int defer_gpu_value_norms(const defer_gpu_cache* cc, uint32_t t0, uin
 // ------------------------------------------------------------------ runs
 
 static int ensure_run_buffers(defer_gpu_cache* c, size_t n_ops, size_t n_stop) {
-  if (n_ops > c->run_cap) {
+  // The capacities are zero while the buffers are being replaced, so a failed
+  // allocation leaves no size that a later call would trust.
+  if (n_ops > c->run_cap || !c->d_tokens || !c->d_words || !c->d_out) {
     (void)hipFree(c->d_tokens);
     (void)hipFree(c->d_words);
     (void)hipFree(c->d_out);
     c->d_tokens = c->d_words = c->d_out = nullptr;
+    c->run_cap = 0;
     const size_t cap = std::max<size_t>(n_ops, 1024);
     HIP_TRY(hipMalloc(&c->d_tokens, cap * sizeof(uint32_t)));
     HIP_TRY(hipMalloc(&c->d_words, cap * sizeof(uint32_t)));
@@ -920,6 +997,7 @@ static int ensure_run_buffers(defer_gpu_cache* c, size_t n_ops, size_t n_stop) {
   if (n_stop > c->stop_cap || !c->d_stop) {
     (void)hipFree(c->d_stop);
     c->d_stop = nullptr;
+    c->stop_cap = 0;
     const size_t cap = std::max<size_t>(n_stop, 16);
     HIP_TRY(hipMalloc(&c->d_stop, cap * sizeof(uint32_t)));
     c->stop_cap = cap;
@@ -1025,6 +1103,20 @@ static int copy_logits(defer_gpu_cache* c, float* out) {
   return DEFER_GPU_OK;
 }
 
+extern "C" int defer_gpu_cache_set_logits(defer_gpu_cache* c, const float* logits) {
+  if (!c || !logits) return fail(DEFER_GPU_E_INVALID, "null argument");
+  if (c->tick == 0)
+    return fail(DEFER_GPU_E_NO_LOGITS, "no forward has run on this cache yet");
+  const Dims& d = c->m->d;
+  const hipStream_t s = c->m->stream;
+  HIP_TRY(hipMemcpyAsync(c->d_logits, logits, (size_t)d.V * sizeof(float), hipMemcpyHostToDevice, s));
+  k_set_logits<<<d.nvc, VCHUNK, 0, s>>>(c->d_args, c->d_logits, gen_lm(d, c->tick - 1));
+  HIP_TRY(hipGetLastError());
+  HIP_TRY(hipStreamSynchronize(s));
+  c->has_logits = true;
+  return DEFER_GPU_OK;
+}
+
 extern "C" int defer_gpu_last_logits(const defer_gpu_cache* cc, float* logits_out) {
   defer_gpu_cache* c = const_cast<defer_gpu_cache*>(cc);
   if (!c || !logits_out) return fail(DEFER_GPU_E_INVALID, "null argument");
@@ -1126,16 +1218,33 @@ extern "C" int defer_gpu_prompt(const defer_gpu_model* m, defer_gpu_cache* c,
   int rc = check_pair(m, c);
   if (rc) return rc;
   if (n_tokens && !tokens) return fail(DEFER_GPU_E_INVALID, "null tokens");
-  if (use_batch(m, n_tokens)) {
-    for (size_t i = 0; i < n_tokens; ++i)
-      if (tokens[i] >= m->d.V) return fail(DEFER_GPU_E_TOKEN, "token id %u out of range", tokens[i]);
-    if ((size_t)c->pos + n_tokens > c->cap)
-      return fail(DEFER_GPU_E_CONTEXT, "context length %u exceeded", m->cfg.max_seq_len);
-    return timed(m, [&] {
-      return feed_batched(const_cast<defer_gpu_model*>(m), c, tokens, n_tokens);
-    });
+  // Session::prompt feeds token by token (engine.rs:62-71): the tokens before
+  // the first one that fails -- out of range (model.rs:417-419), or past the
+  // capacity (model.rs:420-422), checked in that order -- are fed and stay
+  // in the cache, then the error is returned.
+  size_t n_ok = 0;
+  int err = DEFER_GPU_OK;
+  uint32_t bad = 0;
+  for (; n_ok < n_tokens; ++n_ok) {
+    if (tokens[n_ok] >= m->d.V) {
+      err = DEFER_GPU_E_TOKEN;
+      bad = tokens[n_ok];
+      break;
+    }
+    if ((size_t)c->pos + n_ok >= c->cap) {
+      err = DEFER_GPU_E_CONTEXT;
+      break;
+    }
   }
-  return feed_tokens(m, c, tokens, n_tokens, false);
+  if (use_batch(m, n_ok))
+    rc = timed(m, [&] { return feed_batched(const_cast<defer_gpu_model*>(m), c, tokens, n_ok); });
+  else
+    rc = feed_tokens(m, c, tokens, n_ok, false);
+  if (rc) return rc;
+  if (err == DEFER_GPU_E_TOKEN) return fail(err, "token id %u out of range", bad);
+  if (err == DEFER_GPU_E_CONTEXT)
+    return fail(err, "context length %u exceeded", m->cfg.max_seq_len);
+  return DEFER_GPU_OK;
 }
 
 static int check_temperature(float t) {
@@ -1170,6 +1279,8 @@ extern "C" int defer_gpu_generate(const defer_gpu_model* m, defer_gpu_cache* c, 
   r.n_ops = n;
   r.mode = RUN_GENERATE;
   r.sample_from = 0;
+  r.samp_tag0 = c->samp_next;
+  c->samp_next += n;
   r.temperature = temperature;
   r.n_stop = (uint32_t)n_stop;
   r.tokens = c->d_tokens;
@@ -1205,6 +1316,7 @@ extern "C" int defer_gpu_sample(const defer_gpu_model* m, defer_gpu_cache* c, fl
   r.n_ops = 1;
   r.mode = RUN_GENERATE;
   r.sample_from = 0;
+  r.samp_tag0 = c->samp_next++;
   r.temperature = temperature;
   r.tokens = c->d_tokens;
   r.words = c->d_words;
@@ -1268,6 +1380,8 @@ extern "C" int defer_gpu_replay(const defer_gpu_model* m, defer_gpu_cache* c,
   r.n_ops = (uint32_t)n_history;
   r.mode = RUN_REPLAY;
   r.sample_from = (uint32_t)prompt_len;
+  r.samp_tag0 = c->samp_next;
+  c->samp_next += (uint32_t)n_sampled;
   r.temperature = temperature;
   r.tokens = c->d_tokens;
   r.words = c->d_words;
@@ -1362,6 +1476,10 @@ static int ensure_ws(defer_gpu_model* m, uint32_t rows, uint32_t lm) {
   HIP_TRY(hipMalloc(&w.sout, (size_t)L1 * sizeof(uint32_t)));
   HIP_TRY(hipMalloc(&w.st, sizeof(DevState)));
   HIP_TRY(hipMemset(w.st, 0, sizeof(DevState)));
+  // Tags start at 1, so zeroed sums never match a wait; sampled tokens
+  // start in range.
+  HIP_TRY(hipMemset(w.VSUM, 0, (size_t)L1 * d.nvc * sizeof(u64)));
+  HIP_TRY(hipMemset(w.sout, 0, (size_t)L1 * sizeof(uint32_t)));
   w.rows = R;
   w.lm = Lm;
   return DEFER_GPU_OK;
@@ -1642,7 +1760,7 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
     bool planes;
     {
       ProfSpan ps(m, 0, 2.0 * d.qkv_rows * d.h * n);
-      planes = launch_gemm(s, m->ncu, GO_PLAIN, m->p_qkv[l], d.qkv_rows, d.h, w.XP, n, w.Y, ldy,
+      planes = launch_gemm(s, m->gemm_ncu, GO_PLAIN, m->p_qkv[l], d.qkv_rows, d.h, w.XP, n, w.Y, ldy,
                            nullptr, nullptr, nullptr, w.QS, qs_n, nullptr, 0.0f, true);
     }
     k_b_qkv_epi<<<dim3((d.qkv_rows / 2 + 255) / 256, n), 256, 0, s>>>(
@@ -1660,19 +1778,19 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
     bool inv_done;
     {
       ProfSpan ps(m, 0, 2.0 * d.h * d.q * n);
-      inv_done = launch_gemm(s, m->ncu, GO_RESID, m->p_o[l], d.h, d.q, w.XQ, n, w.X, d.h, nullptr,
+      inv_done = launch_gemm(s, m->gemm_ncu, GO_RESID, m->p_o[l], d.h, d.q, w.XQ, n, w.X, d.h, nullptr,
                              nullptr, w.XP, w.QS, qs_n, w.INV, d.eps);
     }
     if (!inv_done) k_b_rms<<<(n + 3) / 4, 256, 0, s>>>(w.X, n, d.h, d.eps, w.INV);
     {
       ProfSpan ps(m, 0, 2.0 * 2 * d.ff * d.h * n);
-      launch_gemm(s, m->ncu, GO_PLAIN, m->p_gu[l], 2 * d.ff, d.h, w.XP, n, w.Y, ldy, nullptr,
+      launch_gemm(s, m->gemm_ncu, GO_PLAIN, m->p_gu[l], 2 * d.ff, d.h, w.XP, n, w.Y, ldy, nullptr,
                   nullptr, nullptr, w.QS, qs_n);
     }
     k_b_act<<<dim3((d.ff + 255) / 256, n), 256, 0, s>>>(w.Y, ldy, w.INV, d.ff, d.act, w.XQ);
     {
       ProfSpan ps(m, 0, 2.0 * d.h * d.ff * n);
-      inv_done = launch_gemm(s, m->ncu, GO_RESID, m->p_d[l], d.h, d.ff, w.XQ, n, w.X, d.h, nullptr,
+      inv_done = launch_gemm(s, m->gemm_ncu, GO_RESID, m->p_d[l], d.h, d.ff, w.XQ, n, w.X, d.h, nullptr,
                              nullptr, w.XP, w.QS, qs_n, w.INV, d.eps);
     }
     if (!inv_done && l + 1 < d.L) k_b_rms<<<(n + 3) / 4, 256, 0, s>>>(w.X, n, d.h, d.eps, w.INV);
@@ -1681,7 +1799,7 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
     k_b_final<<<nl, 64, 0, s>>>(w.X, w.sel, d.h, m->norm, d.eps, w.XQ, w.LINV);
     {
       ProfSpan ps(m, 0, 2.0 * d.V * d.h * nl);
-      launch_gemm(s, m->ncu, GO_TAG, m->p_lm, d.V, d.h, w.XQ, nl, reinterpret_cast<float*>(w.LOGT), d.V,
+      launch_gemm(s, m->gemm_ncu, GO_TAG, m->p_lm, d.V, d.h, w.XQ, nl, reinterpret_cast<float*>(w.LOGT), d.V,
                   w.LINV, w.lgen, nullptr, w.QS, qs_n);
     }
     k_b_chunkmax<<<dim3((d.nvc + 3) / 4, nl), 256, 0, s>>>(d, w.LOGT, w.lgen, w.VMAX, w.VARG, nl);
@@ -1730,7 +1848,9 @@ static int batch_sample(defer_gpu_model* m, defer_gpu_cache* const* ocache, cons
   if (T != 0.0f)
     HIP_TRY(hipMemcpyAsync(w.swords, words, nops * sizeof(uint32_t), hipMemcpyHostToDevice, s));
   k_begin<<<1, 1, 0, s>>>(w.st);
-  k_b_sample<<<nops, BLOCK, m->lds_rows, s>>>(w.largs, w.stick, w.swords, T, w.sout);
+  const uint32_t tag0 = m->samp_next;
+  m->samp_next += nops;
+  k_b_sample<<<nops, BLOCK, m->lds_rows, s>>>(w.largs, w.stick, w.swords, T, tag0, w.sout);
   HIP_TRY(hipGetLastError());
   if (deferred) return DEFER_GPU_OK;
   HIP_TRY(hipMemcpyAsync(out, w.sout, nops * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
@@ -1874,6 +1994,15 @@ static int forward_batch_impl(defer_gpu_model* m, defer_gpu_cache* const* caches
   float ms = 0.0f;
   HIP_TRY(hipEventElapsedTime(&ms, m->ev0, m->ev1));
   m->last_ms = ms;
+  if (deferred) {
+    // A wait that ran out leaves the rows undefined: nothing is committed.
+    DevState h;
+    HIP_TRY(hipMemcpy(&h, m->bw->st, sizeof(h), hipMemcpyDeviceToHost));
+    if (h.abort) {
+      for (uint32_t b = 0; b < n; ++b) caches[b]->has_logits = false;
+      return fail(DEFER_GPU_E_TIMEOUT, "a device-side wait exceeded its bound; cache state is undefined");
+    }
+  }
   if (logits_out) {
     const BatchWs& w = *m->bw;
     for (uint32_t b = 0; b < n; ++b) {
@@ -1893,12 +2022,7 @@ static int forward_batch_impl(defer_gpu_model* m, defer_gpu_cache* const* caches
       cpos.push_back(rows[b].pos + 1);
       ctick.push_back(rows[b].tick + 1);
     }
-  rc = batch_commit_many(m, cc.data(), cli.data(), cpos.data(), ctick.data(), (uint32_t)cc.size());
-  if (rc || !deferred) return rc;
-  DevState h;
-  HIP_TRY(hipMemcpy(&h, m->bw->st, sizeof(h), hipMemcpyDeviceToHost));
-  if (h.abort) return fail(DEFER_GPU_E_TIMEOUT, "a device-side wait exceeded its bound");
-  return DEFER_GPU_OK;
+  return batch_commit_many(m, cc.data(), cli.data(), cpos.data(), ctick.data(), (uint32_t)cc.size());
 }
 
 extern "C" int defer_gpu_forward_batch(const defer_gpu_model* mc, defer_gpu_cache* const* caches,

@@ -94,6 +94,11 @@ struct RunDesc {
   uint32_t n_ops;
   uint32_t mode;
   uint32_t sample_from;
+  // Tag of the first sampling op's chunk sums (mb_vsum); op i uses
+  // samp_tag0 + (i - sample_from). The host hands out tags from a per-cache
+  // counter that starts at 1 and only grows, so no two sampling events of a
+  // cache share one.
+  uint32_t samp_tag0;
   float temperature;
   uint32_t n_stop;
   const uint32_t* tokens;
@@ -138,9 +143,6 @@ __host__ __device__ inline uint32_t gen_of(const Dims& d, uint32_t tick, uint32_
 }
 __host__ __device__ inline uint32_t gen_lm(const Dims& d, uint32_t tick) {
   return tick * phases_per_tick(d) + d.L * PH_PER_LAYER + 1u;
-}
-__host__ __device__ inline uint32_t gen_sums(const Dims& d, uint32_t tick) {
-  return tick * phases_per_tick(d) + d.L * PH_PER_LAYER + 2u;
 }
 
 // The dimensions device code computes with. In a shape-specialised build the

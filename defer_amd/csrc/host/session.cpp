@@ -6,6 +6,8 @@
 #include <math.h>
 #include <string.h>
 
+#include <algorithm>
+#include <exception>
 #include <vector>
 
 #include "common.h"
@@ -73,11 +75,14 @@ extern "C" int defer_host_session_prompt(defer_host_session* s, const uint32_t* 
   if (n == 0) return DEFER_HOST_OK;
   const uint32_t before = defer_gpu_cache_len(s->c);
   const int rc = defer_gpu_prompt(s->m, s->c, tokens, n);
-  // Tokens fed before an error stay in the history, as feed() would leave them.
+  // Tokens fed before an error stay in the history, as feed() leaves them;
+  // prompt_len only moves when every token was fed (engine.rs:62-71 returns
+  // before setting it), so a failed prompt blocks further prompt calls.
   const uint32_t fed = defer_gpu_cache_len(s->c) - before;
   s->history.insert(s->history.end(), tokens, tokens + fed);
+  if (rc) return gpu_fail(rc);
   s->prompt_len = (uint32_t)s->history.size();
-  return rc ? gpu_fail(rc) : DEFER_HOST_OK;
+  return DEFER_HOST_OK;
 }
 
 extern "C" int defer_host_session_generate(defer_host_session* s, uint32_t max_tokens,
@@ -85,7 +90,15 @@ extern "C" int defer_host_session_generate(defer_host_session* s, uint32_t max_t
                                            uint32_t* tokens_out, uint32_t* n_out) {
   if (!s || (n_stop && !stop) || (max_tokens && !tokens_out))
     return fail(DEFER_HOST_E_INVALID, "null argument");
-  const std::vector<uint32_t> words = words_for(s, max_tokens);
+  // At most the cache's free positions can be sampled (one more request
+  // reports the context error), so no more words than that are drawn.
+  const uint32_t room = defer_gpu_cache_capacity(s->c) - defer_gpu_cache_len(s->c);
+  std::vector<uint32_t> words;
+  try {
+    words = words_for(s, std::min<uint32_t>(max_tokens, room));
+  } catch (const std::exception& e) {
+    return fail(DEFER_HOST_E_INVALID, "cannot draw %u rng words: %s", max_tokens, e.what());
+  }
   uint32_t n = 0;
   const int rc = defer_gpu_generate(s->m, s->c, max_tokens, s->temperature,
                                     words.empty() ? nullptr : words.data(), stop, n_stop,
@@ -140,7 +153,14 @@ extern "C" int defer_host_session_checkout(const defer_gpu_model* m, const uint8
   defer_host_session* s = nullptr;
   int rc = defer_host_session_create(m, base_seed, temperature, capacity, &s);
   if (rc) return rc;
-  const std::vector<uint32_t> words = words_for(s, sampled);
+  std::vector<uint32_t> words;
+  try {
+    words = words_for(s, sampled);
+  } catch (const std::exception& e) {
+    defer_host_session_destroy(s);
+    return fail(DEFER_HOST_E_INVALID, "cannot draw %llu rng words: %s", (unsigned long long)sampled,
+                e.what());
+  }
   int64_t first_div = -1;
   uint32_t at_div = 0;
   rc = defer_gpu_replay(m, s->c, history, n_history, prompt_len, temperature,

@@ -66,8 +66,9 @@ __global__ __launch_bounds__(BLOCK) void k_persistent(const Args* __restrict__ a
     uint32_t tok;
     if (i >= r.sample_from) {
       const uint32_t word = r.temperature != 0.0f ? cptr(r.words)[i - r.sample_from] : 0u;
-      if (r.temperature != 0.0f && !sample_stage_a(a, tick, r.temperature, wg, G, s)) break;
-      if (!sample_stage_b(a, tick, r.temperature, word, s, &tok)) break;
+      const uint32_t gsum = r.samp_tag0 + (i - r.sample_from);
+      if (r.temperature != 0.0f && !sample_stage_a(a, tick, gsum, r.temperature, wg, G, s)) break;
+      if (!sample_stage_b(a, tick, gsum, r.temperature, word, s, &tok)) break;
       if (r.mode == RUN_REPLAY) {
         if (tok != cptr(r.tokens)[i]) {
           if (wg == 0 && threadIdx.x == 0) {

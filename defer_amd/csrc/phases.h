@@ -1266,12 +1266,16 @@ __device__ __forceinline__ float exp_term(float logit, float T, float m) {
 }
 
 // Sampler stage A (temperature > 0): the global max m from the chunk maxima,
-// then exp-sums of this workgroup's chunks, published for stage B.
-__device__ __forceinline__ bool sample_stage_a(const Args& a, uint32_t tick, float T, uint32_t wg, uint32_t G,
-                               const Lds& s) {
+// then exp-sums of this workgroup's chunks, published for stage B under the
+// tag gsum. gsum is unique to one sampling event (a per-cache or
+// per-workspace sequence number handed in by the host), so sums left in the
+// mailbox by an earlier sample of the same logits -- at another temperature,
+// say -- never carry the tag stage B waits for.
+__device__ __forceinline__ bool sample_stage_a(const Args& a, uint32_t tick, uint32_t gsum, float T,
+                                               uint32_t wg, uint32_t G, const Lds& s) {
   const Dims d = shape_dims(a.d);
   const uint32_t nvc = d.nvc;
-  const uint32_t gl = gen_lm(d, tick - 1u), gsum = gen_sums(d, tick);
+  const uint32_t gl = gen_lm(d, tick - 1u);
   float* vmx = s.scr;
   float* varg = vmx + nvc;
   float* chunk = varg + nvc;  // [NWA][VCHUNK]
@@ -1325,11 +1329,11 @@ __device__ __forceinline__ float wave_scan(float x) {
 // scanned element by element, p_v = exp(l_v/T - m) * (1/total), returning
 // the first v with p_v > 0 and r < cumulative, else the last v with p_v > 0.
 // A degenerate total (not > 0, or not finite) falls back to argmax.
-__device__ __forceinline__ bool sample_stage_b(const Args& a, uint32_t tick, float T, uint32_t word,
-                               const Lds& s, uint32_t* tok_out) {
+__device__ __forceinline__ bool sample_stage_b(const Args& a, uint32_t tick, uint32_t gsum, float T,
+                                               uint32_t word, const Lds& s, uint32_t* tok_out) {
   const Dims d = shape_dims(a.d);
   const uint32_t nvc = d.nvc;
-  const uint32_t gl = gen_lm(d, tick - 1u), gsum = gen_sums(d, tick);
+  const uint32_t gl = gen_lm(d, tick - 1u);
   float* vmx = s.scr;
   float* varg = vmx + nvc;
   float* vsum = varg + nvc;

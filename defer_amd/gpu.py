@@ -129,6 +129,12 @@ def lib() -> ctypes.CDLL:
     L.defer_gpu_forward_batch.restype = ctypes.c_int
     L.defer_gpu_step_batch.argtypes = [vp, P(vp), u32, f32, vp, vp]
     L.defer_gpu_step_batch.restype = ctypes.c_int
+    L.defer_gpu_cache_set_logits.argtypes = [vp, vp]
+    L.defer_gpu_cache_set_logits.restype = ctypes.c_int
+    L.defer_gpu_model_set_grid.argtypes = [vp, u32, u32]
+    L.defer_gpu_model_set_grid.restype = ctypes.c_int
+    L.defer_gpu_cache_capacity.argtypes = [vp]
+    L.defer_gpu_cache_capacity.restype = u32
     L.defer_gpu_model_set_profiling.argtypes = [vp, u32]
     L.defer_gpu_model_set_profiling.restype = ctypes.c_int
     L.defer_gpu_batch_stats.argtypes = [vp, P(ctypes.c_double), u32]
@@ -259,6 +265,10 @@ class GpuModel:
         _check(lib().defer_gpu_forward_batch(self._h, hs, _ptr(t), len(t), _ptr(out)))
         return out
 
+    def set_grid(self, workgroups: int = 0, gemm_cus: int = 0) -> None:
+        """Launch geometry (0: the device's); before the first cache only."""
+        _check(lib().defer_gpu_model_set_grid(self._h, int(workgroups), int(gemm_cus)))
+
     def set_profiling(self, on: bool) -> None:
         _check(lib().defer_gpu_model_set_profiling(self._h, 1 if on else 0))
 
@@ -308,6 +318,10 @@ class GpuCache:
     def __len__(self) -> int:
         return int(lib().defer_gpu_cache_len(self._h))
 
+    @property
+    def capacity(self) -> int:
+        return int(lib().defer_gpu_cache_capacity(self._h))
+
     def truncate(self, n: int) -> None:
         _check(lib().defer_gpu_cache_truncate(self._h, int(n)))
 
@@ -333,6 +347,13 @@ class GpuCache:
         out = np.empty((c.num_layers, t1 - t0, c.num_heads), dtype=np.float32)
         _check(lib().defer_gpu_value_norms(self._h, int(t0), int(t1), _ptr(out)))
         return out
+
+    def set_logits(self, logits) -> None:
+        """Replace the last logits (the next sample / step samples these)."""
+        a = np.ascontiguousarray(np.asarray(logits, dtype=np.float32))
+        if a.shape != (self.model.vocab_size,):
+            raise ValueError(f"need {self.model.vocab_size} logits")
+        _check(lib().defer_gpu_cache_set_logits(self._h, _ptr(a)))
 
     def last_logits(self) -> np.ndarray:
         out = np.empty(self.model.vocab_size, dtype=np.float32)

@@ -82,6 +82,9 @@ int defer_gpu_model_set_exec(defer_gpu_model* m, uint32_t mode);
 int defer_gpu_cache_create(const defer_gpu_model* m, uint32_t capacity, defer_gpu_cache** out);
 void defer_gpu_cache_destroy(defer_gpu_cache* c);
 uint32_t defer_gpu_cache_len(const defer_gpu_cache* c);          /* KvCache::len   model.rs:202 */
+/* Positions the cache was created for (the reference's bound is the config's
+ * max_seq_len, model.rs:420-422). */
+uint32_t defer_gpu_cache_capacity(const defer_gpu_cache* c);
 int defer_gpu_cache_truncate(defer_gpu_cache* c, uint32_t n);    /* model.rs:211-220 */
 int defer_gpu_cache_clone(const defer_gpu_cache* c, defer_gpu_cache** out); /* derive(Clone) */
 /* The pub `keys` / `values` fields (model.rs:185-188) of one layer, each as a
@@ -107,6 +110,12 @@ int defer_gpu_forward(const defer_gpu_model* m, defer_gpu_cache* c, uint32_t tok
                       float* trace_out);
 /* Copies the logits of the cache's last forward to the host. */
 int defer_gpu_last_logits(const defer_gpu_cache* c, float* logits_out);
+
+/* The Session's logits (engine.rs:32, `logits: Option<Vec<f32>>`) replaced by
+ * the caller's [V] vector, so the next sample / step / generate samples
+ * exactly these values with the device sampler (used to pin the sampler's
+ * edge cases: ties, NaN, -inf, overflow). Needs a forward on the cache first. */
+int defer_gpu_cache_set_logits(defer_gpu_cache* c, const float* logits);
 
 /* sampler::sample_token (sampler.rs:78-109) on the last forward's logits.
  * temperature == 0 is greedy argmax and ignores rng_word; temperature > 0
@@ -166,6 +175,14 @@ int defer_gpu_forward_batch(const defer_gpu_model* m, defer_gpu_cache* const* ca
  * then the n sampled tokens are fed as one batch. tokens_out [n]. */
 int defer_gpu_step_batch(const defer_gpu_model* m, defer_gpu_cache* const* caches, uint32_t n,
                          float temperature, const uint32_t* rng_words, uint32_t* tokens_out);
+
+/* Launch geometry, for tests of the claim that results never depend on it:
+ * the persistent kernel and the per-phase kernels run `workgroups`
+ * workgroups (0: one per compute unit, capped by the smallest phase's item
+ * count), and the batched path shapes its GEMM launches for `gemm_cus`
+ * compute units (0: the device's). Must be called before the model's first
+ * cache is created. Bits are identical for every setting. */
+int defer_gpu_model_set_grid(defer_gpu_model* m, uint32_t workgroups, uint32_t gemm_cus);
 
 /* Instrumentation of the batched path: when on, every batched call times its
  * GEMM and attention launches with HIP events on the library's stream.

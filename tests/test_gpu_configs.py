@@ -1,0 +1,343 @@
+"""GPU parity at every benchmark configuration's full workload.
+
+The oracle's results come from fixtures (tests/golden/make_fixtures.py,
+which ran the CPU oracle on the same synthetic weights, prompts and seeds).
+Bars:
+  * greedy tokens identical to the oracle's (the smallest top-2 logit gap of
+    the run is printed);
+  * tokens sampled at T > 0 identical, except that a first difference is
+    accepted where the oracle's draw r lay within 1e-5 of the chosen token's
+    CDF edge (a rounding-boundary case: the GPU sums the CDF in chunks, the
+    reference sequentially) -- the run is compared up to that step only;
+  * last-position logits within 1e-3 of the oracle's (every 8th logit and
+    the 32 largest; the observed maximum is printed);
+  * among GPU runs (token by token, batched, replays, lockstep sessions,
+    repeat runs) every bit equal.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from defer_amd import gpu as G
+from defer_amd import host as H
+from defer_amd import synthetic
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+LOGIT_TOL = 1e-3
+CDF_EDGE = 1e-5
+STRIDE = 8
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def fixture(name):
+    path = os.path.join(GOLDEN, f"{name}.npz")
+    if not os.path.exists(path):
+        pytest.skip(f"fixture {name}.npz not generated (tests/golden/make_fixtures.py {name})")
+    return dict(np.load(path, allow_pickle=False))
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def logit_err(logits, fx, prefix):
+    """max |logit - oracle| over the fixture's strided and top-32 logits."""
+    d1 = np.max(np.abs(logits[::STRIDE] - fx[f"{prefix}_logits_strided"]))
+    d2 = np.max(np.abs(logits[fx[f"{prefix}_top_idx"]] - fx[f"{prefix}_top_val"]))
+    return float(max(d1, d2))
+
+
+def check_greedy(got, want, gap, what):
+    got = np.asarray(got, dtype=np.uint32)
+    say(f"{what}: {len(got)} greedy tokens, smallest oracle top-2 gap {float(np.min(gap)):.3e}")
+    assert np.array_equal(got, want), f"{what}: first mismatch at step " \
+        f"{int(np.argmax(got != want))} (gap {gap[int(np.argmax(got != want))]:.3e})"
+
+
+def check_sampled(got, want, margin, what):
+    """Identical, or identical up to a first difference at a CDF edge.
+    Returns the number of steps compared."""
+    got = np.asarray(got, dtype=np.uint32)
+    n = min(len(got), len(want))
+    diff = np.nonzero(got[:n] != want[:n])[0]
+    say(f"{what}: {n} sampled tokens, smallest oracle CDF-edge margin {float(np.min(margin[:n])):.3e}")
+    if len(diff) == 0:
+        assert len(got) == len(want)
+        return n
+    i = int(diff[0])
+    say(f"{what}: first difference at step {i}, oracle margin {margin[i]:.3e}")
+    assert margin[i] < CDF_EDGE, f"{what}: step {i} differs and is no CDF-boundary case"
+    return i
+
+
+def model_for(name, layers=None):
+    cfg = dict(synthetic.CONFIGS[name])
+    if layers:
+        cfg["num_layers"] = layers
+    w = synthetic.make_weights(cfg, 0)
+    return cfg, w, G.GpuModel(G.Config.from_dict(cfg), w)
+
+
+# ------------------------------------------------------------------- C1
+
+def test_c1_135m_decode_greedy_and_sampled():
+    """32-token prompt; 128 greedy tokens; 128 at T = 0.7 with seed 42 (a
+    second session), one token at a time; a repeat of the sampled session
+    is bit-identical."""
+    fx = fixture("c1")
+    cfg, w, gm = model_for("smollm2-135m")
+    prompt = [int(x) for x in fx["prompt"]]
+    say("c1: session A, 32 prompt + 128 greedy")
+    a = H.Session(gm, H.seed_from_u64(42), 0.0, capacity=512)
+    a.prompt(prompt)
+    ta = a.generate(128)
+    check_greedy(ta, fx["greedy_tokens"], fx["greedy_gap"], "c1 greedy")
+    d = logit_err(a.cache.last_logits(), fx, "greedy_last")
+    say(f"c1 greedy: max|dlogit| at position 160 = {d:.3e}")
+    assert d <= LOGIT_TOL
+    assert a.rng_word_pos == 0
+    say("c1: session B, 32 prompt + 128 at T=0.7 seed 42")
+    words = H.chacha8_words(H.seed_from_u64(42), 0, 128)
+    assert np.array_equal(np.asarray(words, np.uint32), fx["sampled_words"])
+    runs = []
+    for _ in range(2):
+        b = H.Session(gm, H.seed_from_u64(42), 0.7, capacity=512)
+        b.prompt(prompt)
+        tb = b.generate(128)
+        runs.append((tb, b.cache.last_logits(), b.cache.read(29)))
+        b.close()
+    n = check_sampled(runs[0][0], fx["sampled_tokens"], fx["sampled_margin"], "c1 T=0.7")
+    if n == 128:
+        d = logit_err(runs[0][1], fx, "sampled_last")
+        say(f"c1 T=0.7: max|dlogit| at position 160 = {d:.3e}")
+        assert d <= LOGIT_TOL
+    assert runs[0][0] == runs[1][0]
+    assert np.array_equal(bits(runs[0][1]), bits(runs[1][1]))
+    for x, y in zip(runs[0][2], runs[1][2]):
+        assert np.array_equal(bits(x), bits(y))
+    a.close()
+    gm.close()
+
+
+# ------------------------------------------------------------------- C2
+
+def test_c2_135m_2048_position_replay():
+    """512-token prompt + 1536 tokens at T = 0.7, seed 7, generated on the GPU
+    and logged to a WAL; the checkout rebuilds all 2048 positions token by
+    token and batched, bit for bit; the oracle's own session, fed to the GPU,
+    gives the oracle's argmax at every position."""
+    fx = fixture("c2")
+    cfg, w, gm = model_for("smollm2-135m")
+    prompt = [int(x) for x in fx["prompt"]]
+    seed = H.seed_from_u64(7)
+    say("c2: live session, 512 prompt + 1536 at T=0.7 seed 7")
+    live = H.Session(gm, seed, 0.7, capacity=2048)
+    live.prompt(prompt)
+    toks = live.generate(1536)
+    check_sampled(toks, fx["tokens"], fx["margin"], "c2 T=0.7")
+    import tempfile
+
+    path = os.path.join(tempfile.mkdtemp(prefix="c2-"), "session.wal")
+    sig = bytes(32)
+    wal = H.Wal.create(path, sig, seed, 0.7, 512, 0, prompt)
+    for i, t in enumerate(toks):
+        wal.append(t, i + 1)
+    wal.close()
+    log = H.Wal.read(path)
+    assert log["history"] == live.history and not log["torn_tail"]
+    for batching in (0, 16):
+        say(f"c2: checkout of the WAL, batching {batching}")
+        gm.set_batching(batching)
+        s = H.Session.checkout(gm, log["base_seed"], log["temperature"], log["history"],
+                               log["prompt_len"], log["rng_word_pos"], capacity=2048)
+        assert np.array_equal(bits(s.cache.last_logits()), bits(live.cache.last_logits()))
+        for l in (0, 15, 29):
+            for x, y in zip(s.cache.read(l), live.cache.read(l)):
+                assert np.array_equal(bits(x), bits(y)), (batching, l)
+        s.close()
+    gm.set_batching(16)
+    say("c2: the oracle's 2048-token session fed as one batch, argmax at every position")
+    hist = prompt + [int(x) for x in fx["tokens"]]
+    c = gm.new_cache(2048)
+    lg = gm.forward_batch([c] * 2048, hist, logits=True)
+    am = np.argmax(lg, axis=1).astype(np.uint32)
+    gap = fx["gap"]
+    bad = np.nonzero(am != fx["argmax"])[0]
+    say(f"c2: argmax equal at {2048 - len(bad)} of 2048 positions; smallest oracle gap "
+        f"{float(np.min(gap)):.3e}; last-position max|dlogit| {logit_err(lg[-1], fx, 'last'):.3e}")
+    assert all(gap[i] < 2 * LOGIT_TOL for i in bad), [(int(i), float(gap[i])) for i in bad]
+    assert logit_err(lg[-1], fx, "last") <= LOGIT_TOL
+    c.close()
+    live.close()
+    gm.close()
+
+
+# ------------------------------------------------------------------- C3
+
+def test_c3_360m_4224_positions():
+    """128-token prompt + 4096 tokens at T = 0.8, seed 1: the oracle's session
+    replayed on the GPU token by token (every sampled position re-sampled and
+    compared), batched replay bit-identical, then 16 greedy tokens past
+    position 4224."""
+    fx = fixture("c3")
+    cfg, w, gm = model_for("smollm2-360m")
+    hist = [int(x) for x in fx["prompt"]] + [int(x) for x in fx["tokens"]]
+    words = [int(x) for x in fx["words"]]
+    say("c3: replay of the oracle's 4224 positions, token by token")
+    gm.set_batching(0)
+    a = gm.new_cache(4352)
+    fd, at = gm.replay(a, hist, 128, 0.8, words)
+    if fd >= 0:
+        i = fd - 128
+        say(f"c3: replay diverged at position {fd} (oracle margin {fx['margin'][i]:.3e})")
+        assert fx["margin"][i] < CDF_EDGE
+        return
+    say("c3: the same replay batched")
+    gm.set_batching(16)
+    b = gm.new_cache(4352)
+    fd2, _ = gm.replay(b, hist, 128, 0.8, words)
+    assert fd2 == -1
+    assert np.array_equal(bits(a.last_logits()), bits(b.last_logits()))
+    for l in (0, 31):
+        for x, y in zip(a.read(l), b.read(l)):
+            assert np.array_equal(bits(x), bits(y))
+    d = logit_err(a.last_logits(), fx, "sampled_last")
+    say(f"c3: max|dlogit| at position 4224 = {d:.3e}")
+    assert d <= LOGIT_TOL
+    tail = gm.generate(a, 16, 0.0)
+    check_greedy(tail, fx["tail_tokens"], fx["tail_gap"], "c3 greedy tail")
+    d = logit_err(a.last_logits(), fx, "tail_last")
+    say(f"c3: max|dlogit| at position 4240 = {d:.3e}")
+    assert d <= LOGIT_TOL
+    a.close()
+    b.close()
+    gm.close()
+
+
+# ------------------------------------------------------------------- C4
+
+def test_c4_1b_64_sessions_lockstep():
+    """64 sessions x (256-token prompt + 256 greedy tokens) stepping together
+    on the full 16-layer 1B shape: every session bit-identical to its own
+    batch-1 decode; sessions 0 and 63 equal to the oracle."""
+    fx = fixture("c4")
+    cfg, w, gm = model_for("llama-3.2-1b")
+    V = cfg["vocab_size"]
+    n_sess, n_gen = 64, 256
+    prompts = [synthetic.make_prompt(V, 256, seed=1000 + k) for k in range(n_sess)]
+    say("c4: 64 batched prefills of 256 tokens")
+    A = [gm.new_cache(512) for _ in range(n_sess)]
+    for c, p in zip(A, prompts):
+        gm.prompt(c, p)
+    say("c4: 256 lockstep greedy steps of 64 sessions")
+    steps = np.asarray([gm.step_batch(A, 0.0) for _ in range(n_gen)], dtype=np.uint32)
+    for k in (0, 63):
+        check_greedy(steps[:, k], fx[f"s{k}_tokens"], fx[f"s{k}_gap"], f"c4 session {k}")
+        d = logit_err(A[k].last_logits(), fx, f"s{k}_last")
+        say(f"c4 session {k}: max|dlogit| at position 512 = {d:.3e}")
+        assert d <= LOGIT_TOL
+    say("c4: every session alone (batch-1 decode) against its lockstep run")
+    gm.set_batching(0)
+    for k in range(n_sess):
+        b = gm.new_cache(512)
+        gm.prompt(b, prompts[k])
+        toks = gm.generate(b, n_gen, 0.0)
+        assert np.array_equal(np.asarray(toks, np.uint32), steps[:, k]), k
+        assert np.array_equal(bits(b.last_logits()), bits(A[k].last_logits())), k
+        if k in (0, 31, 63):
+            for l in (0, 15):
+                for x, y in zip(b.read(l), A[k].read(l)):
+                    assert np.array_equal(bits(x), bits(y)), (k, l)
+        b.close()
+    gm.set_batching(16)
+    for c in A:
+        c.close()
+    gm.close()
+
+
+# ------------------------------------------------------------------- C5
+
+def test_c5_8b_all_layers_greedy():
+    """64-token prompt + 512 greedy tokens at batch 1 on the full 32-layer 8B
+    shape (32 GB of weights in HBM)."""
+    fx = fixture("c5")
+    say("c5: 8B-shaped weights (32 GB)")
+    cfg, w, gm = model_for("llama-3-8b")
+    del w
+    prompt = [int(x) for x in fx["prompt"]]
+    a = gm.new_cache(640)
+    gm.prompt(a, prompt)
+    say("c5: 512 greedy tokens")
+    toks = gm.generate(a, 512, 0.0)
+    check_greedy(toks, fx["tokens"], fx["gap"], "c5 greedy")
+    d = logit_err(a.last_logits(), fx, "last")
+    say(f"c5: max|dlogit| at position 576 = {d:.3e}")
+    assert d <= LOGIT_TOL
+    say("c5: prompt token by token equals the batched prompt")
+    gm.set_batching(0)
+    b = gm.new_cache(640)
+    gm.prompt(b, prompt)
+    gm.set_batching(16)
+    assert gm.generate(b, 4, 0.0) == toks[:4]
+    c = gm.new_cache(640)
+    gm.prompt(c, prompt)
+    assert gm.generate(c, 4, 0.0) == toks[:4]
+    assert np.array_equal(bits(b.last_logits()), bits(c.last_logits()))
+    for x in (a, b, c):
+        x.close()
+    gm.close()
+
+
+# ------------------------------------------------------------ launch geometry
+
+@pytest.mark.parametrize("name,grids", [
+    ("tiny", ((0, 0), (3, 128), (2, 48))),
+    ("smollm2-135m", ((0, 0), (64, 128), (37, 48))),
+])
+def test_results_independent_of_grid(name, grids):
+    """Smaller persistent grids (the tiny model's full grid is 4 workgroups,
+    the 135M shape's 256; at 64 and 37 the 135M rows no longer fit the LDS
+    staging and are read from HBM) and GEMMs shaped for 128 and 48 compute
+    units give the bits of the full grid: decode (greedy and T > 0),
+    batched prefill and lockstep sessions."""
+    cfg = dict(synthetic.CONFIGS[name])
+    w = synthetic.make_weights(cfg, 11)
+    V = cfg["vocab_size"]
+    prompt = synthetic.make_prompt(V, 40, seed=4)
+    words = H.chacha8_words(H.seed_from_u64(3), 0, 24)
+    results = []
+    for grid, gemm in grids:
+        say(f"{name}: grid {grid or 'full'}, GEMMs for {gemm or 'all'} CUs")
+        gm = G.GpuModel(G.Config.from_dict(cfg), w)
+        gm.set_grid(grid, gemm)
+        a = gm.new_cache(256)
+        gm.prompt(a, prompt)  # batched
+        ta = gm.generate(a, 12, 0.0) + gm.generate(a, 12, 0.7, words[:12])
+        gm.set_batching(0)
+        b = gm.new_cache(256)
+        gm.prompt(b, prompt[:20])
+        gm.set_batching(16)
+        cs = [gm.new_cache(256) for _ in range(5)]
+        for k, c in enumerate(cs):
+            gm.prompt(c, synthetic.make_prompt(V, 17 + k, seed=50 + k))
+        lock = [gm.step_batch(cs, 0.0) for _ in range(3)]
+        results.append((ta, a.last_logits(), b.last_logits(), lock,
+                        [c.last_logits() for c in cs], a.read(0)))
+        for c in [a, b] + cs:
+            c.close()
+        gm.close()
+    base = results[0]
+    for r in results[1:]:
+        assert r[0] == base[0] and r[3] == base[3]
+        for x, y in zip(r[1:3], base[1:3]):
+            assert np.array_equal(bits(x), bits(y))
+        for x, y in zip(r[4], base[4]):
+            assert np.array_equal(bits(x), bits(y))
+        for x, y in zip(r[5], base[5]):
+            assert np.array_equal(bits(x), bits(y))
