@@ -1298,6 +1298,106 @@ extern "C" int defer_gpu_generate(const defer_gpu_model* m, defer_gpu_cache* c, 
   return DEFER_GPU_OK;
 }
 
+// ------------------------------------------------- allocation-free generate
+//
+// defer_gpu_generate_static: defer_gpu_generate without any allocation, for
+// callers that cannot allocate device memory. The run's staging -- the rng
+// words handed in, the stop list and the tokens handed back, which
+// defer_gpu_generate keeps in buffers the library allocates on demand --
+// lives in `scratch`, a file-scope device array each GPU holds for the life
+// of the process. Every call on a GPU shares that GPU's copy: calls that
+// overlap on one GPU (from several host threads) race.
+constexpr uint32_t STATIC_MAX_TOKENS = 1u << 16;  // tokens per call at most
+constexpr uint32_t STATIC_MAX_STOP = 256;          // stop tokens per call at most
+constexpr size_t STATIC_WORDS = 2 * (size_t)STATIC_MAX_TOKENS + STATIC_MAX_STOP;
+static __device__ __align__(256) uint32_t scratch[STATIC_WORDS];  // 513 KB per GPU
+
+// The array's address on each device. In host code `scratch` names a host
+// stand-in, never the device memory: only these pointers are handed to
+// kernels and copies.
+constexpr int STATIC_MAX_DEVICES = 64;
+static uint32_t* g_scratch[STATIC_MAX_DEVICES];
+
+static int scratch_on(int device, uint32_t** out) {
+  if (device < 0 || device >= STATIC_MAX_DEVICES)
+    return fail(DEFER_GPU_E_INVALID, "device %d beyond the %d the static scratch serves", device,
+                STATIC_MAX_DEVICES);
+  if (!g_scratch[device]) {
+    int cur = 0;
+    HIP_TRY(hipGetDevice(&cur));
+    if (cur != device) HIP_TRY(hipSetDevice(device));
+    uint32_t* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress((void**)&p, HIP_SYMBOL(scratch));
+    if (cur != device) HIP_TRY(hipSetDevice(cur));
+    if (e != hipSuccess || !p)
+      return fail(DEFER_GPU_E_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    g_scratch[device] = p;
+  }
+  *out = g_scratch[device];
+  return DEFER_GPU_OK;
+}
+
+extern "C" int defer_gpu_generate_static(const defer_gpu_model* m, defer_gpu_cache* c,
+                                         uint32_t max_tokens, float temperature,
+                                         const uint32_t* rng_words, const uint32_t* stop,
+                                         size_t n_stop, uint32_t* tokens_out, uint32_t* n_out) {
+  int rc = check_pair(m, c);
+  if (rc) return rc;
+  if (n_out) *n_out = 0;
+  rc = check_temperature(temperature);
+  if (rc) return rc;
+  if (max_tokens > STATIC_MAX_TOKENS)
+    return fail(DEFER_GPU_E_INVALID, "defer_gpu_generate_static: %u tokens exceed the %u a call may take",
+                max_tokens, STATIC_MAX_TOKENS);
+  if (n_stop > STATIC_MAX_STOP)
+    return fail(DEFER_GPU_E_INVALID, "defer_gpu_generate_static: %zu stop tokens exceed the %u a call may take",
+                n_stop, STATIC_MAX_STOP);
+  if (max_tokens == 0) return DEFER_GPU_OK;
+  if (!c->has_logits) return fail(DEFER_GPU_E_NO_LOGITS, "no context: provide a non-empty prompt");
+  if (temperature != 0.0f && !rng_words) return fail(DEFER_GPU_E_INVALID, "null rng words");
+  if (n_stop && !stop) return fail(DEFER_GPU_E_INVALID, "null stop tokens");
+  if (!tokens_out) return fail(DEFER_GPU_E_INVALID, "null tokens_out");
+  const uint32_t room = c->cap - c->pos;
+  const uint32_t n = std::min(max_tokens, room);
+  if (n == 0) return fail(DEFER_GPU_E_CONTEXT, "context length %u exceeded", m->cfg.max_seq_len);
+  uint32_t* base = nullptr;
+  rc = scratch_on(m->device, &base);
+  if (rc) return rc;
+  uint32_t* d_words = base;
+  uint32_t* d_stop = base + STATIC_MAX_TOKENS;
+  uint32_t* d_out = base + STATIC_MAX_TOKENS + STATIC_MAX_STOP;
+  const hipStream_t s = m->stream;
+  // Every word the kernels read is written here first (words, stop list);
+  // the tokens are read back only up to the ops the run completed.
+  if (temperature != 0.0f)
+    HIP_TRY(hipMemcpyAsync(d_words, rng_words, n * sizeof(uint32_t), hipMemcpyHostToDevice, s));
+  if (n_stop)
+    HIP_TRY(hipMemcpyAsync(d_stop, stop, n_stop * sizeof(uint32_t), hipMemcpyHostToDevice, s));
+  RunDesc r;
+  memset(&r, 0, sizeof(r));
+  r.n_ops = n;
+  r.mode = RUN_GENERATE;
+  r.sample_from = 0;
+  r.samp_tag0 = c->samp_next;
+  c->samp_next += n;
+  r.temperature = temperature;
+  r.n_stop = (uint32_t)n_stop;
+  r.tokens = d_words;  // unused by generate ops
+  r.words = d_words;
+  r.stop = d_stop;
+  r.out_tokens = d_out;
+  // A graph would be instantiated (allocated) on first use: in graph mode the
+  // same phase kernels run one by one instead (identical bits).
+  rc = run_ops(c, r, m->exec_mode == DEFER_GPU_EXEC_GRAPH);
+  if (rc) return rc;
+  const DevState h = read_state(c);
+  if (h.n_done) HIP_TRY(hipMemcpy(tokens_out, d_out, h.n_done * sizeof(uint32_t), hipMemcpyDeviceToHost));
+  if (n_out) *n_out = h.n_done;
+  if (n < max_tokens && !h.halt)
+    return fail(DEFER_GPU_E_CONTEXT, "context length %u exceeded", m->cfg.max_seq_len);
+  return DEFER_GPU_OK;
+}
+
 extern "C" int defer_gpu_sample(const defer_gpu_model* m, defer_gpu_cache* c, float temperature,
                                 uint32_t rng_word, uint32_t* token_out) {
   // A sample without the feed: run the sampler kernels alone on the current

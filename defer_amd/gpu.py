@@ -115,6 +115,8 @@ def lib() -> ctypes.CDLL:
     L.defer_gpu_step.restype = ctypes.c_int
     L.defer_gpu_generate.argtypes = [vp, vp, u32, f32, vp, vp, sz, vp, P(u32)]
     L.defer_gpu_generate.restype = ctypes.c_int
+    L.defer_gpu_generate_static.argtypes = [vp, vp, u32, f32, vp, vp, sz, vp, P(u32)]
+    L.defer_gpu_generate_static.restype = ctypes.c_int
     L.defer_gpu_prompt.argtypes = [vp, vp, vp, sz]
     L.defer_gpu_prompt.restype = ctypes.c_int
     L.defer_gpu_replay.argtypes = [vp, vp, vp, sz, sz, f32, vp, P(ctypes.c_int64), P(u32)]
@@ -233,6 +235,21 @@ class GpuModel:
         _check(lib().defer_gpu_generate(self._h, cache._h, int(max_tokens), float(temperature),
                                         _ptr(w), _ptr(s), 0 if s is None else len(s), _ptr(out),
                                         ctypes.byref(n)))
+        return [int(x) for x in out[: n.value]]
+
+    def generate_static(self, cache: "GpuCache", max_tokens: int, temperature: float,
+                        words: Optional[Sequence[int]] = None, stop: Sequence[int] = ()) -> list:
+        """generate() through the allocation-free entry point."""
+        w = _u32(words) if words is not None else None
+        if temperature != 0.0 and (w is None or len(w) < max_tokens):
+            raise ValueError("need one rng word per token when temperature > 0")
+        s = _u32(stop) if len(stop) else None
+        out = np.zeros(max(max_tokens, 1), dtype=np.uint32)
+        n = ctypes.c_uint32()
+        _check(lib().defer_gpu_generate_static(self._h, cache._h, int(max_tokens),
+                                               float(temperature), _ptr(w), _ptr(s),
+                                               0 if s is None else len(s), _ptr(out),
+                                               ctypes.byref(n)))
         return [int(x) for x in out[: n.value]]
 
     def replay(self, cache: "GpuCache", history: Sequence[int], prompt_len: int,

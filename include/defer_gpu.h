@@ -135,6 +135,19 @@ int defer_gpu_generate(const defer_gpu_model* m, defer_gpu_cache* c, uint32_t ma
                        float temperature, const uint32_t* rng_words, const uint32_t* stop,
                        size_t n_stop, uint32_t* tokens_out, uint32_t* n_out);
 
+/* defer_gpu_generate without any allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). The rng words, stop list and tokens of the run are staged in a
+ * static device array of 513 KB per GPU, kept until the process ends, so a
+ * call takes at most 65536 tokens and 256 stop tokens (more is rejected with
+ * DEFER_GPU_E_INVALID before anything runs). Same arguments, results and
+ * errors as defer_gpu_generate, bit for bit. Calls that overlap on one GPU
+ * (from several host threads, on any caches) share that array and race. */
+int defer_gpu_generate_static(const defer_gpu_model* m, defer_gpu_cache* c, uint32_t max_tokens,
+                              float temperature, const uint32_t* rng_words, const uint32_t* stop,
+                              size_t n_stop, uint32_t* tokens_out, uint32_t* n_out);
+
 /* Session::prompt (engine.rs:62-71): forward each token in order. */
 int defer_gpu_prompt(const defer_gpu_model* m, defer_gpu_cache* c, const uint32_t* tokens,
                      size_t n_tokens);
