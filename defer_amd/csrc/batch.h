@@ -635,15 +635,17 @@ __global__ __launch_bounds__(BLOCK) void k_b_attn(const Args* __restrict__ rargs
 //    L + 64 from +0, then the wave tree over the 64 slots -- with 16 lanes
 //    per (query, head), lane s holding slots s + 16v, so a wave takes four
 //    (query, head) rows at once;
-//  * value[d]: 24 position groups (wave w, group pl: positions
-//    4w + pl + 24k, k ascending), each a chain, then per w the tree over its
-//    four groups and the sum w = 0..5 in order, from +0.
+//  * value[d]: 16 position groups (attention wave w, group pl: positions
+//    4w + pl + 16k, k ascending), each a chain, then per w the tree over its
+//    four groups and the sum w = 0..3 in order, from +0.
 // Positions past a query's own (t > pos) carry probability +0 and zero V
 // rows, which leave an accumulator unchanged (a chain started at +0 never
 // holds -0). The scores reuse the LDS of K and Q once every wave is done
 // with them, so with three query heads per kv head two workgroups fit a CU.
 
-constexpr uint32_t AT_HD = 64, AT_CH = 128, AT_VROWS = 192;  // 24 groups x 8 positions
+constexpr uint32_t AT_HD = 64, AT_CH = 128, AT_VROWS = 128;  // 16 groups x 8 positions
+constexpr int AT_VG = 16;  // value position groups (phase_attn: NCW waves x 4)
+static_assert(AT_VG == NCW * 4, "the value groups are phase_attn's");
 constexpr uint32_t AT_KP = 65, AT_VP = 66, AT_QP = 65, AT_SP = 193;  // LDS row pitches (floats)
 
 // Floats of the K + Q region, which the scores then take.
@@ -830,32 +832,32 @@ __global__ __launch_bounds__(256, 2) void k_b_attn_tile(const Dims d, const BRow
   __syncthreads();
   // 4. values: wave w computes dims 16w..16w+15 of every head; the V
   // operands are read once for all heads.
-  float vop[24][2];
+  float vop[AT_VG][2];
 #pragma unroll
-  for (int gi = 0; gi < 24; ++gi)
+  for (int gi = 0; gi < AT_VG; ++gi)
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm) {
-      const uint32_t pos = gi + 24 * (4 * mm + lc);  // group gi = 4*w' + pl
+      const uint32_t pos = gi + AT_VG * (4 * mm + lc);  // group gi = 4*w' + pl
       vop[gi][mm] = pos < AT_CH ? Vs[pos * AT_VP + 16 * wave + lr] : 0.0f;
     }
   for (uint32_t j = 0; j < grp; ++j) {
-    float pop[24][2];
+    float pop[AT_VG][2];
 #pragma unroll
-    for (int gi = 0; gi < 24; ++gi)
+    for (int gi = 0; gi < AT_VG; ++gi)
 #pragma unroll
-      for (int mm = 0; mm < 2; ++mm) pop[gi][mm] = Ss[(j * 16 + lr) * AT_SP + gi + 24 * (4 * mm + lc)];
-    f4v acc[24];
+      for (int mm = 0; mm < 2; ++mm) pop[gi][mm] = Ss[(j * 16 + lr) * AT_SP + gi + AT_VG * (4 * mm + lc)];
+    f4v acc[AT_VG];
 #pragma unroll
-    for (int gi = 0; gi < 24; ++gi) acc[gi] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int gi = 0; gi < AT_VG; ++gi) acc[gi] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
-      for (int gi = 0; gi < 24; ++gi)
+      for (int gi = 0; gi < AT_VG; ++gi)
         acc[gi] = __builtin_amdgcn_mfma_f32_16x16x4f32(pop[gi][mm], vop[gi][mm], acc[gi], 0, 0, 0);
     f4v A = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int w6 = 0; w6 < 6; ++w6) {
-      const f4v W = (acc[4 * w6] + acc[4 * w6 + 1]) + (acc[4 * w6 + 2] + acc[4 * w6 + 3]);
+    for (int w4 = 0; w4 < AT_VG / 4; ++w4) {
+      const f4v W = (acc[4 * w4] + acc[4 * w4 + 1]) + (acc[4 * w4 + 2] + acc[4 * w4 + 3]);
       A = A + W;
     }
     const uint32_t hh = g * grp + j;

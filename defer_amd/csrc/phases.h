@@ -643,6 +643,31 @@ __device__ __forceinline__ void items_dot(const Args& a, uint32_t kind, uint32_t
   }
 }
 
+constexpr uint32_t MAX_GROUP = 4;
+constexpr uint32_t KU = 2;  // score passes whose K rows a lane keeps in flight
+constexpr uint32_t VU = 8;  // V float4 a lane keeps in flight
+
+// Lane geometry of the attention (head_dim = 16 * 2^k, at most 256). The
+// attention math runs on the NCW compute waves (attention wave w = wave -
+// NPOLL) while the pollers wait for q/k/v, so the compute waves can have the
+// chunk's K/V rows in flight during the poll without delaying it (a wave's
+// loads complete in order). Every lane holds float4 pieces of rows:
+//  score pass: lps = head_dim/16 lanes per position, 4 float4 each; a wave
+//              scores pw = WAVE/lps positions, the block NCW*pw per pass;
+//  value pass: lv = head_dim/4 lanes per position, 1 float4 each; a wave
+//              takes pv = WAVE/lv positions per step.
+struct AttGeo {
+  uint32_t lps, pw, lv, pv;
+};
+__device__ __forceinline__ AttGeo att_geo(uint32_t hd) {
+  AttGeo g;
+  g.lps = hd / 16;
+  g.pw = WAVE / g.lps;
+  g.lv = hd / 4;
+  g.pv = WAVE / g.lv;
+  return g;
+}
+
 // ------------------------------------------------------------------ QKV
 
 // What the QKV epilogue of item k needs from memory: the RoPE rotation
@@ -754,34 +779,14 @@ __device__ __forceinline__ bool phase_qkv(const Args& a, uint32_t l, uint32_t ti
 
 // ------------------------------------------------------------ attention
 
-constexpr uint32_t MAX_GROUP = 4;
-constexpr uint32_t VU = 2;  // V float4 a lane keeps in flight
-
-// Lane geometry of the attention (head_dim = 16 * 2^k, at most 256). Every
-// lane holds float4 pieces of rows:
-//  score pass: lps = head_dim/16 lanes per position, 4 float4 each; a wave
-//              scores pw = WAVE/lps positions, the block NWA*pw per pass;
-//  value pass: lv = head_dim/4 lanes per position, 1 float4 each; a wave
-//              takes pv = WAVE/lv positions per step.
-struct AttGeo {
-  uint32_t lps, pw, lv, pv;
-};
-__device__ __forceinline__ AttGeo att_geo(uint32_t hd) {
-  AttGeo g;
-  g.lps = hd / 16;
-  g.pw = WAVE / g.lps;
-  g.lv = hd / 4;
-  g.pv = WAVE / g.lv;
-  return g;
-}
-
 // Split-context attention for one (kv head, chunk, query head) item
 // (model.rs:471-497): the chunk's softmax partials of query head j,
 // m = max score, l = sum exp(score - m), acc = sum exp(score - m) v.
 //  1. scores of every position of the chunk into LDS;
 //  2. one wave: m, exp in place, l (lane-strided partials, wave tree);
-//  3. exp-weighted V rows, one partial per (wave, position lane group),
-//     summed in that order.
+//  3. exp-weighted V rows: position group (w, pl) chains positions
+//     t0 + pv*w + pl + NCW*pv*k (k ascending); the groups of a wave are
+//     folded by an xor butterfly over pl, then the waves summed in order.
 // Every order above depends on (pos, head_dim) only.
 // GROUPED = false: one query head per item (items (kv head, chunk, query
 // head); the decode spreads them over the most workgroups). GROUPED = true:
@@ -806,14 +811,16 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
   float* vn = kn + hd;                    // [hd]
   float* ml = vn + hd;                    // [2*MAX_GROUP]
   float* sc = ml + 2 * MAX_GROUP;         // [MAX_GROUP][CH]
-  float* wp = sc + MAX_GROUP * CH;        // [NWA][grp][hd]
+  float* wp = sc + MAX_GROUP * CH;        // [NCW][grp][hd]
   const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
   const uint32_t ps = lane / ge.lps, sub = lane % ge.lps;
   const uint32_t pl = lane / ge.lv, dl = lane % ge.lv;
-  const uint32_t sstep = NWA * ge.pw, vstep = NWA * ge.pv;
-  const bool att = wave < NWA;  // loader waves only meet the barriers
-  const uint32_t tw = wave * ge.pw + ps;  // this lane's position offset in a score pass
-  const uint32_t vw = wave * ge.pv + pl;  // ... and in a value step
+  const uint32_t sstep = NCW * ge.pw, vstep = NCW * ge.pv;
+  // pollers and loaders only meet the barriers
+  const bool att = wave >= NPOLL && wave < NPOLL + NCW;
+  const uint32_t aw = att ? wave - NPOLL : 0;  // attention wave
+  const uint32_t tw = aw * ge.pw + ps;  // this lane's position offset in a score pass
+  const uint32_t vw = aw * ge.pv + pl;  // ... and in a value step
   for (uint32_t item = wg; item < n_items; item += G) {
     // item = (g * nch + c) * grp + j0, or g * nch + c when grouped
     const uint32_t gc = GROUPED ? item : item / grp, j0 = GROUPED ? 0 : item - gc * grp;
@@ -822,15 +829,20 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
     const uint32_t t1 = min(t0 + CH, pos + 1);
     const float* kb = a.kc + ((size_t)l * d.nkv + g) * d.cap * d.kvs + sub * 16;
     const float* vb = a.vc + ((size_t)l * d.nkv + g) * d.cap * d.kvs + dl * 4;
-    // The chunk's first K rows (score pass) and V rows (value pass) of the
-    // history are requested before waiting for this token's q/k/v, all in
-    // one straight run (rows past the chunk are clamped to a row of the
-    // cache and never used), so no load waits for another.
-    float4 kr[4], vr[VU];
+    // The chunk's K rows of the first KU score passes and V rows of the
+    // first VU value steps (a whole 128-position chunk at head_dim 64) are
+    // requested before waiting for this token's q/k/v, all in one straight
+    // run (rows past the chunk are clamped to a row of the cache and never
+    // used), so no load of the history sits on the critical path; later
+    // passes and steps keep KU / VU in flight.
+    float4 kr[KU][4], vr[VU];
     if (att) {
-      const float* r = kb + (size_t)min(t0 + tw, d.cap - 1) * d.kvs;
 #pragma unroll
-      for (uint32_t i = 0; i < 4; ++i) kr[i] = ldg4(r + 4 * i);
+      for (uint32_t u = 0; u < KU; ++u) {
+        const float* r = kb + (size_t)min(t0 + tw + u * sstep, d.cap - 1) * d.kvs;
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) kr[u][i] = ldg4(r + 4 * i);
+      }
 #pragma unroll
       for (uint32_t u = 0; u < VU; ++u)
         vr[u] = ldg4(vb + (size_t)min(t0 + vw + u * vstep, d.cap - 1) * d.kvs);
@@ -840,43 +852,47 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
                               gather_vec(a.mb_qkv + d.q + d.kv + g * hd, hd, gen_in, vn), NPOLL,
                               a.st, s.ctl))
       return false;
-    // 1. scores
-    for (uint32_t pb = t0; att && pb < t1; pb += sstep) {
-      const uint32_t ts = pb + tw;
-      const bool live = ts < t1;
-      if (ts == pos) {
+    // 1. scores, KU passes per round (pass u of a round uses kr[u], then
+    // requests the pass KU later into it)
+    for (uint32_t pb0 = t0; att && pb0 < t1; pb0 += KU * sstep) {
 #pragma unroll
-        for (uint32_t i = 0; i < 4; ++i) kr[i] = lds4(kn + sub * 16 + 4 * i);
-      }
-      const bool masked = live && a.mask && ts < pos &&
-                          ((ldg_u32(a.mask + (ts >> 5)) >> (ts & 31)) & 1u);
-      // One head at a time keeps the live registers to this lane's K piece.
-#pragma unroll 1
-      for (uint32_t j = 0; j < NH1; ++j) {
-        float acc = 0.0f;
+      for (uint32_t u = 0; u < KU; ++u) {
+        const uint32_t ts = pb0 + u * sstep + tw;
+        const bool live = ts < t1;
+        if (ts == pos) {
 #pragma unroll
-        for (uint32_t i = 0; i < 4; ++i) {
-          const float4 qq = lds4(qs + j * hd + sub * 16 + 4 * i);
-          acc = fmaf(qq.x, kr[i].x, acc);
-          acc = fmaf(qq.y, kr[i].y, acc);
-          acc = fmaf(qq.z, kr[i].z, acc);
-          acc = fmaf(qq.w, kr[i].w, acc);
+          for (uint32_t i = 0; i < 4; ++i) kr[u][i] = lds4(kn + sub * 16 + 4 * i);
         }
-        const float v = group_sum(acc, ge.lps);
-        if (live && sub == 0) lds_st(sc + j * CH + (ts - t0), masked ? -INFINITY : v * d.scale);
-      }
-      const uint32_t tn = ts + sstep;
-      if (tn < t1 && tn < pos) {
-        const float* r = kb + (size_t)tn * d.kvs;
+        const bool masked = live && a.mask && ts < pos &&
+                            ((ldg_u32(a.mask + (ts >> 5)) >> (ts & 31)) & 1u);
+        // One head at a time keeps the live registers to this lane's K piece.
+#pragma unroll 1
+        for (uint32_t j = 0; j < NH1; ++j) {
+          float acc = 0.0f;
 #pragma unroll
-        for (uint32_t i = 0; i < 4; ++i) kr[i] = ldg4(r + 4 * i);
+          for (uint32_t i = 0; i < 4; ++i) {
+            const float4 qq = lds4(qs + j * hd + sub * 16 + 4 * i);
+            acc = fmaf(qq.x, kr[u][i].x, acc);
+            acc = fmaf(qq.y, kr[u][i].y, acc);
+            acc = fmaf(qq.z, kr[u][i].z, acc);
+            acc = fmaf(qq.w, kr[u][i].w, acc);
+          }
+          const float v = group_sum(acc, ge.lps);
+          if (live && sub == 0) lds_st(sc + j * CH + (ts - t0), masked ? -INFINITY : v * d.scale);
+        }
+        const uint32_t tn = ts + KU * sstep;
+        if (tn < t1 && tn < pos) {
+          const float* r = kb + (size_t)tn * d.kvs;
+#pragma unroll
+          for (uint32_t i = 0; i < 4; ++i) kr[u][i] = ldg4(r + 4 * i);
+        }
       }
     }
     __syncthreads();
-    // 2. softmax statistics, one wave per query head
+    // 2. softmax statistics, one attention wave per query head
     const uint32_t n = t1 - t0;
-    if (wave < NH1) {
-      float* sh = sc + wave * CH;
+    if (att && aw < NH1) {
+      float* sh = sc + aw * CH;
       float m = -INFINITY;
       for (uint32_t i = lane; i < n; i += WAVE) m = fmaxf(m, lds_ld(sh + i));
       m = wave_max(m);
@@ -888,8 +904,8 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
       }
       ls = wave_sum(ls);
       if (lane == 0) {
-        lds_st(ml + 2 * wave, m);
-        lds_st(ml + 2 * wave + 1, ls);
+        lds_st(ml + 2 * aw, m);
+        lds_st(ml + 2 * aw + 1, ls);
       }
     }
     __syncthreads();
@@ -934,7 +950,7 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
 #pragma unroll
     for (uint32_t j = 0; j < MH; ++j)
       if (j < NH1 && att && pl == 0) {
-        float* dst = wp + (wave * NH1 + j) * hd + dl * 4;
+        float* dst = wp + (aw * NH1 + j) * hd + dl * 4;
         lds_st(dst + 0, acc[j].x);
         lds_st(dst + 1, acc[j].y);
         lds_st(dst + 2, acc[j].z);
@@ -943,12 +959,12 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
     __syncthreads();
     for (uint32_t u = threadIdx.x; threadIdx.x < NPOLL * WAVE && u < NH1 * hd; u += NPOLL * WAVE) {
       const uint32_t j = u / hd, dd = u - j * hd;
-      float pw[NWA];
+      float pw[NCW];
 #pragma unroll
-      for (uint32_t w = 0; w < NWA; ++w) pw[w] = lds_ld(wp + (w * NH1 + j) * hd + dd);
+      for (uint32_t w = 0; w < NCW; ++w) pw[w] = lds_ld(wp + (w * NH1 + j) * hd + dd);
       float A = 0.0f;
 #pragma unroll
-      for (uint32_t w = 0; w < NWA; ++w) A += pw[w];
+      for (uint32_t w = 0; w < NCW; ++w) A += pw[w];
       const uint32_t hh = g * grp + j0 + j;
       u64* out = a.mb_part + ((size_t)hh * MAX_ACHUNKS + c) * hs;
       mb_put(out + 2 + dd, A, gen_out);
