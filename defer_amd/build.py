@@ -1,7 +1,11 @@
 """Build recipe for the native libraries (run from any directory).
 
 * libdefer_gpu.so   -- the HIP kernels and the C ABI of include/defer_gpu.h,
-                       compiled by hipcc for gfx950 only.
+                       compiled by hipcc for gfx950 only;
+* libdefer_gpu.a    -- the same objects as a static archive (what a Rust
+                       build.rs links: static=defer_gpu plus the HIP runtime);
+* tests/c_abi/abi_test -- a C program linking the archive (and the oracle, as
+                       its checker) that the GPU tests run.
 * libdefer_host.so  -- the C++ host side (session, WAL, checkpoint, ChaCha8,
                        SHA-256, safetensors) of include/defer_host.h.
 
@@ -42,13 +46,45 @@ def _run(cmd, cwd=ROOT):
         raise RuntimeError(f"build step failed ({r.returncode}): {' '.join(cmd)}")
 
 
+BUILD = os.path.join(ROOT, "_build")
+
+
 def build_gpu() -> str:
+    """Objects compiled once, linked into the shared library and archived
+    into the static one."""
     out = os.path.join(PKG, "libdefer_gpu.so")
-    tmp = out + ".tmp"
+    arc = os.path.join(PKG, "libdefer_gpu.a")
+    os.makedirs(BUILD, exist_ok=True)
     srcs = [os.path.join(CSRC, "defer_gpu.hip")] + sorted(
         os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.startswith("kernels_") and f.endswith(".hip"))
-    _run([HIPCC, *GPU_FLAGS, "-o", tmp, *srcs])
+    flags = [f for f in GPU_FLAGS if f != "-shared"]
+    objs = []
+    for src in srcs:
+        obj = os.path.join(BUILD, os.path.basename(src).replace(".hip", ".o"))
+        _run([HIPCC, *flags, "-c", "-o", obj, src])
+        objs.append(obj)
+    tmp = out + ".tmp"
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs])
     os.replace(tmp, out)
+    if os.path.exists(arc):
+        os.remove(arc)
+    _run(["ar", "rcs", arc, *objs])
+    return out
+
+
+def build_c_abi_test() -> str:
+    """tests/c_abi/abi_test: C, linked against libdefer_gpu.a and the oracle."""
+    d = os.path.join(ROOT, "tests", "c_abi")
+    out = os.path.join(d, "abi_test")
+    os.makedirs(BUILD, exist_ok=True)
+    cflags = ["-O2", "-std=c11", "-ffp-contract=off", "-fno-fast-math", "-Wall"]
+    t_obj = os.path.join(BUILD, "abi_test.o")
+    o_obj = os.path.join(BUILD, "oracle.o")
+    _run(["gcc", *cflags, "-c", "-o", t_obj, os.path.join(d, "abi_test.c")])
+    _run(["gcc", *cflags, "-Wno-unused-parameter", "-c", "-o", o_obj,
+          os.path.join(ROOT, "oracle", "oracle.c")])
+    _run(["g++", "-o", out, t_obj, o_obj, os.path.join(PKG, "libdefer_gpu.a"),
+          "-L/opt/rocm/lib", "-lamdhip64", "-lm", "-Wl,-rpath,/opt/rocm/lib"])
     return out
 
 
@@ -69,9 +105,10 @@ def build_all() -> None:
     build_gpu()
     if os.path.isdir(os.path.join(CSRC, "host")):
         build_host()
+    build_c_abi_test()
 
 
 if __name__ == "__main__":
     which = sys.argv[1:] or ["all"]
     for w in which:
-        {"gpu": build_gpu, "host": build_host, "all": build_all}[w]()
+        {"gpu": build_gpu, "host": build_host, "c_abi": build_c_abi_test, "all": build_all}[w]()

@@ -147,6 +147,7 @@ __global__ __launch_bounds__(BLOCK) void k_op(const Args* __restrict__ ap,
 __global__ void k_commit(const Args* __restrict__ ap, const RunDesc* __restrict__ run) {
   DevState* st = ap->st;
   if (st->halt) return;
+  if (run->ring && run->mode == RUN_GENERATE) ring_commit(run->ring, st->op, st->token);
   st->pos += 1;
   st->tick += 1;
   st->op += 1;
@@ -388,6 +389,9 @@ struct defer_gpu_cache {
   uint32_t* d_out = nullptr;
   size_t run_cap = 0;   // capacity of d_tokens / d_words / d_out
   size_t stop_cap = 0;
+  u64* h_ring = nullptr;  // pinned host words of defer_gpu_generate_cb
+  u64* d_ring = nullptr;  // ... as the device addresses them
+  size_t ring_cap = 0;
   float* d_logits = nullptr;
   float* d_tmp = nullptr;  // kv gather staging
   float* d_trace = nullptr;   // [L][nh][cap] staging of a traced forward
@@ -852,6 +856,7 @@ static void cache_free(defer_gpu_cache* c) {
   (void)hipFree(c->d_tmp);
   (void)hipFree(c->d_trace);
   (void)hipFree(c->d_args);
+  if (c->h_ring) (void)hipHostFree(c->h_ring);
 }
 
 extern "C" int defer_gpu_cache_create(const defer_gpu_model* m, uint32_t capacity,
@@ -1026,8 +1031,9 @@ static int launch_op_kernels(defer_gpu_cache* c, hipStream_t s) {
   return DEFER_GPU_OK;
 }
 
-// Runs n_ops ops described by `r` (host copy, device pointers filled in).
-static int run_ops(defer_gpu_cache* c, RunDesc r, bool force_eager) {
+// Queues n_ops ops described by `r` (host copy, device pointers filled in)
+// on the model's stream; run_finish waits for them.
+static int run_launch(defer_gpu_cache* c, RunDesc r, bool force_eager) {
   defer_gpu_model* m = const_cast<defer_gpu_model*>(c->m);
   const hipStream_t s = m->stream;
   HIP_TRY(hipMemcpyAsync(c->d_run, &r, sizeof(r), hipMemcpyHostToDevice, s));
@@ -1064,7 +1070,12 @@ static int run_ops(defer_gpu_cache* c, RunDesc r, bool force_eager) {
     }
   }
   HIP_TRY(hipEventRecord(m->ev1, s));
-  HIP_TRY(hipStreamSynchronize(s));
+  return DEFER_GPU_OK;
+}
+
+static int run_finish(defer_gpu_cache* c) {
+  defer_gpu_model* m = const_cast<defer_gpu_model*>(c->m);
+  HIP_TRY(hipStreamSynchronize(m->stream));
   float ms = 0.0f;
   HIP_TRY(hipEventElapsedTime(&ms, m->ev0, m->ev1));
   m->last_ms = ms;
@@ -1078,6 +1089,11 @@ static int run_ops(defer_gpu_cache* c, RunDesc r, bool force_eager) {
   c->tick = h.tick;
   if (h.n_done > 0) c->has_logits = true;
   return DEFER_GPU_OK;
+}
+
+static int run_ops(defer_gpu_cache* c, RunDesc r, bool force_eager) {
+  const int rc = run_launch(c, r, force_eager);
+  return rc ? rc : run_finish(c);
 }
 
 static DevState read_state(defer_gpu_cache* c) {
@@ -1292,6 +1308,120 @@ extern "C" int defer_gpu_generate(const defer_gpu_model* m, defer_gpu_cache* c, 
   const DevState h = read_state(c);
   if (h.n_done) HIP_TRY(hipMemcpy(tokens_out, c->d_out, h.n_done * sizeof(uint32_t),
                                   hipMemcpyDeviceToHost));
+  if (n_out) *n_out = h.n_done;
+  if (n < max_tokens && !h.halt)
+    return fail(DEFER_GPU_E_CONTEXT, "context length %u exceeded", m->cfg.max_seq_len);
+  return DEFER_GPU_OK;
+}
+
+// ------------------------------------------------- generate with on_token
+
+static int ensure_ring(defer_gpu_cache* c, size_t n) {
+  if (n <= c->ring_cap && c->h_ring) return DEFER_GPU_OK;
+  if (c->h_ring) (void)hipHostFree(c->h_ring);
+  c->h_ring = c->d_ring = nullptr;
+  c->ring_cap = 0;
+  const size_t cap = std::max<size_t>(n, 1024);
+  // Coherent pinned memory: the device's system-scope stores land where the
+  // host thread polls them while the run goes on.
+  HIP_TRY(hipHostMalloc((void**)&c->h_ring, cap * sizeof(u64), hipHostMallocCoherent));
+  HIP_TRY(hipHostGetDevicePointer((void**)&c->d_ring, c->h_ring, 0));
+  c->ring_cap = cap;
+  return DEFER_GPU_OK;
+}
+
+extern "C" int defer_gpu_generate_cb(const defer_gpu_model* m, defer_gpu_cache* c,
+                                     uint32_t max_tokens, float temperature,
+                                     const uint32_t* rng_words, const uint32_t* stop,
+                                     size_t n_stop, uint32_t* tokens_out, uint32_t* n_out,
+                                     defer_gpu_token_fn on_token, void* user) {
+  int rc = check_pair(m, c);
+  if (rc) return rc;
+  if (n_out) *n_out = 0;
+  rc = check_temperature(temperature);
+  if (rc) return rc;
+  if (max_tokens == 0) return DEFER_GPU_OK;
+  if (!c->has_logits) return fail(DEFER_GPU_E_NO_LOGITS, "no context: provide a non-empty prompt");
+  if (temperature != 0.0f && !rng_words) return fail(DEFER_GPU_E_INVALID, "null rng words");
+  if (n_stop && !stop) return fail(DEFER_GPU_E_INVALID, "null stop tokens");
+  if (!tokens_out) return fail(DEFER_GPU_E_INVALID, "null tokens_out");
+  const uint32_t room = c->cap - c->pos;
+  const uint32_t n = std::min(max_tokens, room);
+  if (n == 0) return fail(DEFER_GPU_E_CONTEXT, "context length %u exceeded", m->cfg.max_seq_len);
+  rc = ensure_run_buffers(c, n, n_stop);
+  if (rc) return rc;
+  rc = ensure_ring(c, n);
+  if (rc) return rc;
+  memset(c->h_ring, 0, n * sizeof(u64));  // no index tag is 0
+  if (temperature != 0.0f)
+    HIP_TRY(hipMemcpy(c->d_words, rng_words, n * sizeof(uint32_t), hipMemcpyHostToDevice));
+  if (n_stop) HIP_TRY(hipMemcpy(c->d_stop, stop, n_stop * sizeof(uint32_t), hipMemcpyHostToDevice));
+  const uint32_t pos0 = c->pos;
+  RunDesc r;
+  memset(&r, 0, sizeof(r));
+  r.n_ops = n;
+  r.mode = RUN_GENERATE;
+  r.sample_from = 0;
+  r.samp_tag0 = c->samp_next;
+  c->samp_next += n;
+  r.temperature = temperature;
+  r.n_stop = (uint32_t)n_stop;
+  r.tokens = c->d_tokens;
+  r.words = c->d_words;
+  r.stop = c->d_stop;
+  r.out_tokens = c->d_out;
+  r.ring = c->d_ring;
+  rc = run_launch(c, r, false);
+  if (rc) return rc;
+  // Hand each committed token to on_token, in order, as it lands; the run
+  // is over once the stream is idle and the slot after the last is unset.
+  const hipStream_t s = m->stream;
+  uint32_t next = 0;
+  int cb_rc = 0;
+  bool idle = false;
+  while (next < n && cb_rc == 0) {
+    const u64 w = __atomic_load_n(c->h_ring + next, __ATOMIC_ACQUIRE);
+    if ((uint32_t)(w >> 32) == next + 1) {
+      tokens_out[next] = (uint32_t)w;
+      if (on_token) cb_rc = on_token(user, next, (uint32_t)w);
+      ++next;
+      continue;
+    }
+    if (idle) break;
+    const hipError_t q = hipStreamQuery(s);
+    if (q == hipSuccess) {
+      idle = true;  // every store of the run is visible now: drain, then stop
+    } else if (q != hipErrorNotReady) {
+      (void)run_finish(c);
+      return fail(DEFER_GPU_E_HIP, "generate: %s", hipGetErrorString(q));
+    }
+  }
+  rc = run_finish(c);
+  if (rc) return rc;
+  const DevState h = read_state(c);
+  if (cb_rc != 0) {
+    // on_token failed at token next - 1: as the reference's generate returns
+    // there, the call ends with the tokens up to it; the ones the device ran
+    // past it are dropped from the cache.
+    const int trc = defer_gpu_cache_truncate(c, pos0 + next);
+    if (n_out) *n_out = next;
+    if (trc) return trc;
+    return fail(DEFER_GPU_E_CALLBACK, "on_token returned %d at token %u", cb_rc, next - 1);
+  }
+  if (next < h.n_done) {
+    // Tokens whose commit the poll did not see (cannot happen once the
+    // stream is idle, kept as a guard): delivered from the run's output.
+    HIP_TRY(hipMemcpy(tokens_out + next, c->d_out + next, (h.n_done - next) * sizeof(uint32_t),
+                      hipMemcpyDeviceToHost));
+    for (; next < h.n_done && cb_rc == 0; ++next)
+      if (on_token) cb_rc = on_token(user, next, tokens_out[next]);
+    if (cb_rc != 0) {
+      const int trc = defer_gpu_cache_truncate(c, pos0 + next);
+      if (n_out) *n_out = next;
+      if (trc) return trc;
+      return fail(DEFER_GPU_E_CALLBACK, "on_token returned %d at token %u", cb_rc, next - 1);
+    }
+  }
   if (n_out) *n_out = h.n_done;
   if (n < max_tokens && !h.halt)
     return fail(DEFER_GPU_E_CONTEXT, "context length %u exceeded", m->cfg.max_seq_len);

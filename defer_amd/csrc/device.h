@@ -105,7 +105,17 @@ struct RunDesc {
   const uint32_t* words;
   const uint32_t* stop;
   uint32_t* out_tokens;
+  // Generate runs only, nullable: pinned host words the host reads while the
+  // run goes on; op i's token is committed as ((i + 1) << 32) | token.
+  u64* ring;
 };
+
+// Commits op i's token to the host ring with one 64-bit system-scope store
+// (its index in the high half, so a reader needs no separate count).
+__device__ __forceinline__ void ring_commit(u64* ring, uint32_t i, uint32_t tok) {
+  __hip_atomic_store(ring + i, ((u64)(i + 1u) << 32) | tok, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_SYSTEM);
+}
 
 struct Args {
   Dims d;

@@ -109,6 +109,47 @@ extern "C" int defer_host_session_generate(defer_host_session* s, uint32_t max_t
   return rc ? gpu_fail(rc) : DEFER_HOST_OK;
 }
 
+namespace {
+// on_token of a logged generate: the WAL record of the token just committed,
+// with the rng position after its sample (main.rs:292-296).
+struct WalLogCtx {
+  defer_host_wal* wal;
+  uint64_t word_pos0;
+  uint32_t wps;
+  int wal_rc;
+};
+int wal_on_token(void* user, uint32_t index, uint32_t token) {
+  WalLogCtx* x = static_cast<WalLogCtx*>(user);
+  x->wal_rc = defer_host_wal_append(x->wal, token, x->word_pos0 + (uint64_t)(index + 1) * x->wps);
+  return x->wal_rc;
+}
+}  // namespace
+
+extern "C" int defer_host_session_generate_logged(defer_host_session* s, uint32_t max_tokens,
+                                                  const uint32_t* stop, size_t n_stop,
+                                                  defer_host_wal* wal, uint32_t* tokens_out,
+                                                  uint32_t* n_out) {
+  if (!s || !wal || (n_stop && !stop) || (max_tokens && !tokens_out))
+    return fail(DEFER_HOST_E_INVALID, "null argument");
+  const uint32_t room = defer_gpu_cache_capacity(s->c) - defer_gpu_cache_len(s->c);
+  std::vector<uint32_t> words;
+  try {
+    words = words_for(s, std::min<uint32_t>(max_tokens, room));
+  } catch (const std::exception& e) {
+    return fail(DEFER_HOST_E_INVALID, "cannot draw %u rng words: %s", max_tokens, e.what());
+  }
+  WalLogCtx ctx{wal, s->word_pos, defer_host_words_per_sample(s->temperature), 0};
+  uint32_t n = 0;
+  const int rc = defer_gpu_generate_cb(s->m, s->c, max_tokens, s->temperature,
+                                       words.empty() ? nullptr : words.data(), stop, n_stop,
+                                       tokens_out, &n, wal_on_token, &ctx);
+  s->history.insert(s->history.end(), tokens_out, tokens_out + n);
+  s->word_pos += (uint64_t)n * ctx.wps;
+  if (n_out) *n_out = n;
+  if (ctx.wal_rc) return ctx.wal_rc;  // the WAL's error, its message kept
+  return rc ? gpu_fail(rc) : DEFER_HOST_OK;
+}
+
 extern "C" int defer_host_session_step(defer_host_session* s, uint32_t* token_out) {
   if (!token_out) return fail(DEFER_HOST_E_INVALID, "null argument");
   uint32_t n = 0;

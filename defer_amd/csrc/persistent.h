@@ -88,6 +88,7 @@ __global__ __launch_bounds__(BLOCK) void k_persistent(const Args* __restrict__ a
     if (!forward_all(a, tok, pos, tick, wg, G, s, sg)) break;
     ++pos;
     ++tick;
+    if (r.ring && r.mode == RUN_GENERATE && wg == 0 && threadIdx.x == 0) ring_commit(r.ring, i, tok);
     if (r.mode == RUN_GENERATE && is_stop(r, tok)) {
       ++i;
       halted = 1;

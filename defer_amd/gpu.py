@@ -28,6 +28,7 @@ E_CONTEXT = 3
 E_HIP = 4
 E_NO_LOGITS = 5
 E_TIMEOUT = 6
+E_CALLBACK = 7
 
 
 class DeferGpuError(RuntimeError):
@@ -67,6 +68,9 @@ class Config(ctypes.Structure):
     def to_dict(self) -> dict:
         return {name: getattr(self, name) for name, _ in self._fields_}
 
+
+# defer_gpu_token_fn: int (*)(void* user, uint32_t index, uint32_t token)
+TOKEN_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32)
 
 _lib = None
 
@@ -115,6 +119,8 @@ def lib() -> ctypes.CDLL:
     L.defer_gpu_step.restype = ctypes.c_int
     L.defer_gpu_generate.argtypes = [vp, vp, u32, f32, vp, vp, sz, vp, P(u32)]
     L.defer_gpu_generate.restype = ctypes.c_int
+    L.defer_gpu_generate_cb.argtypes = [vp, vp, u32, f32, vp, vp, sz, vp, P(u32), TOKEN_FN, vp]
+    L.defer_gpu_generate_cb.restype = ctypes.c_int
     L.defer_gpu_generate_static.argtypes = [vp, vp, u32, f32, vp, vp, sz, vp, P(u32)]
     L.defer_gpu_generate_static.restype = ctypes.c_int
     L.defer_gpu_prompt.argtypes = [vp, vp, vp, sz]
@@ -235,6 +241,25 @@ class GpuModel:
         _check(lib().defer_gpu_generate(self._h, cache._h, int(max_tokens), float(temperature),
                                         _ptr(w), _ptr(s), 0 if s is None else len(s), _ptr(out),
                                         ctypes.byref(n)))
+        return [int(x) for x in out[: n.value]]
+
+    def generate_cb(self, cache: "GpuCache", max_tokens: int, temperature: float,
+                    words: Optional[Sequence[int]] = None, stop: Sequence[int] = (),
+                    on_token=None) -> list:
+        """generate() with on_token(index, token) -> int called per committed
+        token while the device still runs (defer_gpu_generate_cb)."""
+        w = _u32(words) if words is not None else None
+        if temperature != 0.0 and (w is None or len(w) < max_tokens):
+            raise ValueError("need one rng word per token when temperature > 0")
+        s = _u32(stop) if len(stop) else None
+        out = np.zeros(max(max_tokens, 1), dtype=np.uint32)
+        n = ctypes.c_uint32()
+        fn = TOKEN_FN(lambda _u, i, t: int(on_token(int(i), int(t)) or 0)) if on_token else TOKEN_FN(0)
+        rc = lib().defer_gpu_generate_cb(self._h, cache._h, int(max_tokens), float(temperature),
+                                         _ptr(w), _ptr(s), 0 if s is None else len(s), _ptr(out),
+                                         ctypes.byref(n), fn, None)
+        self.last_n = int(n.value)
+        _check(rc)
         return [int(x) for x in out[: n.value]]
 
     def generate_static(self, cache: "GpuCache", max_tokens: int, temperature: float,

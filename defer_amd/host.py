@@ -87,6 +87,7 @@ def lib() -> ctypes.CDLL:
     L.defer_host_session_prompt.argtypes = [vp, vp, sz]
     L.defer_host_session_step.argtypes = [vp, P(u32)]
     L.defer_host_session_generate.argtypes = [vp, u32, vp, sz, vp, P(u32)]
+    L.defer_host_session_generate_logged.argtypes = [vp, u32, vp, sz, vp, vp, P(u32)]
     L.defer_host_session_history.argtypes = [vp, vp]
     L.defer_host_session_history.restype = sz
     L.defer_host_session_prompt_len.argtypes = [vp]
@@ -337,12 +338,21 @@ class Session:
         _check(lib().defer_host_session_step(self._h, ctypes.byref(out)))
         return int(out.value)
 
-    def generate(self, max_tokens: int, stop: Sequence[int] = ()) -> list:
+    def generate(self, max_tokens: int, stop: Sequence[int] = (), wal: Optional["Wal"] = None) -> list:
+        """Session::generate; with `wal`, each token's record is appended and
+        flushed as the device commits it (defer_host_session_generate_logged)."""
         s = np.ascontiguousarray(np.asarray(stop, dtype=np.uint32))
         out = np.zeros(max(max_tokens, 1), dtype=np.uint32)
         n = ctypes.c_uint32()
-        _check(lib().defer_host_session_generate(self._h, int(max_tokens), s.ctypes.data if len(s) else None,
-                                                 len(s), out.ctypes.data, ctypes.byref(n)))
+        sp = s.ctypes.data if len(s) else None
+        if wal is None:
+            rc = lib().defer_host_session_generate(self._h, int(max_tokens), sp, len(s),
+                                                   out.ctypes.data, ctypes.byref(n))
+        else:
+            rc = lib().defer_host_session_generate_logged(self._h, int(max_tokens), sp, len(s),
+                                                          wal._h, out.ctypes.data, ctypes.byref(n))
+        self.last_n = int(n.value)
+        _check(rc)
         return [int(x) for x in out[: n.value]]
 
     @property

@@ -38,6 +38,7 @@ extern "C" {
 #define DEFER_GPU_E_HIP 4        /* HIP runtime error (message in last_error) */
 #define DEFER_GPU_E_NO_LOGITS 5  /* sample with no forward yet (engine.rs:104-108) */
 #define DEFER_GPU_E_TIMEOUT 6    /* a device-side wait exceeded its bound */
+#define DEFER_GPU_E_CALLBACK 7   /* an on_token callback returned non-zero */
 
 /* Model::Config (model.rs:23-39), sizes as the reference names them. */
 typedef struct defer_gpu_config {
@@ -134,6 +135,23 @@ int defer_gpu_step(const defer_gpu_model* m, defer_gpu_cache* c, float temperatu
 int defer_gpu_generate(const defer_gpu_model* m, defer_gpu_cache* c, uint32_t max_tokens,
                        float temperature, const uint32_t* rng_words, const uint32_t* stop,
                        size_t n_stop, uint32_t* tokens_out, uint32_t* n_out);
+
+/* The on_token hook of Session::generate (engine.rs:121-137): called on the
+ * calling thread once per generated token, in order, while the device is
+ * still generating the later ones (each token is handed over as soon as its
+ * forward is committed), e.g. to append and flush a write-ahead log record
+ * (main.rs:292-296, wal.rs:241-250). index counts this call's tokens. A
+ * non-zero return stops the call there, as an error from the reference's
+ * closure does: the call returns DEFER_GPU_E_CALLBACK with *n_out = index + 1
+ * and the cache holding exactly those tokens (tokens the device generated
+ * past it are truncated away; the logits are then not kept). */
+typedef int (*defer_gpu_token_fn)(void* user, uint32_t index, uint32_t token);
+
+/* defer_gpu_generate with on_token (nullable) called per committed token. */
+int defer_gpu_generate_cb(const defer_gpu_model* m, defer_gpu_cache* c, uint32_t max_tokens,
+                          float temperature, const uint32_t* rng_words, const uint32_t* stop,
+                          size_t n_stop, uint32_t* tokens_out, uint32_t* n_out,
+                          defer_gpu_token_fn on_token, void* user);
 
 /* defer_gpu_generate without any allocation. No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code

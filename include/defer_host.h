@@ -157,6 +157,14 @@ int defer_host_session_step(defer_host_session* s, uint32_t* token_out);
 /* Session::generate (engine.rs:121-137), one device launch for the run. */
 int defer_host_session_generate(defer_host_session* s, uint32_t max_tokens, const uint32_t* stop,
                                 size_t n_stop, uint32_t* tokens_out, uint32_t* n_out);
+/* Session::generate with a WAL (main.rs:261-312): each token's record is
+ * appended and flushed (synced when the log is durable) as soon as the device
+ * commits the token, while later tokens are still being generated, with the
+ * rng position after its sample. A failed append stops the call there with
+ * the WAL's error, the session holding the tokens up to that one. */
+int defer_host_session_generate_logged(defer_host_session* s, uint32_t max_tokens,
+                                       const uint32_t* stop, size_t n_stop, defer_host_wal* wal,
+                                       uint32_t* tokens_out, uint32_t* n_out);
 /* Accessors (engine.rs:194-221). */
 size_t defer_host_session_history(const defer_host_session* s, uint32_t* out /* nullable */);
 uint32_t defer_host_session_prompt_len(const defer_host_session* s);

@@ -38,6 +38,19 @@ def test_library_exports_every_declared_symbol(header, prefix, path):
     assert not missing, missing
 
 
+def test_static_archive_defines_every_declared_symbol():
+    """libdefer_gpu.a, the form a Rust build.rs links (static=defer_gpu),
+    defines every defer_gpu_ function of include/defer_gpu.h."""
+    import subprocess
+
+    arc = os.path.join(ROOT, "defer_amd", "libdefer_gpu.a")
+    out = subprocess.run(["nm", "--defined-only", "-g", arc], capture_output=True, text=True,
+                         check=True).stdout
+    defined = set(line.split()[-1] for line in out.splitlines() if " T " in line)
+    missing = [n for n in _declared("defer_gpu.h", "defer_gpu_") if n not in defined]
+    assert not missing, missing
+
+
 # ------------------------------------------------------------------ hashes
 
 def test_crc32_check_value():  # crc32.rs:34
