@@ -227,32 +227,24 @@ bool parse_json(const std::string& s, JVal& out) {
 
 // --------------------------------------------------------- conversions
 
-// IEEE binary16 -> binary32, exact (safetensors.rs:47-72).
+// IEEE 754 binary16 -> binary32, exact (the conversion safetensors.rs:47-72
+// performs). From the definition: a finite half is (-1)^s * M * 2^(E - 25)
+// with the integer significand M = 1024 + m for a biased exponent E >= 1
+// and M = m (E taken as 1) for E = 0; both M and the power of two are exact
+// in binary32, so their product is the value. Exponent 31 is infinity
+// (m = 0) or NaN, whose payload moves to the top of binary32's fraction.
 float f16_to_f32(uint16_t h) {
-  const uint32_t sign = (uint32_t)(h >> 15) << 31;
-  const uint32_t ex = (h >> 10) & 0x1F, mant = h & 0x3FF;
-  uint32_t bits;
-  if (ex == 0) {
-    if (mant == 0) {
-      bits = sign;
-    } else {  // subnormal: normalise
-      int e = 0;
-      uint32_t m = mant;
-      while (!(m & 0x400)) {
-        m <<= 1;
-        --e;
-      }
-      m &= 0x3FF;
-      bits = sign | ((uint32_t)(127 - 14 + e) << 23) | (m << 13);
-    }
-  } else if (ex == 0x1F) {
-    bits = sign | 0x7F800000u | (mant << 13);
-  } else {
-    bits = sign | ((ex + 127 - 15) << 23) | (mant << 13);
+  const bool neg = (h & 0x8000u) != 0;
+  const uint32_t E = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+  if (E == 0x1Fu) {
+    const uint32_t bits = (neg ? 0x80000000u : 0u) | 0x7F800000u | (m << 13);
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
   }
-  float f;
-  memcpy(&f, &bits, 4);
-  return f;
+  const float M = (float)(E ? 1024u + m : m);
+  const float v = ldexpf(M, (int)(E ? E : 1u) - 25);
+  return neg ? -v : v;
 }
 float bf16_to_f32(uint16_t h) {
   const uint32_t bits = (uint32_t)h << 16;

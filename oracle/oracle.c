@@ -487,15 +487,25 @@ void oracle_chacha_block(const uint32_t key[8], uint64_t counter, uint64_t strea
   for (int i = 0; i < 16; ++i) out[i] = x[i] + s[i];
 }
 
+/* PCG32 (O'Neill, PCG-XSH-RR 64/32): the LCG step with the standard
+ * multiplier, and the output permutation of a state. */
+uint64_t oracle_pcg32_step(uint64_t state, uint64_t inc) {
+  return state * 6364136223846793005ull + inc;
+}
+uint32_t oracle_pcg32_output(uint64_t state) {
+  const uint32_t xorshifted = (uint32_t)(((state >> 18) ^ state) >> 27);
+  const uint32_t rot = (uint32_t)(state >> 59);
+  return (xorshifted >> rot) | (xorshifted << ((32 - rot) & 31));
+}
+
 /* rand_core 0.6.4 SeedableRng::seed_from_u64: PCG32 output, 4 bytes at a
- * time, state advanced before each output. */
+ * time, state advanced before each output (the increment is rand_core's
+ * constant). */
 void oracle_seed_from_u64(uint64_t state, uint8_t out[32]) {
-  const uint64_t mul = 6364136223846793005ull, inc = 11634580027462260723ull;
+  const uint64_t inc = 11634580027462260723ull;
   for (int chunk = 0; chunk < 8; ++chunk) {
-    state = state * mul + inc;
-    const uint32_t xorshifted = (uint32_t)(((state >> 18) ^ state) >> 27);
-    const uint32_t rot = (uint32_t)(state >> 59);
-    const uint32_t v = (xorshifted >> rot) | (xorshifted << ((32 - rot) & 31));
+    state = oracle_pcg32_step(state, inc);
+    const uint32_t v = oracle_pcg32_output(state);
     out[chunk * 4 + 0] = (uint8_t)v;
     out[chunk * 4 + 1] = (uint8_t)(v >> 8);
     out[chunk * 4 + 2] = (uint8_t)(v >> 16);

@@ -110,6 +110,8 @@ uint32_t oracle_sample_token(const float* logits, size_t n, float temperature, u
 /* ---- rand_chacha / rand_core (third-party, restated) -------------------- */
 void oracle_chacha_block(const uint32_t key[8], uint64_t counter, uint64_t stream, int rounds,
                          uint32_t out[16]);
+uint64_t oracle_pcg32_step(uint64_t state, uint64_t inc);
+uint32_t oracle_pcg32_output(uint64_t state);
 void oracle_seed_from_u64(uint64_t seed, uint8_t out[32]);
 /* Word `index` of the ChaCha8 stream keyed by `seed` (stream 0). */
 uint32_t oracle_chacha8_word(const uint8_t seed[32], uint64_t index);

@@ -92,6 +92,10 @@ def lib() -> ctypes.CDLL:
     L.oracle_sample_token.restype = u32
     L.oracle_chacha_block.argtypes = [vp, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int, vp]
     L.oracle_seed_from_u64.argtypes = [ctypes.c_uint64, vp]
+    L.oracle_pcg32_step.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
+    L.oracle_pcg32_step.restype = ctypes.c_uint64
+    L.oracle_pcg32_output.argtypes = [ctypes.c_uint64]
+    L.oracle_pcg32_output.restype = ctypes.c_uint32
     L.oracle_chacha8_word.argtypes = [vp, ctypes.c_uint64]
     L.oracle_chacha8_word.restype = u32
     L.oracle_generate.argtypes = [vp, vp, vp, f32, vp, sz, sz, vp, vp]

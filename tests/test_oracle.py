@@ -145,6 +145,26 @@ def test_chacha8_zero_key_keystream():
     assert _le_bytes(O.chacha_block([0] * 8, 0, 0, 8)) == want
 
 
+def test_pcg32_step_and_output_against_published_reference_output():
+    """The PCG32 generator seed_from_u64 is built on (rand_core 0.6.4), pinned
+    by O'Neill's published pcg32 demo output: pcg32_srandom_r(42, 54), i.e.
+    increment 2*54+1 and the state stepped, offset by 42 and stepped again;
+    each pcg32_random_r outputs the permutation of the state before its step
+    (pcg-c-basic, round 1: 0xa15c02b7 0x7b47f409 0xba1d3330 0x83d2f293
+    0xbfa4784b 0xcbed606e). seed_from_u64's own increment constant stays a
+    recalled value (parity unpinned)."""
+    L = O.lib()
+    inc = (54 << 1) | 1
+    state = L.oracle_pcg32_step(0, inc)
+    state = (state + 42) & 0xFFFFFFFFFFFFFFFF
+    state = L.oracle_pcg32_step(state, inc)
+    got = []
+    for _ in range(6):
+        got.append(L.oracle_pcg32_output(state))
+        state = L.oracle_pcg32_step(state, inc)
+    assert got == [0xA15C02B7, 0x7B47F409, 0xBA1D3330, 0x83D2F293, 0xBFA4784B, 0xCBED606E]
+
+
 def test_chacha8_word_stream_indexing():
     seed = bytes(range(32))
     key = list(struct.unpack("<8I", seed))
