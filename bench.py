@@ -47,6 +47,10 @@ TEMPERATURE = 0.7
 SEED = 7
 PEAK_GBS = 8000.0
 PEAK_F32_TFLOPS = 157.3
+EXEC_MODES = {"persistent": 0, "graph": 1, "eager": 2}
+# Per-layer phase kernels in launch order (k_phase's `ph` argument), then
+# the final norm + lm_head + logits phase.
+PHASES = ("qkv", "attn", "comb", "o", "gate_up", "down")
 
 
 def algorithmic_bytes(cfg: dict, weight_bytes: int, first_pos: int, n_pos: int) -> int:
@@ -421,6 +425,114 @@ def replay_workload(args) -> int:
     return 0
 
 
+def _read_csv(d: str, suffix: str) -> list:
+    import csv
+    import glob
+
+    files = sorted(glob.glob(os.path.join(d, "**", "*" + suffix), recursive=True))
+    if not files:
+        raise SystemExit(f"no *{suffix} under {d}")
+    with open(files[0], newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def _pmc_per_dispatch(d: str, counter: str) -> dict:
+    """Dispatch_Id -> the counter's value (KiB), from counter_collection.csv."""
+    out = {}
+    for r in _read_csv(d, "counter_collection.csv"):
+        if r["Counter_Name"] == counter:
+            out[int(r["Dispatch_Id"])] = out.get(int(r["Dispatch_Id"]), 0.0) + float(r["Counter_Value"])
+    return out
+
+
+def phase_table(trace_dir: str, fetch_dir: str | None = None, write_dir: str | None = None,
+                copy_fetch_dir: str | None = None, copy_write_dir: str | None = None,
+                steps: int = 1, warmup: int = 0) -> int:
+    """Per-phase durations, algorithmic HBM bytes and (with PMC dirs) measured
+    bytes of the decode workload run with `--exec eager`, from rocprofv3
+    output. Every op of that run launches k_samp_a, k_op, L x 6 phase
+    kernels, the lm_head phase kernel and k_commit; the run is (warmup +
+    steps) x two sessions x (32 prompt ops at positions 0..31, then 128
+    generate ops at positions 32..159). Only the generate ops are tabled."""
+    from defer_amd import synthetic
+
+    cfg = synthetic.CONFIGS[CFG_NAME]
+    L, h, V = cfg["num_layers"], cfg["hidden_size"], cfg["vocab_size"]
+    ff = cfg["intermediate_size"]
+    q = cfg["num_heads"] * cfg["head_dim"]
+    kv = cfg["num_kv_heads"] * cfg["head_dim"]
+    trace = [r for r in _read_csv(trace_dir, "kernel_trace.csv") if "k_phase" in r["Kernel_Name"]]
+    trace.sort(key=lambda r: int(r["Dispatch_Id"]))
+    per_op = L * len(PHASES) + 1
+    n_ops = (warmup + steps) * 2 * 160
+    if len(trace) != n_ops * per_op:
+        raise SystemExit(f"{len(trace)} k_phase dispatches, expected {n_ops * per_op} "
+                         f"({n_ops} ops x {per_op}) for --steps {steps} --warmup {warmup}")
+    fetch = _pmc_per_dispatch(fetch_dir, "FETCH_SIZE") if fetch_dir else None
+    write = _pmc_per_dispatch(write_dir, "WRITE_SIZE") if write_dir else None
+    f_scale = w_scale = 1.0
+    if copy_fetch_dir and copy_write_dir:
+        cf = [v for v in _pmc_per_dispatch(copy_fetch_dir, "FETCH_SIZE").values()]
+        cw = [v for v in _pmc_per_dispatch(copy_write_dir, "WRITE_SIZE").values()]
+        f_scale, w_scale = 1048576.0 / max(cf), 1048576.0 / max(cw)
+    # algorithmic bytes per dispatch, by phase (weights, the K/V rows read or
+    # written, the vectors are the phase's own input/output)
+    wq = 4 * (q + 2 * kv) * h + 4 * h
+
+    def algo(ph: int, pos: int) -> int:
+        if ph == 0:
+            return wq + 4 * 2 * kv                 # qkv rows + norm; new K/V row written
+        if ph == 1:
+            return 4 * 2 * kv * (pos + 1)          # cached K/V of positions 0..pos, once
+        if ph == 2:
+            return 4 * q                           # the combined attention output
+        if ph == 3:
+            return 4 * h * q
+        if ph == 4:
+            return 4 * 2 * ff * h + 4 * h
+        if ph == 5:
+            return 4 * h * ff
+        return 4 * V * h + 4 * h + 4 * V           # lm_head, final norm, logits
+
+    names = list(PHASES) + ["lm_head"]
+    acc = {k: [0, 0.0, 0, 0.0, 0.0] for k in names}  # n, us, algo B, fetch B, write B
+    for op in range(n_ops):
+        pos = op % 160
+        if pos < 32:
+            continue
+        for j in range(per_op):
+            r = trace[op * per_op + j]
+            ph = j % len(PHASES) if j < L * len(PHASES) else len(PHASES)
+            a = acc[names[ph]]
+            a[0] += 1
+            a[1] += (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+            a[2] += algo(ph, pos)
+            did = int(r["Dispatch_Id"])
+            if fetch is not None:
+                a[3] += fetch.get(did, 0.0) * f_scale * 1024
+            if write is not None:
+                a[4] += write.get(did, 0.0) * w_scale * 1024
+    print(f"| Phase | Dispatches | Avg us | Algorithmic B/dispatch | GB/s | % of {PEAK_GBS:.0f} |"
+          + (" HBM B/dispatch (PMC) | PMC / algorithmic |" if fetch is not None else ""))
+    print("|---|---:|---:|---:|---:|---:|" + ("---:|---:|" if fetch is not None else ""))
+    tot = [0, 0.0, 0, 0.0, 0.0]
+    for k in names:
+        n, us, ab, fb, wb = acc[k]
+        for i, v in enumerate(acc[k]):
+            tot[i] += v
+        gbs = ab / (us * 1e3)
+        line = f"| {k} | {n} | {us / n:.2f} | {ab / n:,.0f} | {gbs:.1f} | {100 * gbs / PEAK_GBS:.2f} |"
+        if fetch is not None:
+            line += f" {(fb + wb) / n:,.0f} | {(fb + wb) / ab:.2f} |"
+        print(line)
+    n_tok = n_ops * 128 // 160
+    print(f"\nGenerate ops: {n_tok}; phase-kernel time per token {tot[1] / n_tok:.1f} us; "
+          f"algorithmic {tot[2] / n_tok / 1e6:.1f} MB per token = "
+          f"{tot[2] / (tot[1] * 1e3):.1f} GB/s over the phase kernels' own time"
+          + (f"; FETCH_SIZE x {f_scale:.5f}, WRITE_SIZE x {w_scale:.5f}" if fetch is not None else ""))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -434,9 +546,18 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-replay", action="store_true",
                     help="skip the replay figures in the decode line's config")
+    ap.add_argument("--exec", choices=list(EXEC_MODES), default="persistent",
+                    help="how a token step runs: one persistent kernel (default), a captured "
+                         "graph of per-phase kernels, or the same kernels launched one by one")
+    ap.add_argument("--phase-table", nargs="+", metavar="DIR",
+                    help="no GPU: print the per-phase table of a rocprofv3 run of "
+                         "`--exec eager` (DIR = its --kernel-trace output; optional FETCH_SIZE, "
+                         "WRITE_SIZE dirs of the same command and of `--copy-probe 1024`)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only copy MIB MiB device-to-device once (calibrates HBM byte counters)")
     args = ap.parse_args()
+    if args.phase_table:
+        return phase_table(*args.phase_table, steps=args.steps, warmup=args.warmup)
     if args.copy_probe:
         import torch
 
@@ -472,6 +593,7 @@ def main() -> int:
     from defer_amd import host as H
 
     model = G.GpuModel(G.Config.from_dict(cfg), weights)
+    model.set_exec(EXEC_MODES[args.exec])
     model.set_batching(0)
     ref = None
     for _ in range(args.warmup):
@@ -485,6 +607,7 @@ def main() -> int:
             raise SystemExit("decode is not repeatable: tokens differ between steps")
         ref = (ta, tb)
     model.set_batching(16)
+    model.set_exec(EXEC_MODES["persistent"])
     n_tok = 256 * args.steps
     wbytes = synthetic.weight_bytes_streamed(cfg)
     algo = 2 * algorithmic_bytes(cfg, wbytes, 32, 128) * args.steps
@@ -510,6 +633,7 @@ def main() -> int:
                         "greedy tokens, session B 128 tokens at T=0.7 (seed 42); one step = both "
                         "sessions (256 tokens at positions 32..160, prompts untimed)",
             "tokens_per_step": 256,
+            "exec": args.exec,
             "us_per_token": round(wall / n_tok * 1e6, 1),
             "device_us_per_token": round(dev / n_tok * 1e3, 1),
             "weight_bytes_per_token": wbytes,
@@ -519,12 +643,15 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "k_persistent (one launch per 128-token generate call)",
+            "kernel": "k_persistent (one launch per 128-token generate call)"
+                      if args.exec == "persistent" else
+                      f"k_phase ({args.exec}: 184 launches per token, the device time of all)",
             "achieved": round(achieved, 2),
             "peak": PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_GBS, 4),
-            "traffic": measured_traffic("k_persistent_decode_135m.md", "traffic_bytes_per_launch"),
+            "traffic": measured_traffic("k_persistent_decode_135m.md", "traffic_bytes_per_launch")
+                       if args.exec == "persistent" else None,
         },
     }
     if cpu is not None:
