@@ -488,6 +488,8 @@ static int apply_layout(defer_gpu_model* m, uint32_t G) {
                         (size_t)d.lds_pub * 2 * sizeof(u64);
     d.lds_stg = (base + (size_t)stg * sizeof(float) <= LDS_BYTES_MAX) ? stg : 0;
   }
+  // A shape-specialised persistent kernel stages its rows only.
+  m->persistent = d.lds_stg ? persistent_kernel_for(d) : (const void*)k_persistent;
   m->lds_bytes = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr + d.lds_stg) * sizeof(float) +
                  (size_t)d.lds_pub * 2 * sizeof(u64);
   m->lds_rows = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr) * sizeof(float);
@@ -696,7 +698,6 @@ extern "C" int defer_gpu_model_create(const defer_gpu_config* cfg, const float* 
     e = hipMemcpy(m->rope, rope.data(), rope.size() * sizeof(float2), hipMemcpyHostToDevice);
   if (e != hipSuccess) return cleanup(fail(DEFER_GPU_E_HIP, "rope table: %s", hipGetErrorString(e)));
 
-  m->persistent = persistent_kernel_for(d);
   rc = apply_layout(m, std::min<uint32_t>(m->ncu, min_items));
   if (rc) return cleanup(rc);
   {

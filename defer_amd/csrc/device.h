@@ -391,7 +391,43 @@ struct SegT {
   float4 v[NF];
 };
 
-// Chunks i0 .. i0+NF-1 of segment s of the global row w.
+// Loads and fmas of whole chunks (every lane's four elements inside the
+// row) carry no per-lane condition, so the compiler counts the loads in
+// flight exactly: a use waits only for the loads its values need. A
+// per-lane condition around a load instead makes every later use wait for
+// all loads in flight, which serialises a double-buffered stream.
+
+// Chunks i0 .. i0+NF-1 of segment s of the global row w, all whole chunks.
+template <int NF>
+__device__ __forceinline__ void seg_load_in(SegT<NF>& r, const float* __restrict__ w, uint32_t s,
+                                            uint32_t i0) {
+  const float* wb = w + 64u * i0 + 4u * s;
+#pragma unroll
+  for (int k = 0; k < NF; ++k) r.v[k] = ldg4(wb + 64 * k);
+}
+
+// The fmas of whole chunks i0 .. i0+n-1 (n <= NF, wave-uniform) held in r,
+// against the LDS vector x, in chunk order. ORDERED keeps each chunk's x
+// read next to its fmas (a compiler barrier between chunks), so no more than
+// one chunk of x is live: for callers at the edge of the register budget.
+template <int NF, bool ORDERED = false>
+__device__ __forceinline__ float seg_fma_in(const SegT<NF>& r, const float* x, uint32_t s,
+                                            uint32_t i0, float acc, int n = NF) {
+  const float* xb = pin(x + 64u * i0 + 4u * s);
+#pragma unroll
+  for (int k = 0; k < NF; ++k)
+    if (k < n) {
+      if (ORDERED) asm volatile("" ::: "memory");
+      const float4 xv = lds4(xb + 64 * k);
+      acc = fmaf(r.v[k].x, xv.x, acc);
+      acc = fmaf(r.v[k].y, xv.y, acc);
+      acc = fmaf(r.v[k].z, xv.z, acc);
+      acc = fmaf(r.v[k].w, xv.w, acc);
+    }
+  return acc;
+}
+
+// Chunks i0 .. i0+NF-1 of segment s of the global row w (those below K).
 template <int NF>
 __device__ __forceinline__ void seg_load(SegT<NF>& r, const float* __restrict__ w, uint32_t K,
                                          uint32_t s, uint32_t i0) {
@@ -421,23 +457,60 @@ __device__ __forceinline__ float seg_fma(const SegT<NF>& r, const float* x, uint
   return acc;
 }
 
+// The chunks of segment s of row w from i on that are not whole blocks of
+// NF: the whole chunks with clamped (always issued) loads, then a partial
+// last chunk with per-lane tests.
+template <int NF>
+__device__ __forceinline__ float seg_rest(const float* __restrict__ w, const float* x, uint32_t K,
+                                          uint32_t s, uint32_t i, float acc) {
+  const uint32_t nwhole = K / 64;
+  if (i < nwhole) {
+    const int n = (int)(nwhole - i);  // < NF whole chunks
+    SegT<NF> r;
+    const float* wb = w + 4u * s;
+#pragma unroll
+    for (int k = 0; k < NF; ++k) r.v[k] = ldg4(wb + 64u * min(i + k, nwhole - 1));
+    acc = seg_fma_in(r, x, s, i, acc, n);
+    i = nwhole;
+  }
+  if (64u * i < K) {
+    SegT<1> r;
+    seg_load(r, w, K, s, i);
+    acc = seg_fma(r, x, K, s, i, acc);
+  }
+  return acc;
+}
+
 // Segment s of the global row w from chunk i0 on, NF chunks at a time with
 // the next NF in flight, added to acc.
 template <int NF>
 __device__ __forceinline__ float seg_stream(const float* __restrict__ w, const float* x, uint32_t K,
                                             uint32_t s, uint32_t i0, float acc) {
-  const uint32_t nch = (K + 63) / 64;
-  if (i0 >= nch) return acc;
-  SegT<NF> a, b;
-  seg_load(a, w, K, s, i0);
-  for (uint32_t i = i0; i < nch; i += 2 * NF) {
-    if (i + NF < nch) seg_load(b, w, K, s, i + NF);
-    acc = seg_fma(a, x, K, s, i, acc);
-    if (i + NF >= nch) break;
-    if (i + 2 * NF < nch) seg_load(a, w, K, s, i + 2 * NF);
-    acc = seg_fma(b, x, K, s, i + NF, acc);
+  const uint32_t nwhole = K / 64;
+  const uint32_t nb = nwhole > i0 ? (nwhole - i0) / NF : 0;  // whole blocks
+  uint32_t i = i0;
+  if (nb > 0) {
+    SegT<NF> a, b;
+    seg_load_in(a, w, s, i);
+    uint32_t blk = 0;
+    for (; blk + 2 < nb; blk += 2) {  // both following blocks exist
+      seg_load_in(b, w, s, i + NF);
+      acc = seg_fma_in(a, x, s, i, acc);
+      seg_load_in(a, w, s, i + 2 * NF);
+      acc = seg_fma_in(b, x, s, i + NF, acc);
+      i += 2 * NF;
+    }
+    if (blk + 2 == nb) {
+      seg_load_in(b, w, s, i + NF);
+      acc = seg_fma_in(a, x, s, i, acc);
+      acc = seg_fma_in(b, x, s, i + NF, acc);
+      i += 2 * NF;
+    } else {
+      acc = seg_fma_in(a, x, s, i, acc);
+      i += NF;
+    }
   }
-  return acc;
+  return seg_rest<NF>(w, x, K, s, i, acc);
 }
 
 // LDS segment reads four chunks at a time: group g holds the chunks at
@@ -496,16 +569,15 @@ __device__ __forceinline__ float seg_lds(const float* w, const float* x, uint32_
 }
 
 // Segment s of the global row w given its first NF chunks already in r;
-// longer rows stream the rest NF chunks at a time through r (consumed).
+// longer rows stream the rest double-buffered (seg_stream).
 template <int NF>
 __device__ __forceinline__ float seg_tail(SegT<NF>& r, const float* __restrict__ w, const float* x,
                                           uint32_t K, uint32_t s) {
-  float acc = seg_fma(r, x, K, s, 0, 0.0f);
-  for (uint32_t i0 = NF; 64u * i0 < K; i0 += NF) {
-    seg_load(r, w, K, s, i0);
-    acc = seg_fma(r, x, K, s, i0, acc);
+  if (64u * NF <= K) {
+    const float acc = seg_fma_in<NF, true>(r, x, s, 0, 0.0f);
+    return seg_stream<NF>(w, x, K, s, NF, acc);
   }
-  return acc;
+  return seg_fma(r, x, K, s, 0, 0.0f);
 }
 
 // The four row values of a quad pass from the lanes' segment sums: y[r] is

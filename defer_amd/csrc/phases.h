@@ -23,6 +23,15 @@
 
 namespace DG_NS {
 
+// A kernel specialised for one model shape runs only where that shape's
+// weight rows are staged in LDS (the host picks the generic kernel
+// otherwise), so its streaming matvec path is compiled out.
+#if defined(DG_SHAPE_SMOLLM2_135M)
+constexpr bool STAGED_ONLY = true;
+#else
+constexpr bool STAGED_ONLY = false;
+#endif
+
 constexpr uint32_t NPOLL = 2;
 constexpr uint32_t NCW = 4;
 constexpr uint32_t NLOAD = NWAVES - NPOLL - NCW;
@@ -623,7 +632,7 @@ __device__ __forceinline__ void items_dot(const Args& a, uint32_t kind, uint32_t
         if (k + NCW * u < cnt) body(k + NCW * u, y[u], 0.0f);
     }
   };
-  if (sg.on) {
+  if (STAGED_ONLY || sg.on) {
     if (!P.any) return;
     emit(cw, pass_pre(P, staged_slot(sg, kind, cw, r, cnt), x, K, s));
     for (uint32_t k = cw + step; k < cnt; k += step) {
@@ -1184,8 +1193,19 @@ __device__ __forceinline__ bool phase_lm(const Args& a, uint32_t tick, uint32_t 
     const uint32_t rr = 4 * q + qrow(lane);
     return rr < nrows && vocab_row(rr) < d.V;
   };
-  auto row_of = [&](uint32_t q) { return a.head + (size_t)vocab_row(4 * q + qrow(lane)) * d.h; };
-  if (lmw && live(wave)) seg_load(A, row_of(wave), d.h, sgm, 0);
+  // Rows past the vocabulary (or past the workgroup's rows) are clamped to
+  // the last row and computed but never used, so every load is issued
+  // unconditionally (seg_load_in) and counted exactly.
+  auto row_of = [&](uint32_t q) {
+    return a.head + (size_t)min(vocab_row(4 * q + qrow(lane)), d.V - 1) * d.h;
+  };
+  auto first = [&](SegT<LMF>& r, uint32_t q) {
+    if (64u * LMF <= d.h)
+      seg_load_in(r, row_of(q), sgm, 0);
+    else
+      seg_load(r, row_of(q), d.h, sgm, 0);
+  };
+  if (lmw) first(A, wave);
   if (!poll_gather<8>(gather_vec(rep_of(a, a.mb_xd, wg), d.h, gen_of(d, tick, d.L - 1, PH_D), s.vec), NPOLL, a.st,
                       s.ctl))
     return false;
@@ -1194,9 +1214,9 @@ __device__ __forceinline__ bool phase_lm(const Args& a, uint32_t tick, uint32_t 
   const float inv = rms_inv(s.vec, d.h, d.eps, lane);
   const uint32_t gen = gen_lm(d, tick);
   for (uint32_t q = wave; lmw && 4 * q < nrows; q += NWA) {
-    if (live(q + NWA)) seg_load(B, row_of(q + NWA), d.h, sgm, 0);
+    first(B, q + NWA);
     const bool lv = live(q);
-    const float acc = lv ? seg_tail(A, row_of(q), xs, d.h, sgm) : 0.0f;
+    const float acc = seg_tail(A, row_of(q), xs, d.h, sgm);
     const float y = inv * group_sum(acc, 16);
     if (lv && sgm == 0) {
       const uint32_t rr = 4 * q + qrow(lane);
