@@ -33,6 +33,11 @@ constexpr bool STAGED_ONLY = false;
 #endif
 
 constexpr uint32_t NPOLL = 2;
+// Words a polling lane owns per round in the per-layer gathers, sized so the
+// specialised shape's vectors (576 and 1536 words) take one round of NWA
+// polling waves; larger shapes take a few rounds.
+constexpr uint32_t PW_H = STAGED_ONLY ? 2 : 4;  // hidden-size gathers
+constexpr uint32_t PW_F = STAGED_ONLY ? 4 : 6;  // intermediate-size gathers
 constexpr uint32_t NCW = 4;
 constexpr uint32_t NLOAD = NWAVES - NPOLL - NCW;
 constexpr uint32_t NWA = NPOLL + NCW;  // waves 0..NWA-1 compute attention, lm_head, sampler
@@ -107,20 +112,25 @@ __device__ __forceinline__ void poll_init(PollState<P>& ps, const Gather& g, uin
   for (uint32_t k = 0; k < P; ++k)
     if (base + tid + k * npl < n) ps.pend |= 1u << k;
 }
+// Every lane loads all P of its slots (a slot past the gather's end re-reads
+// the gather's last word, and is never pending), so the loads carry no
+// per-lane condition and the compiler counts them exactly: a check waits for
+// its own round only, not for a round issued after it.
 template <uint32_t P>
-__device__ __forceinline__ void poll_issue(PollState<P>& ps, const Gather& g, uint32_t base,
-                                           uint32_t tid, uint32_t npl) {
+__device__ __forceinline__ void poll_issue(u64 (&w)[P > 0 ? P : 1], const Gather& g, uint32_t n,
+                                           uint32_t base, uint32_t tid, uint32_t npl) {
+  if (P == 0 || n == 0) return;
 #pragma unroll
-  for (uint32_t k = 0; k < P; ++k)
-    if (ps.pend & (1u << k)) ps.w[k] = mb_load(g.src + gather_off(g, base + tid + k * npl));
+  for (uint32_t k = 0; k < P; ++k) w[k] = mb_load(g.src + gather_off(g, min(base + tid + k * npl, n - 1)));
 }
 template <uint32_t P>
-__device__ __forceinline__ void poll_check(PollState<P>& ps, const Gather& g, uint32_t base,
-                                           uint32_t tid, uint32_t npl) {
+__device__ __forceinline__ void poll_check(PollState<P>& ps, const u64 (&w)[P > 0 ? P : 1],
+                                           const Gather& g, uint32_t base, uint32_t tid,
+                                           uint32_t npl) {
 #pragma unroll
   for (uint32_t k = 0; k < P; ++k)
-    if ((ps.pend & (1u << k)) && (uint32_t)(ps.w[k] >> 32) == g.gen) {
-      lds_st(g.dst + base + tid + k * npl, __uint_as_float((uint32_t)ps.w[k]));
+    if ((ps.pend & (1u << k)) && (uint32_t)(w[k] >> 32) == g.gen) {
+      lds_st(g.dst + base + tid + k * npl, __uint_as_float((uint32_t)w[k]));
       ps.pend &= ~(1u << k);
     }
 }
@@ -141,9 +151,14 @@ struct NoHook {
 
 // Wait until every element of up to three gathers carries its generation and
 // copy the values to LDS. Only the first `npoll_waves` waves read memory; a
-// polling lane keeps P0 + P1 + P2 words in flight per round (sized to the call
-// site), loops until its own words are all current, and the block then meets
-// at a barrier. Returns false (uniformly) if the run was aborted.
+// polling lane owns P0 + P1 + P2 words per round (sized to the call site)
+// and keeps two polls of them in flight: the second is issued a fraction of
+// a memory round trip after the first, and each is re-issued as soon as it
+// has been checked, so a word that becomes current is seen about one round
+// trip later rather than up to two. The lane loops until its own words are
+// all current, and the block then meets at a barrier. Returns false
+// (uniformly) if the run was aborted.
+constexpr uint32_t POLL_STAGGER = 8;  // s_sleep units (64 cycles) between the two polls
 template <uint32_t P0, uint32_t P1 = 0, uint32_t P2 = 0, class H = NoHook>
 __device__ __forceinline__ bool poll_gather(const Gather& g0, const Gather& g1, const Gather& g2,
                                             uint32_t npoll_waves, DevState* st, WaitCtl* ctl,
@@ -160,20 +175,36 @@ __device__ __forceinline__ bool poll_gather(const Gather& g0, const Gather& g1, 
     const uint32_t rounds = max(max(rounds_for(n0, P0 * npl), rounds_for(n1, P1 * npl)),
                                 rounds_for(n2, P2 * npl));
     for (uint32_t r = 0; r < rounds; ++r) {
+      const uint32_t b0 = r * P0 * npl, b1 = r * P1 * npl, b2 = r * P2 * npl;
       PollState<P0> s0;
       PollState<P1> s1;
       PollState<P2> s2;
-      poll_init(s0, g0, n0, r * P0 * npl, tid, npl);
-      poll_init(s1, g1, n1, r * P1 * npl, tid, npl);
-      poll_init(s2, g2, n2, r * P2 * npl, tid, npl);
+      poll_init(s0, g0, n0, b0, tid, npl);
+      poll_init(s1, g1, n1, b1, tid, npl);
+      poll_init(s2, g2, n2, b2, tid, npl);
+      u64 x0[P0 > 0 ? P0 : 1], x1[P1 > 0 ? P1 : 1], x2[P2 > 0 ? P2 : 1];  // the second poll
+      poll_issue<P0>(s0.w, g0, n0, b0, tid, npl);
+      poll_issue<P1>(s1.w, g1, n1, b1, tid, npl);
+      poll_issue<P2>(s2.w, g2, n2, b2, tid, npl);
+      __builtin_amdgcn_s_sleep(POLL_STAGGER);
+      poll_issue<P0>(x0, g0, n0, b0, tid, npl);
+      poll_issue<P1>(x1, g1, n1, b1, tid, npl);
+      poll_issue<P2>(x2, g2, n2, b2, tid, npl);
       for (uint32_t spins = 0;; ++spins) {
-        poll_issue(s0, g0, r * P0 * npl, tid, npl);
-        poll_issue(s1, g1, r * P1 * npl, tid, npl);
-        poll_issue(s2, g2, r * P2 * npl, tid, npl);
-        poll_check(s0, g0, r * P0 * npl, tid, npl);
-        poll_check(s1, g1, r * P1 * npl, tid, npl);
-        poll_check(s2, g2, r * P2 * npl, tid, npl);
+        poll_check(s0, s0.w, g0, b0, tid, npl);
+        poll_check(s1, s1.w, g1, b1, tid, npl);
+        poll_check(s2, s2.w, g2, b2, tid, npl);
         if (__all((s0.pend | s1.pend | s2.pend) == 0)) break;
+        poll_issue<P0>(s0.w, g0, n0, b0, tid, npl);
+        poll_issue<P1>(s1.w, g1, n1, b1, tid, npl);
+        poll_issue<P2>(s2.w, g2, n2, b2, tid, npl);
+        poll_check(s0, x0, g0, b0, tid, npl);
+        poll_check(s1, x1, g1, b1, tid, npl);
+        poll_check(s2, x2, g2, b2, tid, npl);
+        if (__all((s0.pend | s1.pend | s2.pend) == 0)) break;
+        poll_issue<P0>(x0, g0, n0, b0, tid, npl);
+        poll_issue<P1>(x1, g1, n1, b1, tid, npl);
+        poll_issue<P2>(x2, g2, n2, b2, tid, npl);
         if (spins >= SPIN_LIMIT) {
           st_coherent_u32(&st->abort, 1u);
           ctl->abort_seen = 1;
@@ -183,7 +214,6 @@ __device__ __forceinline__ bool poll_gather(const Gather& g0, const Gather& g1, 
           ctl->abort_seen = 1;
           break;
         }
-        __builtin_amdgcn_s_sleep(1);
       }
       if (ctl->abort_seen) break;
     }
@@ -740,7 +770,7 @@ __device__ __forceinline__ bool phase_qkv(const Args& a, uint32_t l, uint32_t ti
       lds_st(s.vec + i, ldg(e + i));
     __syncthreads();
     hk.post_b2();
-  } else if (!poll_gather<8>(gather_vec(rep_of(a, a.mb_xd, wg), d.h, gen_of(d, tick, l - 1, PH_D), s.vec), NPOLL,
+  } else if (!poll_gather<PW_H>(gather_vec(rep_of(a, a.mb_xd, wg), d.h, gen_of(d, tick, l - 1, PH_D), s.vec), NWA,
                              a.st, s.ctl, hk)) {
     return false;
   }
@@ -856,7 +886,7 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
       for (uint32_t u = 0; u < VU; ++u)
         vr[u] = ldg4(vb + (size_t)min(t0 + vw + u * vstep, d.cap - 1) * d.kvs);
     }
-    if (!poll_gather<GROUPED ? 4 : 2, 1, 1>(gather_vec(a.mb_qkv + (size_t)(g * grp + j0) * hd, NH1 * hd, gen_in, qs),
+    if (!poll_gather<GROUPED ? 4 : 1, 1, 1>(gather_vec(a.mb_qkv + (size_t)(g * grp + j0) * hd, NH1 * hd, gen_in, qs),
                               gather_vec(a.mb_qkv + d.q + g * hd, hd, gen_in, kn),
                               gather_vec(a.mb_qkv + d.q + d.kv + g * hd, hd, gen_in, vn), NPOLL,
                               a.st, s.ctl))
@@ -1074,7 +1104,7 @@ __device__ __forceinline__ bool phase_o(const Args& a, uint32_t l, uint32_t tick
     op.layer = l + 1 < d.L ? l + 1 : 0;
     op.wait = sg.wait[IK_O];
   }
-  if (!poll_gather<12, 1>(ga, gr, NPOLL, a.st, s.ctl, mv_hook(sg, op, P, IK_O))) return false;
+  if (!poll_gather<4, 1>(ga, gr, NWA, a.st, s.ctl, mv_hook(sg, op, P, IK_O))) return false;
   if (l == 0 && threadIdx.x < R) lds_st(xres + threadIdx.x, emb);
   if (inl)
     for (uint32_t u = threadIdx.x; u < d.q && threadIdx.x < NWA * WAVE; u += NWA * WAVE) {
@@ -1106,7 +1136,7 @@ __device__ __forceinline__ bool phase_gu(const Args& a, uint32_t l, uint32_t tic
     op.layer = l + 1 < d.L ? l + 1 : 0;
     op.wait = sg.wait[IK_GU];
   }
-  if (!poll_gather<8>(gather_vec(rep_of(a, a.mb_xo, wg), d.h, gen_of(d, tick, l, PH_O), s.vec), NPOLL, a.st, s.ctl,
+  if (!poll_gather<PW_H>(gather_vec(rep_of(a, a.mb_xo, wg), d.h, gen_of(d, tick, l, PH_O), s.vec), NWA, a.st, s.ctl,
                       mv_hook(sg, op, P, IK_GU)))
     return false;
   if (wave >= NPOLL && wave < NWA) {
@@ -1137,7 +1167,7 @@ __device__ __forceinline__ bool phase_d(const Args& a, uint32_t l, uint32_t tick
     op.layer = l + 1 < d.L ? l + 1 : 0;
     op.wait = sg.wait[IK_D];
   }
-  if (!poll_gather<12, 1>(gather_vec(rep_of(a, a.mb_g, wg), d.ff, gen_of(d, tick, l, PH_GU), s.vec), gr, NPOLL,
+  if (!poll_gather<PW_F, 1>(gather_vec(rep_of(a, a.mb_g, wg), d.ff, gen_of(d, tick, l, PH_GU), s.vec), gr, NWA,
                           a.st, s.ctl, mv_hook(sg, op, P, IK_D)))
     return false;
   if (wave >= NPOLL && wave < NWA) {
@@ -1206,7 +1236,7 @@ __device__ __forceinline__ bool phase_lm(const Args& a, uint32_t tick, uint32_t 
       seg_load(r, row_of(q), d.h, sgm, 0);
   };
   if (lmw) first(A, wave);
-  if (!poll_gather<8>(gather_vec(rep_of(a, a.mb_xd, wg), d.h, gen_of(d, tick, d.L - 1, PH_D), s.vec), NPOLL, a.st,
+  if (!poll_gather<5>(gather_vec(rep_of(a, a.mb_xd, wg), d.h, gen_of(d, tick, d.L - 1, PH_D), s.vec), NPOLL, a.st,
                       s.ctl))
     return false;
   for (uint32_t i = threadIdx.x; i < d.h; i += BLOCK) lds_st(xs + i, lds_ld(s.vec + i) * lds_ld(nrm + i));
@@ -1315,7 +1345,7 @@ __device__ __forceinline__ bool sample_stage_a(const Args& a, uint32_t tick, uin
   float* vmx = s.scr;
   float* varg = vmx + nvc;
   float* chunk = varg + nvc;  // [NWA][VCHUNK]
-  if (!poll_gather<4, 4>(gather_vec(a.mb_vmax, nvc, gl, vmx), gather_vec(a.mb_varg, nvc, gl, varg),
+  if (!poll_gather<2, 2>(gather_vec(a.mb_vmax, nvc, gl, vmx), gather_vec(a.mb_varg, nvc, gl, varg),
                    NWA, a.st, s.ctl))
     return false;
   float bv;
@@ -1375,7 +1405,7 @@ __device__ __forceinline__ bool sample_stage_b(const Args& a, uint32_t tick, uin
   float* vsum = varg + nvc;
   float* chunk = vsum + nvc;  // [VCHUNK]
   float* wtot = chunk + VCHUNK;  // [NWAVES + 2]
-  if (!poll_gather<4, 4, 4>(gather_vec(a.mb_vmax, nvc, gl, vmx), gather_vec(a.mb_varg, nvc, gl, varg),
+  if (!poll_gather<2, 2, 2>(gather_vec(a.mb_vmax, nvc, gl, vmx), gather_vec(a.mb_varg, nvc, gl, varg),
                    T != 0.0f ? gather_vec(a.mb_vsum, nvc, gsum, vsum) : no_gather(), NWA, a.st,
                    s.ctl))
     return false;
