@@ -461,7 +461,7 @@ static int apply_layout(defer_gpu_model* m, uint32_t G) {
   const uint32_t hs = d.hd + 2;
   const uint32_t rmax = (d.h + G - 1) / G;
   const uint32_t scr_attn = MAX_GROUP * d.hd + 2 * d.hd + 2 * MAX_GROUP +
-                            MAX_GROUP * attn_chunk(d.cap - 1) + NWA * 256 * d.group;
+                            MAX_GROUP * attn_chunk(d.cap - 1) + NCW * d.hd * d.group;
   const uint32_t scr_o = INLINE_COMB_MAX + rmax;
   const uint32_t scr_comb = MAX_ACHUNKS * hs;
   const uint32_t scr_samp = 3 * d.nvc + VCHUNK + NWAVES + 2 + NWA * VCHUNK;
