@@ -280,7 +280,7 @@ def decode_workload(args, name: str) -> int:
             "peak": PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic("k_persistent_decode_8b.md") if name == "8b" else None,
         },
     }
     s.close()
