@@ -871,20 +871,22 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
     // The chunk's K rows of the first KU score passes and V rows of the
     // first VU value steps (a whole 128-position chunk at head_dim 64) are
     // requested before waiting for this token's q/k/v, all in one straight
-    // run (rows past the chunk are clamped to a row of the cache and never
-    // used), so no load of the history sits on the critical path; later
-    // passes and steps keep KU / VU in flight.
+    // run, so no load of the history sits on the critical path; later
+    // passes and steps keep KU / VU in flight. Rows at or past pos are
+    // clamped to row pos - 1 and never used (row pos comes from the poll):
+    // a row is never read before the token that writes it, so no XCD's
+    // cache can hold a copy older than its agent-scope store.
     float4 kr[KU][4], vr[VU];
-    if (att) {
+    if (att && pos > 0) {
 #pragma unroll
       for (uint32_t u = 0; u < KU; ++u) {
-        const float* r = kb + (size_t)min(t0 + tw + u * sstep, d.cap - 1) * d.kvs;
+        const float* r = kb + (size_t)min(t0 + tw + u * sstep, pos - 1) * d.kvs;
 #pragma unroll
         for (uint32_t i = 0; i < 4; ++i) kr[u][i] = ldg4(r + 4 * i);
       }
 #pragma unroll
       for (uint32_t u = 0; u < VU; ++u)
-        vr[u] = ldg4(vb + (size_t)min(t0 + vw + u * vstep, d.cap - 1) * d.kvs);
+        vr[u] = ldg4(vb + (size_t)min(t0 + vw + u * vstep, pos - 1) * d.kvs);
     }
     if (!poll_gather<GROUPED ? 4 : 1, 1, 1>(gather_vec(a.mb_qkv + (size_t)(g * grp + j0) * hd, NH1 * hd, gen_in, qs),
                               gather_vec(a.mb_qkv + d.q + g * hd, hd, gen_in, kn),
