@@ -450,8 +450,8 @@ static uint32_t min_phase_items(const Dims& d) {
 }
 
 // Everything that depends on the persistent grid G: the LDS regions (the
-// publish list, the weight staging of the busiest workgroup, the scratch the
-// O phase and lm_head size per workgroup), the kernels' LDS attribute and the
+// weight staging of the busiest workgroup, the scratch the O phase and
+// lm_head size per workgroup), the kernels' LDS attribute and the
 // co-residency check. Results never depend on G (an item is computed the same
 // way whichever workgroup owns it); only the layout does.
 static int apply_layout(defer_gpu_model* m, uint32_t G) {
@@ -467,12 +467,6 @@ static int apply_layout(defer_gpu_model* m, uint32_t G) {
   const uint32_t scr_samp = 3 * d.nvc + VCHUNK + NWAVES + 2 + NWA * VCHUNK;
   const uint32_t scr_lm = ((d.nvc + G - 1) / G) * VCHUNK;
   d.lds_scr = (std::max({scr_attn, scr_o, scr_comb, scr_samp, scr_lm, 2 * NWAVES}) + 3) & ~3u;
-  // Publish list: one entry per matvec result of a phase (four per QKV item).
-  {
-    const uint32_t per_wg[4] = {4 * ((d.qkv_rows / 2 + G - 1) / G), (d.h + G - 1) / G,
-                                (d.ff + G - 1) / G, (d.h + G - 1) / G};
-    d.lds_pub = std::max({per_wg[0], per_wg[1], per_wg[2], per_wg[3]});
-  }
   // Weight staging for the persistent kernel: each kind's rows of one layer
   // for the workgroup with the most items, if that fits the CU's LDS.
   {
@@ -484,14 +478,26 @@ static int apply_layout(defer_gpu_model* m, uint32_t G) {
       d.stg_off[k] = stg;
       stg += (n_items[k] + G - 1) / G * rows[k] * K[k];
     }
-    const size_t base = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr) * sizeof(float) +
-                        (size_t)d.lds_pub * 2 * sizeof(u64);
+    const size_t base = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr) * sizeof(float);
     d.lds_stg = (base + (size_t)stg * sizeof(float) <= LDS_BYTES_MAX) ? stg : 0;
+  }
+  // Streamed rows (the persistent kernel where rows are not staged, the
+  // per-phase kernels always): each compute wave keeps its passes' four row
+  // values until its last pass (items_dot).
+  {
+    uint32_t passes = 0;
+    const uint32_t n_items[4] = {d.qkv_rows / 2, d.h, d.ff, d.h};
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t per_wg = (n_items[k] + G - 1) / G;
+      const uint32_t step = NCW * pass_items(k == IK_QKV || k == IK_GU);
+      passes = std::max(passes, (per_wg + step - 1) / step);
+    }
+    d.lds_ys = NCW * 4 * passes;
   }
   // A shape-specialised persistent kernel stages its rows only.
   m->persistent = d.lds_stg ? persistent_kernel_for(d) : (const void*)k_persistent;
-  m->lds_bytes = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr + d.lds_stg) * sizeof(float) +
-                 (size_t)d.lds_pub * 2 * sizeof(u64);
+  m->lds_bytes =
+      (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr + d.lds_stg + d.lds_ys) * sizeof(float);
   m->lds_rows = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr) * sizeof(float);
 
   m->G = G;

@@ -6,9 +6,13 @@
 // same way whoever computes it.
 //
 // Roles inside a workgroup (BLOCK = 512 threads = 8 waves):
-//  * pollers (waves 0..NPOLL-1) alone read mailboxes in the matvec phases,
-//    so a poll round waits for nothing but its own words;
-//  * compute waves (the next NCW) compute the matvec items dealt to them;
+//  * pollers (waves 0..NPOLL-1) read mailboxes; in the matvec phases the
+//    compute waves poll beside them (NWA waves), since they have no load in
+//    flight there, while in the attention and the lm_head, where they do,
+//    the pollers poll alone, so a poll round waits for nothing but its own
+//    words;
+//  * compute waves (the next NCW) compute the matvec items dealt to them
+//    and store each result as soon as they have it;
 //  * loaders (the last NLOAD waves) stage weight rows into LDS with direct
 //    global->LDS loads (persistent kernel only, when a layer's share of the
 //    workgroup fits): each kind's rows for the next layer are requested as
@@ -50,7 +54,7 @@ struct Lds {
   float* vec2;  // d.lds_vec2 floats: the normalised lm_head input
   float* scr;   // d.lds_scr floats
   float* stg;   // d.lds_stg floats: staged weight rows (persistent kernel)
-  u64* pub;     // d.lds_pub entries of {word, address}: results the pollers store
+  float* ys;    // d.lds_ys floats: streamed passes' row values (items_dot)
 };
 
 __device__ inline Lds lds_layout(float* base, const Dims& d) {
@@ -61,7 +65,7 @@ __device__ inline Lds lds_layout(float* base, const Dims& d) {
   s.vec2 = s.vec + d.lds_vec;
   s.scr = s.vec2 + d.lds_vec2;
   s.stg = s.scr + d.lds_scr;
-  s.pub = reinterpret_cast<u64*>(s.stg + d.lds_stg);
+  s.ys = s.stg + d.lds_stg;
   return s;
 }
 
@@ -249,57 +253,28 @@ __device__ __forceinline__ uint32_t item_of(uint32_t n, uint32_t wg, uint32_t G,
 
 // ------------------------------------------------------------ publishing
 //
-// Compute waves hand their results to the pollers through LDS instead of
-// storing them: a wave's vector-memory counter then never holds a store, so
-// no later wait of a compute wave can stall on one. A phase ends with a
-// barrier, after which the pollers issue the stores of entries [0, n).
+// A compute wave stores each result as soon as it has it: a tagged mailbox
+// word (agent-scope relaxed 64-bit store, lane 0), the eight replicas of a
+// replicated mailbox (lanes 0..7, one each), or a plain float to the K/V
+// cache (lane 0). No barrier ends a
+// phase: the next phase's first barrier (in its poll) is the point after
+// which LDS the phase used may be rewritten. (Handing the results to the
+// pollers through LDS and storing them after a phase-end barrier, so that
+// no compute wave ever has a store in flight, cost 25 us per token more at
+// 135M: the barrier and the second LDS trip sat on every hand-off.)
 
-// Entry i: a tagged mailbox word for `slot`.
-__device__ __forceinline__ void pub_word(const Lds& s, uint32_t i, u64* slot, float v, uint32_t gen) {
-  AS_LDS u64* e = lptr(s.pub + 2 * i);
-  e[0] = ((u64)gen << 32) | (u64)__float_as_uint(v);
-  e[1] = (u64)(uintptr_t)slot;
-}
-// Entry i: a plain float for `p` (address bit 0 marks the kind).
-__device__ __forceinline__ void pub_float(const Lds& s, uint32_t i, float* p, float v) {
-  AS_LDS u64* e = lptr(s.pub + 2 * i);
-  e[0] = (u64)__float_as_uint(v);
-  e[1] = (u64)(uintptr_t)p | 1u;
-}
-__device__ __forceinline__ void pub_none(const Lds& s, uint32_t i) { lptr(s.pub + 2 * i)[1] = 0; }
-// Entry i: a tagged word for every replica of a replicated mailbox (address
-// bit 1 marks it).
-__device__ __forceinline__ void pub_word_rep(const Lds& s, uint32_t i, u64* slot, float v,
-                                             uint32_t gen) {
-  AS_LDS u64* e = lptr(s.pub + 2 * i);
-  e[0] = ((u64)gen << 32) | (u64)__float_as_uint(v);
-  e[1] = (u64)(uintptr_t)slot | 2u;
+// A tagged mailbox word.
+__device__ __forceinline__ void pub_word(u64* slot, float v, uint32_t gen) { mb_put(slot, v, gen); }
+// The same word in replica `rep` of a replicated mailbox (replicas
+// rep_words apart); lanes 0..MB_REPS-1 of a wave store one replica each.
+__device__ __forceinline__ void pub_word_rep(u64* slot, float v, uint32_t gen, uint32_t rep_words,
+                                             uint32_t rep) {
+  __hip_atomic_store(gptr(slot + (size_t)rep * rep_words), ((u64)gen << 32) | (u64)__float_as_uint(v),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // A workgroup's replica of a replicated mailbox.
 __device__ __forceinline__ const u64* rep_of(const Args& a, const u64* base, uint32_t wg) {
   return base + (size_t)(wg % MB_REPS) * a.rep_words;
-}
-
-// The barrier that ends a matvec phase, then the pollers' stores.
-__device__ __forceinline__ void pub_flush(const Lds& s, uint32_t n, uint32_t rep_words = 0) {
-  __syncthreads();
-  if (threadIdx.x >= NPOLL * WAVE) return;
-  for (uint32_t i = threadIdx.x; i < n; i += NPOLL * WAVE) {
-    const AS_LDS u64* e = lptr(s.pub + 2 * i);
-    const u64 w = e[0], addr = e[1];
-    if (addr & 1u) {
-      st_coherent(reinterpret_cast<float*>((uintptr_t)(addr & ~(u64)1)), __uint_as_float((uint32_t)w));
-    } else if (addr & 2u) {
-      u64* p = reinterpret_cast<u64*>((uintptr_t)(addr & ~(u64)2));
-#pragma unroll
-      for (uint32_t r = 0; r < MB_REPS; ++r)
-        __hip_atomic_store(gptr(p + (size_t)r * rep_words), w, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-    } else if (addr) {
-      __hip_atomic_store(gptr(reinterpret_cast<u64*>((uintptr_t)addr)), w, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
 }
 
 // ------------------------------------------------------------- matvec items
@@ -383,6 +358,8 @@ struct Stager {
   // those of the two kinds whose phases came since (the kind before X is
   // requested only after that barrier).
   uint32_t wait[4];
+  float* ys;             // streamed passes' row values, ys_per_wave floats per compute wave
+  uint32_t ys_per_wave;
 };
 
 // 16 bytes per lane from global memory straight into LDS: lane i's bytes
@@ -439,6 +416,8 @@ __device__ __forceinline__ Stager make_stager(const Args& a, const Lds& s, uint3
   sg.on = on;
   sg.a = &a;
   sg.stg = s.stg;
+  sg.ys = s.ys;
+  sg.ys_per_wave = a.d.lds_ys / NCW;
   sg.wg = wg;
   sg.G = G;
   const uint32_t wave = threadIdx.x / WAVE;
@@ -650,9 +629,7 @@ __device__ __forceinline__ void items_dot(const Args& a, uint32_t kind, uint32_t
   const bool pair = kind_rows(kind) == 2;
   const uint32_t r = qrow(lane), s = qseg(lane);
   const uint32_t step = NCW * pass_items(pair);
-  auto emit = [&](uint32_t k, float acc) {
-    float y[4];
-    quad_sums(acc, y);
+  auto emit_y = [&](uint32_t k, const float (&y)[4]) {
     if (pair) {
       body(k, y[0], y[1]);
       if (k + NCW < cnt) body(k + NCW, y[2], y[3]);
@@ -661,6 +638,11 @@ __device__ __forceinline__ void items_dot(const Args& a, uint32_t kind, uint32_t
       for (uint32_t u = 0; u < 4; ++u)
         if (k + NCW * u < cnt) body(k + NCW * u, y[u], 0.0f);
     }
+  };
+  auto emit = [&](uint32_t k, float acc) {
+    float y[4];
+    quad_sums(acc, y);
+    emit_y(k, y);
   };
   if (STAGED_ONLY || sg.on) {
     if (!P.any) return;
@@ -671,14 +653,30 @@ __device__ __forceinline__ void items_dot(const Args& a, uint32_t kind, uint32_t
     }
     return;
   }
-  for (uint32_t k = cw; k < cnt; k += step) {
+  // Streamed rows: the passes' four row values wait in LDS (sg.ys, this
+  // wave's slice) until the wave's last pass, and only then go to body,
+  // which stores them: a store issued between the stream's loads would hold
+  // back every later wait for a block (the vector-memory counter completes
+  // in order).
+  float* ys = sg.ys + cw * sg.ys_per_wave;
+  uint32_t np = 0;
+  for (uint32_t k = cw; k < cnt; k += step, ++np) {
     const uint32_t it = slot_item(pair, k, r);
     float acc = 0.0f;
     if (it < cnt) {
       const ItemRows rw = item_rows(a, kind, l, it, wg, G);
       acc = seg_stream<KF>(pair && (r & 1u) ? rw.w1 : rw.w0, x, K, s, 0, 0.0f);
     }
-    emit(k, acc);
+    float y[4];
+    quad_sums(acc, y);
+    if (lane < 4) lds_st(ys + 4 * np + lane, y[lane]);
+  }
+  np = 0;
+  for (uint32_t k = cw; k < cnt; k += step, ++np) {
+    float y[4];
+#pragma unroll
+    for (uint32_t u = 0; u < 4; ++u) y[u] = lds_ld(ys + 4 * np + u);
+    emit_y(k, y);
   }
 }
 
@@ -797,22 +795,18 @@ __device__ __forceinline__ bool phase_qkv(const Args& a, uint32_t l, uint32_t ti
         a1 = y1 * e.x + y0 * e.y;
       }
       if (lane == 0) {
-        pub_word(s, 4 * k, a.mb_qkv + r0, a0, gen);
-        pub_word(s, 4 * k + 1, a.mb_qkv + r1, a1, gen);
-        if (hb >= d.nh) {
+        if (hb >= d.nh) {  // the cache rows first: attention reads them a token later
           const bool is_k = hb < d.nh + d.nkv;
           const uint32_t g = is_k ? hb - d.nh : hb - d.nh - d.nkv;
           float* row = (is_k ? a.kc : a.vc) + (((size_t)l * d.nkv + g) * d.cap + pos) * d.kvs;
-          pub_float(s, 4 * k + 2, row + i, a0);
-          pub_float(s, 4 * k + 3, row + i + d.half, a1);
-        } else {
-          pub_none(s, 4 * k + 2);
-          pub_none(s, 4 * k + 3);
+          st_coherent(row + i, a0);
+          st_coherent(row + i + d.half, a1);
         }
+        pub_word(a.mb_qkv + r0, a0, gen);
+        pub_word(a.mb_qkv + r1, a1, gen);
       }
     });
   }
-  pub_flush(s, 4 * cnt);
   return true;
 }
 
@@ -1117,10 +1111,9 @@ __device__ __forceinline__ bool phase_o(const Args& a, uint32_t l, uint32_t tick
   if (wave >= NPOLL && wave < NWA) {
     const uint32_t gen = gen_of(d, tick, l, PH_O);
     items_dot(a, IK_O, wave - NPOLL, l, sg, P, s.vec, wg, G, lane, [&](uint32_t k, float y, float) {
-      if (lane == 0) pub_word_rep(s, k, a.mb_xo + item_of(d.h, wg, G, k), lds_ld(xres + k) + y, gen);
+      if (lane < MB_REPS) pub_word_rep(a.mb_xo + item_of(d.h, wg, G, k), lds_ld(xres + k) + y, gen, a.rep_words, lane);
     });
   }
-  pub_flush(s, R, a.rep_words);
   return true;
 }
 
@@ -1146,11 +1139,10 @@ __device__ __forceinline__ bool phase_gu(const Args& a, uint32_t l, uint32_t tic
     const uint32_t gen = gen_of(d, tick, l, PH_GU);
     items_dot(a, IK_GU, wave - NPOLL, l, sg, P, s.vec, wg, G, lane,
               [&](uint32_t k, float gate, float up) {
-                if (lane == 0)
-                  pub_word_rep(s, k, a.mb_g + item_of(d.ff, wg, G, k), act_fn(gate * inv, d.act) * (up * inv), gen);
+                if (lane < MB_REPS)
+                  pub_word_rep(a.mb_g + item_of(d.ff, wg, G, k), act_fn(gate * inv, d.act) * (up * inv), gen, a.rep_words, lane);
               });
   }
-  pub_flush(s, rows_owned(d.ff, wg, G), a.rep_words);
   return true;
 }
 
@@ -1175,10 +1167,9 @@ __device__ __forceinline__ bool phase_d(const Args& a, uint32_t l, uint32_t tick
   if (wave >= NPOLL && wave < NWA) {
     const uint32_t gen = gen_of(d, tick, l, PH_D);
     items_dot(a, IK_D, wave - NPOLL, l, sg, P, s.vec, wg, G, lane, [&](uint32_t k, float y, float) {
-      if (lane == 0) pub_word_rep(s, k, a.mb_xd + item_of(d.h, wg, G, k), lds_ld(s.scr + k) + y, gen);
+      if (lane < MB_REPS) pub_word_rep(a.mb_xd + item_of(d.h, wg, G, k), lds_ld(s.scr + k) + y, gen, a.rep_words, lane);
     });
   }
-  pub_flush(s, R, a.rep_words);
   return true;
 }
 
