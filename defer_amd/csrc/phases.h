@@ -345,6 +345,13 @@ __device__ __forceinline__ ItemRows item_rows(const Args& a, uint32_t kind, uint
   return r;
 }
 
+// Offset of kind X's rows in the staging region, by selects rather than an
+// indexed load (a run-time index into the Dims copy would put it on the
+// stack).
+__device__ __forceinline__ uint32_t stg_off_of(const Dims& d, uint32_t kind) {
+  return kind == 0 ? d.stg_off[0] : kind == 1 ? d.stg_off[1] : kind == 2 ? d.stg_off[2] : d.stg_off[3];
+}
+
 // Staging of the workgroup's rows in LDS (persistent kernel). Kind X's items
 // sit back to back at s.stg + d.stg_off[X], item k's rows contiguous.
 struct Stager {
@@ -439,7 +446,7 @@ __device__ __forceinline__ void stage_issue(const Stager& sg, uint32_t kind, uin
   const uint32_t lane = threadIdx.x % WAVE;
   const uint32_t cnt = rows_owned(kind_items(d, kind), sg.wg, sg.G);
   const uint32_t K = kind_k(d, kind), nr = kind_rows(kind), nseg = (K + 255) / 256;
-  const uint32_t base = (uint32_t)(uintptr_t)(sg.stg + d.stg_off[kind]);
+  const uint32_t base = (uint32_t)(uintptr_t)(sg.stg + stg_off_of(d, kind));
   for (uint32_t k = sg.ld; k < cnt; k += NLOAD) {
     const ItemRows r = item_rows(a, kind, l, k, sg.wg, sg.G);
     for (uint32_t row = 0; row < nr; ++row) {
@@ -471,7 +478,7 @@ __device__ __forceinline__ LoadOp no_load() {
 // Staged rows of item k of a kind (pairs: second row at +K).
 __device__ __forceinline__ const float* staged_item(const Stager& sg, uint32_t kind, uint32_t k) {
   const Dims d = shape_dims(sg.a->d);
-  return sg.stg + d.stg_off[kind] + k * kind_rows(kind) * kind_k(d, kind);
+  return sg.stg + stg_off_of(d, kind) + k * kind_rows(kind) * kind_k(d, kind);
 }
 
 // Lane partial of x . x over the elements 4*lane + 256*i of a length-K
