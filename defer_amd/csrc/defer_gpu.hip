@@ -481,23 +481,18 @@ static int apply_layout(defer_gpu_model* m, uint32_t G) {
     const size_t base = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr) * sizeof(float);
     d.lds_stg = (base + (size_t)stg * sizeof(float) <= LDS_BYTES_MAX) ? stg : 0;
   }
-  // Streamed rows (the persistent kernel where rows are not staged, the
-  // per-phase kernels always): each compute wave keeps its passes' four row
-  // values until its last pass (items_dot).
+  // Listed results (phases.h: Pub): one entry per matvec result of a phase
+  // (four per QKV item), where rows are streamed (the per-phase kernels
+  // always).
   {
-    uint32_t passes = 0;
-    const uint32_t n_items[4] = {d.qkv_rows / 2, d.h, d.ff, d.h};
-    for (int k = 0; k < 4; ++k) {
-      const uint32_t per_wg = (n_items[k] + G - 1) / G;
-      const uint32_t step = NCW * pass_items(k == IK_QKV || k == IK_GU);
-      passes = std::max(passes, (per_wg + step - 1) / step);
-    }
-    d.lds_ys = NCW * 4 * passes;
+    const uint32_t per_wg[4] = {4 * ((d.qkv_rows / 2 + G - 1) / G), (d.h + G - 1) / G,
+                                (d.ff + G - 1) / G, (d.h + G - 1) / G};
+    d.lds_pub = std::max({per_wg[0], per_wg[1], per_wg[2], per_wg[3]});
   }
   // A shape-specialised persistent kernel stages its rows only.
   m->persistent = d.lds_stg ? persistent_kernel_for(d) : (const void*)k_persistent;
-  m->lds_bytes =
-      (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr + d.lds_stg + d.lds_ys) * sizeof(float);
+  m->lds_bytes = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr + d.lds_stg) * sizeof(float) +
+                 (size_t)d.lds_pub * 2 * sizeof(u64);
   m->lds_rows = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr) * sizeof(float);
 
   m->G = G;

@@ -55,7 +55,7 @@ struct Dims {
   uint32_t lds_scr;    // floats of the scratch LDS region
   uint32_t lds_stg;    // floats of the weight staging region (0: rows are not staged)
   uint32_t stg_off[4]; // float offset of each item kind's rows in the staging region
-  uint32_t lds_ys;     // floats of the streamed passes' row values (NCW slices)
+  uint32_t lds_pub;    // entries of the listed results (rows streamed)
   float eps, scale;
 };
 

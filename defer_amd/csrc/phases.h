@@ -54,7 +54,7 @@ struct Lds {
   float* vec2;  // d.lds_vec2 floats: the normalised lm_head input
   float* scr;   // d.lds_scr floats
   float* stg;   // d.lds_stg floats: staged weight rows (persistent kernel)
-  float* ys;    // d.lds_ys floats: streamed passes' row values (items_dot)
+  u64* pub;     // d.lds_pub entries of {word, address}: listed results (Pub)
 };
 
 __device__ inline Lds lds_layout(float* base, const Dims& d) {
@@ -65,7 +65,7 @@ __device__ inline Lds lds_layout(float* base, const Dims& d) {
   s.vec2 = s.vec + d.lds_vec;
   s.scr = s.vec2 + d.lds_vec2;
   s.stg = s.scr + d.lds_scr;
-  s.ys = s.stg + d.lds_stg;
+  s.pub = reinterpret_cast<u64*>(s.stg + d.lds_stg);
   return s;
 }
 
@@ -253,28 +253,98 @@ __device__ __forceinline__ uint32_t item_of(uint32_t n, uint32_t wg, uint32_t G,
 
 // ------------------------------------------------------------ publishing
 //
-// A compute wave stores each result as soon as it has it: a tagged mailbox
-// word (agent-scope relaxed 64-bit store, lane 0), the eight replicas of a
-// replicated mailbox (lanes 0..7, one each), or a plain float to the K/V
-// cache (lane 0). No barrier ends a
-// phase: the next phase's first barrier (in its poll) is the point after
-// which LDS the phase used may be rewritten. (Handing the results to the
-// pollers through LDS and storing them after a phase-end barrier, so that
-// no compute wave ever has a store in flight, cost 25 us per token more at
-// 135M: the barrier and the second LDS trip sat on every hand-off.)
-
-// A tagged mailbox word.
-__device__ __forceinline__ void pub_word(u64* slot, float v, uint32_t gen) { mb_put(slot, v, gen); }
-// The same word in replica `rep` of a replicated mailbox (replicas
-// rep_words apart); lanes 0..MB_REPS-1 of a wave store one replica each.
-__device__ __forceinline__ void pub_word_rep(u64* slot, float v, uint32_t gen, uint32_t rep_words,
-                                             uint32_t rep) {
-  __hip_atomic_store(gptr(slot + (size_t)rep * rep_words), ((u64)gen << 32) | (u64)__float_as_uint(v),
-                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Where weight rows are staged in LDS, a compute wave stores each result as
+// soon as it has it: a tagged mailbox word (agent-scope relaxed 64-bit
+// store, lane 0), the eight replicas of a replicated mailbox (lanes 0..7,
+// one each), or a plain float to the K/V cache (lane 0); no barrier ends the
+// phase, the next phase's first barrier orders the reuse of its LDS.
+// (Handing the results over through LDS for other waves to store after a
+// phase-end barrier cost 25 us per token more at 135M.) Where rows are
+// streamed from HBM, a store would sit in the compute wave's in-order
+// vector-memory counter ahead of its next loads and polls while HBM is
+// saturated, so results are listed in LDS instead ({word, address | kind},
+// entry i per result) and, after a phase-end barrier, the loader waves --
+// idle when nothing is staged -- store them (pub_flush).
+struct Pub {
+  bool list;  // wave-uniform: list the results (rows streamed) or store them now
+  u64* ent;   // LDS entries
+};
+__device__ __forceinline__ Pub pub_for(bool staged, const Lds& s) {
+  Pub p;
+  p.list = !(STAGED_ONLY || staged);
+  p.ent = s.pub;
+  return p;
+}
+// Result i: a tagged mailbox word.
+__device__ __forceinline__ void pub_word(const Pub& p, uint32_t i, u64* slot, float v, uint32_t gen,
+                                         uint32_t lane) {
+  if (lane != 0) return;
+  if (p.list) {
+    AS_LDS u64* e = lptr(p.ent + 2 * i);
+    e[0] = ((u64)gen << 32) | (u64)__float_as_uint(v);
+    e[1] = (u64)(uintptr_t)slot;
+  } else {
+    mb_put(slot, v, gen);
+  }
+}
+// Result i: a plain float (address bit 0 marks the kind in a list).
+__device__ __forceinline__ void pub_float(const Pub& p, uint32_t i, float* ptr, float v, uint32_t lane) {
+  if (lane != 0) return;
+  if (p.list) {
+    AS_LDS u64* e = lptr(p.ent + 2 * i);
+    e[0] = (u64)__float_as_uint(v);
+    e[1] = (u64)(uintptr_t)ptr | 1u;
+  } else {
+    st_coherent(ptr, v);
+  }
+}
+// Result i: nothing (a list entry that stores nothing).
+__device__ __forceinline__ void pub_none(const Pub& p, uint32_t i, uint32_t lane) {
+  if (p.list && lane == 0) lptr(p.ent + 2 * i)[1] = 0;
+}
+// Result i: the same word in every replica of a replicated mailbox (replicas
+// rep_words apart; address bit 1 marks the kind in a list).
+__device__ __forceinline__ void pub_word_rep(const Pub& p, uint32_t i, u64* slot, float v,
+                                             uint32_t gen, uint32_t rep_words, uint32_t lane) {
+  const u64 w = ((u64)gen << 32) | (u64)__float_as_uint(v);
+  if (p.list) {
+    if (lane == 0) {
+      AS_LDS u64* e = lptr(p.ent + 2 * i);
+      e[0] = w;
+      e[1] = (u64)(uintptr_t)slot | 2u;
+    }
+  } else if (lane < MB_REPS) {
+    __hip_atomic_store(gptr(slot + (size_t)lane * rep_words), w, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 // A workgroup's replica of a replicated mailbox.
 __device__ __forceinline__ const u64* rep_of(const Args& a, const u64* base, uint32_t wg) {
   return base + (size_t)(wg % MB_REPS) * a.rep_words;
+}
+
+// A listed phase's end: a barrier, then the loader waves store entries
+// [0, n).
+__device__ __forceinline__ void pub_flush(const Pub& p, uint32_t n, uint32_t rep_words = 0) {
+  if (!p.list) return;
+  __syncthreads();
+  if (threadIdx.x < NWA * WAVE) return;
+  for (uint32_t i = threadIdx.x - NWA * WAVE; i < n; i += NLOAD * WAVE) {
+    const AS_LDS u64* e = lptr(p.ent + 2 * i);
+    const u64 w = e[0], addr = e[1];
+    if (addr & 1u) {
+      st_coherent(reinterpret_cast<float*>((uintptr_t)(addr & ~(u64)1)), __uint_as_float((uint32_t)w));
+    } else if (addr & 2u) {
+      u64* q = reinterpret_cast<u64*>((uintptr_t)(addr & ~(u64)2));
+#pragma unroll
+      for (uint32_t r = 0; r < MB_REPS; ++r)
+        __hip_atomic_store(gptr(q + (size_t)r * rep_words), w, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    } else if (addr) {
+      __hip_atomic_store(gptr(reinterpret_cast<u64*>((uintptr_t)addr)), w, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 }
 
 // ------------------------------------------------------------- matvec items
@@ -365,8 +435,6 @@ struct Stager {
   // those of the two kinds whose phases came since (the kind before X is
   // requested only after that barrier).
   uint32_t wait[4];
-  float* ys;             // streamed passes' row values, ys_per_wave floats per compute wave
-  uint32_t ys_per_wave;
 };
 
 // 16 bytes per lane from global memory straight into LDS: lane i's bytes
@@ -423,8 +491,6 @@ __device__ __forceinline__ Stager make_stager(const Args& a, const Lds& s, uint3
   sg.on = on;
   sg.a = &a;
   sg.stg = s.stg;
-  sg.ys = s.ys;
-  sg.ys_per_wave = a.d.lds_ys / NCW;
   sg.wg = wg;
   sg.G = G;
   const uint32_t wave = threadIdx.x / WAVE;
@@ -636,7 +702,9 @@ __device__ __forceinline__ void items_dot(const Args& a, uint32_t kind, uint32_t
   const bool pair = kind_rows(kind) == 2;
   const uint32_t r = qrow(lane), s = qseg(lane);
   const uint32_t step = NCW * pass_items(pair);
-  auto emit_y = [&](uint32_t k, const float (&y)[4]) {
+  auto emit = [&](uint32_t k, float acc) {
+    float y[4];
+    quad_sums(acc, y);
     if (pair) {
       body(k, y[0], y[1]);
       if (k + NCW < cnt) body(k + NCW, y[2], y[3]);
@@ -645,11 +713,6 @@ __device__ __forceinline__ void items_dot(const Args& a, uint32_t kind, uint32_t
       for (uint32_t u = 0; u < 4; ++u)
         if (k + NCW * u < cnt) body(k + NCW * u, y[u], 0.0f);
     }
-  };
-  auto emit = [&](uint32_t k, float acc) {
-    float y[4];
-    quad_sums(acc, y);
-    emit_y(k, y);
   };
   if (STAGED_ONLY || sg.on) {
     if (!P.any) return;
@@ -660,30 +723,14 @@ __device__ __forceinline__ void items_dot(const Args& a, uint32_t kind, uint32_t
     }
     return;
   }
-  // Streamed rows: the passes' four row values wait in LDS (sg.ys, this
-  // wave's slice) until the wave's last pass, and only then go to body,
-  // which stores them: a store issued between the stream's loads would hold
-  // back every later wait for a block (the vector-memory counter completes
-  // in order).
-  float* ys = sg.ys + cw * sg.ys_per_wave;
-  uint32_t np = 0;
-  for (uint32_t k = cw; k < cnt; k += step, ++np) {
+  for (uint32_t k = cw; k < cnt; k += step) {
     const uint32_t it = slot_item(pair, k, r);
     float acc = 0.0f;
     if (it < cnt) {
       const ItemRows rw = item_rows(a, kind, l, it, wg, G);
       acc = seg_stream<KF>(pair && (r & 1u) ? rw.w1 : rw.w0, x, K, s, 0, 0.0f);
     }
-    float y[4];
-    quad_sums(acc, y);
-    if (lane < 4) lds_st(ys + 4 * np + lane, y[lane]);
-  }
-  np = 0;
-  for (uint32_t k = cw; k < cnt; k += step, ++np) {
-    float y[4];
-#pragma unroll
-    for (uint32_t u = 0; u < 4; ++u) y[u] = lds_ld(ys + 4 * np + u);
-    emit_y(k, y);
+    emit(k, acc);
   }
 }
 
@@ -758,6 +805,7 @@ __device__ __forceinline__ bool phase_qkv(const Args& a, uint32_t l, uint32_t ti
     }
   }
   Preload P;
+  const Pub pub = pub_for(sg.on, s);
   LoadOp op = no_load();
   if (sg.on) {
     op.issue = IK_D;  // the previous layer's D rows are used: this layer's
@@ -801,19 +849,21 @@ __device__ __forceinline__ bool phase_qkv(const Args& a, uint32_t l, uint32_t ti
         a0 = y0 * e.x - y1 * e.y;
         a1 = y1 * e.x + y0 * e.y;
       }
-      if (lane == 0) {
-        if (hb >= d.nh) {  // the cache rows first: attention reads them a token later
-          const bool is_k = hb < d.nh + d.nkv;
-          const uint32_t g = is_k ? hb - d.nh : hb - d.nh - d.nkv;
-          float* row = (is_k ? a.kc : a.vc) + (((size_t)l * d.nkv + g) * d.cap + pos) * d.kvs;
-          st_coherent(row + i, a0);
-          st_coherent(row + i + d.half, a1);
-        }
-        pub_word(a.mb_qkv + r0, a0, gen);
-        pub_word(a.mb_qkv + r1, a1, gen);
+      if (hb >= d.nh) {  // the cache rows first: attention reads them a token later
+        const bool is_k = hb < d.nh + d.nkv;
+        const uint32_t g = is_k ? hb - d.nh : hb - d.nh - d.nkv;
+        float* row = (is_k ? a.kc : a.vc) + (((size_t)l * d.nkv + g) * d.cap + pos) * d.kvs;
+        pub_float(pub, 4 * k, row + i, a0, lane);
+        pub_float(pub, 4 * k + 1, row + i + d.half, a1, lane);
+      } else {
+        pub_none(pub, 4 * k, lane);
+        pub_none(pub, 4 * k + 1, lane);
       }
+      pub_word(pub, 4 * k + 2, a.mb_qkv + r0, a0, gen, lane);
+      pub_word(pub, 4 * k + 3, a.mb_qkv + r1, a1, gen, lane);
     });
   }
+  pub_flush(pub, 4 * cnt);
   return true;
 }
 
@@ -1101,6 +1151,7 @@ __device__ __forceinline__ bool phase_o(const Args& a, uint32_t l, uint32_t tick
   float emb = 0.0f;
   if (l == 0 && threadIdx.x < R) emb = ldg(a.embed + (size_t)token * d.h + item_of(d.h, wg, G, threadIdx.x));
   Preload P;
+  const Pub pub = pub_for(sg.on, s);
   LoadOp op = no_load();
   if (sg.on) {
     op.issue = IK_QKV;  // the QKV rows are used: request the next layer's
@@ -1118,9 +1169,10 @@ __device__ __forceinline__ bool phase_o(const Args& a, uint32_t l, uint32_t tick
   if (wave >= NPOLL && wave < NWA) {
     const uint32_t gen = gen_of(d, tick, l, PH_O);
     items_dot(a, IK_O, wave - NPOLL, l, sg, P, s.vec, wg, G, lane, [&](uint32_t k, float y, float) {
-      if (lane < MB_REPS) pub_word_rep(a.mb_xo + item_of(d.h, wg, G, k), lds_ld(xres + k) + y, gen, a.rep_words, lane);
+      pub_word_rep(pub, k, a.mb_xo + item_of(d.h, wg, G, k), lds_ld(xres + k) + y, gen, a.rep_words, lane);
     });
   }
+  pub_flush(pub, R, a.rep_words);
   return true;
 }
 
@@ -1132,6 +1184,7 @@ __device__ __forceinline__ bool phase_gu(const Args& a, uint32_t l, uint32_t tic
   const Dims d = shape_dims(a.d);
   const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
   Preload P;
+  const Pub pub = pub_for(sg.on, s);
   LoadOp op = no_load();
   if (sg.on) {
     op.issue = IK_O;
@@ -1146,10 +1199,10 @@ __device__ __forceinline__ bool phase_gu(const Args& a, uint32_t l, uint32_t tic
     const uint32_t gen = gen_of(d, tick, l, PH_GU);
     items_dot(a, IK_GU, wave - NPOLL, l, sg, P, s.vec, wg, G, lane,
               [&](uint32_t k, float gate, float up) {
-                if (lane < MB_REPS)
-                  pub_word_rep(a.mb_g + item_of(d.ff, wg, G, k), act_fn(gate * inv, d.act) * (up * inv), gen, a.rep_words, lane);
+                pub_word_rep(pub, k, a.mb_g + item_of(d.ff, wg, G, k), act_fn(gate * inv, d.act) * (up * inv), gen, a.rep_words, lane);
               });
   }
+  pub_flush(pub, rows_owned(d.ff, wg, G), a.rep_words);
   return true;
 }
 
@@ -1162,6 +1215,7 @@ __device__ __forceinline__ bool phase_d(const Args& a, uint32_t l, uint32_t tick
   const Gather gr = R > 0 ? gather_vec(rep_of(a, a.mb_xo, wg) + item_of(d.h, wg, G, 0), R, gen_of(d, tick, l, PH_O), s.scr)
                           : no_gather();
   Preload P;
+  const Pub pub = pub_for(sg.on, s);
   LoadOp op = no_load();
   if (sg.on) {
     op.issue = IK_GU;
@@ -1174,9 +1228,10 @@ __device__ __forceinline__ bool phase_d(const Args& a, uint32_t l, uint32_t tick
   if (wave >= NPOLL && wave < NWA) {
     const uint32_t gen = gen_of(d, tick, l, PH_D);
     items_dot(a, IK_D, wave - NPOLL, l, sg, P, s.vec, wg, G, lane, [&](uint32_t k, float y, float) {
-      if (lane < MB_REPS) pub_word_rep(a.mb_xd + item_of(d.h, wg, G, k), lds_ld(s.scr + k) + y, gen, a.rep_words, lane);
+      pub_word_rep(pub, k, a.mb_xd + item_of(d.h, wg, G, k), lds_ld(s.scr + k) + y, gen, a.rep_words, lane);
     });
   }
+  pub_flush(pub, R, a.rep_words);
   return true;
 }
 
