@@ -620,6 +620,34 @@ __global__ __launch_bounds__(BLOCK) void k_b_attn(const Args* __restrict__ rargs
   phase_attn<true>(a, l, r.tick, r.pos, x, 0x10000u, s);  // stride past every item: just item x
 }
 
+// The same items with workgroups of the NCW attention waves alone (they
+// also poll and publish) and only the attention's LDS, so that several
+// items share a CU: one row's chunk is a chain of dependent loads and
+// barriers that a lone workgroup cannot keep the CU busy with.
+__device__ __forceinline__ Lds lds_init_attn() {
+  extern __shared__ float lds_raw[];
+  Lds s;
+  s.ctl = reinterpret_cast<WaitCtl*>(lds_raw);
+  s.red = lds_raw + 4;
+  s.vec = s.vec2 = s.stg = nullptr;
+  s.scr = lds_raw + 4 + 64;
+  s.pub = nullptr;
+  if (threadIdx.x == 0) s.ctl->abort_seen = 0;
+  __syncthreads();
+  return s;
+}
+// One score pass and four value steps in flight per lane keep the kernel
+// within 128 VGPRs, four workgroups per CU.
+__global__ __launch_bounds__(NCW * WAVE) __attribute__((amdgpu_waves_per_eu(4))) void k_b_attn_w(
+    const Args* __restrict__ rargs, const BRow* __restrict__ rows,
+    const uint32_t* __restrict__ items, uint32_t l) {
+  const uint32_t e = items[blockIdx.x], b = e >> 16, x = e & 0xffffu;
+  const Args& a = rargs[b];
+  const Lds s = lds_init_attn();
+  const BRow r = rows[b];
+  phase_attn<true, 0, NCW, 1, 4>(a, l, r.tick, r.pos, x, 0x10000u, s);
+}
+
 // ----------------------------------------------------- tiled attention
 //
 // Rows of one cache at consecutive positions (a prefill or a replay) share

@@ -351,6 +351,7 @@ struct defer_gpu_model {
   uint32_t batch_min = 16;
   uint32_t samp_next = 1;  // tag of the next batched sampling op's chunk sums (workspace)
   size_t lds_rows = 0;  // LDS of the batched kernels that run one-token functions
+  size_t lds_attn = 0;  // LDS of k_b_attn_w (the attention's scratch)
   float* panels = nullptr;
   std::vector<const float*> p_qkv, p_o, p_gu, p_d;
   const float* p_lm = nullptr;
@@ -494,6 +495,7 @@ static int apply_layout(defer_gpu_model* m, uint32_t G) {
   m->lds_bytes = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr + d.lds_stg) * sizeof(float) +
                  (size_t)d.lds_pub * 2 * sizeof(u64);
   m->lds_rows = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr) * sizeof(float);
+  m->lds_attn = (size_t)(4 + 64 + ((scr_attn + 3) & ~3u)) * sizeof(float);
 
   m->G = G;
   const void* kernels[] = {m->persistent, (const void*)k_phase, (const void*)k_samp_a,
@@ -511,6 +513,12 @@ static int apply_layout(defer_gpu_model* m, uint32_t G) {
     if (e != hipSuccess)
       return fail(DEFER_GPU_E_HIP, "LDS attribute (%zu bytes): %s", m->lds_rows,
                   hipGetErrorString(e));
+  }
+  {
+    const hipError_t e = hipFuncSetAttribute((const void*)k_b_attn_w,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)m->lds_attn);
+    if (e != hipSuccess)
+      return fail(DEFER_GPU_E_HIP, "LDS attribute (%zu bytes): %s", m->lds_attn, hipGetErrorString(e));
   }
   int occ = 0;
   const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, m->persistent, BLOCK,
@@ -2003,7 +2011,7 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
         k_b_attn_tile<<<(uint32_t)items.size(), 256, attn_tile_lds(d.group), s>>>(
             d, w.drows, w.items, w.tiles, l, w.QKVT, w.PART, part_words(d));
       else
-        k_b_attn<<<(uint32_t)items.size(), BLOCK, m->lds_rows, s>>>(w.rargs, w.drows, w.items, l);
+        k_b_attn_w<<<(uint32_t)items.size(), NCW * WAVE, m->lds_attn, s>>>(w.rargs, w.drows, w.items, l);
     }
     k_b_comb<<<dim3(n, (d.nh + COMB_HEADS_PER_BLOCK - 1) / COMB_HEADS_PER_BLOCK), 256, 0, s>>>(
         d, w.drows, w.PART, part_words(d), w.XQ);

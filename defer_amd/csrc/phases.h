@@ -735,8 +735,8 @@ __device__ __forceinline__ void items_dot(const Args& a, uint32_t kind, uint32_t
 }
 
 constexpr uint32_t MAX_GROUP = 4;
-constexpr uint32_t KU = 2;  // score passes whose K rows a lane keeps in flight
-constexpr uint32_t VU = 8;  // V float4 a lane keeps in flight
+constexpr uint32_t KU_DEF = 2;  // score passes whose K rows a lane keeps in flight
+constexpr uint32_t VU_DEF = 8;  // V float4 a lane keeps in flight
 
 // Lane geometry of the attention (head_dim = 16 * 2^k, at most 256). The
 // attention math runs on the NCW compute waves (attention wave w = wave -
@@ -884,7 +884,13 @@ __device__ __forceinline__ bool phase_qkv(const Args& a, uint32_t l, uint32_t ti
 // path, whose rows bring workgroups enough, reads each K/V row once per item
 // instead of once per head). The heads of a GQA group share K/V rows but
 // nothing else, so both give each head the same arithmetic, bit for bit.
-template <bool GROUPED = false>
+// AW0: the first attention wave (the persistent kernel's waves 0..NPOLL-1
+// poll while the attention waves load; a workgroup of the NCW attention
+// waves alone passes 0). NPW: the waves that poll q/k/v and publish the
+// partials. KU, VU: the loads in flight. None of these changes the
+// arithmetic.
+template <bool GROUPED = false, uint32_t AW0 = NPOLL, uint32_t NPW = NPOLL, uint32_t KU = KU_DEF,
+          uint32_t VU = VU_DEF>
 __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t tick, uint32_t pos,
                                            uint32_t wg, uint32_t G, const Lds& s) {
   const Dims d = shape_dims(a.d);
@@ -907,8 +913,8 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
   const uint32_t pl = lane / ge.lv, dl = lane % ge.lv;
   const uint32_t sstep = NCW * ge.pw, vstep = NCW * ge.pv;
   // pollers and loaders only meet the barriers
-  const bool att = wave >= NPOLL && wave < NPOLL + NCW;
-  const uint32_t aw = att ? wave - NPOLL : 0;  // attention wave
+  const bool att = wave >= AW0 && wave < AW0 + NCW;
+  const uint32_t aw = att ? wave - AW0 : 0;  // attention wave
   const uint32_t tw = aw * ge.pw + ps;  // this lane's position offset in a score pass
   const uint32_t vw = aw * ge.pv + pl;  // ... and in a value step
   for (uint32_t item = wg; item < n_items; item += G) {
@@ -939,9 +945,9 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
       for (uint32_t u = 0; u < VU; ++u)
         vr[u] = ldg4(vb + (size_t)min(t0 + vw + u * vstep, pos - 1) * d.kvs);
     }
-    if (!poll_gather<GROUPED ? 4 : 1, 1, 1>(gather_vec(a.mb_qkv + (size_t)(g * grp + j0) * hd, NH1 * hd, gen_in, qs),
+    if (!poll_gather<GROUPED ? 8 / NPW : 1, 1, 1>(gather_vec(a.mb_qkv + (size_t)(g * grp + j0) * hd, NH1 * hd, gen_in, qs),
                               gather_vec(a.mb_qkv + d.q + g * hd, hd, gen_in, kn),
-                              gather_vec(a.mb_qkv + d.q + d.kv + g * hd, hd, gen_in, vn), NPOLL,
+                              gather_vec(a.mb_qkv + d.q + d.kv + g * hd, hd, gen_in, vn), NPW,
                               a.st, s.ctl))
       return false;
     // 1. scores, KU passes per round (pass u of a round uses kr[u], then
@@ -1049,7 +1055,7 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
         lds_st(dst + 3, acc[j].w);
       }
     __syncthreads();
-    for (uint32_t u = threadIdx.x; threadIdx.x < NPOLL * WAVE && u < NH1 * hd; u += NPOLL * WAVE) {
+    for (uint32_t u = threadIdx.x; threadIdx.x < NPW * WAVE && u < NH1 * hd; u += NPW * WAVE) {
       const uint32_t j = u / hd, dd = u - j * hd;
       float pw[NCW];
 #pragma unroll
