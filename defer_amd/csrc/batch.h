@@ -347,12 +347,13 @@ __global__ __launch_bounds__(512) void k_gemm_n(const float* __restrict__ Wp, ui
 // ways. Quarter q of tree16 is ((s_4q + s_4q+1) + (s_4q+2 + s_4q+3)), a
 // subtree of its own, and it needs only quarter q of every chunk (one
 // contiguous 1 KB block per tile and chunk in the panel layout), so a task
-// is (row group of four row tiles, quarter q, pair of column tiles): it
-// reads a quarter of the rows' weights and of two column tiles' panel, and
-// writes its subtree to plane q of Q ([4][B][M]); k_gemm_qcomb forms
-// (t_0 + t_1) + (t_2 + t_3), the same tree16, and applies OUT. Eight waves:
-// wave w owns row tile w % 4 and column tile w / 4 of the pair. A chunk's
-// six 1 KB blocks (four row tiles, two column tiles) take one copy each
+// is (pair of row tiles, quarter q, four column tiles): it reads a quarter
+// of the rows' weights and of four column tiles' panel, and writes its
+// subtree to plane q of Q ([4][B][M]); k_gemm_qcomb forms (t_0 + t_1) +
+// (t_2 + t_3), the same tree16, and applies OUT. With all four column tiles
+// of B <= 64 in one task, each weight quarter is read by one task only.
+// Eight waves: wave w owns row tile w % 2 and column tile w / 2. A chunk's
+// six 1 KB blocks (two row tiles, four column tiles) take one copy each
 // from waves 0..5; a stage holds GEMMQ_CPB chunks (one barrier per stage),
 // GEMMQ_STAGES - 1 stages ahead.
 constexpr uint32_t GEMMQ_CPB = 8, GEMMQ_STAGES = 3;
@@ -365,24 +366,24 @@ __global__ __launch_bounds__(512) void k_gemm_q(const float* __restrict__ Wp, ui
                                                 float* __restrict__ Q) {
   extern __shared__ float4 gsm[];  // [stages][GEMMQ_CPB chunks][6 blocks][64 lanes]
   const uint32_t wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-  const uint32_t rt = wave % 4, ct = wave / 4;
+  const uint32_t rt = wave % 2, ct = wave / 2;
   const uint32_t nch = panel_chunks(K), nrt = (M + 15) / 16, nct = (B + 15) / 16;
   const uint32_t nsc = (nch + GEMMQ_CPB - 1) / GEMMQ_CPB;  // stages of chunks per task
-  const uint32_t nrg = (nrt + 3) / 4, ncg = (nct + 1) / 2, ntask = 4 * nrg * ncg;
+  const uint32_t nrg = (nrt + 1) / 2, ncg = (nct + 3) / 4, ntask = 4 * nrg * ncg;
   const uint32_t mine = blockIdx.x < ntask ? (ntask - blockIdx.x + gridDim.x - 1) / gridDim.x : 0;
   const uint32_t total = mine * nsc;
   const uint32_t nld = wave < 6 ? GEMMQ_CPB : 0u;  // copies per stage
   const uint32_t lds0 = (uint32_t)(uintptr_t)gsm;
   // Task t = (x * 4 + q) * ncg + cg. Stage g's chunks into LDS stage st:
-  // block `wave` of each is row tile 4x + wave (waves 0..3) or column tile
-  // 2cg + wave - 4, quarter q. Tiles and chunks past the last load a real
+  // block `wave` of each is row tile 2x + wave (waves 0, 1) or column tile
+  // 4cg + wave - 2, quarter q. Tiles and chunks past the last load a real
   // one (never used), so every copying wave issues GEMMQ_CPB per stage.
   auto issue = [&](uint32_t g, uint32_t st) {
     const uint32_t t = blockIdx.x + gridDim.x * (g / nsc), i0 = (g % nsc) * GEMMQ_CPB;
     const uint32_t cg = t % ncg, xq = t / ncg, x = xq / 4, q = xq % 4;
     if (wave >= 6) return;
-    const float* src = wave < 4 ? Wp + (size_t)min(4 * x + wave, nrt - 1) * nch * PANEL_TILE
-                                : Xp + (size_t)min(2 * cg + wave - 4, nct - 1) * nch * PANEL_TILE;
+    const float* src = wave < 2 ? Wp + (size_t)min(2 * x + wave, nrt - 1) * nch * PANEL_TILE
+                                : Xp + (size_t)min(4 * cg + wave - 2, nct - 1) * nch * PANEL_TILE;
 #pragma unroll
     for (uint32_t c = 0; c < GEMMQ_CPB; ++c)
       dma16(src + (size_t)min(i0 + c, nch - 1) * PANEL_TILE + q * 256 + lane * 4,
@@ -408,7 +409,7 @@ __global__ __launch_bounds__(512) void k_gemm_q(const float* __restrict__ Wp, ui
 #pragma unroll
       for (uint32_t c = 0; c < GEMMQ_CPB; ++c) {
         a[c] = sa[(c * 6 + rt) * 64 + lane];
-        b[c] = sa[(c * 6 + 4 + ct) * 64 + lane];
+        b[c] = sa[(c * 6 + 2 + ct) * 64 + lane];
       }
 #pragma unroll
       for (uint32_t c = 0; c < GEMMQ_CPB; ++c) {
@@ -422,9 +423,9 @@ __global__ __launch_bounds__(512) void k_gemm_q(const float* __restrict__ Wp, ui
         }
       }
     }
-    const uint32_t T = 4 * x + rt, o = T * 16 + 4 * (lane / 16);
+    const uint32_t T = 2 * x + rt, o = T * 16 + 4 * (lane / 16);
     const f4v r = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-    const uint32_t bc = (2 * cg + ct) * 16 + lane % 16;
+    const uint32_t bc = (4 * cg + ct) * 16 + lane % 16;
     if (T < nrt && bc < B) {
       float* dst = Q + ((size_t)q * B + bc) * M + o;
       if (o + 4 <= M && (((size_t)q * B + bc) * M + o) % 4 == 0) {
@@ -538,34 +539,28 @@ __global__ __launch_bounds__(256) void k_b_rms(const float* __restrict__ X, uint
   if (lane == 0) inv[b] = r;
 }
 
-// QKV epilogue of the one-token path (phase_qkv), per (row, pair): scale,
-// bias, RoPE; q/k/v words tagged for the attention item; k, v into the
-// row's cache at its position.
-// QS (if not null): the product is still k_gemm_q's four subtree planes
-// ([4][nb][qkv_rows]), combined here as k_gemm_qcomb would.
-__global__ void k_b_qkv_epi(const Args* __restrict__ ap, const BRow* __restrict__ rows, uint32_t l,
-                            const float* __restrict__ Y, uint32_t ldy, const float* __restrict__ inv,
-                            u64* __restrict__ qkvt, uint32_t ldq, const float* __restrict__ QS,
-                            uint32_t nb) {
-  const Dims& d = ap->d;
-  const uint32_t b = blockIdx.y;
-  const uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
-  if (p >= d.qkv_rows / 2) return;
-  const BRow r = rows[b];
-  const uint32_t hb = p / d.half, i = p - hb * d.half;
+// QKV epilogue of the one-token path (phase_qkv) for pair i of head block
+// hb of batch row b: the product's rows r0 = hb * hd + i and r1 = r0 + half
+// (from Y, or combined from k_gemm_q's four subtree planes QS ([4][nb]
+// [qkv_rows]) as k_gemm_qcomb would), scaled by the row's 1/rms, biased,
+// and rotated (q and k heads) -- phase_qkv's expressions.
+__device__ __forceinline__ float2 qkv_epi_pair(const Args& a, uint32_t l, uint32_t pos, uint32_t b,
+                                               uint32_t hb, uint32_t i, const float* __restrict__ Y,
+                                               uint32_t ldy, const float* __restrict__ QS,
+                                               uint32_t nb, float iv) {
+  const Dims& d = a.d;
   const uint32_t r0 = hb * d.hd + i, r1 = r0 + d.half;
   float4 e = make_float4(1.0f, 0.0f, 0.0f, 0.0f);
   if (hb < d.nh + d.nkv) {
-    const float2 cs = ap->rope[(size_t)r.pos * d.half + i];
+    const float2 cs = a.rope[(size_t)pos * d.half + i];
     e.x = cs.x;
     e.y = cs.y;
   }
-  const float* bias = ap->layers[l].bqkv;
+  const float* bias = a.layers[l].bqkv;
   if (bias) {
     e.z = bias[r0];
     e.w = bias[r0 + d.half];
   }
-  const float iv = inv[b];
   float y0, y1;
   if (QS) {
     const size_t plane = (size_t)nb * d.qkv_rows, e0 = (size_t)b * d.qkv_rows + r0, e1 = e0 + d.half;
@@ -582,16 +577,38 @@ __global__ void k_b_qkv_epi(const Args* __restrict__ ap, const BRow* __restrict_
     a0 = y0 * e.x - y1 * e.y;
     a1 = y1 * e.x + y0 * e.y;
   }
+  return make_float2(a0, a1);
+}
+
+// k (hb < nh + nkv) or v rows of head block hb into the row's cache at its
+// position (model.rs:466-467).
+__device__ __forceinline__ void qkv_epi_cache(const Dims& d, const BRow& r, uint32_t l, uint32_t hb,
+                                              uint32_t i, float2 v) {
+  const bool is_k = hb < d.nh + d.nkv;
+  const uint32_t gi = is_k ? hb - d.nh : hb - d.nh - d.nkv;
+  float* row = (is_k ? r.kc : r.vc) + (((size_t)l * d.nkv + gi) * r.cap + r.pos) * d.kvs;
+  row[i] = v.x;
+  row[i + d.half] = v.y;
+}
+
+// QKV epilogue per (row, pair): q/k/v words tagged for the attention items;
+// k, v into the row's cache at its position.
+__global__ void k_b_qkv_epi(const Args* __restrict__ ap, const BRow* __restrict__ rows, uint32_t l,
+                            const float* __restrict__ Y, uint32_t ldy, const float* __restrict__ inv,
+                            u64* __restrict__ qkvt, uint32_t ldq, const float* __restrict__ QS,
+                            uint32_t nb) {
+  const Dims& d = ap->d;
+  const uint32_t b = blockIdx.y;
+  const uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= d.qkv_rows / 2) return;
+  const BRow r = rows[b];
+  const uint32_t hb = p / d.half, i = p - hb * d.half;
+  const uint32_t r0 = hb * d.hd + i, r1 = r0 + d.half;
+  const float2 v = qkv_epi_pair(*ap, l, r.pos, b, hb, i, Y, ldy, QS, nb, inv[b]);
   const u64 g = (u64)gen_of(d, r.tick, l, PH_QKV) << 32;
-  qkvt[(size_t)b * ldq + r0] = g | __float_as_uint(a0);
-  qkvt[(size_t)b * ldq + r1] = g | __float_as_uint(a1);
-  if (hb >= d.nh) {
-    const bool is_k = hb < d.nh + d.nkv;
-    const uint32_t gi = is_k ? hb - d.nh : hb - d.nh - d.nkv;
-    float* row = (is_k ? r.kc : r.vc) + (((size_t)l * d.nkv + gi) * r.cap + r.pos) * d.kvs;
-    row[i] = a0;
-    row[i + d.half] = a1;
-  }
+  qkvt[(size_t)b * ldq + r0] = g | __float_as_uint(v.x);
+  qkvt[(size_t)b * ldq + r1] = g | __float_as_uint(v.y);
+  if (hb >= d.nh) qkv_epi_cache(d, r, l, hb, i, v);
 }
 
 // LDS of the batched kernels that run one-token functions: no weight
@@ -604,26 +621,8 @@ __device__ __forceinline__ Lds lds_init_rows(const Dims& d) {
   return s;
 }
 
-// Attention items of every row, one per workgroup: entry x of `items` is
-// (row, item) packed as row << 16 | item, and the workgroup runs that item
-// with the one-token path's phase_attn in its grouped form (item = (kv head,
-// chunk) with all the group's query heads; each head's arithmetic is the
-// one-token path's), reading the row's tagged q/k/v and writing its tagged
-// partials.
-__global__ __launch_bounds__(BLOCK) void k_b_attn(const Args* __restrict__ rargs,
-                                                  const BRow* __restrict__ rows,
-                                                  const uint32_t* __restrict__ items, uint32_t l) {
-  const uint32_t e = items[blockIdx.x], b = e >> 16, x = e & 0xffffu;
-  const Args& a = rargs[b];
-  const Lds s = lds_init_rows(a.d);
-  const BRow r = rows[b];
-  phase_attn<true>(a, l, r.tick, r.pos, x, 0x10000u, s);  // stride past every item: just item x
-}
-
-// The same items with workgroups of the NCW attention waves alone (they
-// also poll and publish) and only the attention's LDS, so that several
-// items share a CU: one row's chunk is a chain of dependent loads and
-// barriers that a lone workgroup cannot keep the CU busy with.
+// LDS of the attention-only workgroups: the wait control words, then the
+// attention's scratch.
 __device__ __forceinline__ Lds lds_init_attn() {
   extern __shared__ float lds_raw[];
   Lds s;
@@ -636,8 +635,18 @@ __device__ __forceinline__ Lds lds_init_attn() {
   __syncthreads();
   return s;
 }
-// One score pass and four value steps in flight per lane keep the kernel
-// within 128 VGPRs, four workgroups per CU.
+
+// Attention items of every row, one per workgroup: entry x of `items` is
+// (row, item) packed as row << 16 | item, and the workgroup runs that item
+// with the one-token path's phase_attn in its grouped form (item = (kv head,
+// chunk) with all the group's query heads; each head's arithmetic is the
+// one-token path's), reading the row's tagged q/k/v and writing its tagged
+// partials. The workgroups are the NCW attention waves alone (they also
+// poll and publish) with only the attention's LDS, so that several items
+// share a CU: one row's chunk is a chain of dependent loads and barriers
+// that a lone workgroup cannot keep the CU busy with. One score pass and
+// four value steps in flight per lane keep the kernel within 128 VGPRs,
+// four workgroups per CU.
 __global__ __launch_bounds__(NCW * WAVE) __attribute__((amdgpu_waves_per_eu(4))) void k_b_attn_w(
     const Args* __restrict__ rargs, const BRow* __restrict__ rows,
     const uint32_t* __restrict__ items, uint32_t l) {
@@ -646,6 +655,74 @@ __global__ __launch_bounds__(NCW * WAVE) __attribute__((amdgpu_waves_per_eu(4)))
   const Lds s = lds_init_attn();
   const BRow r = rows[b];
   phase_attn<true, 0, NCW, 1, 4>(a, l, r.tick, r.pos, x, 0x10000u, s);
+}
+
+// The same attention items of rows with distinct caches (a lockstep step)
+// with the QKV epilogue before and the chunk combine after, so that one
+// launch replaces three. Each item forms its kv group's q/k/v from the QKV
+// product itself (qkv_epi_pair; the chunk-0 item also writes k and v into
+// the cache: no item of the step reads that row, as position pos comes from
+// LDS), runs phase_attn, and counts itself done in cnt[b][g] (an
+// agent-scope add); the group's last item waits for the tags of the group's
+// chunk partials, combines them (combine_scales / combine_value, as
+// k_b_comb) into the attention panel and sets the count back to 0.
+__global__ __launch_bounds__(NCW * WAVE) __attribute__((amdgpu_waves_per_eu(4))) void k_b_attn_f(
+    const Args* __restrict__ rargs, const BRow* __restrict__ rows,
+    const uint32_t* __restrict__ items, uint32_t l, const float* __restrict__ Y, uint32_t ldy,
+    const float* __restrict__ QS, uint32_t nb, const float* __restrict__ inv,
+    uint32_t* __restrict__ cnt, float* __restrict__ attp) {
+  const uint32_t e = items[blockIdx.x], b = e >> 16, x = e & 0xffffu;
+  const Args& a = rargs[b];
+  const Lds s = lds_init_attn();
+  const BRow r = rows[b];
+  const Dims& d = a.d;
+  const uint32_t nch = attn_nchunks(r.pos), g = x / nch, c = x - g * nch;
+  const float iv = inv[b];
+  auto fill = [&](uint32_t gg, float* qs, float* kn, float* vn) {
+    for (uint32_t u = threadIdx.x; u < (d.group + 2) * d.half; u += blockDim.x) {
+      const uint32_t j = u / d.half, i = u - j * d.half;
+      const uint32_t hb = j < d.group ? gg * d.group + j : (j == d.group ? d.nh + gg : d.nh + d.nkv + gg);
+      const float2 v = qkv_epi_pair(a, l, r.pos, b, hb, i, Y, ldy, QS, nb, iv);
+      float* dst = j < d.group ? qs + j * d.hd : (j == d.group ? kn : vn);
+      lds_st(dst + i, v.x);
+      lds_st(dst + i + d.half, v.y);
+      if (j >= d.group && c == 0) qkv_epi_cache(d, r, l, hb, i, v);
+    }
+    __syncthreads();
+    return true;
+  };
+  phase_attn<true, 0, NCW, 1, 4>(a, l, r.tick, r.pos, x, 0x10000u, s, fill);
+  // Every wave has issued its partials' stores. No fence: the last item
+  // waits for the partials' tags instead (a device-scope fence would write
+  // back and invalidate the whole L2 of the XCD).
+  __syncthreads();
+  AS_LDS uint32_t* last = lptr(reinterpret_cast<uint32_t*>(s.red));
+  if (threadIdx.x == 0) {
+    uint32_t* cg = cnt + (size_t)b * d.nkv + g;
+    const uint32_t done = __hip_atomic_fetch_add(cg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *last = done + 1 == nch;
+    if (done + 1 == nch) __hip_atomic_store(cg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!*last) return;
+  const uint32_t hs = d.hd + 2, grp = d.group, n1 = nch * hs;
+  float* part = s.scr;                      // [grp][nch][hs]
+  float* sc = part + MAX_GROUP * MAX_ACHUNKS * hs;  // [MAX_GROUP][MAX_ACHUNKS]
+  float* ls = sc + MAX_GROUP * MAX_ACHUNKS;  // [MAX_GROUP]
+  if (!poll_gather<4>(gather_strided(a.mb_part + (size_t)g * grp * MAX_ACHUNKS * hs, n1, grp,
+                                     MAX_ACHUNKS * hs, gen_of(d, r.tick, l, PH_ATTN), part),
+                      NCW, a.st, s.ctl))
+    return;
+  for (uint32_t k = threadIdx.x; k < grp; k += blockDim.x)
+    ls[k] = combine_scales([&](uint32_t i) { return lds_ld(part + k * n1 + i); }, nch, hs,
+                           sc + k * MAX_ACHUNKS);
+  __syncthreads();
+  for (uint32_t v = threadIdx.x; v < grp * d.hd; v += blockDim.x) {
+    const uint32_t k = v / d.hd, dd = v - k * d.hd, u = (g * grp + k) * d.hd + dd;
+    attp[panel_at(b, u, panel_chunks(d.q))] =
+        combine_value([&](uint32_t i) { return lds_ld(part + k * n1 + i); }, nch, hs, dd,
+                      sc + k * MAX_ACHUNKS, ls[k]);
+  }
 }
 
 // ----------------------------------------------------- tiled attention

@@ -495,7 +495,9 @@ static int apply_layout(defer_gpu_model* m, uint32_t G) {
   m->lds_bytes = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr + d.lds_stg) * sizeof(float) +
                  (size_t)d.lds_pub * 2 * sizeof(u64);
   m->lds_rows = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr) * sizeof(float);
-  m->lds_attn = (size_t)(4 + 64 + ((scr_attn + 3) & ~3u)) * sizeof(float);
+  // k_b_attn_f's combine: the group's chunk partials, their weights and totals.
+  const uint32_t scr_fcomb = MAX_GROUP * MAX_ACHUNKS * hs + MAX_GROUP * MAX_ACHUNKS + MAX_GROUP;
+  m->lds_attn = (size_t)(4 + 64 + ((std::max(scr_attn, scr_fcomb) + 3) & ~3u)) * sizeof(float);
 
   m->G = G;
   const void* kernels[] = {m->persistent, (const void*)k_phase, (const void*)k_samp_a,
@@ -507,16 +509,16 @@ static int apply_layout(defer_gpu_model* m, uint32_t G) {
       return fail(DEFER_GPU_E_HIP, "LDS attribute (%zu bytes): %s", m->lds_bytes,
                   hipGetErrorString(e));
   }
-  for (const void* kf : {(const void*)k_b_attn, (const void*)k_b_sample}) {
+  for (const void* kf : {(const void*)k_b_sample}) {
     const hipError_t e =
         hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)m->lds_rows);
     if (e != hipSuccess)
       return fail(DEFER_GPU_E_HIP, "LDS attribute (%zu bytes): %s", m->lds_rows,
                   hipGetErrorString(e));
   }
-  {
-    const hipError_t e = hipFuncSetAttribute((const void*)k_b_attn_w,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)m->lds_attn);
+  for (const void* kf : {(const void*)k_b_attn_w, (const void*)k_b_attn_f}) {
+    const hipError_t e =
+        hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)m->lds_attn);
     if (e != hipSuccess)
       return fail(DEFER_GPU_E_HIP, "LDS attribute (%zu bytes): %s", m->lds_attn, hipGetErrorString(e));
   }
@@ -1658,6 +1660,7 @@ struct BatchWs {
   uint32_t *sel = nullptr, *lgen = nullptr, *stick = nullptr, *swords = nullptr, *sout = nullptr;
   uint32_t* items = nullptr;  // attention (row, item) list, or tiled attention tasks
   uint32_t* tiles = nullptr;  // tiled attention: first batch row of each tile
+  uint32_t* CNT = nullptr;    // [rows][nkv] finished attention items (k_b_attn_f), 0 between launches
   StateSet* sets = nullptr;   // [rows] cache states to set after a batch
   DevState* st = nullptr;
 };
@@ -1666,7 +1669,7 @@ static void batch_ws_release(BatchWs* w) {
   if (!w) return;
   void* ps[] = {w->X, w->Y, w->INV, w->XP, w->XQ, w->LINV, w->QS, w->QKVT, w->PART,
                 w->LOGT, w->VMAX, w->VARG, w->VSUM, w->drows, w->rargs, w->largs, w->sel,
-                w->lgen, w->stick, w->swords, w->sout, w->items, w->tiles, w->sets, w->st};
+                w->lgen, w->stick, w->swords, w->sout, w->items, w->tiles, w->CNT, w->sets, w->st};
   for (void* p : ps) (void)hipFree(p);
   *w = BatchWs();
 }
@@ -1700,6 +1703,8 @@ static int ensure_ws(defer_gpu_model* m, uint32_t rows, uint32_t lm) {
   HIP_TRY(hipMalloc(&w.rargs, (size_t)R * sizeof(Args)));
   HIP_TRY(hipMalloc(&w.items, (size_t)R * d.nkv * MAX_ACHUNKS * d.group * sizeof(uint32_t)));
   HIP_TRY(hipMalloc(&w.tiles, ((size_t)R / 16 + 2) * sizeof(uint32_t)));
+  HIP_TRY(hipMalloc(&w.CNT, (size_t)R * d.nkv * sizeof(uint32_t)));
+  HIP_TRY(hipMemset(w.CNT, 0, (size_t)R * d.nkv * sizeof(uint32_t)));
   HIP_TRY(hipMalloc(&w.sets, (size_t)R * sizeof(StateSet)));
   const uint32_t L1 = std::max(Lm, 1u);
   HIP_TRY(hipMalloc(&w.XQ, panel_floats(std::max(R, L1), kmax) * sizeof(float)));
@@ -1804,7 +1809,7 @@ static bool launch_gemm_out(hipStream_t s, const float* Wp, uint32_t M, uint32_t
   // (the subtrees in QS, then combined); otherwise one row tile per task.
   if (nct <= 4 && !(nct == 4 && nrg >= ncu) && QS && nrg < ncu && (size_t)4 * B * M <= qs_floats) {
     const uint32_t per_cu = gemm_q_lds_bytes() <= 80 * 1024 ? 2 : 1;
-    const uint32_t grid = std::min(4 * nrg * ((nct + 1) / 2), per_cu * ncu);
+    const uint32_t grid = std::min(4 * ((M + 31) / 32) * ((nct + 3) / 4), per_cu * ncu);
     if (K % 64 == 0)
       k_gemm_q<false><<<grid, GEMM_WAVES * WAVE, gemm_q_lds_bytes(), s>>>(Wp, M, K, Xp, B, QS);
     else
@@ -1953,6 +1958,15 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
   bool tiled = d.hd == AT_HD && d.kvs == AT_HD && rows[n - 1].pos < ACHUNK * MAX_ACHUNKS;
   for (uint32_t b = 1; b < n && tiled; ++b)
     tiled = rcache[b] == rcache[0] && rows[b].pos == rows[0].pos + b;
+  // Rows of distinct caches (a lockstep step) run the attention with its
+  // QKV epilogue and combine in one launch (k_b_attn_f): no row reads a
+  // cache row that another row's epilogue writes.
+  bool fused = !tiled;
+  if (fused) {
+    std::vector<const defer_gpu_cache*> cs(rcache, rcache + n);
+    std::sort(cs.begin(), cs.end());
+    fused = std::adjacent_find(cs.begin(), cs.end()) == cs.end();
+  }
   std::vector<uint32_t> items, tiles;
   if (tiled) {
     tiles.push_back(0);
@@ -2003,18 +2017,25 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
       planes = launch_gemm(s, m->gemm_ncu, GO_PLAIN, m->p_qkv[l], d.qkv_rows, d.h, w.XP, n, w.Y, ldy,
                            nullptr, nullptr, nullptr, w.QS, qs_n, nullptr, 0.0f, true);
     }
-    k_b_qkv_epi<<<dim3((d.qkv_rows / 2 + 255) / 256, n), 256, 0, s>>>(
-        w.rargs, w.drows, l, w.Y, ldy, w.INV, w.QKVT, d.qkv_rows, planes ? w.QS : nullptr, n);
-    {
+    if (fused) {
       ProfSpan ps(m, 1, attn_flop);
-      if (tiled)
-        k_b_attn_tile<<<(uint32_t)items.size(), 256, attn_tile_lds(d.group), s>>>(
-            d, w.drows, w.items, w.tiles, l, w.QKVT, w.PART, part_words(d));
-      else
-        k_b_attn_w<<<(uint32_t)items.size(), NCW * WAVE, m->lds_attn, s>>>(w.rargs, w.drows, w.items, l);
+      k_b_attn_f<<<(uint32_t)items.size(), NCW * WAVE, m->lds_attn, s>>>(
+          w.rargs, w.drows, w.items, l, w.Y, ldy, planes ? w.QS : nullptr, n, w.INV, w.CNT, w.XQ);
+    } else {
+      k_b_qkv_epi<<<dim3((d.qkv_rows / 2 + 255) / 256, n), 256, 0, s>>>(
+          w.rargs, w.drows, l, w.Y, ldy, w.INV, w.QKVT, d.qkv_rows, planes ? w.QS : nullptr, n);
+      {
+        ProfSpan ps(m, 1, attn_flop);
+        if (tiled)
+          k_b_attn_tile<<<(uint32_t)items.size(), 256, attn_tile_lds(d.group), s>>>(
+              d, w.drows, w.items, w.tiles, l, w.QKVT, w.PART, part_words(d));
+        else
+          k_b_attn_w<<<(uint32_t)items.size(), NCW * WAVE, m->lds_attn, s>>>(w.rargs, w.drows,
+                                                                              w.items, l);
+      }
+      k_b_comb<<<dim3(n, (d.nh + COMB_HEADS_PER_BLOCK - 1) / COMB_HEADS_PER_BLOCK), 256, 0, s>>>(
+          d, w.drows, w.PART, part_words(d), w.XQ);
     }
-    k_b_comb<<<dim3(n, (d.nh + COMB_HEADS_PER_BLOCK - 1) / COMB_HEADS_PER_BLOCK), 256, 0, s>>>(
-        d, w.drows, w.PART, part_words(d), w.XQ);
     bool inv_done;
     {
       ProfSpan ps(m, 0, 2.0 * d.h * d.q * n);

@@ -23,6 +23,8 @@
 // Attention, lm_head and the sampler run on pollers and compute waves.
 #pragma once
 
+#include <type_traits>
+
 #include "device.h"
 
 namespace DG_NS {
@@ -889,10 +891,15 @@ __device__ __forceinline__ bool phase_qkv(const Args& a, uint32_t l, uint32_t ti
 // waves alone passes 0). NPW: the waves that poll q/k/v and publish the
 // partials. KU, VU: the loads in flight. None of these changes the
 // arithmetic.
+// FillFn: where q/k/v come from. NoFill polls the tagged words of the QKV
+// phase; otherwise fill(g, qs, kn, vn) writes kv group g's query rows, k and
+// v into LDS itself (all threads call it; it ends with a barrier).
+struct NoFill {};
 template <bool GROUPED = false, uint32_t AW0 = NPOLL, uint32_t NPW = NPOLL, uint32_t KU = KU_DEF,
-          uint32_t VU = VU_DEF>
+          uint32_t VU = VU_DEF, class FillFn = NoFill>
 __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t tick, uint32_t pos,
-                                           uint32_t wg, uint32_t G, const Lds& s) {
+                                           uint32_t wg, uint32_t G, const Lds& s,
+                                           const FillFn& fill = FillFn()) {
   const Dims d = shape_dims(a.d);
   const uint32_t nch = attn_nchunks(pos), CH = attn_chunk(pos);
   const uint32_t n_items = GROUPED ? d.nkv * nch : attn_items(d, pos);
@@ -945,11 +952,15 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
       for (uint32_t u = 0; u < VU; ++u)
         vr[u] = ldg4(vb + (size_t)min(t0 + vw + u * vstep, pos - 1) * d.kvs);
     }
-    if (!poll_gather<GROUPED ? 8 / NPW : 1, 1, 1>(gather_vec(a.mb_qkv + (size_t)(g * grp + j0) * hd, NH1 * hd, gen_in, qs),
-                              gather_vec(a.mb_qkv + d.q + g * hd, hd, gen_in, kn),
-                              gather_vec(a.mb_qkv + d.q + d.kv + g * hd, hd, gen_in, vn), NPW,
-                              a.st, s.ctl))
-      return false;
+    bool got;
+    if constexpr (std::is_same<FillFn, NoFill>::value)
+      got = poll_gather<GROUPED ? 8 / NPW : 1, 1, 1>(
+          gather_vec(a.mb_qkv + (size_t)(g * grp + j0) * hd, NH1 * hd, gen_in, qs),
+          gather_vec(a.mb_qkv + d.q + g * hd, hd, gen_in, kn),
+          gather_vec(a.mb_qkv + d.q + d.kv + g * hd, hd, gen_in, vn), NPW, a.st, s.ctl);
+    else
+      got = fill(g, qs, kn, vn);
+    if (!got) return false;
     // 1. scores, KU passes per round (pass u of a round uses kr[u], then
     // requests the pass KU later into it)
     for (uint32_t pb0 = t0; att && pb0 < t1; pb0 += KU * sstep) {
