@@ -119,31 +119,51 @@ __global__ __launch_bounds__(512) void k_gemm(const float* __restrict__ Wp, uint
   constexpr uint32_t NT = 4 + TN;                    // tiles per stage
   constexpr uint32_t WN = TN >= 2 ? TN / 2 : 1;      // column tiles per wave
   constexpr uint32_t NQ = 4 * NT;                    // 1 KB copies per stage
-  const uint32_t wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+  // The wave index is uniform: scalar registers and branches for it.
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE), lane = threadIdx.x % WAVE;
   const uint32_t rt = wave % 4, half = wave / 4;
   const bool mfma_wave = TN >= 2 || half == 0;
   const uint32_t nld = (NQ - wave + GEMM_WAVES - 1) / GEMM_WAVES;  // this wave's copies per stage
+  const uint32_t gdx = gridDim.x;  // kept in a register (a reload would wait for every LDS read)
   const uint32_t nch = panel_chunks(K), nrt = (M + 15) / 16, nct = (B + 15) / 16;
   const uint32_t nrg = (nrt + 3) / 4, ngy = (ncols + TN - 1) / TN, ntask = nrg * ngy;
-  const uint32_t mine = blockIdx.x < ntask ? (ntask - blockIdx.x + gridDim.x - 1) / gridDim.x : 0;
+  const uint32_t mine = blockIdx.x < ntask ? (ntask - blockIdx.x + gdx - 1) / gdx : 0;
   const uint32_t total = mine * nch;  // chunks of this workgroup's tasks, in order
   const uint32_t lds0 = (uint32_t)(uintptr_t)gsm;
-  // Chunk g into stage st: copies wave, wave + 8, ... of the stage's
-  // (tile, quarter) list. Tiles past the last one load a real tile (never
-  // used), so a wave issues the same number of copies for every chunk.
-  auto issue = [&](uint32_t g, uint32_t st) {
-    const uint32_t t = blockIdx.x + gridDim.x * (g / nch), i = g % nch;
-    const uint32_t x = t % nrg, y = t / nrg, C0 = cbase + y * TN;
-    const uint32_t sb = lds0 + st * NT * PANEL_TILE * 4;
+  // The copies run ahead of the MFMAs through the workgroup's chunks in
+  // order: chunk ci of task ct is next. A wave's copies of a stage are
+  // entries wave, wave + 8, ... of the stage's (tile, quarter) list; cb[j]
+  // is the tile of its copy j in task ct (tiles past the last one load a
+  // real tile, never used, so a wave issues the same number of copies for
+  // every chunk). Only a new task divides.
+  constexpr uint32_t MAXJ = (NQ + GEMM_WAVES - 1) / GEMM_WAVES;
+  uint32_t ct = blockIdx.x, ci = 0;
+  const float* cb[MAXJ];
+  auto set_task = [&]() {
+    const uint32_t x = ct % nrg, C0 = cbase + (ct / nrg) * TN;
 #pragma unroll
-    for (uint32_t f = wave; f < NQ; f += GEMM_WAVES) {
-      const uint32_t tile = f / 4, q = f % 4;
-      const float* src = tile < 4 ? Wp + ((size_t)min(4 * x + tile, nrt - 1) * nch + i) * PANEL_TILE
-                                  : Xp + ((size_t)min(C0 + tile - 4, nct - 1) * nch + i) * PANEL_TILE;
-      dma16(src + q * 256 + lane * 4, sb + f * 1024);
+    for (uint32_t j = 0; j < MAXJ; ++j) {
+      const uint32_t tile = (wave + GEMM_WAVES * j) / 4;
+      cb[j] = tile < 4 ? Wp + (size_t)min(4 * x + tile, nrt - 1) * nch * PANEL_TILE
+                       : Xp + (size_t)min(C0 + tile - 4, nct - 1) * nch * PANEL_TILE;
     }
   };
-  for (uint32_t g = 0; g + 1 < GEMM_STAGES && g < total; ++g) issue(g, g);
+  set_task();
+  // The next chunk into stage st.
+  auto issue = [&](uint32_t st) {
+    const uint32_t sb = lds0 + st * NT * PANEL_TILE * 4;
+#pragma unroll
+    for (uint32_t j = 0; j < MAXJ; ++j) {
+      const uint32_t f = wave + GEMM_WAVES * j;
+      if (f < NQ) dma16(cb[j] + (size_t)ci * PANEL_TILE + (f % 4) * 256 + lane * 4, sb + f * 1024);
+    }
+    if (++ci == nch) {
+      ci = 0;
+      ct += gdx;
+      set_task();
+    }
+  };
+  for (uint32_t g = 0; g + 1 < GEMM_STAGES && g < total; ++g) issue(g);
   for (uint32_t k = 0; k < mine; ++k) {
     f4v acc[WN][16];
 #pragma unroll
@@ -158,8 +178,7 @@ __global__ __launch_bounds__(512) void k_gemm(const float* __restrict__ Wp, uint
       const uint32_t g = k * nch + i;
       stage_wait(min(GEMM_STAGES - 2, total - 1 - g) * nld);
       __syncthreads();
-      if (g + GEMM_STAGES - 1 < total)
-        issue(g + GEMM_STAGES - 1, (g + GEMM_STAGES - 1) % GEMM_STAGES);
+      if (g + GEMM_STAGES - 1 < total) issue((g + GEMM_STAGES - 1) % GEMM_STAGES);
       const float4* sa = gsm + (g % GEMM_STAGES) * NT * 256;
 #pragma unroll
       for (int q = 0; q < 4; ++q) a[q] = sa[(rt * 4 + q) * 64 + lane];
@@ -200,7 +219,7 @@ __global__ __launch_bounds__(512) void k_gemm(const float* __restrict__ Wp, uint
       }
     }
     // The task's outputs, one tile at a time.
-    const uint32_t tk = blockIdx.x + gridDim.x * k;
+    const uint32_t tk = blockIdx.x + gdx * k;
     const uint32_t T = 4 * (tk % nrg) + rt, C0 = cbase + (tk / nrg) * TN + half * WN;
 #pragma unroll
     for (int t = 0; t < (int)WN; ++t) {
@@ -262,15 +281,16 @@ __global__ __launch_bounds__(512) void k_gemm_n(const float* __restrict__ Wp, ui
   extern __shared__ float4 gsm[];  // [stages][5 tiles][4 quarters][64 lanes], then [4][64] f4v
   constexpr uint32_t NT = 5, NQ = 4 * NT;
   f4v* half_sum = reinterpret_cast<f4v*>(gsm + GEMMN_STAGES * NT * 256);
-  const uint32_t wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE), lane = threadIdx.x % WAVE;
+  const uint32_t gdx = gridDim.x;  // kept in a register (a reload would wait for every LDS read)
   const uint32_t ct = wave % 4, h = wave / 4;
   const uint32_t nch = panel_chunks(K), nrt = (M + 15) / 16, nct = (B + 15) / 16;
   const uint32_t nld = (NQ - wave + GEMM_WAVES - 1) / GEMM_WAVES;
-  const uint32_t mine = blockIdx.x < nrt ? (nrt - blockIdx.x + gridDim.x - 1) / gridDim.x : 0;
+  const uint32_t mine = blockIdx.x < nrt ? (nrt - blockIdx.x + gdx - 1) / gdx : 0;
   const uint32_t total = mine * nch;
   const uint32_t lds0 = (uint32_t)(uintptr_t)gsm;
   auto issue = [&](uint32_t g, uint32_t st) {
-    const uint32_t T = blockIdx.x + gridDim.x * (g / nch), i = g % nch;
+    const uint32_t T = blockIdx.x + gdx * (g / nch), i = g % nch;
     const uint32_t sb = lds0 + st * NT * PANEL_TILE * 4;
 #pragma unroll
     for (uint32_t f = wave; f < NQ; f += GEMM_WAVES) {
@@ -315,7 +335,7 @@ __global__ __launch_bounds__(512) void k_gemm_n(const float* __restrict__ Wp, ui
     const f4v t8 = (p4[0] + p4[1]) + (p4[2] + p4[3]);
     if (h == 1) half_sum[ct * 64 + lane] = t8;
     __syncthreads();
-    const uint32_t T = blockIdx.x + gridDim.x * k;
+    const uint32_t T = blockIdx.x + gdx * k;
     if (h == 0 && ct < nct) {
       const f4v r = t8 + half_sum[ct * 64 + lane];
       const uint32_t b = ct * 16 + lane % 16;
@@ -365,12 +385,13 @@ __global__ __launch_bounds__(512) void k_gemm_q(const float* __restrict__ Wp, ui
                                                 const float* __restrict__ Xp, uint32_t B,
                                                 float* __restrict__ Q) {
   extern __shared__ float4 gsm[];  // [stages][GEMMQ_CPB chunks][6 blocks][64 lanes]
-  const uint32_t wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE), lane = threadIdx.x % WAVE;
+  const uint32_t gdx = gridDim.x;  // kept in a register (a reload would wait for every LDS read)
   const uint32_t rt = wave % 2, ct = wave / 2;
   const uint32_t nch = panel_chunks(K), nrt = (M + 15) / 16, nct = (B + 15) / 16;
   const uint32_t nsc = (nch + GEMMQ_CPB - 1) / GEMMQ_CPB;  // stages of chunks per task
   const uint32_t nrg = (nrt + 1) / 2, ncg = (nct + 3) / 4, ntask = 4 * nrg * ncg;
-  const uint32_t mine = blockIdx.x < ntask ? (ntask - blockIdx.x + gridDim.x - 1) / gridDim.x : 0;
+  const uint32_t mine = blockIdx.x < ntask ? (ntask - blockIdx.x + gdx - 1) / gdx : 0;
   const uint32_t total = mine * nsc;
   const uint32_t nld = wave < 6 ? GEMMQ_CPB : 0u;  // copies per stage
   const uint32_t lds0 = (uint32_t)(uintptr_t)gsm;
@@ -379,7 +400,7 @@ __global__ __launch_bounds__(512) void k_gemm_q(const float* __restrict__ Wp, ui
   // 4cg + wave - 2, quarter q. Tiles and chunks past the last load a real
   // one (never used), so every copying wave issues GEMMQ_CPB per stage.
   auto issue = [&](uint32_t g, uint32_t st) {
-    const uint32_t t = blockIdx.x + gridDim.x * (g / nsc), i0 = (g % nsc) * GEMMQ_CPB;
+    const uint32_t t = blockIdx.x + gdx * (g / nsc), i0 = (g % nsc) * GEMMQ_CPB;
     const uint32_t cg = t % ncg, xq = t / ncg, x = xq / 4, q = xq % 4;
     if (wave >= 6) return;
     const float* src = wave < 2 ? Wp + (size_t)min(2 * x + wave, nrt - 1) * nch * PANEL_TILE
@@ -391,7 +412,7 @@ __global__ __launch_bounds__(512) void k_gemm_q(const float* __restrict__ Wp, ui
   };
   for (uint32_t g = 0; g + 1 < GEMMQ_STAGES && g < total; ++g) issue(g, g);
   for (uint32_t k = 0; k < mine; ++k) {
-    const uint32_t t = blockIdx.x + gridDim.x * k;
+    const uint32_t t = blockIdx.x + gdx * k;
     const uint32_t cg = t % ncg, xq = t / ncg, x = xq / 4, q = xq % 4;
     f4v acc[4];
 #pragma unroll
