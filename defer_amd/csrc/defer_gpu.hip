@@ -1979,12 +1979,18 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
         for (uint32_t g = 0; g < d.nkv; ++g) items.push_back(t << 16 | c << 8 | g);
     }
   } else {
-    items.reserve((size_t)n * d.nkv);
-    for (uint32_t b = 0; b < n; ++b) {
-      // Grouped items (kv head, chunk): every query head of the group in one.
-      const uint32_t ni = d.nkv * attn_nchunks(rows[b].pos);
-      for (uint32_t x = 0; x < ni; ++x) items.push_back(b << 16 | x);  // rows <= 2048, items < 2^16
-    }
+    // Grouped items x = (kv head, chunk): every query head of the group in
+    // one (rows <= 2048, items < 2^16). Full chunks are listed before each
+    // row's last, shorter one, so that the longest items are dispatched
+    // first and the short ones fill in behind them.
+    items.reserve((size_t)n * d.nkv * 2);
+    for (int last = 0; last < 2; ++last)
+      for (uint32_t b = 0; b < n; ++b) {
+        const uint32_t nch = attn_nchunks(rows[b].pos);
+        for (uint32_t g = 0; g < d.nkv; ++g)
+          for (uint32_t c = last ? nch - 1 : 0; c < (last ? nch : nch - 1); ++c)
+            items.push_back(b << 16 | (g * nch + c));
+      }
   }
   // attention flop per layer: scores and weighted values, 2 * hd each per
   // (query head, position)
