@@ -583,12 +583,14 @@ __device__ __forceinline__ float rms_inv(const float* x, uint32_t n, float eps, 
 
 // Matvec passes. A compute wave takes the rows of its items four at a time
 // (a quad pass, device.h): lane 16*r + s computes segment s of row slot r.
-// Pair kinds put items k and k + NCW in the slots (gate/up or the two RoPE
-// rows of each), single-row kinds items k, k + NCW, k + 2*NCW, k + 3*NCW; a
-// wave's passes start at items cw, cw + PSTEP, ...
+// Pair kinds put items k and k + n in the slots (gate/up or the two RoPE
+// rows of each), single-row kinds items k, k + n, k + 2n, k + 3n, where n is
+// the number of waves that share the phase's items (NCW where rows are
+// staged, every wave where they are streamed); a wave's passes start at
+// items cw, cw + n * pass_items, ...
 __host__ __device__ constexpr uint32_t pass_items(bool pair) { return pair ? 2u : 4u; }
-__device__ __forceinline__ uint32_t slot_item(bool pair, uint32_t k, uint32_t r) {
-  return k + NCW * (pair ? r / 2 : r);
+__device__ __forceinline__ uint32_t slot_item(bool pair, uint32_t k, uint32_t r, uint32_t n = NCW) {
+  return k + n * (pair ? r / 2 : r);
 }
 
 // A compute wave's first pass of a staged matvec phase: the lane's
@@ -690,49 +692,81 @@ __device__ __forceinline__ MvHook mv_hook(const Stager& sg, LoadOp op, Preload& 
   return h;
 }
 
-// body(k, y0, y1) for every item k of `kind` dealt to compute wave cw, with
-// its dot products against the LDS vector x (y1 = 0 for single-row kinds),
-// wave-uniform. Staged: the preloaded first pass, then further passes read
-// from LDS. Otherwise each lane streams its segment of its row from memory.
+// The waves that compute a matvec phase's items: the NCW compute waves
+// where its rows are staged in LDS (the pollers and loaders have their own
+// work then). Where each lane streams its rows from memory nothing else runs
+// after the poll, and a phase of more passes than NCW waves but no more than
+// NWAVES takes every wave (one round of passes instead of two; with more
+// passes, twice the waves only compete for the same bandwidth). An item's
+// arithmetic does not depend on which wave takes it.
+struct MvWaves {
+  bool on;       // this wave computes items
+  uint32_t cw;   // its index among them
+  uint32_t n;    // how many there are
+};
+__device__ __forceinline__ MvWaves mv_waves(const Stager& sg, uint32_t wave, const Args& a,
+                                            uint32_t kind, uint32_t wg, uint32_t G) {
+  MvWaves m;
+  bool all = false;
+  if (!(STAGED_ONLY || sg.on)) {
+    const uint32_t cnt = rows_owned(kind_items(shape_dims(a.d), kind), wg, G);
+    const uint32_t per = pass_items(kind_rows(kind) == 2);
+    const uint32_t passes = (cnt + per - 1) / per;
+    all = passes > NCW && passes <= NWAVES;
+  }
+  m.on = all || (wave >= NPOLL && wave < NWA);
+  m.cw = all ? wave : wave - NPOLL;
+  m.n = all ? NWAVES : NCW;
+  return m;
+}
+
+// body(k, y0, y1) for every item k of `kind` dealt to wave mw.cw of mw.n,
+// with its dot products against the LDS vector x (y1 = 0 for single-row
+// kinds), wave-uniform. Staged: the preloaded first pass, then further
+// passes read from LDS. Otherwise each lane streams its segment of its row
+// from memory.
 template <class F>
-__device__ __forceinline__ void items_dot(const Args& a, uint32_t kind, uint32_t cw, uint32_t l,
+__device__ __forceinline__ void items_dot(const Args& a, uint32_t kind, MvWaves mw, uint32_t l,
                                           const Stager& sg, const Preload& P, const float* x,
                                           uint32_t wg, uint32_t G, uint32_t lane, F body) {
+  const uint32_t cw = mw.cw;
   const Dims dd = shape_dims(a.d);
   const uint32_t cnt = rows_owned(kind_items(dd, kind), wg, G);
   const uint32_t K = kind_k(dd, kind);
   const bool pair = kind_rows(kind) == 2;
   const uint32_t r = qrow(lane), s = qseg(lane);
-  const uint32_t step = NCW * pass_items(pair);
-  auto emit = [&](uint32_t k, float acc) {
+  // The results of the pass at item k, whose slots are nw items apart.
+  auto emit = [&](uint32_t k, float acc, uint32_t nw) {
     float y[4];
     quad_sums(acc, y);
     if (pair) {
       body(k, y[0], y[1]);
-      if (k + NCW < cnt) body(k + NCW, y[2], y[3]);
+      if (k + nw < cnt) body(k + nw, y[2], y[3]);
     } else {
 #pragma unroll
       for (uint32_t u = 0; u < 4; ++u)
-        if (k + NCW * u < cnt) body(k + NCW * u, y[u], 0.0f);
+        if (k + nw * u < cnt) body(k + nw * u, y[u], 0.0f);
     }
   };
   if (STAGED_ONLY || sg.on) {
     if (!P.any) return;
-    emit(cw, pass_pre(P, staged_slot(sg, kind, cw, r, cnt), x, K, s));
+    const uint32_t step = NCW * pass_items(pair);
+    emit(cw, pass_pre(P, staged_slot(sg, kind, cw, r, cnt), x, K, s), NCW);
     for (uint32_t k = cw + step; k < cnt; k += step) {
       const float* w = staged_slot(sg, kind, k, r, cnt);
-      emit(k, w ? seg_lds(w, x, K, s, 0, 0.0f) : 0.0f);
+      emit(k, w ? seg_lds(w, x, K, s, 0, 0.0f) : 0.0f, NCW);
     }
     return;
   }
+  const uint32_t nw = mw.n, step = nw * pass_items(pair);
   for (uint32_t k = cw; k < cnt; k += step) {
-    const uint32_t it = slot_item(pair, k, r);
+    const uint32_t it = slot_item(pair, k, r, nw);
     float acc = 0.0f;
     if (it < cnt) {
       const ItemRows rw = item_rows(a, kind, l, it, wg, G);
       acc = seg_stream<KF>(pair && (r & 1u) ? rw.w1 : rw.w0, x, K, s, 0, 0.0f);
     }
-    emit(k, acc);
+    emit(k, acc, nw);
   }
 }
 
@@ -794,15 +828,16 @@ __device__ __forceinline__ bool phase_qkv(const Args& a, uint32_t l, uint32_t ti
                                           const Stager& sg) {
   const Dims d = shape_dims(a.d);
   const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
-  const bool compute = wave >= NPOLL && wave < NWA;
-  const uint32_t cw = wave - NPOLL;  // meaningful for compute waves only
+  const MvWaves mw = mv_waves(sg, wave, a, IK_QKV, wg, G);
+  const bool compute = mw.on;
+  const uint32_t cw = mw.cw;  // meaningful for computing waves only
   const uint32_t cnt = rows_owned(d.qkv_rows / 2, wg, G);
   // The epilogue inputs of the wave's first items are loaded before the wait.
   float4 pre[QKV_PRE];
   if (compute) {
 #pragma unroll
     for (uint32_t u = 0; u < QKV_PRE; ++u) {
-      const uint32_t k = cw + NCW * u;
+      const uint32_t k = cw + mw.n * u;
       if (k < cnt) pre[u] = qkv_epi_load(a, l, pos, k, wg, G);
     }
   }
@@ -832,8 +867,8 @@ __device__ __forceinline__ bool phase_qkv(const Args& a, uint32_t l, uint32_t ti
   if (compute && cnt > 0) {
     const float inv = rms_inv(s.vec, d.h, d.eps, lane);
     const uint32_t gen = gen_of(d, tick, l, PH_QKV);
-    items_dot(a, IK_QKV, cw, l, sg, P, s.vec, wg, G, lane, [&](uint32_t k, float y0, float y1) {
-      const uint32_t u = (k - cw) / NCW;
+    items_dot(a, IK_QKV, mw, l, sg, P, s.vec, wg, G, lane, [&](uint32_t k, float y0, float y1) {
+      const uint32_t u = (k - cw) / mw.n;
       float4 e;
       if (u == 0)
         e = pre[0];
@@ -1183,9 +1218,10 @@ __device__ __forceinline__ bool phase_o(const Args& a, uint32_t l, uint32_t tick
       lds_st(s.vec + u, combine_one(part + hh * nch * hs, nch, hs, dd));
     }
   __syncthreads();
-  if (wave >= NPOLL && wave < NWA) {
+  const MvWaves mw = mv_waves(sg, wave, a, IK_O, wg, G);
+  if (mw.on) {
     const uint32_t gen = gen_of(d, tick, l, PH_O);
-    items_dot(a, IK_O, wave - NPOLL, l, sg, P, s.vec, wg, G, lane, [&](uint32_t k, float y, float) {
+    items_dot(a, IK_O, mw, l, sg, P, s.vec, wg, G, lane, [&](uint32_t k, float y, float) {
       pub_word_rep(pub, k, a.mb_xo + item_of(d.h, wg, G, k), lds_ld(xres + k) + y, gen, a.rep_words, lane);
     });
   }
@@ -1211,10 +1247,11 @@ __device__ __forceinline__ bool phase_gu(const Args& a, uint32_t l, uint32_t tic
   if (!poll_gather<PW_H>(gather_vec(rep_of(a, a.mb_xo, wg), d.h, gen_of(d, tick, l, PH_O), s.vec), NWA, a.st, s.ctl,
                       mv_hook(sg, op, P, IK_GU)))
     return false;
-  if (wave >= NPOLL && wave < NWA) {
+  const MvWaves mw = mv_waves(sg, wave, a, IK_GU, wg, G);
+  if (mw.on) {
     const float inv = rms_inv(s.vec, d.h, d.eps, lane);
     const uint32_t gen = gen_of(d, tick, l, PH_GU);
-    items_dot(a, IK_GU, wave - NPOLL, l, sg, P, s.vec, wg, G, lane,
+    items_dot(a, IK_GU, mw, l, sg, P, s.vec, wg, G, lane,
               [&](uint32_t k, float gate, float up) {
                 pub_word_rep(pub, k, a.mb_g + item_of(d.ff, wg, G, k), act_fn(gate * inv, d.act) * (up * inv), gen, a.rep_words, lane);
               });
@@ -1242,9 +1279,10 @@ __device__ __forceinline__ bool phase_d(const Args& a, uint32_t l, uint32_t tick
   if (!poll_gather<PW_F, 1>(gather_vec(rep_of(a, a.mb_g, wg), d.ff, gen_of(d, tick, l, PH_GU), s.vec), gr, NWA,
                           a.st, s.ctl, mv_hook(sg, op, P, IK_D)))
     return false;
-  if (wave >= NPOLL && wave < NWA) {
+  const MvWaves mw = mv_waves(sg, wave, a, IK_D, wg, G);
+  if (mw.on) {
     const uint32_t gen = gen_of(d, tick, l, PH_D);
-    items_dot(a, IK_D, wave - NPOLL, l, sg, P, s.vec, wg, G, lane, [&](uint32_t k, float y, float) {
+    items_dot(a, IK_D, mw, l, sg, P, s.vec, wg, G, lane, [&](uint32_t k, float y, float) {
       pub_word_rep(pub, k, a.mb_xd + item_of(d.h, wg, G, k), lds_ld(s.scr + k) + y, gen, a.rep_words, lane);
     });
   }
