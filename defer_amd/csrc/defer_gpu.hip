@@ -970,6 +970,13 @@ extern "C" int defer_gpu_cache_read(const defer_gpu_cache* cc, uint32_t layer, f
   return DEFER_GPU_OK;
 }
 
+extern "C" int defer_gpu_cache_shape(const defer_gpu_cache* c, uint32_t* layers, uint32_t* kv_dim) {
+  if (!c || !layers || !kv_dim) return fail(DEFER_GPU_E_INVALID, "null argument");
+  *layers = c->m->d.L;
+  *kv_dim = c->m->d.kv;
+  return DEFER_GPU_OK;
+}
+
 extern "C" int defer_gpu_value_norms(const defer_gpu_cache* cc, uint32_t t0, uint32_t t1,
                                      float* out) {
   defer_gpu_cache* c = const_cast<defer_gpu_cache*>(cc);

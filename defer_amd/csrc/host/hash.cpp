@@ -1,6 +1,9 @@
 // hash.cpp -- CRC-32 and SHA-256 for the WAL / checkpoint formats and the
-// cache fingerprint (crc32.rs:4-28, sha256.rs:15-134 of the reference).
+// cache fingerprint (crc32.rs:4-28, sha256.rs:15-134, model.rs:233-242 of
+// the reference).
 #include <string.h>
+
+#include <vector>
 
 #include "common.h"
 #include "defer_host.h"
@@ -116,4 +119,38 @@ extern "C" void defer_host_sha256(const uint8_t* data, size_t n, uint8_t out[32]
   dh::Sha256 s;
   s.update(data, n);
   s.finish(out);
+}
+
+// KvCache::fingerprint (model.rs:233-242): SHA-256 of the length as a
+// little-endian u64, then for each layer every key, then every value, as
+// the little-endian bits of each f32 (positions 0..len, kv_dim per row).
+extern "C" int defer_host_cache_fingerprint(const defer_gpu_cache* c, uint8_t out[32]) {
+  if (!c || !out) return dh::fail(DEFER_HOST_E_INVALID, "null argument");
+  uint32_t layers = 0, kv = 0;
+  int rc = defer_gpu_cache_shape(c, &layers, &kv);
+  if (rc) return dh::fail(DEFER_HOST_E_GPU, "defer_gpu error %d: %s", rc, defer_gpu_last_error());
+  const uint64_t len = defer_gpu_cache_len(c);
+  dh::Sha256 h;
+  uint8_t lb[8];
+  for (int k = 0; k < 8; ++k) lb[k] = (uint8_t)(len >> (8 * k));
+  h.update(lb, 8);
+  const size_t n = (size_t)len * kv;
+  std::vector<float> keys(n), values(n);
+  std::vector<uint8_t> bytes(4 * n);
+  auto feed = [&](const std::vector<float>& v) {
+    for (size_t i = 0; i < n; ++i) {
+      uint32_t b;
+      memcpy(&b, &v[i], 4);
+      for (int k = 0; k < 4; ++k) bytes[4 * i + k] = (uint8_t)(b >> (8 * k));
+    }
+    h.update(bytes.data(), bytes.size());
+  };
+  for (uint32_t l = 0; l < layers; ++l) {
+    rc = defer_gpu_cache_read(c, l, keys.data(), values.data());
+    if (rc) return dh::fail(DEFER_HOST_E_GPU, "defer_gpu error %d: %s", rc, defer_gpu_last_error());
+    feed(keys);
+    feed(values);
+  }
+  h.finish(out);
+  return DEFER_HOST_OK;
 }

@@ -107,6 +107,8 @@ def lib() -> ctypes.CDLL:
     L.defer_gpu_cache_clone.restype = ctypes.c_int
     L.defer_gpu_cache_read.argtypes = [vp, u32, vp, vp]
     L.defer_gpu_cache_read.restype = ctypes.c_int
+    L.defer_gpu_cache_shape.argtypes = [vp, P(u32), P(u32)]
+    L.defer_gpu_cache_shape.restype = ctypes.c_int
     L.defer_gpu_value_norms.argtypes = [vp, u32, u32, vp]
     L.defer_gpu_value_norms.restype = ctypes.c_int
     L.defer_gpu_forward.argtypes = [vp, vp, u32, vp, sz, vp, vp]
@@ -371,6 +373,12 @@ class GpuCache:
         h = ctypes.c_void_p()
         _check(lib().defer_gpu_cache_clone(self._h, ctypes.byref(h)))
         return GpuCache(self.model, _handle=h)
+
+    def shape(self) -> tuple:
+        """(layers, kv_dim): the shape of each layer's keys / values rows."""
+        nl, kv = ctypes.c_uint32(), ctypes.c_uint32()
+        _check(lib().defer_gpu_cache_shape(self._h, ctypes.byref(nl), ctypes.byref(kv)))
+        return int(nl.value), int(kv.value)
 
     def read(self, layer: int):
         """(keys, values) of one layer as [len, kv_dim] arrays."""

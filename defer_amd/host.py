@@ -67,6 +67,8 @@ def lib() -> ctypes.CDLL:
     L.defer_host_crc32.restype = u32
     L.defer_host_sha256.argtypes = [u8p, sz, u8p]
     L.defer_host_sha256.restype = None
+    L.defer_host_cache_fingerprint.argtypes = [vp, u8p]
+    L.defer_host_cache_fingerprint.restype = ctypes.c_int
     L.defer_host_seed_from_u64.argtypes = [u64, u8p]
     L.defer_host_seed_from_u64.restype = None
     L.defer_host_chacha8_words.argtypes = [u8p, u64, sz, vp]
@@ -139,6 +141,14 @@ def sha256(data: bytes) -> bytes:
     out = ctypes.create_string_buffer(32)
     lib().defer_host_sha256(_buf(data), len(data), out)
     return out.raw
+
+
+def cache_fingerprint(cache: "gpu.GpuCache") -> bytes:
+    """KvCache::fingerprint (model.rs:233-242) of a device cache: SHA-256 of
+    len (u64 LE), then per layer all keys, then all values (f32 LE bits)."""
+    out = (ctypes.c_uint8 * 32)()
+    _check(lib().defer_host_cache_fingerprint(cache._h, out))
+    return bytes(out)
 
 
 def seed_from_u64(seed: int) -> bytes:

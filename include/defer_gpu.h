@@ -91,6 +91,9 @@ int defer_gpu_cache_clone(const defer_gpu_cache* c, defer_gpu_cache** out); /* d
 /* The pub `keys` / `values` fields (model.rs:185-188) of one layer, each as a
  * [len, kv_dim] row-major host array. */
 int defer_gpu_cache_read(const defer_gpu_cache* c, uint32_t layer, float* keys, float* values);
+/* The cache's layer count and its pub `kv_dim` field (model.rs:185-188):
+ * the shape of what defer_gpu_cache_read returns per layer. */
+int defer_gpu_cache_shape(const defer_gpu_cache* c, uint32_t* layers, uint32_t* kv_dim);
 
 /* ValueNorms::sync (attribution.rs:116-148), the extension step: for cached
  * positions t in [t0, t1), every layer l and query head h,

@@ -8,6 +8,7 @@
  * Reference interfaces restated (paths under the reference's src/):
  *   defer_host_crc32            crc32::crc32                     crc32.rs:4-28
  *   defer_host_sha256           sha256::sha256                   sha256.rs:15-134
+ *   defer_host_cache_fingerprint KvCache::fingerprint            model.rs:233-242
  *   defer_host_seed_from_u64    engine::seed_from_u64            engine.rs:19-21
  *   defer_host_chacha8_words    ChaCha8Rng word stream           engine.rs:51, 213-215
  *   defer_host_words_per_sample sampler::words_per_sample        sampler.rs:15-21
@@ -47,6 +48,10 @@ const char* defer_host_last_error(void);
 uint32_t defer_host_crc32(const uint8_t* data, size_t n);
 /* SHA-256 (FIPS 180-4). */
 void defer_host_sha256(const uint8_t* data, size_t n, uint8_t out[32]);
+/* KvCache::fingerprint (model.rs:233-242) of a device cache: SHA-256 of
+ * len as a little-endian u64, then per layer all keys, then all values, as
+ * little-endian f32 bits. Reads the cache to the host (verification only). */
+int defer_host_cache_fingerprint(const defer_gpu_cache* c, uint8_t out[32]);
 
 /* -------------------------------------------------------------- randomness */
 

@@ -49,6 +49,48 @@ def test_session_sampling_matches_oracle(tiny):
     assert s.history == prompt + toks and s.prompt_len == 9
 
 
+def _fingerprint_of_rows(cache) -> bytes:
+    """model.rs:233-242 over the cache's host copy: len as u64 LE, then per
+    layer every key, then every value, as f32 LE bits (hashlib's SHA-256)."""
+    import hashlib
+
+    h = hashlib.sha256(len(cache).to_bytes(8, "little"))
+    layers, kvd = cache.shape()
+    for l in range(layers):
+        k, v = cache.read(l)
+        assert k.shape == v.shape == (len(cache), kvd)
+        h.update(k.astype("<f4").tobytes())
+        h.update(v.astype("<f4").tobytes())
+    return h.digest()
+
+
+def test_cache_fingerprint_and_repeat_runs(tiny):
+    """KvCache::fingerprint on a device cache equals an independent SHA-256
+    of its rows, an empty cache hashes 8 zero bytes, and repeated sessions
+    give the same tokens and the same fingerprint (verification.rs:46-59,
+    here 5 runs)."""
+    import hashlib
+
+    cfg, w, gm, om = tiny
+    say("tiny: cache fingerprint vs hashlib, empty cache, 5 repeat runs of prompt 7 + 24 at T=0.9")
+    empty = gm.new_cache(16)
+    assert H.cache_fingerprint(empty) == hashlib.sha256(bytes(8)).digest()
+    assert empty.shape() == (cfg["num_layers"], cfg["num_kv_heads"] * cfg["head_dim"])
+    prompt = [int(x) for x in synthetic.make_prompt(cfg["vocab_size"], 7, seed=3)]
+    runs = []
+    for _ in range(5):
+        s = H.Session(gm, H.seed_from_u64(21), 0.9)
+        s.prompt(prompt)
+        toks = s.generate(24)
+        fp = H.cache_fingerprint(s.cache)
+        assert fp == _fingerprint_of_rows(s.cache)
+        runs.append((toks, fp))
+    assert all(r == runs[0] for r in runs)
+    c = s.cache
+    c.truncate(10)
+    assert H.cache_fingerprint(c) == _fingerprint_of_rows(c) != runs[0][1]
+
+
 def test_session_steps_equal_generate(tiny):
     cfg, w, gm, om = tiny
     say("tiny: 20 single steps vs one generate of 20")
