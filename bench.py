@@ -220,7 +220,7 @@ def sessions_workload(args) -> int:
             "peak": PEAK_F32_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_F32_TFLOPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic("k_gemm_lockstep_1b.md", "gemm_traffic_bytes_per_step"),
         },
     }
     for c in caches:
