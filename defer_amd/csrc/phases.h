@@ -12,7 +12,10 @@
 //    the pollers poll alone, so a poll round waits for nothing but its own
 //    words;
 //  * compute waves (the next NCW) compute the matvec items dealt to them
-//    and store each result as soon as they have it;
+//    and store each result as soon as they have it (where rows are streamed
+//    from memory instead of staged, a phase with more passes than NCW takes
+//    every wave after its poll, and the results are listed in LDS and
+//    stored after the phase: mv_waves, Pub);
 //  * loaders (the last NLOAD waves) stage weight rows into LDS with direct
 //    global->LDS loads (persistent kernel only, when a layer's share of the
 //    workgroup fits): each kind's rows for the next layer are requested as
