@@ -1330,7 +1330,10 @@ __device__ __forceinline__ bool phase_lm(const Args& a, uint32_t tick, uint32_t 
   auto vocab_row = [&](uint32_t r) { return (wg + G * (r / VCHUNK)) * VCHUNK + r % VCHUNK; };
   const uint32_t sgm = qseg(lane);
   SegT<LMF> A, B;
-  const bool lmw = wave < NWA;  // loader waves only meet the barriers
+  // The loader waves only meet the barriers where they stage rows; where
+  // nothing is staged every wave streams lm_head rows.
+  const uint32_t nlm = (STAGED_ONLY || sg.on) ? NWA : NWAVES;
+  const bool lmw = wave < nlm;
   // Quad q: local rows 4q .. 4q+3, this lane's 4q + qrow(lane).
   auto live = [&](uint32_t q) {
     const uint32_t rr = 4 * q + qrow(lane);
@@ -1356,8 +1359,8 @@ __device__ __forceinline__ bool phase_lm(const Args& a, uint32_t tick, uint32_t 
   __syncthreads();
   const float inv = rms_inv(s.vec, d.h, d.eps, lane);
   const uint32_t gen = gen_lm(d, tick);
-  for (uint32_t q = wave; lmw && 4 * q < nrows; q += NWA) {
-    first(B, q + NWA);
+  for (uint32_t q = wave; lmw && 4 * q < nrows; q += nlm) {
+    first(B, q + nlm);
     const bool lv = live(q);
     const float acc = seg_tail(A, row_of(q), xs, d.h, sgm);
     const float y = inv * group_sum(acc, 16);
@@ -1370,7 +1373,7 @@ __device__ __forceinline__ bool phase_lm(const Args& a, uint32_t tick, uint32_t 
   }
   __syncthreads();
   // Chunk (max, argmax): one wave per chunk, one lane per row.
-  for (uint32_t k = wave; lmw && k < nown; k += NWA) {
+  for (uint32_t k = wave; lmw && k < nown; k += nlm) {
     const uint32_t c = wg + G * k;
     const uint32_t v = c * VCHUNK + lane;
     float bv = -INFINITY;
