@@ -493,7 +493,7 @@ static int apply_layout(defer_gpu_model* m, uint32_t G) {
   // A shape-specialised persistent kernel stages its rows only.
   m->persistent = d.lds_stg ? persistent_kernel_for(d) : (const void*)k_persistent;
   m->lds_bytes = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr + d.lds_stg) * sizeof(float) +
-                 (size_t)d.lds_pub * 2 * sizeof(u64);
+                 (size_t)d.lds_pub * 2 * sizeof(u64) + (d.lds_stg ? 0 : 1024);
   m->lds_rows = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr) * sizeof(float);
   // k_b_attn_f's combine: the group's chunk partials, their weights and totals.
   const uint32_t scr_fcomb = MAX_GROUP * MAX_ACHUNKS * hs + MAX_GROUP * MAX_ACHUNKS + MAX_GROUP;

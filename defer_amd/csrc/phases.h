@@ -22,7 +22,10 @@
 //    soon as this layer's rows of that kind have been used, and a loader
 //    waits for them (exact vector-memory counts) only at the barrier before
 //    their use. Loaders issue no other memory instruction, so those counts
-//    hold, and no other wave ever waits for a weight load.
+//    hold, and no other wave ever waits for a weight load. Where rows are
+//    streamed instead, the loaders pull the first blocks of the compute
+//    waves' first pass into the L2 during the poll (prefetch_first) and
+//    store the listed results after the phase (pub_flush).
 // Attention, lm_head and the sampler run on pollers and compute waves.
 #pragma once
 
@@ -60,6 +63,7 @@ struct Lds {
   float* scr;   // d.lds_scr floats
   float* stg;   // d.lds_stg floats: staged weight rows (persistent kernel)
   u64* pub;     // d.lds_pub entries of {word, address}: listed results (Pub)
+  float* trash; // 1 KB that direct-to-LDS prefetches land in (streamed kernels)
 };
 
 __device__ inline Lds lds_layout(float* base, const Dims& d) {
@@ -71,6 +75,7 @@ __device__ inline Lds lds_layout(float* base, const Dims& d) {
   s.scr = s.vec2 + d.lds_vec2;
   s.stg = s.scr + d.lds_scr;
   s.pub = reinterpret_cast<u64*>(s.stg + d.lds_stg);
+  s.trash = reinterpret_cast<float*>(s.pub + 2 * d.lds_pub);
   return s;
 }
 
@@ -723,6 +728,30 @@ __device__ __forceinline__ MvWaves mv_waves(const Stager& sg, uint32_t wave, con
   return m;
 }
 
+// Streamed phases whose items take only the compute waves: while the input
+// is polled for, the loader waves pull the first 1024 elements (the first
+// two blocks a lane streams) of the rows of every compute wave's first pass
+// into the L2 (direct-to-LDS loads into a line nothing reads; no wave waits
+// for them), so the compute waves' first loads after the poll hit the L2
+// instead of HBM.
+__device__ __forceinline__ void prefetch_first(const Args& a, uint32_t kind, uint32_t l, uint32_t wg,
+                                               uint32_t G, const Lds& s, uint32_t lw, uint32_t lane) {
+  const Dims d = shape_dims(a.d);
+  if (d.lds_stg) return;  // the 1 KB line exists only in layouts without staged rows
+  const uint32_t cnt = rows_owned(kind_items(d, kind), wg, G);
+  const bool pair = kind_rows(kind) == 2;
+  const uint32_t nit = min(cnt, NCW * pass_items(pair));
+  const uint32_t K = kind_k(d, kind), lim = min(K, 1024u);
+  const uint32_t trash = (uint32_t)(uintptr_t)s.trash;
+  for (uint32_t k = lw; k < nit; k += NLOAD) {
+    const ItemRows rw = item_rows(a, kind, l, k, wg, G);
+    for (uint32_t off = 0; off + 256 <= lim; off += 256) {
+      dma16(rw.w0 + off + lane * 4, trash);
+      if (pair) dma16(rw.w1 + off + lane * 4, trash);
+    }
+  }
+}
+
 // body(k, y0, y1) for every item k of `kind` dealt to wave mw.cw of mw.n,
 // with its dot products against the LDS vector x (y1 = 0 for single-row
 // kinds), wave-uniform. Staged: the preloaded first pass, then further
@@ -832,6 +861,7 @@ __device__ __forceinline__ bool phase_qkv(const Args& a, uint32_t l, uint32_t ti
   const Dims d = shape_dims(a.d);
   const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
   const MvWaves mw = mv_waves(sg, wave, a, IK_QKV, wg, G);
+  if (!(STAGED_ONLY || sg.on) && mw.n == NCW && wave >= NWA) prefetch_first(a, IK_QKV, l, wg, G, s, wave - NWA, lane);
   const bool compute = mw.on;
   const uint32_t cw = mw.cw;  // meaningful for computing waves only
   const uint32_t cnt = rows_owned(d.qkv_rows / 2, wg, G);
@@ -1213,6 +1243,10 @@ __device__ __forceinline__ bool phase_o(const Args& a, uint32_t l, uint32_t tick
     op.layer = l + 1 < d.L ? l + 1 : 0;
     op.wait = sg.wait[IK_O];
   }
+  {
+    const MvWaves m0 = mv_waves(sg, wave, a, IK_O, wg, G);
+    if (!(STAGED_ONLY || sg.on) && m0.n == NCW && wave >= NWA) prefetch_first(a, IK_O, l, wg, G, s, wave - NWA, lane);
+  }
   if (!poll_gather<4, 1>(ga, gr, NWA, a.st, s.ctl, mv_hook(sg, op, P, IK_O))) return false;
   if (l == 0 && threadIdx.x < R) lds_st(xres + threadIdx.x, emb);
   if (inl)
@@ -1247,6 +1281,10 @@ __device__ __forceinline__ bool phase_gu(const Args& a, uint32_t l, uint32_t tic
     op.layer = l + 1 < d.L ? l + 1 : 0;
     op.wait = sg.wait[IK_GU];
   }
+  {
+    const MvWaves m0 = mv_waves(sg, wave, a, IK_GU, wg, G);
+    if (!(STAGED_ONLY || sg.on) && m0.n == NCW && wave >= NWA) prefetch_first(a, IK_GU, l, wg, G, s, wave - NWA, lane);
+  }
   if (!poll_gather<PW_H>(gather_vec(rep_of(a, a.mb_xo, wg), d.h, gen_of(d, tick, l, PH_O), s.vec), NWA, a.st, s.ctl,
                       mv_hook(sg, op, P, IK_GU)))
     return false;
@@ -1278,6 +1316,10 @@ __device__ __forceinline__ bool phase_d(const Args& a, uint32_t l, uint32_t tick
     op.issue = IK_GU;
     op.layer = l + 1 < d.L ? l + 1 : 0;
     op.wait = sg.wait[IK_D];
+  }
+  {
+    const MvWaves m0 = mv_waves(sg, wave, a, IK_D, wg, G);
+    if (!(STAGED_ONLY || sg.on) && m0.n == NCW && wave >= NWA) prefetch_first(a, IK_D, l, wg, G, s, wave - NWA, lane);
   }
   if (!poll_gather<PW_F, 1>(gather_vec(rep_of(a, a.mb_g, wg), d.ff, gen_of(d, tick, l, PH_GU), s.vec), gr, NWA,
                           a.st, s.ctl, mv_hook(sg, op, P, IK_D)))
