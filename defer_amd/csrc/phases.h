@@ -706,7 +706,9 @@ __device__ __forceinline__ MvHook mv_hook(const Stager& sg, LoadOp op, Preload& 
 // after the poll, and a phase of more passes than NCW waves but no more than
 // NWAVES takes every wave (one round of passes instead of two; with more
 // passes, twice the waves only compete for the same bandwidth). An item's
-// arithmetic does not depend on which wave takes it.
+// arithmetic does not depend on which wave takes it. (The phases test the
+// staged-only kernel's compute waves directly before calling this: the same
+// test made through it costs that kernel a spilled register.)
 struct MvWaves {
   bool on;       // this wave computes items
   uint32_t cw;   // its index among them
@@ -1255,8 +1257,8 @@ __device__ __forceinline__ bool phase_o(const Args& a, uint32_t l, uint32_t tick
       lds_st(s.vec + u, combine_one(part + hh * nch * hs, nch, hs, dd));
     }
   __syncthreads();
-  const MvWaves mw = mv_waves(sg, wave, a, IK_O, wg, G);
-  if (mw.on) {
+  if (STAGED_ONLY ? (wave >= NPOLL && wave < NWA) : mv_waves(sg, wave, a, IK_O, wg, G).on) {
+    const MvWaves mw = mv_waves(sg, wave, a, IK_O, wg, G);
     const uint32_t gen = gen_of(d, tick, l, PH_O);
     items_dot(a, IK_O, mw, l, sg, P, s.vec, wg, G, lane, [&](uint32_t k, float y, float) {
       pub_word_rep(pub, k, a.mb_xo + item_of(d.h, wg, G, k), lds_ld(xres + k) + y, gen, a.rep_words, lane);
@@ -1288,8 +1290,8 @@ __device__ __forceinline__ bool phase_gu(const Args& a, uint32_t l, uint32_t tic
   if (!poll_gather<PW_H>(gather_vec(rep_of(a, a.mb_xo, wg), d.h, gen_of(d, tick, l, PH_O), s.vec), NWA, a.st, s.ctl,
                       mv_hook(sg, op, P, IK_GU)))
     return false;
-  const MvWaves mw = mv_waves(sg, wave, a, IK_GU, wg, G);
-  if (mw.on) {
+  if (STAGED_ONLY ? (wave >= NPOLL && wave < NWA) : mv_waves(sg, wave, a, IK_GU, wg, G).on) {
+    const MvWaves mw = mv_waves(sg, wave, a, IK_GU, wg, G);
     const float inv = rms_inv(s.vec, d.h, d.eps, lane);
     const uint32_t gen = gen_of(d, tick, l, PH_GU);
     items_dot(a, IK_GU, mw, l, sg, P, s.vec, wg, G, lane,
@@ -1324,8 +1326,8 @@ __device__ __forceinline__ bool phase_d(const Args& a, uint32_t l, uint32_t tick
   if (!poll_gather<PW_F, 1>(gather_vec(rep_of(a, a.mb_g, wg), d.ff, gen_of(d, tick, l, PH_GU), s.vec), gr, NWA,
                           a.st, s.ctl, mv_hook(sg, op, P, IK_D)))
     return false;
-  const MvWaves mw = mv_waves(sg, wave, a, IK_D, wg, G);
-  if (mw.on) {
+  if (STAGED_ONLY ? (wave >= NPOLL && wave < NWA) : mv_waves(sg, wave, a, IK_D, wg, G).on) {
+    const MvWaves mw = mv_waves(sg, wave, a, IK_D, wg, G);
     const uint32_t gen = gen_of(d, tick, l, PH_D);
     items_dot(a, IK_D, mw, l, sg, P, s.vec, wg, G, lane, [&](uint32_t k, float y, float) {
       pub_word_rep(pub, k, a.mb_xd + item_of(d.h, wg, G, k), lds_ld(s.scr + k) + y, gen, a.rep_words, lane);
