@@ -24,11 +24,17 @@
 using namespace dg;
 
 // Persistent kernels specialised for known model shapes (kernels_*.hip).
-namespace dg135 {
-struct Args;
-struct RunDesc;
-__global__ void k_persistent(const Args* ap, const RunDesc* run);
-}  // namespace dg135
+#define DG_DECLARE_SPECIALISED(NS)                            \
+  namespace NS {                                              \
+  struct Args;                                                \
+  struct RunDesc;                                             \
+  __global__ void k_persistent(const Args* ap, const RunDesc* run); \
+  }
+DG_DECLARE_SPECIALISED(dg135)
+DG_DECLARE_SPECIALISED(dg360)
+DG_DECLARE_SPECIALISED(dg1b)
+DG_DECLARE_SPECIALISED(dg8b)
+#undef DG_DECLARE_SPECIALISED
 
 // ------------------------------------------------------------------ errors
 
@@ -365,12 +371,19 @@ struct defer_gpu_model {
   double pstat[6] = {0, 0, 0, 0, 0, 0};
 };
 
-// A persistent kernel compiled for this exact shape, if there is one.
+// A persistent kernel compiled for this exact shape, if there is one. The
+// 135M kernel has no streaming path, so it runs only where every kind's rows
+// are staged.
+static bool has_shape(const Dims& d, const Dims& f) {
+  return d.h == f.h && d.nh == f.nh && d.nkv == f.nkv && d.hd == f.hd && d.ff == f.ff &&
+         d.V == f.V && d.L == f.L && d.act == f.act && d.has_bias == f.has_bias && d.tied == f.tied;
+}
 static const void* persistent_kernel_for(const Dims& d) {
-  const bool smollm2_135m = d.h == 576 && d.nh == 9 && d.nkv == 3 && d.hd == 64 &&
-                            d.ff == 1536 && d.V == 49152 && d.L == 30 && d.act == 0 &&
-                            d.has_bias == 0 && d.tied == 1;
-  if (smollm2_135m) return (const void*)dg135::k_persistent;
+  if (has_shape(d, fix_shape(d, DG_SHAPE_ARGS_135M)) && d.stg_mask == 0xFu)
+    return (const void*)dg135::k_persistent;
+  if (has_shape(d, fix_shape(d, DG_SHAPE_ARGS_360M))) return (const void*)dg360::k_persistent;
+  if (has_shape(d, fix_shape(d, DG_SHAPE_ARGS_1B))) return (const void*)dg1b::k_persistent;
+  if (has_shape(d, fix_shape(d, DG_SHAPE_ARGS_8B))) return (const void*)dg8b::k_persistent;
   return (const void*)k_persistent;
 }
 
@@ -468,20 +481,6 @@ static int apply_layout(defer_gpu_model* m, uint32_t G) {
   const uint32_t scr_samp = 3 * d.nvc + VCHUNK + NWAVES + 2 + NWA * VCHUNK;
   const uint32_t scr_lm = ((d.nvc + G - 1) / G) * VCHUNK;
   d.lds_scr = (std::max({scr_attn, scr_o, scr_comb, scr_samp, scr_lm, 2 * NWAVES}) + 3) & ~3u;
-  // Weight staging for the persistent kernel: each kind's rows of one layer
-  // for the workgroup with the most items, if that fits the CU's LDS.
-  {
-    const uint32_t n_items[4] = {d.qkv_rows / 2, d.h, d.ff, d.h};
-    const uint32_t rows[4] = {2, 1, 2, 1};
-    const uint32_t K[4] = {d.h, d.q, d.h, d.ff};
-    uint32_t stg = 0;
-    for (int k = 0; k < 4; ++k) {
-      d.stg_off[k] = stg;
-      stg += (n_items[k] + G - 1) / G * rows[k] * K[k];
-    }
-    const size_t base = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr) * sizeof(float);
-    d.lds_stg = (base + (size_t)stg * sizeof(float) <= LDS_BYTES_MAX) ? stg : 0;
-  }
   // Listed results (phases.h: Pub): one entry per matvec result of a phase
   // (four per QKV item), where rows are streamed (the per-phase kernels
   // always).
@@ -490,8 +489,54 @@ static int apply_layout(defer_gpu_model* m, uint32_t G) {
                                 (d.ff + G - 1) / G, (d.h + G - 1) / G};
     d.lds_pub = std::max({per_wg[0], per_wg[1], per_wg[2], per_wg[3]});
   }
-  // A shape-specialised persistent kernel stages its rows only.
-  m->persistent = d.lds_stg ? persistent_kernel_for(d) : (const void*)k_persistent;
+  // Weight staging for the persistent kernel: each kind's rows of one layer
+  // for the workgroup with the most items. Where all four kinds do not fit
+  // the CU's LDS, the smallest kinds that fit are staged and the others
+  // streamed: a small kind's share per workgroup is a few rows, which a
+  // stream pays a memory latency for, while a large kind's stream runs long
+  // enough to hide it. With any kind staged the loader waves stage rows, so
+  // the streamed phases lose what the loaders do for them when nothing is
+  // staged (storing the listed results, warming the L2, streaming beside the
+  // compute waves); so a partial staging is kept only where the staged rows
+  // are at least as many bytes as the streamed ones (360M shape: QKV, O and
+  // down staged, 6.4 % faster than all streamed; 1B shape: O alone would be
+  // staged, 5.8 % slower).
+  {
+    const uint32_t n_items[4] = {d.qkv_rows / 2, d.h, d.ff, d.h};
+    const uint32_t rows[4] = {2, 1, 2, 1};
+    const uint32_t K[4] = {d.h, d.q, d.h, d.ff};
+    size_t need[4], total = 0;
+    for (int k = 0; k < 4; ++k) {
+      need[k] = (size_t)(n_items[k] + G - 1) / G * rows[k] * K[k];
+      total += need[k];
+    }
+    const size_t base = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr) * sizeof(float) +
+                        (size_t)d.lds_pub * 2 * sizeof(u64);
+    uint32_t mask = 0;
+    if (base + total * sizeof(float) <= LDS_BYTES_MAX) {
+      mask = 0xFu;
+    } else {
+      int order[4] = {0, 1, 2, 3};
+      std::stable_sort(order, order + 4, [&](int x, int y) { return need[x] < need[y]; });
+      size_t used = 0;
+      for (int i = 0; i < 4; ++i) {
+        const int k = order[i];
+        if (base + (used + need[k]) * sizeof(float) <= LDS_BYTES_MAX) {
+          mask |= 1u << k;
+          used += need[k];
+        }
+      }
+      if (used < total - used) mask = 0;
+    }
+    uint32_t stg = 0;
+    for (int k = 0; k < 4; ++k) {
+      d.stg_off[k] = stg;
+      if (mask >> k & 1u) stg += (uint32_t)need[k];
+    }
+    d.stg_mask = mask;
+    d.lds_stg = stg;
+  }
+  m->persistent = persistent_kernel_for(d);
   m->lds_bytes = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr + d.lds_stg) * sizeof(float) +
                  (size_t)d.lds_pub * 2 * sizeof(u64) + (d.lds_stg ? 0 : 1024);
   m->lds_rows = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr) * sizeof(float);

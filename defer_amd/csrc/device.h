@@ -54,7 +54,8 @@ struct Dims {
   uint32_t lds_vec2;   // floats of the second vector region (h)
   uint32_t lds_scr;    // floats of the scratch LDS region
   uint32_t lds_stg;    // floats of the weight staging region (0: rows are not staged)
-  uint32_t stg_off[4]; // float offset of each item kind's rows in the staging region
+  uint32_t stg_mask;   // bit k: item kind k's rows are staged (the rest are streamed)
+  uint32_t stg_off[4]; // float offset of each staged kind's rows in the staging region
   uint32_t lds_pub;    // entries of the listed results (rows streamed)
   float eps, scale;
 };
@@ -160,28 +161,50 @@ __host__ __device__ inline uint32_t gen_lm(const Dims& d, uint32_t tick) {
 // arithmetic folds); the per-cache and per-launch fields (capacity, LDS
 // layout) always come from the arguments. The values are identical either
 // way, so specialised and generic kernels produce the same bits.
-__device__ __forceinline__ Dims shape_dims(const Dims& r) {
-  Dims d = r;
+// The shapes with a specialised persistent kernel: hidden, heads, kv heads,
+// head_dim, intermediate, vocabulary, layers, tied head (SwiGLU, no biases).
+#define DG_SHAPE_ARGS_135M 576, 9, 3, 64, 1536, 49152, 30, 1
+#define DG_SHAPE_ARGS_360M 960, 15, 5, 64, 2560, 49152, 32, 1
+#define DG_SHAPE_ARGS_1B 2048, 32, 8, 64, 8192, 128256, 16, 1
+#define DG_SHAPE_ARGS_8B 4096, 32, 8, 128, 14336, 128256, 32, 0
 #if defined(DG_SHAPE_SMOLLM2_135M)
-  d.h = 576;
-  d.nh = 9;
-  d.nkv = 3;
-  d.hd = 64;
-  d.half = 32;
-  d.ff = 1536;
-  d.V = 49152;
-  d.L = 30;
-  d.q = 576;
-  d.kv = 192;
-  d.qkv_rows = 960;
-  d.group = 3;
+#define DG_FIXED_SHAPE DG_SHAPE_ARGS_135M
+#elif defined(DG_SHAPE_SMOLLM2_360M)
+#define DG_FIXED_SHAPE DG_SHAPE_ARGS_360M
+#elif defined(DG_SHAPE_LLAMA32_1B)
+#define DG_FIXED_SHAPE DG_SHAPE_ARGS_1B
+#elif defined(DG_SHAPE_LLAMA3_8B)
+#define DG_FIXED_SHAPE DG_SHAPE_ARGS_8B
+#endif
+// The derived fields follow the host's model set-up (defer_gpu.hip).
+__host__ __device__ constexpr Dims fix_shape(Dims d, uint32_t h, uint32_t nh, uint32_t nkv,
+                                             uint32_t hd, uint32_t ff, uint32_t V, uint32_t L,
+                                             uint32_t tied) {
+  d.h = h;
+  d.nh = nh;
+  d.nkv = nkv;
+  d.hd = hd;
+  d.half = hd / 2;
+  d.ff = ff;
+  d.V = V;
+  d.L = L;
+  d.q = nh * hd;
+  d.kv = nkv * hd;
+  d.qkv_rows = nh * hd + 2 * nkv * hd;
+  d.group = nh / nkv;
   d.act = 0;
   d.has_bias = 0;
-  d.tied = 1;
-  d.kvs = 64;
-  d.nvc = 768;
-#endif
+  d.tied = tied;
+  d.kvs = hd > 32 ? hd : 32;
+  d.nvc = (V + VCHUNK - 1) / VCHUNK;
   return d;
+}
+__device__ __forceinline__ Dims shape_dims(const Dims& r) {
+#if defined(DG_FIXED_SHAPE)
+  return fix_shape(r, DG_FIXED_SHAPE);
+#else
+  return r;
+#endif
 }
 
 // Attention chunking: a function of the query position only, so results
@@ -493,6 +516,9 @@ __device__ __forceinline__ float seg_stream(const float* __restrict__ w, const f
     SegT<NF> a, b;
     seg_load_in(a, w, s, i);
     uint32_t blk = 0;
+    // Not unrolled: in a shape-specialised build nb is a constant, and the
+    // unrolled blocks' loads, hoisted together, spill registers.
+#pragma unroll 1
     for (; blk + 2 < nb; blk += 2) {  // both following blocks exist
       seg_load_in(b, w, s, i + NF);
       acc = seg_fma_in(a, x, s, i, acc);

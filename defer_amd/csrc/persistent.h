@@ -54,12 +54,13 @@ __global__ __launch_bounds__(BLOCK) void k_persistent(const Args* __restrict__ a
   uint32_t pos = cptr(st)->pos, tick = cptr(st)->tick;
   const uint32_t wg = blockIdx.x, G = gridDim.x;
   lm_prime(a, s);
-  // Weight rows are staged in LDS when a layer's share fits: the loaders
-  // request layer 0's QKV, O and GU rows now (the D rows follow at the first
-  // QKV phase, as in every later layer).
+  // The kinds whose rows of a layer fit in LDS are staged there: the loaders
+  // request layer 0's QKV, O and GU rows now, where staged (the D rows follow
+  // at the first QKV phase, as in every later layer).
   const Stager sg = make_stager(a, s, wg, G, a.d.lds_stg != 0);
   if (sg.on && sg.loader)
-    for (uint32_t k = 0; k < 3; ++k) stage_issue(sg, k, 0);
+    for (uint32_t k = 0; k < 3; ++k)
+      if (staged(sg, k)) stage_issue(sg, k, 0);
   uint32_t i = 0;
   uint32_t halted = 0;
   for (; i < r.n_ops; ++i) {

@@ -435,7 +435,8 @@ __device__ __forceinline__ uint32_t stg_off_of(const Dims& d, uint32_t kind) {
 // Staging of the workgroup's rows in LDS (persistent kernel). Kind X's items
 // sit back to back at s.stg + d.stg_off[X], item k's rows contiguous.
 struct Stager {
-  bool on;             // rows are staged (else compute waves load them)
+  bool on;             // some kind's rows are staged: the loader waves stage them
+  uint32_t mask;       // bit k: kind k's rows are staged (else compute waves stream them)
   const Args* a;
   float* stg;
   uint32_t wg, G, ld;  // ld: this wave's loader index (loaders only)
@@ -446,6 +447,10 @@ struct Stager {
   // requested only after that barrier).
   uint32_t wait[4];
 };
+// Kind X's rows are staged in LDS (a wave-uniform test).
+__device__ __forceinline__ bool staged(const Stager& sg, uint32_t kind) {
+  return STAGED_ONLY || (sg.mask >> kind & 1u);
+}
 
 // 16 bytes per lane from global memory straight into LDS: lane i's bytes
 // land at LDS byte address lds_base + 16*i (lds_base is wave-uniform). M0,
@@ -498,7 +503,8 @@ __device__ __forceinline__ uint32_t stage_loads(const Dims& d, uint32_t kind, ui
 __device__ __forceinline__ Stager make_stager(const Args& a, const Lds& s, uint32_t wg, uint32_t G,
                                               bool on) {
   Stager sg;
-  sg.on = on;
+  sg.mask = STAGED_ONLY ? 0xFu : (on ? a.d.stg_mask : 0u);
+  sg.on = sg.mask != 0;
   sg.a = &a;
   sg.stg = s.stg;
   sg.wg = wg;
@@ -508,7 +514,7 @@ __device__ __forceinline__ Stager make_stager(const Args& a, const Lds& s, uint3
   sg.ld = sg.loader ? wave - NWA : 0;
   uint32_t n[4], tot = 0;
   for (uint32_t k = 0; k < 4; ++k) {
-    n[k] = stage_loads(shape_dims(a.d), k, wg, G, sg.ld);
+    n[k] = (sg.mask >> k & 1u) ? stage_loads(shape_dims(a.d), k, wg, G, sg.ld) : 0u;
     tot += n[k];
   }
   for (uint32_t k = 0; k < 4; ++k) sg.wait[k] = tot - n[k] - n[(k + 3) % 4];
@@ -682,7 +688,7 @@ struct MvHook {
     if (sg->on && sg->loader && op.wait != NO_WAIT) stage_wait(op.wait);
   }
   __device__ __forceinline__ void post_b1() const {
-    if (!sg->on) return;
+    if (!staged(*sg, kind)) return;
     const uint32_t wave = threadIdx.x / WAVE;
     if (!sg->loader && wave >= NPOLL) preload_rows(*pre, *sg, kind, wave - NPOLL, threadIdx.x % WAVE);
   }
@@ -782,7 +788,7 @@ __device__ __forceinline__ void items_dot(const Args& a, uint32_t kind, MvWaves 
         if (k + nw * u < cnt) body(k + nw * u, y[u], 0.0f);
     }
   };
-  if (STAGED_ONLY || sg.on) {
+  if (staged(sg, kind)) {
     if (!P.any) return;
     const uint32_t step = NCW * pass_items(pair);
     emit(cw, pass_pre(P, staged_slot(sg, kind, cw, r, cnt), x, K, s), NCW);
@@ -879,11 +885,11 @@ __device__ __forceinline__ bool phase_qkv(const Args& a, uint32_t l, uint32_t ti
   Preload P;
   const Pub pub = pub_for(sg.on, s);
   LoadOp op = no_load();
-  if (sg.on) {
+  if (staged(sg, IK_D)) {
     op.issue = IK_D;  // the previous layer's D rows are used: this layer's
     op.layer = l;
-    op.wait = sg.wait[IK_QKV];
   }
+  if (staged(sg, IK_QKV)) op.wait = sg.wait[IK_QKV];
   const MvHook hk = mv_hook(sg, op, P, IK_QKV);
   if (l == 0) {
     // The embedding row (model.rs:428), read by the pollers only.
@@ -1240,11 +1246,11 @@ __device__ __forceinline__ bool phase_o(const Args& a, uint32_t l, uint32_t tick
   Preload P;
   const Pub pub = pub_for(sg.on, s);
   LoadOp op = no_load();
-  if (sg.on) {
+  if (staged(sg, IK_QKV)) {
     op.issue = IK_QKV;  // the QKV rows are used: request the next layer's
     op.layer = l + 1 < d.L ? l + 1 : 0;
-    op.wait = sg.wait[IK_O];
   }
+  if (staged(sg, IK_O)) op.wait = sg.wait[IK_O];
   {
     const MvWaves m0 = mv_waves(sg, wave, a, IK_O, wg, G);
     if (!(STAGED_ONLY || sg.on) && m0.n == NCW && wave >= NWA) prefetch_first(a, IK_O, l, wg, G, s, wave - NWA, lane);
@@ -1278,11 +1284,11 @@ __device__ __forceinline__ bool phase_gu(const Args& a, uint32_t l, uint32_t tic
   Preload P;
   const Pub pub = pub_for(sg.on, s);
   LoadOp op = no_load();
-  if (sg.on) {
+  if (staged(sg, IK_O)) {
     op.issue = IK_O;
     op.layer = l + 1 < d.L ? l + 1 : 0;
-    op.wait = sg.wait[IK_GU];
   }
+  if (staged(sg, IK_GU)) op.wait = sg.wait[IK_GU];
   {
     const MvWaves m0 = mv_waves(sg, wave, a, IK_GU, wg, G);
     if (!(STAGED_ONLY || sg.on) && m0.n == NCW && wave >= NWA) prefetch_first(a, IK_GU, l, wg, G, s, wave - NWA, lane);
@@ -1314,11 +1320,11 @@ __device__ __forceinline__ bool phase_d(const Args& a, uint32_t l, uint32_t tick
   Preload P;
   const Pub pub = pub_for(sg.on, s);
   LoadOp op = no_load();
-  if (sg.on) {
+  if (staged(sg, IK_GU)) {
     op.issue = IK_GU;
     op.layer = l + 1 < d.L ? l + 1 : 0;
-    op.wait = sg.wait[IK_D];
   }
+  if (staged(sg, IK_D)) op.wait = sg.wait[IK_D];
   {
     const MvWaves m0 = mv_waves(sg, wave, a, IK_D, wg, G);
     if (!(STAGED_ONLY || sg.on) && m0.n == NCW && wave >= NWA) prefetch_first(a, IK_D, l, wg, G, s, wave - NWA, lane);

@@ -299,13 +299,18 @@ def test_c5_8b_all_layers_greedy():
 @pytest.mark.parametrize("name,grids", [
     ("tiny", ((0, 0), (3, 128), (2, 48))),
     ("smollm2-135m", ((0, 0), (64, 128), (37, 48))),
+    ("smollm2-360m", ((0, 0), (64, 128))),
 ])
 def test_results_independent_of_grid(name, grids):
     """Smaller persistent grids (the tiny model's full grid is 4 workgroups,
-    the 135M shape's 256; at 64 and 37 the 135M rows no longer fit the LDS
-    staging and are read from HBM) and GEMMs shaped for 128 and 48 compute
+    the 135M and 360M shapes' 256) and GEMMs shaped for 128 and 48 compute
     units give the bits of the full grid: decode (greedy and T > 0),
-    batched prefill and lockstep sessions."""
+    batched prefill and lockstep sessions. The grids change how each
+    workgroup's rows reach the LDS: the 135M shape stages every kind at the
+    full grid (the specialised kernel), QKV, O and down at 64 workgroups
+    (the generic kernel) and nothing at 37; the 360M shape stages QKV, O and
+    down at the full grid and nothing at 64, both in its specialised
+    kernel."""
     cfg = dict(synthetic.CONFIGS[name])
     w = synthetic.make_weights(cfg, 11)
     V = cfg["vocab_size"]
