@@ -285,7 +285,8 @@ def decode_workload(args, name: str) -> int:
             "peak": PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_GBS, 4),
-            "traffic": measured_traffic("k_persistent_decode_8b.md") if name == "8b" else None,
+            "traffic": measured_traffic("k_persistent_decode_8b.md" if name == "8b"
+                                        else "k_persistent_decode_360m.md"),
         },
     }
     s.close()

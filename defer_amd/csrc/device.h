@@ -37,9 +37,11 @@ constexpr uint32_t ACHUNK = 128;       // attention positions per chunk (base si
 constexpr uint32_t MAX_ACHUNKS = 16;   // attention chunks per head at most
 constexpr uint32_t INLINE_COMB_MAX = 1536;  // floats of partials combined inside the O phase
 constexpr uint32_t SPIN_LIMIT = 1u << 21;
+// The dispatcher places workgroup w on XCD w % NXCD.
+constexpr uint32_t NXCD = 8;
 // Replicas of the all-to-all mailboxes (xo, xd, g): one per XCD, so the
 // 32 workgroups of an XCD poll their own copy.
-constexpr uint32_t MB_REPS = 8;
+constexpr uint32_t MB_REPS = NXCD;
 constexpr uint32_t NO_INDEX = 0xffffffffu;
 
 // ------------------------------------------------------------------ layout

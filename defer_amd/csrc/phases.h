@@ -1000,9 +1000,28 @@ __device__ __forceinline__ bool phase_attn(const Args& a, uint32_t l, uint32_t t
   const uint32_t aw = att ? wave - AW0 : 0;  // attention wave
   const uint32_t tw = aw * ge.pw + ps;  // this lane's position offset in a score pass
   const uint32_t vw = aw * ge.pv + pl;  // ... and in a value step
-  for (uint32_t item = wg; item < n_items; item += G) {
-    // item = (g * nch + c) * grp + j0, or g * nch + c when grouped
-    const uint32_t gc = GROUPED ? item : item / grp, j0 = GROUPED ? 0 : item - gc * grp;
+  // One query head per item: the items of one (kv head, chunk) read the same
+  // K/V rows. With at least NXCD such pairs they take slots NXCD apart --
+  // workgroups on one XCD -- so the rows are fetched into one L2 rather than
+  // one per head: slot NXCD * (grp * b + j0) + x is pair gc = NXCD * b + x,
+  // query head j0, and slots past the last pair are empty (360M shape, 4096
+  // tokens: 1.8 % faster, K/V fetched once instead of three times). Fewer
+  // pairs take consecutive slots (slot = gc * grp + j0), as do all in the
+  // staged-only kernel, whose decode the placement made 1 % slower.
+  const uint32_t ngc = GROUPED ? n_items : d.nkv * nch;
+  const bool by_xcd = !GROUPED && !STAGED_ONLY && ngc >= NXCD;
+  const uint32_t n_slots = by_xcd ? NXCD * grp * ((ngc + NXCD - 1) / NXCD) : n_items;
+  for (uint32_t slot = wg; slot < n_slots; slot += G) {
+    uint32_t gc = slot, j0 = 0;
+    if (by_xcd) {
+      const uint32_t x = slot % NXCD, b = slot / NXCD;
+      j0 = b % grp;
+      gc = (b / grp) * NXCD + x;
+      if (gc >= ngc) continue;
+    } else if (!GROUPED) {
+      gc = slot / grp;
+      j0 = slot - gc * grp;
+    }
     const uint32_t g = gc / nch, c = gc - g * nch;
     const uint32_t t0 = c * CH;
     const uint32_t t1 = min(t0 + CH, pos + 1);
