@@ -481,6 +481,17 @@ static int apply_layout(defer_gpu_model* m, uint32_t G) {
   const uint32_t scr_samp = 3 * d.nvc + VCHUNK + NWAVES + 2 + NWA * VCHUNK;
   const uint32_t scr_lm = ((d.nvc + G - 1) / G) * VCHUNK;
   d.lds_scr = (std::max({scr_attn, scr_o, scr_comb, scr_samp, scr_lm, 2 * NWAVES}) + 3) & ~3u;
+  // O rows skip the workgroups that take the attention items at positions
+  // below 2 * ACHUNK (2 * nh items, one per query head and chunk, on the
+  // first workgroups) where that leaves the busiest workgroup's O rows as
+  // they are (135M shape: 576 rows on 238 instead of 256 workgroups, still
+  // at most 3 each). Those workgroups' O rows waited for their attention to
+  // finish, and every gate/up workgroup waits for the last O row.
+  d.o_skip = 0;
+  {
+    const uint32_t skip = 2 * d.nh;
+    if (skip < G && (d.h + G - skip - 1) / (G - skip) == (d.h + G - 1) / G) d.o_skip = skip;
+  }
   // Listed results (phases.h: Pub): one entry per matvec result of a phase
   // (four per QKV item), where rows are streamed (the per-phase kernels
   // always).

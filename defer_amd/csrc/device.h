@@ -59,6 +59,7 @@ struct Dims {
   uint32_t stg_mask;   // bit k: item kind k's rows are staged (the rest are streamed)
   uint32_t stg_off[4]; // float offset of each staged kind's rows in the staging region
   uint32_t lds_pub;    // entries of the listed results (rows streamed)
+  uint32_t o_skip;     // workgroups 0 .. o_skip-1 own no O rows (they run attention items)
   float eps, scale;
 };
 

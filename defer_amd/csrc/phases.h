@@ -363,7 +363,7 @@ enum ItemKind : uint32_t { IK_QKV = 0, IK_O = 1, IK_GU = 2, IK_D = 3 };
 
 // Items of each kind: QKV pairs (rows i, i + hd/2 of one head, so RoPE needs
 // no exchange), O rows, GU pairs (gate row j, up row j), D rows. Item k of a
-// kind owned by workgroup wg is number item_of(n, wg, G, k); compute wave
+// kind owned by workgroup wg is number own_item(d, kind, wg, G, k); compute wave
 // k % NCW computes it and loader k % NLOAD stages it.
 __device__ __forceinline__ uint32_t kind_items(const Dims& d, uint32_t kind) {
   return kind == IK_QKV ? d.qkv_rows / 2 : (kind == IK_GU ? d.ff : d.h);
@@ -373,6 +373,20 @@ __device__ __forceinline__ uint32_t kind_k(const Dims& d, uint32_t kind) {
 }
 __device__ __forceinline__ uint32_t kind_rows(uint32_t kind) {
   return (kind == IK_QKV || kind == IK_GU) ? 2u : 1u;
+}
+
+// The workgroups' items of a kind. O rows skip the first d.o_skip
+// workgroups, which take the attention items of the usual positions: their
+// O rows would wait for their attention to finish, and every gate/up
+// workgroup waits for the last O row.
+__device__ __forceinline__ uint32_t own_count(const Dims& d, uint32_t kind, uint32_t wg, uint32_t G) {
+  if (kind == IK_O) return wg < d.o_skip ? 0u : rows_owned(d.h, wg - d.o_skip, G - d.o_skip);
+  return rows_owned(kind_items(d, kind), wg, G);
+}
+__device__ __forceinline__ uint32_t own_item(const Dims& d, uint32_t kind, uint32_t wg, uint32_t G,
+                                             uint32_t k) {
+  if (kind == IK_O) return item_of(d.h, wg - d.o_skip, G - d.o_skip, k);
+  return item_of(kind_items(d, kind), wg, G, k);
 }
 
 // The layer table entry of layer l (scalar loads: see cptr).
@@ -401,7 +415,7 @@ __device__ __forceinline__ ItemRows item_rows(const Args& a, uint32_t kind, uint
                                               uint32_t wg, uint32_t G) {
   const Dims d = shape_dims(a.d);
   const LayerW W = layer_w(a, l);
-  const uint32_t it = item_of(kind_items(d, kind), wg, G, k);
+  const uint32_t it = own_item(d, kind, wg, G, k);
   ItemRows r;
   if (kind == IK_QKV) {
     const uint32_t hb = it / d.half, i = it - hb * d.half;
@@ -495,7 +509,7 @@ __device__ __forceinline__ void stage_wait(uint32_t n) {
 // Loads one loader wave issues for its items of a kind: 1 KB per load.
 __device__ __forceinline__ uint32_t stage_loads(const Dims& d, uint32_t kind, uint32_t wg,
                                                 uint32_t G, uint32_t ld) {
-  const uint32_t cnt = rows_owned(kind_items(d, kind), wg, G);
+  const uint32_t cnt = own_count(d, kind, wg, G);
   const uint32_t mine = cnt > ld ? (cnt - ld + NLOAD - 1) / NLOAD : 0;
   return mine * kind_rows(kind) * ((kind_k(d, kind) + 255) / 256);
 }
@@ -526,7 +540,7 @@ __device__ __forceinline__ void stage_issue(const Stager& sg, uint32_t kind, uin
   const Args& a = *sg.a;
   const Dims d = shape_dims(a.d);
   const uint32_t lane = threadIdx.x % WAVE;
-  const uint32_t cnt = rows_owned(kind_items(d, kind), sg.wg, sg.G);
+  const uint32_t cnt = own_count(d, kind, sg.wg, sg.G);
   const uint32_t K = kind_k(d, kind), nr = kind_rows(kind), nseg = (K + 255) / 256;
   const uint32_t base = (uint32_t)(uintptr_t)(sg.stg + stg_off_of(d, kind));
   for (uint32_t k = sg.ld; k < cnt; k += NLOAD) {
@@ -630,7 +644,7 @@ __device__ __forceinline__ const float* staged_slot(const Stager& sg, uint32_t k
 __device__ __forceinline__ void preload_rows(Preload& P, const Stager& sg, uint32_t kind,
                                              uint32_t cw, uint32_t lane) {
   const Dims d = shape_dims(sg.a->d);
-  const uint32_t cnt = rows_owned(kind_items(d, kind), sg.wg, sg.G);
+  const uint32_t cnt = own_count(d, kind, sg.wg, sg.G);
   const uint32_t K = kind_k(d, kind), s = qseg(lane);
   P.any = cw < cnt;
   if (!P.any) return;
@@ -725,7 +739,7 @@ __device__ __forceinline__ MvWaves mv_waves(const Stager& sg, uint32_t wave, con
   MvWaves m;
   bool all = false;
   if (!(STAGED_ONLY || sg.on)) {
-    const uint32_t cnt = rows_owned(kind_items(shape_dims(a.d), kind), wg, G);
+    const uint32_t cnt = own_count(shape_dims(a.d), kind, wg, G);
     const uint32_t per = pass_items(kind_rows(kind) == 2);
     const uint32_t passes = (cnt + per - 1) / per;
     all = passes > NCW && passes <= NWAVES;
@@ -746,7 +760,7 @@ __device__ __forceinline__ void prefetch_first(const Args& a, uint32_t kind, uin
                                                uint32_t G, const Lds& s, uint32_t lw, uint32_t lane) {
   const Dims d = shape_dims(a.d);
   if (d.lds_stg) return;  // the 1 KB line exists only in layouts without staged rows
-  const uint32_t cnt = rows_owned(kind_items(d, kind), wg, G);
+  const uint32_t cnt = own_count(d, kind, wg, G);
   const bool pair = kind_rows(kind) == 2;
   const uint32_t nit = min(cnt, NCW * pass_items(pair));
   const uint32_t K = kind_k(d, kind), lim = min(K, 1024u);
@@ -771,7 +785,7 @@ __device__ __forceinline__ void items_dot(const Args& a, uint32_t kind, MvWaves 
                                           uint32_t wg, uint32_t G, uint32_t lane, F body) {
   const uint32_t cw = mw.cw;
   const Dims dd = shape_dims(a.d);
-  const uint32_t cnt = rows_owned(kind_items(dd, kind), wg, G);
+  const uint32_t cnt = own_count(dd, kind, wg, G);
   const uint32_t K = kind_k(dd, kind);
   const bool pair = kind_rows(kind) == 2;
   const uint32_t r = qrow(lane), s = qseg(lane);
@@ -1247,21 +1261,23 @@ __device__ __forceinline__ bool phase_o(const Args& a, uint32_t l, uint32_t tick
   const Dims d = shape_dims(a.d);
   const uint32_t nch = attn_nchunks(pos), hs = d.hd + 2;
   const bool inl = comb_inline(d, pos);
-  const uint32_t R = rows_owned(d.h, wg, G);
+  const uint32_t R = own_count(d, IK_O, wg, G);
   const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
   float* part = s.scr;
   float* xres = s.scr + (inl ? d.nh * nch * hs : 0);
+  // A workgroup without O rows only meets the barriers (its loaders' work).
   const Gather ga =
-      inl ? gather_strided(a.mb_part, nch * hs, d.nh, MAX_ACHUNKS * hs, gen_of(d, tick, l, PH_ATTN),
-                           part)
-          : gather_vec(a.mb_att, d.q, gen_of(d, tick, l, PH_COMB), s.vec);
+      R == 0 ? no_gather()
+      : inl  ? gather_strided(a.mb_part, nch * hs, d.nh, MAX_ACHUNKS * hs, gen_of(d, tick, l, PH_ATTN),
+                              part)
+             : gather_vec(a.mb_att, d.q, gen_of(d, tick, l, PH_COMB), s.vec);
   const Gather gr = (l > 0 && R > 0)
-                        ? gather_vec(rep_of(a, a.mb_xd, wg) + item_of(d.h, wg, G, 0), R, gen_of(d, tick, l - 1, PH_D), xres)
+                        ? gather_vec(rep_of(a, a.mb_xd, wg) + own_item(d, IK_O, wg, G, 0), R, gen_of(d, tick, l - 1, PH_D), xres)
                         : no_gather();
   // Layer 0's residual is the embedding row: its words are loaded before the
   // wait (pollers, one word per thread).
   float emb = 0.0f;
-  if (l == 0 && threadIdx.x < R) emb = ldg(a.embed + (size_t)token * d.h + item_of(d.h, wg, G, threadIdx.x));
+  if (l == 0 && threadIdx.x < R) emb = ldg(a.embed + (size_t)token * d.h + own_item(d, IK_O, wg, G, threadIdx.x));
   Preload P;
   const Pub pub = pub_for(sg.on, s);
   LoadOp op = no_load();
@@ -1276,7 +1292,7 @@ __device__ __forceinline__ bool phase_o(const Args& a, uint32_t l, uint32_t tick
   }
   if (!poll_gather<4, 1>(ga, gr, NWA, a.st, s.ctl, mv_hook(sg, op, P, IK_O))) return false;
   if (l == 0 && threadIdx.x < R) lds_st(xres + threadIdx.x, emb);
-  if (inl)
+  if (inl && R > 0)
     for (uint32_t u = threadIdx.x; u < d.q && threadIdx.x < NWA * WAVE; u += NWA * WAVE) {
       const uint32_t hh = u / d.hd, dd = u - hh * d.hd;
       lds_st(s.vec + u, combine_one(part + hh * nch * hs, nch, hs, dd));
@@ -1286,7 +1302,7 @@ __device__ __forceinline__ bool phase_o(const Args& a, uint32_t l, uint32_t tick
     const MvWaves mw = mv_waves(sg, wave, a, IK_O, wg, G);
     const uint32_t gen = gen_of(d, tick, l, PH_O);
     items_dot(a, IK_O, mw, l, sg, P, s.vec, wg, G, lane, [&](uint32_t k, float y, float) {
-      pub_word_rep(pub, k, a.mb_xo + item_of(d.h, wg, G, k), lds_ld(xres + k) + y, gen, a.rep_words, lane);
+      pub_word_rep(pub, k, a.mb_xo + own_item(d, IK_O, wg, G, k), lds_ld(xres + k) + y, gen, a.rep_words, lane);
     });
   }
   pub_flush(pub, R, a.rep_words);
