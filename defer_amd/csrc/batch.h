@@ -1071,37 +1071,59 @@ __global__ __launch_bounds__(64) void k_b_final(const float* __restrict__ X,
 // Chunk (max, argmax) of the tagged logits of each logits row, tagged for
 // the sampler (phase_lm's chunk step; argmax is a total order, so any tree
 // gives its answer). One wave per (chunk, row).
+// Chunk (max, argmax) of every logits row: each wave takes CM_CPW
+// consecutive chunks, one lane per row of a chunk, with all its loads issued
+// before the first reduction (the same reduction per chunk as the lm_head
+// phase's, so the same values).
+constexpr uint32_t CM_CPW = 4;
 __global__ __launch_bounds__(256) void k_b_chunkmax(const Dims d, const u64* __restrict__ logt,
                                                     const uint32_t* __restrict__ gen,
                                                     u64* __restrict__ vmax, u64* __restrict__ varg,
                                                     uint32_t nlm) {
-  const uint32_t c = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+  const uint32_t c0 = (blockIdx.x * 4 + threadIdx.x / WAVE) * CM_CPW, lane = threadIdx.x % WAVE;
   const uint32_t i = blockIdx.y;
-  if (c >= d.nvc || i >= nlm) return;
-  const uint32_t v = c * VCHUNK + lane;
-  float bv = -INFINITY;
-  uint32_t bi = NO_INDEX;
-  if (v < d.V) {
-    const float y = __uint_as_float((uint32_t)logt[(size_t)i * d.V + v]);
-    if (!isnan(y)) {
-      bv = y;
-      bi = v;
-    }
+  if (c0 >= d.nvc || i >= nlm) return;
+  u64 raw[CM_CPW];
+#pragma unroll
+  for (uint32_t u = 0; u < CM_CPW; ++u) {
+    const uint32_t v = (c0 + u) * VCHUNK + lane;
+    raw[u] = (c0 + u < d.nvc && v < d.V) ? logt[(size_t)i * d.V + v] : 0;
   }
-  for (int o = 32; o > 0; o >>= 1) {
-    const float v2 = __shfl_xor(bv, o);
-    const uint32_t i2 = __shfl_xor(bi, o);
-    if (better(v2, i2, bv, bi)) {
-      bv = v2;
-      bi = i2;
+  const u64 g = (u64)gen[i] << 32;
+#pragma unroll
+  for (uint32_t u = 0; u < CM_CPW; ++u) {
+    const uint32_t c = c0 + u;
+    if (c >= d.nvc) break;
+    const uint32_t v = c * VCHUNK + lane;
+    float bv = -INFINITY;
+    uint32_t bi = NO_INDEX;
+    if (v < d.V) {
+      const float y = __uint_as_float((uint32_t)raw[u]);
+      if (!isnan(y)) {
+        bv = y;
+        bi = v;
+      }
     }
-  }
-  if (lane == 0) {
-    const u64 g = (u64)gen[i] << 32;
-    vmax[(size_t)i * d.nvc + c] = g | __float_as_uint(bv);
-    varg[(size_t)i * d.nvc + c] = g | bi;
+    for (int o = 32; o > 0; o >>= 1) {
+      const float v2 = __shfl_xor(bv, o);
+      const uint32_t i2 = __shfl_xor(bi, o);
+      if (better(v2, i2, bv, bi)) {
+        bv = v2;
+        bi = i2;
+      }
+    }
+    if (lane == 0) {
+      vmax[(size_t)i * d.nvc + c] = g | __float_as_uint(bv);
+      varg[(size_t)i * d.nvc + c] = g | bi;
+    }
   }
 }
+
+// Chunks per wave and round of k_b_sample's stage A: the one workgroup of an
+// op walks all the row's chunks, so rounds of NWA chunks would each wait a
+// full memory latency. Its LDS holds NWA * SAMP_CPW chunks past the rows
+// layout's scratch start (samp_lds_bytes).
+constexpr uint32_t SAMP_CPW = 8;
 
 // One sampling op per workgroup (the one-token sampler, stages A and B on
 // one workgroup): op j samples logits row lrow[j] for generation base
@@ -1116,7 +1138,7 @@ __global__ __launch_bounds__(BLOCK) void k_b_sample(const Args* __restrict__ lar
   // A row whose wait runs out still leaves a token in range (0), so a
   // following batched embedding never reads outside the table.
   if (threadIdx.x == 0) out[j] = 0u;
-  if (T != 0.0f && !sample_stage_a(a, tick[j], tag0 + j, T, 0, 1, s)) return;
+  if (T != 0.0f && !sample_stage_a<SAMP_CPW, 8>(a, tick[j], tag0 + j, T, 0, 1, s)) return;
   uint32_t tok = 0;
   if (!sample_stage_b(a, tick[j], tag0 + j, T, T != 0.0f ? words[j] : 0u, s, &tok)) return;
   if (threadIdx.x == 0) out[j] = tok;

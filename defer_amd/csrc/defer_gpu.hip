@@ -371,6 +371,16 @@ struct defer_gpu_model {
   double pstat[6] = {0, 0, 0, 0, 0, 0};
 };
 
+// k_b_sample's LDS: the rows layout, with stage A's chunk area (NWA *
+// SAMP_CPW chunks from 2 * nvc floats into the scratch) wherever it runs
+// past that layout's end.
+static size_t samp_lds_bytes(const defer_gpu_model* m) {
+  const Dims& d = m->d;
+  const size_t chunk_end =
+      (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + 2 * d.nvc + NWA * SAMP_CPW * VCHUNK) * sizeof(float);
+  return std::max(m->lds_rows, chunk_end);
+}
+
 // A persistent kernel compiled for this exact shape, if there is one. The
 // 135M kernel has no streaming path, so it runs only where every kind's rows
 // are staged.
@@ -567,9 +577,9 @@ static int apply_layout(defer_gpu_model* m, uint32_t G) {
   }
   for (const void* kf : {(const void*)k_b_sample}) {
     const hipError_t e =
-        hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)m->lds_rows);
+        hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)samp_lds_bytes(m));
     if (e != hipSuccess)
-      return fail(DEFER_GPU_E_HIP, "LDS attribute (%zu bytes): %s", m->lds_rows,
+      return fail(DEFER_GPU_E_HIP, "LDS attribute (%zu bytes): %s", samp_lds_bytes(m),
                   hipGetErrorString(e));
   }
   for (const void* kf : {(const void*)k_b_attn_w, (const void*)k_b_attn_f}) {
@@ -2132,7 +2142,8 @@ static int batch_run(defer_gpu_model* m, const BRow* rows, defer_gpu_cache* cons
       launch_gemm(s, m->gemm_ncu, GO_TAG, m->p_lm, d.V, d.h, w.XQ, nl, reinterpret_cast<float*>(w.LOGT), d.V,
                   w.LINV, w.lgen, nullptr, w.QS, qs_n);
     }
-    k_b_chunkmax<<<dim3((d.nvc + 3) / 4, nl), 256, 0, s>>>(d, w.LOGT, w.lgen, w.VMAX, w.VARG, nl);
+    k_b_chunkmax<<<dim3((d.nvc + 4 * CM_CPW - 1) / (4 * CM_CPW), nl), 256, 0, s>>>(d, w.LOGT, w.lgen, w.VMAX,
+                                                                                   w.VARG, nl);
   }
   HIP_TRY(hipGetLastError());
   if (deferred && !m->prof) return DEFER_GPU_OK;
@@ -2180,7 +2191,7 @@ static int batch_sample(defer_gpu_model* m, defer_gpu_cache* const* ocache, cons
   k_begin<<<1, 1, 0, s>>>(w.st);
   const uint32_t tag0 = m->samp_next;
   m->samp_next += nops;
-  k_b_sample<<<nops, BLOCK, m->lds_rows, s>>>(w.largs, w.stick, w.swords, T, tag0, w.sout);
+  k_b_sample<<<nops, BLOCK, samp_lds_bytes(m), s>>>(w.largs, w.stick, w.swords, T, tag0, w.sout);
   HIP_TRY(hipGetLastError());
   if (deferred) return DEFER_GPU_OK;
   HIP_TRY(hipMemcpyAsync(out, w.sout, nops * sizeof(uint32_t), hipMemcpyDeviceToHost, s));

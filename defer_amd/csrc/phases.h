@@ -1539,6 +1539,10 @@ __device__ __forceinline__ float exp_term(float logit, float T, float m) {
 // per-workspace sequence number handed in by the host), so sums left in the
 // mailbox by an earlier sample of the same logits -- at another temperature,
 // say -- never carry the tag stage B waits for.
+// CPW: chunks per polling/computing wave per round (the chunk area holds
+// NWA * CPW chunks); PA: words per lane per poll round. A chunk's sum is the
+// same arithmetic whichever wave and round computes it.
+template <uint32_t CPW = 1, uint32_t PA = 2>
 __device__ __forceinline__ bool sample_stage_a(const Args& a, uint32_t tick, uint32_t gsum, float T,
                                                uint32_t wg, uint32_t G, const Lds& s) {
   const Dims d = shape_dims(a.d);
@@ -1546,7 +1550,7 @@ __device__ __forceinline__ bool sample_stage_a(const Args& a, uint32_t tick, uin
   const uint32_t gl = gen_lm(d, tick - 1u);
   float* vmx = s.scr;
   float* varg = vmx + nvc;
-  float* chunk = varg + nvc;  // [NWA][VCHUNK]
+  float* chunk = varg + nvc;  // [NWA * CPW][VCHUNK]
   if (!poll_gather<2, 2>(gather_vec(a.mb_vmax, nvc, gl, vmx), gather_vec(a.mb_varg, nvc, gl, varg),
                    NWA, a.st, s.ctl))
     return false;
@@ -1556,8 +1560,8 @@ __device__ __forceinline__ bool sample_stage_a(const Args& a, uint32_t tick, uin
   const float m = (bi == NO_INDEX) ? -INFINITY : bv / T;
   const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
   const uint32_t nown = wg < nvc ? (nvc - wg + G - 1) / G : 0;
-  for (uint32_t k0 = 0; k0 < nown; k0 += NWA) {
-    const uint32_t nb = min(NWA, nown - k0);
+  for (uint32_t k0 = 0; k0 < nown; k0 += NWA * CPW) {
+    const uint32_t nb = min(NWA * CPW, nown - k0);
     // chunks wg + G*(k0 + b), b < nb; the last one may be short
     const u64* src0 = a.mb_logit + (size_t)(wg + G * k0) * VCHUNK;
     const uint32_t clast = wg + G * (k0 + nb - 1);
@@ -1567,11 +1571,11 @@ __device__ __forceinline__ bool sample_stage_a(const Args& a, uint32_t tick, uin
     const Gather gb = short_last ? gather_vec(a.mb_logit + (size_t)clast * VCHUNK,
                                               d.V - clast * VCHUNK, gl, chunk + (nb - 1) * VCHUNK)
                                  : no_gather();
-    if (!poll_gather<2, 1>(ga, gb, NWA, a.st, s.ctl)) return false;
-    if (wave < nb) {
-      const uint32_t c = wg + G * (k0 + wave);
+    if (!poll_gather<PA, 1>(ga, gb, NWA, a.st, s.ctl)) return false;
+    for (uint32_t b = wave; wave < NWA && b < nb; b += NWA) {
+      const uint32_t c = wg + G * (k0 + b);
       const uint32_t v = c * VCHUNK + lane;
-      const float e = (v < d.V) ? exp_term(chunk[wave * VCHUNK + lane], T, m) : 0.0f;
+      const float e = (v < d.V) ? exp_term(chunk[b * VCHUNK + lane], T, m) : 0.0f;
       const float S = wave_sum(e);
       if (lane == 0) mb_put(a.mb_vsum + c, S, gsum);
     }
