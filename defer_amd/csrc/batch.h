@@ -1002,8 +1002,9 @@ __global__ __launch_bounds__(256, 2) void k_b_attn_tile(const Dims d, const BRow
 }
 
 // Combine of the chunk partials (combine_scales / combine_value, as the O
-// phase does) into the panel of att[b][q]: one workgroup per row; the weights of a
-// head's chunks are formed once in LDS, then a thread per (head, dim). The
+// phase does) into the panel of att[b][q]: one workgroup per row and group of
+// heads; the weights of a head's chunks are formed once in LDS (a wave per
+// head, a lane per chunk), then a thread per (head, dim). The
 // partials were written by earlier launches on the same stream, so their
 // values are read directly (the low half of each tagged word).
 constexpr uint32_t COMB_MAX_HEADS = 64;
@@ -1017,17 +1018,49 @@ __global__ __launch_bounds__(256) void k_b_comb(const Dims d, const BRow* __rest
   const uint32_t nh = min(COMB_HEADS_PER_BLOCK, d.nh - h0);
   const uint32_t nch = attn_nchunks(rows[b].pos), hs = d.hd + 2;
   const u64* pb = part + (size_t)b * part_w;
-  auto ld_head = [&](uint32_t hh) {
-    const u64* p = pb + (size_t)hh * MAX_ACHUNKS * hs;
-    return [p](uint32_t i) { return __uint_as_float((uint32_t)p[i]); };
-  };
-  for (uint32_t k = threadIdx.x; k < nh; k += blockDim.x)
-    ls[k] = combine_scales(ld_head(h0 + k), nch, hs, sc[k]);
+  const uint32_t wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+  auto val = [](const u64* p) { return __uint_as_float((uint32_t)*p); };
+  // combine_scales for head h0 + wave, one lane per chunk: M is a maximum
+  // (the same in any order, NaN maxima dropped as fmaxf from -inf drops
+  // them), each weight the same expf, and the weighted total summed in
+  // chunk order by lane 0 from the lanes' products (no contraction).
+  if (wave < nh) {
+    const u64* p = pb + (size_t)(h0 + wave) * MAX_ACHUNKS * hs;
+    if (nch == 1) {
+      if (lane == 0) ls[wave] = val(p + 1) * 1.0f;
+    } else {
+      const float mc = lane < nch ? val(p + lane * hs) : -INFINITY;
+      const float lc = lane < nch ? val(p + lane * hs + 1) : 0.0f;
+      float M = fmaxf(-INFINITY, mc);
+      for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+      const float w = (mc == -INFINITY) ? 0.0f : expf(mc - M);
+      const float prod = lc * w;
+      if (lane < nch) sc[wave][lane] = w;
+      float Ls = 0.0f;
+      for (uint32_t c = 0; c < nch; ++c) Ls = Ls + __shfl(prod, c);
+      if (lane == 0) ls[wave] = Ls;
+    }
+  }
   __syncthreads();
+  // combine_value, with the chunks' values loaded before the sum (the same
+  // sum in chunk order).
   for (uint32_t v = threadIdx.x; v < nh * d.hd; v += blockDim.x) {
     const uint32_t k = v / d.hd, dd = v - k * d.hd, u = (h0 + k) * d.hd + dd;
-    attp[panel_at(b, u, panel_chunks(d.q))] =
-        combine_value(ld_head(h0 + k), nch, hs, dd, sc[k], ls[k]);
+    const u64* p = pb + (size_t)(h0 + k) * MAX_ACHUNKS * hs + 2 + dd;
+    float x[MAX_ACHUNKS];
+#pragma unroll
+    for (uint32_t c = 0; c < MAX_ACHUNKS; ++c) x[c] = c < nch ? val(p + c * hs) : 0.0f;
+    float out;
+    if (nch == 1) {
+      out = (x[0] * 1.0f) / ls[k];
+    } else {
+      float A = 0.0f;
+#pragma unroll
+      for (uint32_t c = 0; c < MAX_ACHUNKS; ++c)
+        if (c < nch) A = A + x[c] * sc[k][c];
+      out = A / ls[k];
+    }
+    attp[panel_at(b, u, panel_chunks(d.q))] = out;
   }
 }
 
