@@ -6,6 +6,8 @@
                        build.rs links: static=defer_gpu plus the HIP runtime);
 * tests/c_abi/abi_test -- a C program linking the archive (and the oracle, as
                        its checker) that the GPU tests run.
+* tests/probe/libexact_probe.so -- test-only entry points into the exact
+                       sampler's device code (tests/test_exact.py).
 * libdefer_host.so  -- the C++ host side (session, WAL, checkpoint, ChaCha8,
                        SHA-256, safetensors) of include/defer_host.h.
 
@@ -58,11 +60,13 @@ def build_gpu() -> str:
     srcs = [os.path.join(CSRC, "defer_gpu.hip")] + sorted(
         os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.startswith("kernels_") and f.endswith(".hip"))
     flags = [f for f in GPU_FLAGS if f != "-shared"]
-    objs = []
-    for src in srcs:
-        obj = os.path.join(BUILD, os.path.basename(src).replace(".hip", ".o"))
-        _run([HIPCC, *flags, "-c", "-o", obj, src])
-        objs.append(obj)
+    objs = [os.path.join(BUILD, os.path.basename(src).replace(".hip", ".o")) for src in srcs]
+    # the translation units compile independently: one hipcc each, at once
+    from concurrent.futures import ThreadPoolExecutor
+
+    with ThreadPoolExecutor(max_workers=min(len(srcs), 6)) as ex:
+        for f in [ex.submit(_run, [HIPCC, *flags, "-c", "-o", obj, src]) for src, obj in zip(srcs, objs)]:
+            f.result()
     tmp = out + ".tmp"
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs])
     os.replace(tmp, out)
@@ -88,6 +92,17 @@ def build_c_abi_test() -> str:
     return out
 
 
+def build_probe() -> str:
+    """tests/probe/libexact_probe.so: test-only entry points into the exact
+    sampler's device code (expf_ref, the wave scan, the walker)."""
+    d = os.path.join(ROOT, "tests", "probe")
+    out = os.path.join(d, "libexact_probe.so")
+    tmp = out + ".tmp"
+    _run([HIPCC, *GPU_FLAGS, "-o", tmp, os.path.join(d, "exact_probe.hip")])
+    os.replace(tmp, out)
+    return out
+
+
 def build_host() -> str:
     out = os.path.join(PKG, "libdefer_host.so")
     srcs = sorted(
@@ -106,9 +121,11 @@ def build_all() -> None:
     if os.path.isdir(os.path.join(CSRC, "host")):
         build_host()
     build_c_abi_test()
+    build_probe()
 
 
 if __name__ == "__main__":
     which = sys.argv[1:] or ["all"]
     for w in which:
-        {"gpu": build_gpu, "host": build_host, "c_abi": build_c_abi_test, "all": build_all}[w]()
+        {"gpu": build_gpu, "host": build_host, "c_abi": build_c_abi_test, "probe": build_probe,
+         "all": build_all}[w]()

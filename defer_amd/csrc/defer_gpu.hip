@@ -362,6 +362,7 @@ struct defer_gpu_model {
   std::vector<const float*> p_qkv, p_o, p_gu, p_d;
   const float* p_lm = nullptr;
   struct BatchWs* bw = nullptr;
+  uint64_t coop_refused = 0;  // persistent launches refused and run as per-phase kernels
   // Optional timing of the batched path's GEMM and attention launches.
   bool prof = false;
   std::vector<hipEvent_t> pev;   // event pool; pairs (start, end) per timed launch
@@ -868,8 +869,8 @@ static int cache_alloc(const defer_gpu_model* m, uint32_t cap, defer_gpu_cache* 
   HIP_TRY(hipMalloc(&c->vc, kvn * sizeof(float)));
   const size_t hs = d.hd + 2;
   // xo, xd, g: MB_REPS replicas of one block, each on its own 32 KB boundary
-  const size_t rep_words = ((size_t)2 * d.h + d.ff + 4095) / 4096 * 4096;
-  const size_t base_words = (d.qkv_rows + (size_t)d.nh * MAX_ACHUNKS * hs + d.q + d.V +
+  const size_t rep_words = ((size_t)2 * d.h + d.ff + 1 + 4095) / 4096 * 4096;
+  const size_t base_words = (d.qkv_rows + (size_t)d.nh * MAX_ACHUNKS * hs + d.q + 2 * (size_t)d.V +
                              3 * (size_t)d.nvc + 64 + 4095) / 4096 * 4096;
   const size_t words = base_words + MB_REPS * rep_words;
   c->mb_words = words;
@@ -898,10 +899,12 @@ static int cache_alloc(const defer_gpu_model* m, uint32_t cap, defer_gpu_cache* 
   a.mb_vmax = p; p += d.nvc;
   a.mb_varg = p; p += d.nvc;
   a.mb_vsum = p; p += d.nvc;
+  a.mb_p = p; p += d.V;
   p = c->mb + base_words;
   a.mb_xo = p;
   a.mb_xd = p + d.h;
   a.mb_g = p + 2 * d.h;
+  a.mb_tok = p + 2 * d.h + d.ff;
   a.rep_words = (uint32_t)rep_words;
   a.st = c->st;
   a.mask = nullptr;
@@ -1131,8 +1134,19 @@ static int run_launch(defer_gpu_cache* c, RunDesc r, bool force_eager) {
       const Args* a = c->d_args;
       const RunDesc* dr = c->d_run;
       void* params[] = {&a, &dr};
-      HIP_TRY(hipLaunchCooperativeKernel(m->persistent, dim3(m->G), dim3(BLOCK),
-                                         params, (unsigned)m->lds_bytes, s));
+      const hipError_t e = hipLaunchCooperativeKernel(m->persistent, dim3(m->G), dim3(BLOCK), params,
+                                                      (unsigned)m->lds_bytes, s);
+      if (e != hipSuccess) {
+        // Refused at launch (nothing ran): the device grants cooperative
+        // launches to one process at a time. The per-phase kernels compute
+        // the same bits without one.
+        (void)hipGetLastError();
+        ++m->coop_refused;
+        for (uint32_t i = 0; i < r.n_ops; ++i) {
+          const int rc = launch_op_kernels(c, s);
+          if (rc) return rc;
+        }
+      }
     } else if (mode == DEFER_GPU_EXEC_GRAPH) {
       if (!c->graph) {
         hipGraph_t g;
@@ -1365,11 +1379,13 @@ extern "C" int defer_gpu_generate(const defer_gpu_model* m, defer_gpu_cache* c, 
   if (rc) return rc;
   if (max_tokens == 0) return DEFER_GPU_OK;
   if (!c->has_logits) return fail(DEFER_GPU_E_NO_LOGITS, "no context: provide a non-empty prompt");
-  if (temperature != 0.0f && !rng_words) return fail(DEFER_GPU_E_INVALID, "null rng words");
-  if (!tokens_out) return fail(DEFER_GPU_E_INVALID, "null tokens_out");
+  // A full cache is a context error before anything else (sampler.rs draws
+  // its word first, then forward_ext fails: model.rs:420-422).
   const uint32_t room = c->cap - c->pos;
   const uint32_t n = std::min(max_tokens, room);
   if (n == 0) return fail(DEFER_GPU_E_CONTEXT, "context length %u exceeded", m->cfg.max_seq_len);
+  if (temperature != 0.0f && !rng_words) return fail(DEFER_GPU_E_INVALID, "null rng words");
+  if (!tokens_out) return fail(DEFER_GPU_E_INVALID, "null tokens_out");
   rc = ensure_run_buffers(c, n, n_stop);
   if (rc) return rc;
   if (temperature != 0.0f)
@@ -1427,12 +1443,14 @@ extern "C" int defer_gpu_generate_cb(const defer_gpu_model* m, defer_gpu_cache* 
   if (rc) return rc;
   if (max_tokens == 0) return DEFER_GPU_OK;
   if (!c->has_logits) return fail(DEFER_GPU_E_NO_LOGITS, "no context: provide a non-empty prompt");
-  if (temperature != 0.0f && !rng_words) return fail(DEFER_GPU_E_INVALID, "null rng words");
-  if (n_stop && !stop) return fail(DEFER_GPU_E_INVALID, "null stop tokens");
-  if (!tokens_out) return fail(DEFER_GPU_E_INVALID, "null tokens_out");
+  // A full cache is a context error before anything else (sampler.rs draws
+  // its word first, then forward_ext fails: model.rs:420-422).
   const uint32_t room = c->cap - c->pos;
   const uint32_t n = std::min(max_tokens, room);
   if (n == 0) return fail(DEFER_GPU_E_CONTEXT, "context length %u exceeded", m->cfg.max_seq_len);
+  if (temperature != 0.0f && !rng_words) return fail(DEFER_GPU_E_INVALID, "null rng words");
+  if (n_stop && !stop) return fail(DEFER_GPU_E_INVALID, "null stop tokens");
+  if (!tokens_out) return fail(DEFER_GPU_E_INVALID, "null tokens_out");
   rc = ensure_run_buffers(c, n, n_stop);
   if (rc) return rc;
   rc = ensure_ring(c, n);
@@ -1569,12 +1587,14 @@ extern "C" int defer_gpu_generate_static(const defer_gpu_model* m, defer_gpu_cac
                 n_stop, STATIC_MAX_STOP);
   if (max_tokens == 0) return DEFER_GPU_OK;
   if (!c->has_logits) return fail(DEFER_GPU_E_NO_LOGITS, "no context: provide a non-empty prompt");
-  if (temperature != 0.0f && !rng_words) return fail(DEFER_GPU_E_INVALID, "null rng words");
-  if (n_stop && !stop) return fail(DEFER_GPU_E_INVALID, "null stop tokens");
-  if (!tokens_out) return fail(DEFER_GPU_E_INVALID, "null tokens_out");
+  // A full cache is a context error before anything else (sampler.rs draws
+  // its word first, then forward_ext fails: model.rs:420-422).
   const uint32_t room = c->cap - c->pos;
   const uint32_t n = std::min(max_tokens, room);
   if (n == 0) return fail(DEFER_GPU_E_CONTEXT, "context length %u exceeded", m->cfg.max_seq_len);
+  if (temperature != 0.0f && !rng_words) return fail(DEFER_GPU_E_INVALID, "null rng words");
+  if (n_stop && !stop) return fail(DEFER_GPU_E_INVALID, "null stop tokens");
+  if (!tokens_out) return fail(DEFER_GPU_E_INVALID, "null tokens_out");
   uint32_t* base = nullptr;
   rc = scratch_on(m->device, &base);
   if (rc) return rc;
@@ -1726,7 +1746,7 @@ struct BatchWs {
   float* LINV = nullptr;
   float* QS = nullptr;  // quarter-split GEMM subtrees [4][B][M], B <= 64, M <= batch_ldy
   u64 *QKVT = nullptr, *PART = nullptr, *LOGT = nullptr, *VMAX = nullptr, *VARG = nullptr,
-      *VSUM = nullptr;
+      *VSUM = nullptr, *VP = nullptr;
   BRow* drows = nullptr;
   Args* rargs = nullptr;
   Args* largs = nullptr;
@@ -1741,7 +1761,7 @@ struct BatchWs {
 static void batch_ws_release(BatchWs* w) {
   if (!w) return;
   void* ps[] = {w->X, w->Y, w->INV, w->XP, w->XQ, w->LINV, w->QS, w->QKVT, w->PART,
-                w->LOGT, w->VMAX, w->VARG, w->VSUM, w->drows, w->rargs, w->largs, w->sel,
+                w->LOGT, w->VMAX, w->VARG, w->VSUM, w->VP, w->drows, w->rargs, w->largs, w->sel,
                 w->lgen, w->stick, w->swords, w->sout, w->items, w->tiles, w->CNT, w->sets, w->st};
   for (void* p : ps) (void)hipFree(p);
   *w = BatchWs();
@@ -1786,6 +1806,7 @@ static int ensure_ws(defer_gpu_model* m, uint32_t rows, uint32_t lm) {
   HIP_TRY(hipMalloc(&w.VMAX, (size_t)L1 * d.nvc * sizeof(u64)));
   HIP_TRY(hipMalloc(&w.VARG, (size_t)L1 * d.nvc * sizeof(u64)));
   HIP_TRY(hipMalloc(&w.VSUM, (size_t)L1 * d.nvc * sizeof(u64)));
+  HIP_TRY(hipMalloc(&w.VP, (size_t)L1 * d.V * sizeof(u64)));
   HIP_TRY(hipMalloc(&w.largs, (size_t)L1 * sizeof(Args)));
   HIP_TRY(hipMalloc(&w.sel, (size_t)L1 * sizeof(uint32_t)));
   HIP_TRY(hipMalloc(&w.lgen, (size_t)L1 * sizeof(uint32_t)));
@@ -1797,6 +1818,7 @@ static int ensure_ws(defer_gpu_model* m, uint32_t rows, uint32_t lm) {
   // Tags start at 1, so zeroed sums never match a wait; sampled tokens
   // start in range.
   HIP_TRY(hipMemset(w.VSUM, 0, (size_t)L1 * d.nvc * sizeof(u64)));
+  HIP_TRY(hipMemset(w.VP, 0, (size_t)L1 * d.V * sizeof(u64)));
   HIP_TRY(hipMemset(w.sout, 0, (size_t)L1 * sizeof(uint32_t)));
   w.rows = R;
   w.lm = Lm;
@@ -2180,6 +2202,7 @@ static int batch_sample(defer_gpu_model* m, defer_gpu_cache* const* ocache, cons
       a.mb_varg = w.VARG + (size_t)lrow[j] * d.nvc;
     }
     a.mb_vsum = w.VSUM + (size_t)j * d.nvc;
+    a.mb_p = w.VP + (size_t)j * d.V;
     a.st = w.st;
     a.mask = nullptr;
     la[j] = a;

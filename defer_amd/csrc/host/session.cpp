@@ -91,7 +91,10 @@ extern "C" int defer_host_session_generate(defer_host_session* s, uint32_t max_t
   if (!s || (n_stop && !stop) || (max_tokens && !tokens_out))
     return fail(DEFER_HOST_E_INVALID, "null argument");
   // At most the cache's free positions can be sampled (one more request
-  // reports the context error), so no more words than that are drawn.
+  // reports the context error), so no more words than that are drawn. The
+  // step that hits the full cache still counts its word, as the reference's
+  // does: Session::step samples (one word) before feed fails
+  // (engine.rs:113-117, model.rs:420-422).
   const uint32_t room = defer_gpu_cache_capacity(s->c) - defer_gpu_cache_len(s->c);
   std::vector<uint32_t> words;
   try {
@@ -104,7 +107,7 @@ extern "C" int defer_host_session_generate(defer_host_session* s, uint32_t max_t
                                     words.empty() ? nullptr : words.data(), stop, n_stop,
                                     tokens_out, &n);
   s->history.insert(s->history.end(), tokens_out, tokens_out + n);
-  s->word_pos += (uint64_t)n * defer_host_words_per_sample(s->temperature);
+  s->word_pos += (uint64_t)(n + (rc == DEFER_GPU_E_CONTEXT)) * defer_host_words_per_sample(s->temperature);
   if (n_out) *n_out = n;
   return rc ? gpu_fail(rc) : DEFER_HOST_OK;
 }
@@ -144,7 +147,7 @@ extern "C" int defer_host_session_generate_logged(defer_host_session* s, uint32_
                                        words.empty() ? nullptr : words.data(), stop, n_stop,
                                        tokens_out, &n, wal_on_token, &ctx);
   s->history.insert(s->history.end(), tokens_out, tokens_out + n);
-  s->word_pos += (uint64_t)n * ctx.wps;
+  s->word_pos += (uint64_t)(n + (rc == DEFER_GPU_E_CONTEXT)) * ctx.wps;
   if (n_out) *n_out = n;
   if (ctx.wal_rc) return ctx.wal_rc;  // the WAL's error, its message kept
   return rc ? gpu_fail(rc) : DEFER_HOST_OK;

@@ -32,6 +32,7 @@
 #include <type_traits>
 
 #include "device.h"
+#include "exact.h"
 
 namespace DG_NS {
 
@@ -1527,21 +1528,17 @@ __device__ __forceinline__ float unit_f32(uint32_t word) {
   return (float)(word >> 8) * (1.0f / 16777216.0f);
 }
 
-// p_v before normalisation: exp(l/T - m), NaN -> 0 (sampler.rs:55-57).
-__device__ __forceinline__ float exp_term(float logit, float T, float m) {
-  const float sv = logit / T;
-  return isnan(sv) ? 0.0f : expf(sv - m);
-}
-
 // Sampler stage A (temperature > 0): the global max m from the chunk maxima,
-// then exp-sums of this workgroup's chunks, published for stage B under the
-// tag gsum. gsum is unique to one sampling event (a per-cache or
-// per-workspace sequence number handed in by the host), so sums left in the
-// mailbox by an earlier sample of the same logits -- at another temperature,
-// say -- never carry the tag stage B waits for.
+// then, for this workgroup's chunks, every p_v = exp(l_v/T - m) with the
+// reference's exp (exact.h) and each chunk's sum of them (any order: the
+// exact sampler uses it only to guess where the running sum's float spacing
+// changes). The p_v and the sums are published under the tag gsum, unique
+// to one sampling event (a per-cache or per-workspace sequence number handed
+// in by the host), so values left in the mailboxes by an earlier sample of
+// the same logits -- at another temperature, say -- never carry the tag the
+// exact sampler waits for.
 // CPW: chunks per polling/computing wave per round (the chunk area holds
-// NWA * CPW chunks); PA: words per lane per poll round. A chunk's sum is the
-// same arithmetic whichever wave and round computes it.
+// NWA * CPW chunks); PA: words per lane per poll round.
 template <uint32_t CPW = 1, uint32_t PA = 2>
 __device__ __forceinline__ bool sample_stage_a(const Args& a, uint32_t tick, uint32_t gsum, float T,
                                                uint32_t wg, uint32_t G, const Lds& s) {
@@ -1575,7 +1572,8 @@ __device__ __forceinline__ bool sample_stage_a(const Args& a, uint32_t tick, uin
     for (uint32_t b = wave; wave < NWA && b < nb; b += NWA) {
       const uint32_t c = wg + G * (k0 + b);
       const uint32_t v = c * VCHUNK + lane;
-      const float e = (v < d.V) ? exp_term(chunk[b * VCHUNK + lane], T, m) : 0.0f;
+      const float e = (v < d.V) ? prob_term(chunk[b * VCHUNK + lane], T, m) : 0.0f;
+      if (v < d.V) mb_put(a.mb_p + v, e, gsum);
       const float S = wave_sum(e);
       if (lane == 0) mb_put(a.mb_vsum + c, S, gsum);
     }
@@ -1584,124 +1582,307 @@ __device__ __forceinline__ bool sample_stage_a(const Args& a, uint32_t tick, uin
   return true;
 }
 
-// Inclusive scan over the 64 lanes (fixed Hillis-Steele steps).
-__device__ __forceinline__ float wave_scan(float x) {
-  const uint32_t lane = threadIdx.x % WAVE;
+// ------------------------------------------------------------ exact sampler
+//
+// sample_token (sampler.rs:78-109) for T > 0, on one workgroup, with the
+// reference's arithmetic: p_v = exp(l_v/T - m) (exact.h's expf), the
+// sequential float total of the p_v, inv = 1/total, q_v = p_v * inv, and the
+// first v with r < (the sequential float sum of q_0..q_v), else the last v
+// with q_v > 0. Both sequential sums are formed as exact.h describes: chunks
+// of 64 terms are summarised in parallel as integer totals in the units of
+// the float spacing their running sum is expected to have, one wave walks
+// the summaries and uses a chunk's total only where the exact running sum
+// is in that spacing and stays in it; any other chunk it sums term by term
+// (chunk_exact). The result does not depend on the guesses.
+
+constexpr double SAMP_MARGIN = 1.0 / 16384;  // relative slack of the region guesses
+
+// This lane's words ptr[k] (k < N) once each carries `tag`; false (uniform
+// over the wave) if the run was aborted meanwhile.
+template <int N>
+__device__ __forceinline__ bool load_tagged(const u64* const (&ptr)[N], uint32_t tag, float (&v)[N],
+                                            DevState* st, WaitCtl* ctl) {
+  uint32_t pend = 0;
+  u64 w[N];
 #pragma unroll
-  for (uint32_t o = 1; o < WAVE; o <<= 1) {
-    const float y = __shfl_up(x, o);
-    if (lane >= o) x += y;
+  for (int k = 0; k < N; ++k) w[k] = mb_load(ptr[k]);
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    if ((uint32_t)(w[k] >> 32) == tag) v[k] = __uint_as_float((uint32_t)w[k]);
+    else pend |= 1u << k;
   }
-  return x;
+  for (uint32_t spins = 0; __any(pend != 0); ++spins) {
+    if (spins >= SPIN_LIMIT) {
+      st_coherent_u32(&st->abort, 1u);
+      ctl->abort_seen = 1;
+      return false;
+    }
+    if ((spins & 63) == 63 && ld_coherent_u32(&st->abort)) {
+      ctl->abort_seen = 1;
+      return false;
+    }
+#pragma unroll
+    for (int k = 0; k < N; ++k)
+      if (pend & (1u << k)) {
+        const u64 x = mb_load(ptr[k]);
+        if ((uint32_t)(x >> 32) == tag) {
+          v[k] = __uint_as_float((uint32_t)x);
+          pend &= ~(1u << k);
+        }
+      }
+  }
+  return true;
 }
 
-// Sampler stage B: the token (sampler.rs:78-109). Greedy is the global argmax
-// (0 when every logit is NaN). With T > 0 the chunk exp-sums give the total
-// and a chunk-level scan of the CDF; the chunk holding the crossing is then
-// scanned element by element, p_v = exp(l_v/T - m) * (1/total), returning
-// the first v with p_v > 0 and r < cumulative, else the last v with p_v > 0.
-// A degenerate total (not > 0, or not finite) falls back to argmax.
-__device__ __forceinline__ bool sample_stage_b(const Args& a, uint32_t tick, uint32_t gsum, float T,
-                                               uint32_t word, const Lds& s, uint32_t* tok_out) {
+// The terms of one chunk (n <= 64 of them, lane j the j-th), added to the
+// exact running sum s one rounded step at a time, in parallel: with s in
+// grid E, the steps before the first term that leaves the region (or is a
+// tie) are an integer prefix sum; that term is one float addition; repeat.
+// FIND: stops at the first term j with r < the sum after it (hit = j; 64 if
+// none). Wave-uniform; returns false on abort.
+template <bool FIND>
+__device__ __forceinline__ bool chunk_exact(const u64* pw, uint32_t n, uint32_t tag, float inv, float r,
+                                            float& s, uint32_t& hit, DevState* st, WaitCtl* ctl) {
+  const uint32_t lane = threadIdx.x % WAVE;
+  const u64* ptr[1] = {pw + min(lane, n - 1)};
+  float v[1];
+  hit = 64;
+  if (!load_tagged<1>(ptr, tag, v, st, ctl)) return false;
+  const float x = lane < n ? (FIND ? v[0] * inv : v[0]) : 0.0f;
+  uint32_t jstart = 0;
+  for (;;) {
+    const int E = grid_of(s);
+    const uint32_t k = grid_units(s, E);
+    const bool act = lane >= jstart && lane < n;
+    const GridTerm g = grid_term(x, E);
+    const uint32_t rho = (act && !g.big) ? g.rho : 0u, aa = (act && !g.big) ? g.a : 0u;
+    const uint32_t P = wave_scan_u32(rho), Pex = P - rho;
+    const bool bad = act && (g.big || g.tie || k + Pex + aa >= GRID_TOP);
+    const uint32_t jb = first_lane(__ballot(bad));
+    if (FIND) {
+      const bool h = act && lane < jb && r < __builtin_ldexpf((float)(k + P), E);
+      const uint32_t jh = first_lane(__ballot(h));
+      if (jh < 64) {
+        hit = jh;
+        s = __builtin_ldexpf((float)(k + lane_u32(P, jh)), E);
+        return true;
+      }
+    }
+    if (jb >= 64) {
+      s = __builtin_ldexpf((float)(k + lane_u32(P, 63)), E);
+      return true;
+    }
+    s = __builtin_ldexpf((float)(k + lane_u32(Pex, jb)), E);
+    s = s + lane_f32(x, jb);
+    if (FIND && r < s) {
+      hit = jb;
+      return true;
+    }
+    jstart = jb + 1;
+    if (jstart >= n) return true;
+  }
+}
+
+// One sequential sum over the V terms x_v = p_v (FIND false) or p_v * inv
+// (FIND true), on one workgroup. A: the chunk sums of p from stage A (LDS);
+// sw: nvc summary words (LDS); dred: NWAVES doubles of LDS; res: two words.
+// Returns the total (FIND false) or the index sample_token returns (FIND
+// true) in *out (float bits / index). false on abort.
+template <bool FIND>
+__device__ __forceinline__ bool exact_walk(const Args& a, uint32_t tag, float inv, float r, const float* A, uint32_t* sw,
+                           double* dred, uint32_t* res, const Lds& s, uint32_t* out) {
+  const Dims d = shape_dims(a.d);
+  const uint32_t nvc = d.nvc, V = d.V;
+  const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+  // 1. Guess each chunk's grid from an approximate prefix of the chunk sums;
+  // a chunk whose approximate range meets a region boundary (or, FIND,
+  // lies past r) is summed term by term if the walk reaches it.
+  {
+    const uint32_t cpt = (nvc + BLOCK - 1) / BLOCK;
+    const uint32_t ca = min(threadIdx.x * cpt, nvc), cb = min(ca + cpt, nvc);
+    double own = 0.0;
+    for (uint32_t c = ca; c < cb; ++c) own += (double)lds_ld(A + c);
+    double incl = own;
+#pragma unroll
+    for (uint32_t o = 1; o < WAVE; o <<= 1) {
+      const double y = __shfl_up(incl, o);
+      if (lane >= o) incl += y;
+    }
+    if (lane == WAVE - 1) dred[wave] = incl;
+    __syncthreads();
+    double pre = incl - own;
+    for (uint32_t w = 0; w < wave; ++w) pre += dred[w];
+    const double scale = FIND ? (double)inv : 1.0;
+    for (uint32_t c = ca; c < cb; ++c) {
+      const double ac = (double)lds_ld(A + c);
+      const double lo = pre * scale * (1.0 - SAMP_MARGIN), hi = (pre + ac) * scale * (1.0 + SAMP_MARGIN);
+      const int El = grid_of((float)lo);
+      bool ev = El != grid_of((float)hi);
+      if (FIND && lo > (double)r) ev = true;
+      sw[c] = sum_word(El, ev ? SUM_EVENT : 0u);
+      pre += ac;
+    }
+    __syncthreads();
+  }
+  // 2. Integer totals of the other chunks in their guessed grid: eight lanes
+  // per chunk, eight terms per lane, on the polling and computing waves (the
+  // loader waves of the persistent kernel issue only their staging loads).
+  // A tie or a term past the region makes the chunk a term-by-term one.
+  {
+    const uint32_t grp = lane / 8, sub = lane % 8;
+    bool ok = true;
+    for (uint32_t c0 = wave * 8; wave < NWA && c0 < nvc; c0 += NWA * 8) {
+      const uint32_t c = min(c0 + grp, nvc - 1);
+      const uint32_t w0 = sw[c];
+      const bool ev = c0 + grp >= nvc || sum_total(w0) == SUM_EVENT;
+      if (__all(ev)) continue;
+      const uint32_t j0 = c * VCHUNK + sub * 8;
+      const u64* ptr[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ptr[e] = a.mb_p + min(j0 + e, V - 1);
+      float x[8];
+      if (!load_tagged<8>(ptr, tag, x, a.st, s.ctl)) {
+        ok = false;
+        break;
+      }
+      const int E = sum_grid(w0);
+      uint32_t tot = 0;
+      bool flag = false;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float xv = (j0 + e < V) ? (FIND ? x[e] * inv : x[e]) : 0.0f;
+        const GridTerm g = grid_term(xv, E);
+        flag = flag || g.big || g.tie;
+        tot += g.big ? 0u : g.rho;
+      }
+      tot += __shfl_xor(tot, 1);
+      tot += __shfl_xor(tot, 2);
+      tot += __shfl_xor(tot, 4);
+      uint32_t fl = flag ? 1u : 0u;
+      fl |= __shfl_xor(fl, 1);
+      fl |= __shfl_xor(fl, 2);
+      fl |= __shfl_xor(fl, 4);
+      if (!ev && sub == 0) sw[c] = sum_word(E, fl ? SUM_EVENT : tot);
+    }
+    if (!ok && lane == 0) s.ctl->abort_seen = 1;
+    __syncthreads();
+    if (s.ctl->abort_seen) return false;
+  }
+  // 3. The walk, on wave 0: windows of 64 chunk summaries; the usable prefix
+  // of a window is one integer sum, the first unusable chunk goes term by
+  // term.
+  if (wave == 0) {
+    float sum = 0.0f;
+    uint32_t found = NO_INDEX;
+    bool ok = true;
+    uint32_t c0 = 0;
+    while (c0 < nvc) {
+      const int E = grid_of(sum);
+      const uint32_t k = grid_units(sum, E);
+      const uint32_t c = c0 + lane;
+      const uint32_t w = c < nvc ? sw[c] : SUM_EVENT;
+      const uint32_t I = sum_total(w);
+      bool use = c < nvc && I != SUM_EVENT && sum_grid(w) == E;
+      const uint32_t P = wave_scan_u32(use ? I : 0u);
+      use = use && k + P < GRID_TOP;
+      bool stop = !use;
+      if (FIND) stop = stop || r < __builtin_ldexpf((float)(k + P), E);
+      const uint32_t fb = first_lane(__ballot(stop));
+      const uint32_t pre = fb ? lane_u32(P, fb - 1) : 0u;
+      sum = __builtin_ldexpf((float)(k + pre), E);
+      c0 += fb;
+      if (fb < 64 && c0 < nvc) {
+        const uint32_t base = c0 * VCHUNK;
+        uint32_t hit;
+        if (!chunk_exact<FIND>(a.mb_p + base, min(VCHUNK, V - base), tag, inv, r, sum, hit, a.st, s.ctl)) {
+          ok = false;
+          break;
+        }
+        if (FIND && hit < 64) {
+          found = base + hit;
+          break;
+        }
+        ++c0;
+      }
+    }
+    // No crossing (the rounded total stayed at or below r): the last v with
+    // q_v > 0 (sampler.rs:103-108), 0 if none.
+    for (uint32_t cc = nvc; FIND && ok && found == NO_INDEX && cc-- > 0;) {
+      const uint32_t base = cc * VCHUNK, n = min(VCHUNK, V - base);
+      const u64* ptr[1] = {a.mb_p + base + min(lane, n - 1)};
+      float v[1];
+      if (!load_tagged<1>(ptr, tag, v, a.st, s.ctl)) {
+        ok = false;
+        break;
+      }
+      const unsigned long long nz = __ballot(lane < n && v[0] * inv > 0.0f);
+      if (nz) found = base + 63u - (uint32_t)__clzll((long long)nz);
+    }
+    if (FIND && ok && found == NO_INDEX) found = 0;
+    if (lane == 0) {
+      res[0] = FIND ? found : __float_as_uint(sum);
+      res[1] = ok ? 1u : 0u;
+    }
+  }
+  __syncthreads();
+  const bool ok = res[1] != 0;
+  *out = res[0];
+  __syncthreads();
+  return ok;
+}
+
+// sample_token for T > 0 on one workgroup (stage A has run on every
+// workgroup): the chunk maxima give m; where m is not finite the reference's
+// total is NaN or 0 and it falls back to argmax (sampler.rs:60-69); else
+// the exact total, then the exact CDF scan.
+__device__ __forceinline__ bool sample_exact(const Args& a, uint32_t tick, uint32_t gsum, float T, uint32_t word, const Lds& s,
+                             uint32_t* tok_out) {
   const Dims d = shape_dims(a.d);
   const uint32_t nvc = d.nvc;
   const uint32_t gl = gen_lm(d, tick - 1u);
   float* vmx = s.scr;
   float* varg = vmx + nvc;
-  float* vsum = varg + nvc;
-  float* chunk = vsum + nvc;  // [VCHUNK]
-  float* wtot = chunk + VCHUNK;  // [NWAVES + 2]
+  float* A = varg + nvc;
+  uint32_t* sw = reinterpret_cast<uint32_t*>(vmx);  // reused once the argmax is formed
+  double* dred = reinterpret_cast<double*>(s.scr + ((3 * nvc + 1) & ~1u));
+  uint32_t* res = reinterpret_cast<uint32_t*>(dred + NWAVES);
   if (!poll_gather<2, 2, 2>(gather_vec(a.mb_vmax, nvc, gl, vmx), gather_vec(a.mb_varg, nvc, gl, varg),
-                   T != 0.0f ? gather_vec(a.mb_vsum, nvc, gsum, vsum) : no_gather(), NWA, a.st,
-                   s.ctl))
+                            gather_vec(a.mb_vsum, nvc, gsum, A), NWA, a.st, s.ctl))
     return false;
   float bv;
   uint32_t bi;
   global_argmax(vmx, varg, nvc, s.red, &bv, &bi);
-  const uint32_t greedy = (bi == NO_INDEX) ? 0u : bi;
-  if (T == 0.0f) {
-    *tok_out = greedy;
-    return true;
-  }
   const float m = (bi == NO_INDEX) ? -INFINITY : bv / T;
-  // total = fixed-tree sum of the chunk sums
-  float part = 0.0f;
-  for (uint32_t c = threadIdx.x; c < nvc; c += BLOCK) part += vsum[c];
-  const float total = block_sum(part, s.red);
-  if (!(total > 0.0f) || !isfinite(total)) {
-    *tok_out = greedy;
+  if (!isfinite(m)) {
+    *tok_out = (bi == NO_INDEX) ? 0u : bi;
     return true;
   }
-  const float inv = 1.0f / total;
-  const float r = unit_f32(word);
-  // Chunk-level exclusive prefix of P_c = S_c * inv: each thread owns a
-  // contiguous run of chunks, then lanes, then waves, in fixed order.
-  const uint32_t per = (nvc + BLOCK - 1) / BLOCK;
-  const uint32_t c0 = threadIdx.x * per, c1 = min(c0 + per, nvc);
-  float own = 0.0f;
-  for (uint32_t c = c0; c < c1; ++c) own += vsum[c] * inv;
-  const float incl = wave_scan(own);
-  const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
-  __syncthreads();
-  if (lane == WAVE - 1) wtot[wave] = incl;
-  __syncthreads();
-  float base = 0.0f;
-  for (uint32_t w = 0; w < wave; ++w) base += wtot[w];
-  float cum = base + (incl - own);
-  uint32_t first = NO_INDEX;
-  float first_cum = 0.0f;
-  for (uint32_t c = c0; c < c1; ++c) {
-    const float pc = vsum[c] * inv;
-    if (vsum[c] > 0.0f && r < cum + pc) {
-      first = c;
-      first_cum = cum;
-      break;
-    }
-    cum += pc;
-  }
-  // lowest chunk index with a crossing, and its starting cumulative value
-  uint32_t fc = first;
-  for (int o = 32; o > 0; o >>= 1) fc = min(fc, (uint32_t)__shfl_xor(fc, o));
-  __syncthreads();
-  if (lane == 0) reinterpret_cast<uint32_t*>(wtot)[wave] = fc;
-  __syncthreads();
-  uint32_t cstar = NO_INDEX;
-  for (uint32_t w = 0; w < NWAVES; ++w) cstar = min(cstar, reinterpret_cast<uint32_t*>(wtot)[w]);
-  __syncthreads();
-  if (first != NO_INDEX && first == cstar) wtot[NWAVES] = first_cum;
-  __syncthreads();
-  float run = (cstar != NO_INDEX) ? wtot[NWAVES] : 0.0f;
-  __syncthreads();
-  // Element scan from chunk cstar onwards (normally one chunk).
-  for (uint32_t c = cstar; c < nvc; ++c) {
-    const uint32_t v0 = c * VCHUNK, nv = min(VCHUNK, d.V - v0);
-    if (!poll_gather<1>(gather_vec(a.mb_logit + v0, nv, gl, chunk), NWA, a.st, s.ctl)) return false;
-    const float p = (lane < nv) ? exp_term(chunk[lane], T, m) * inv : 0.0f;
-    const float sc = wave_scan(p > 0.0f ? p : 0.0f);
-    const bool hit = p > 0.0f && r < run + sc;
-    const unsigned long long hits = __ballot(hit);
-    if (hits) {
-      *tok_out = v0 + (uint32_t)__ffsll((long long)hits) - 1u;
-      __syncthreads();
-      return true;
-    }
-    run = run + __shfl(sc, WAVE - 1);
-    __syncthreads();
-  }
-  // No crossing (rounding): the last token with p > 0.
-  for (uint32_t cc = nvc; cc-- > 0;) {
-    if (!(vsum[cc] > 0.0f)) continue;
-    const uint32_t v0 = cc * VCHUNK, nv = min(VCHUNK, d.V - v0);
-    if (!poll_gather<1>(gather_vec(a.mb_logit + v0, nv, gl, chunk), NWA, a.st, s.ctl)) return false;
-    const float p = (lane < nv) ? exp_term(chunk[lane], T, m) * inv : 0.0f;
-    const unsigned long long nz = __ballot(p > 0.0f);
-    __syncthreads();
-    if (nz) {
-      *tok_out = v0 + 63u - (uint32_t)__clzll((long long)nz);
-      return true;
-    }
-  }
-  *tok_out = 0;
+  uint32_t sum_bits, tok;
+  if (!exact_walk<false>(a, gsum, 1.0f, 0.0f, A, sw, dred, res, s, &sum_bits)) return false;
+  const float inv = 1.0f / __uint_as_float(sum_bits);
+  if (!exact_walk<true>(a, gsum, inv, unit_f32(word), A, sw, dred, res, s, &tok)) return false;
+  *tok_out = tok;
+  return true;
+}
+
+// Sampler stage B: the token (sampler.rs:78-109). Greedy is the global argmax
+// of the chunk maxima (0 when every logit is NaN), on every workgroup that
+// calls it; T > 0 is sample_exact, on one workgroup.
+__device__ __forceinline__ bool sample_stage_b(const Args& a, uint32_t tick, uint32_t gsum, float T,
+                                               uint32_t word, const Lds& s, uint32_t* tok_out) {
+  if (T != 0.0f) return sample_exact(a, tick, gsum, T, word, s, tok_out);
+  const Dims d = shape_dims(a.d);
+  const uint32_t nvc = d.nvc;
+  const uint32_t gl = gen_lm(d, tick - 1u);
+  float* vmx = s.scr;
+  float* varg = vmx + nvc;
+  if (!poll_gather<2, 2>(gather_vec(a.mb_vmax, nvc, gl, vmx), gather_vec(a.mb_varg, nvc, gl, varg), NWA,
+                         a.st, s.ctl))
+    return false;
+  float bv;
+  uint32_t bi;
+  global_argmax(vmx, varg, nvc, s.red, &bv, &bi);
+  *tok_out = (bi == NO_INDEX) ? 0u : bi;
   return true;
 }
 

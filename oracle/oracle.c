@@ -418,27 +418,79 @@ void oracle_softmax_with_temperature(const float* logits, size_t n, float temper
 /* rand 0.8 `Standard` for f32: the top 24 bits of one u32, times 2^-24. */
 float oracle_unit_f32(uint32_t word) { return (float)(word >> 8) * (1.0f / 16777216.0f); }
 
+/* The CDF scan of sampler.rs:94-108 over normalised probabilities: the
+ * first i with p_i > 0 and r < the sequential float sum of p_0..p_i, else the
+ * last i with p_i > 0 (0 if none). *lo / *hi (nullable): the cumulative sum
+ * before and after the returned index, in that same float arithmetic. */
+static uint32_t cdf_scan(const float* probs, size_t n, float r, float* lo, float* hi) {
+  float cumulative = 0.0f;
+  size_t last_nonzero = 0;
+  float before_last = 0.0f;
+  for (size_t i = 0; i < n; ++i) {
+    const float p = probs[i];
+    if (p > 0.0f) {
+      const float before = cumulative;
+      last_nonzero = i;
+      before_last = before;
+      cumulative += p;
+      if (r < cumulative) {
+        if (lo) *lo = before;
+        if (hi) *hi = cumulative;
+        return (uint32_t)i;
+      }
+    }
+  }
+  if (lo) *lo = before_last;
+  if (hi) *hi = cumulative;
+  return (uint32_t)last_nonzero;
+}
+
 /* sampler.rs:78-109 */
 uint32_t oracle_sample_token(const float* logits, size_t n, float temperature, uint32_t word) {
   if (temperature == 0.0f) return oracle_argmax(logits, n);
   float* probs = (float*)malloc(n * sizeof(float));
   oracle_softmax_with_temperature(logits, n, temperature, probs);
-  const float r = oracle_unit_f32(word);
-  float cumulative = 0.0f;
-  size_t last_nonzero = 0;
-  for (size_t i = 0; i < n; ++i) {
-    const float p = probs[i];
-    if (p > 0.0f) {
-      last_nonzero = i;
-      cumulative += p;
-      if (r < cumulative) {
-        free(probs);
-        return (uint32_t)i;
-      }
-    }
-  }
+  const uint32_t tok = cdf_scan(probs, n, oracle_unit_f32(word), NULL, NULL);
   free(probs);
-  return (uint32_t)last_nonzero;
+  return tok;
+}
+
+/* sample_token at T > 0 plus how close the draw was: *margin = min(r - lo,
+ * hi - r) with lo / hi the cumulative sums around the chosen token in the
+ * reference's own arithmetic (sampler.rs:52-75 sums and normalises
+ * sequentially in float; 94-106 accumulates the CDF the same way). */
+uint32_t oracle_sample_margin(const float* logits, size_t n, float temperature, uint32_t word,
+                              float* margin) {
+  float* probs = (float*)malloc(n * sizeof(float));
+  oracle_softmax_with_temperature(logits, n, temperature, probs);
+  const float r = oracle_unit_f32(word);
+  float lo = 0.0f, hi = 0.0f;
+  const uint32_t tok = cdf_scan(probs, n, r, &lo, &hi);
+  free(probs);
+  const float a = r - lo, b = hi - r;
+  *margin = a < b ? a : b;
+  return tok;
+}
+
+/* sampler.rs:58-108 on un-normalised terms p (what softmax_with_temperature
+ * forms before its sum, 55-57): the sequential float total, inv = 1/total,
+ * p_i * inv, then the CDF scan for the draw of `word`. Returns the index;
+ * *total gets the sum. Degenerate totals are the caller's business. */
+uint32_t oracle_sample_terms(const float* p, size_t n, uint32_t word, float* total) {
+  float sum = 0.0f;
+  for (size_t i = 0; i < n; ++i) sum += p[i];
+  *total = sum;
+  const float inv = 1.0f / sum;
+  float* probs = (float*)malloc(n * sizeof(float));
+  for (size_t i = 0; i < n; ++i) probs[i] = p[i] * inv;
+  const uint32_t tok = cdf_scan(probs, n, oracle_unit_f32(word), NULL, NULL);
+  free(probs);
+  return tok;
+}
+
+/* The reference's f32::exp (the platform libm's expf) over an array. */
+void oracle_expf_array(const float* x, float* y, size_t n) {
+  for (size_t i = 0; i < n; ++i) y[i] = expf(x[i]);
 }
 
 /* ----------------------------------------- rand_chacha 0.3.1 / rand_core 0.6.4 */

@@ -106,6 +106,10 @@ void oracle_softmax_with_temperature(const float* logits, size_t n, float temper
 float oracle_unit_f32(uint32_t word);
 /* One ChaCha8 word `word` is consumed iff temperature > 0. */
 uint32_t oracle_sample_token(const float* logits, size_t n, float temperature, uint32_t word);
+uint32_t oracle_sample_margin(const float* logits, size_t n, float temperature, uint32_t word,
+                              float* margin);
+uint32_t oracle_sample_terms(const float* p, size_t n, uint32_t word, float* total);
+void oracle_expf_array(const float* x, float* y, size_t n);
 
 /* ---- rand_chacha / rand_core (third-party, restated) -------------------- */
 void oracle_chacha_block(const uint32_t key[8], uint64_t counter, uint64_t stream, int rounds,

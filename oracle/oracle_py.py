@@ -90,6 +90,12 @@ def lib() -> ctypes.CDLL:
     L.oracle_unit_f32.restype = f32
     L.oracle_sample_token.argtypes = [vp, sz, f32, u32]
     L.oracle_sample_token.restype = u32
+    L.oracle_sample_margin.argtypes = [vp, sz, f32, u32, P(f32)]
+    L.oracle_sample_margin.restype = u32
+    L.oracle_sample_terms.argtypes = [vp, sz, u32, P(f32)]
+    L.oracle_sample_terms.restype = u32
+    L.oracle_expf_array.argtypes = [vp, vp, sz]
+    L.oracle_expf_array.restype = None
     L.oracle_chacha_block.argtypes = [vp, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int, vp]
     L.oracle_seed_from_u64.argtypes = [ctypes.c_uint64, vp]
     L.oracle_pcg32_step.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
@@ -210,6 +216,31 @@ def unit_f32(word: int) -> float:
 def sample_token(logits, t: float, word: int) -> int:
     l = f32a(logits)
     return int(lib().oracle_sample_token(_p(l), l.size, t, word & 0xFFFFFFFF))
+
+
+def sample_margin(logits, t: float, word: int):
+    """(token, margin): sample_token at T > 0 and the distance of the draw
+    from the chosen token's CDF edges, in the reference's float arithmetic."""
+    l = f32a(logits)
+    m = ctypes.c_float()
+    tok = int(lib().oracle_sample_margin(_p(l), l.size, t, word & 0xFFFFFFFF, ctypes.byref(m)))
+    return tok, float(m.value)
+
+
+def sample_terms(p, word: int):
+    """(index, total): sampler.rs:58-108 on un-normalised terms p."""
+    a = f32a(p)
+    tot = ctypes.c_float()
+    tok = int(lib().oracle_sample_terms(_p(a), a.size, word & 0xFFFFFFFF, ctypes.byref(tot)))
+    return tok, np.float32(tot.value)
+
+
+def expf(x) -> np.ndarray:
+    """The reference's f32::exp (libm expf) elementwise."""
+    a = f32a(x)
+    out = np.empty_like(a)
+    lib().oracle_expf_array(_p(a), _p(out), a.size)
+    return out
 
 
 # ---- rng -----------------------------------------------------------------------

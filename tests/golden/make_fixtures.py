@@ -12,7 +12,10 @@ configuration); the GPU box only reads the `.npz` files.
 Every fixture holds, per sampled step: the token, and how close the choice
 was (greedy: the gap between the two largest logits; T > 0: the distance in
 probability between the draw r and the nearer edge of the chosen token's CDF
-interval), so a test can tell a real mismatch from a rounding-boundary case.
+interval, formed in the reference's own float arithmetic), so a test can tell
+a real mismatch from a rounding-boundary case. The T > 0 sessions (c1 B, c2,
+c3) also hold the argmax and top-2 gap after every fed position, so the GPU
+can be teacher-forced along the oracle's history and checked at each one.
 Last-position logits are stored as every 8th value plus the 32 largest.
 
 Workloads (weights N(0, 0.02) from seed 0, defer_amd.synthetic):
@@ -20,8 +23,9 @@ Workloads (weights N(0, 0.02) from seed 0, defer_amd.synthetic):
       session B 128 tokens at T = 0.7 with seed 42.
   c2  135M shape: 512-token prompt (seed 7) + 1536 tokens at T = 0.7, seed 7;
       plus the argmax and top-2 gap at every one of the 2048 positions.
-  c3  360M shape: 128-token prompt (seed 1) + 4096 tokens at T = 0.8, seed 1;
-      then 16 greedy tokens past position 4224 from the same cache.
+  c3  360M shape: 128-token prompt (seed 1) + 4096 tokens at T = 0.8, seed 1,
+      with the argmax and gap at all 4224 positions; then 16 greedy tokens
+      past position 4224 from the same cache.
   c4  1B shape: session k's 256-token prompt (seed 1000 + k) + 256 greedy
       tokens, for sessions 0 and 63.
   c5  8B shape: 64-token prompt (seed 0) + 512 greedy tokens.
@@ -53,19 +57,13 @@ def top2_gap(logits: np.ndarray) -> float:
 
 
 def cdf_margin(logits: np.ndarray, T: float, word: int, tok: int) -> float:
-    """Distance of r from the edges of token tok's CDF interval, with the
-    probabilities formed as sampler.rs:43-75 forms them (float32, sequential
-    cumulative sum)."""
-    s = (logits.astype(np.float32) / np.float32(T)).astype(np.float32)
-    m = np.max(s[~np.isnan(s)])
-    p = np.where(np.isnan(s), np.float32(0), np.exp(s - m)).astype(np.float32)
-    tot = np.float32(np.sum(p, dtype=np.float64))
-    p = (p * (np.float32(1) / tot)).astype(np.float32)
-    c = np.cumsum(p, dtype=np.float32)
-    r = float(O.unit_f32(word))
-    hi = float(c[tok])
-    lo = float(c[tok - 1]) if tok > 0 else 0.0
-    return min(r - lo, hi - r)
+    """Distance of the draw r from the edges of token tok's CDF interval, in
+    the reference's own arithmetic (sampler.rs:43-109: float32 sequential
+    total, normalisation and cumulative sum; oracle_sample_margin), so it is
+    >= 0 for the token the oracle chose."""
+    got, m = O.sample_margin(logits, T, word)
+    assert got == tok
+    return m
 
 
 def logits_summary(prefix: str, logits: np.ndarray) -> dict:
@@ -77,14 +75,23 @@ def logits_summary(prefix: str, logits: np.ndarray) -> dict:
     }
 
 
-def run_session(om, prompt, n_gen: int, T: float, seed_u64: int, say):
+def run_session(om, prompt, n_gen: int, T: float, seed_u64: int, say, per_position=None):
     """Session::prompt then n_gen steps (engine.rs:62-137) on the oracle,
-    with the per-step diagnostics."""
+    with the per-step diagnostics. per_position (a dict, optional) gets the
+    argmax and top-2 gap of the logits after every fed position."""
     seed = O.seed_from_u64(seed_u64)
     cache = om.new_cache()
     logits = None
+    am, gp = [], []
+
+    def note(lg):
+        if per_position is not None:
+            am.append(int(np.argmax(lg)))
+            gp.append(top2_gap(lg))
+
     for t in prompt:
         logits = om.forward(int(t), cache)
+        note(logits)
     toks, words, close = [], [], []
     t0 = time.time()
     for g in range(n_gen):
@@ -94,8 +101,12 @@ def run_session(om, prompt, n_gen: int, T: float, seed_u64: int, say):
         toks.append(tok)
         words.append(w)
         logits = om.forward(tok, cache)
+        note(logits)
         if g % 64 == 63:
             say(f"  {g + 1}/{n_gen} tokens, {time.time() - t0:.0f} s")
+    if per_position is not None:
+        per_position["argmax"] = np.asarray(am, np.uint32)
+        per_position["gap"] = np.asarray(gp, np.float64)
     return cache, np.asarray(toks, np.uint32), np.asarray(words, np.uint32), \
         np.asarray(close, np.float64), logits
 
@@ -116,8 +127,10 @@ def fixture_c1():
     _, ta, _, ga, la = run_session(om, prompt, 128, 0.0, 42, say)
     out.update(greedy_tokens=ta, greedy_gap=ga, **logits_summary("greedy_last", la))
     say("session B: 128 at T=0.7, seed 42")
-    _, tb, wb, mb, lb = run_session(om, prompt, 128, 0.7, 42, say)
+    pp = {}
+    _, tb, wb, mb, lb = run_session(om, prompt, 128, 0.7, 42, say, pp)
     out.update(sampled_tokens=tb, sampled_words=wb, sampled_margin=mb,
+               sampled_argmax=pp["argmax"], sampled_gap=pp["gap"],
                **logits_summary("sampled_last", lb))
     return out
 
@@ -164,9 +177,10 @@ def fixture_c3():
     om = O.OracleModel(cfg, synthetic.make_weights(cfg, 0))
     prompt = synthetic.make_prompt(cfg["vocab_size"], 128, seed=1)
     say("128 prompt + 4096 at T=0.8, seed 1")
-    cache, toks, words, margin, logits = run_session(om, prompt, 4096, 0.8, 1, say)
+    pp = {}
+    cache, toks, words, margin, logits = run_session(om, prompt, 4096, 0.8, 1, say, pp)
     out = {"prompt": prompt, "tokens": toks, "words": words, "margin": margin,
-           **logits_summary("sampled_last", logits)}
+           "argmax": pp["argmax"], "gap": pp["gap"], **logits_summary("sampled_last", logits)}
     say("16 greedy tokens past position 4224")
     tail, gaps = [], []
     for _ in range(16):

@@ -7,9 +7,10 @@ result against the oracle; it exits 0 only when all checks hold.
 
 The program is a separate process, and the cooperative launch of the
 persistent kernel uses the device's global wave synchronisation, which the
-driver grants one process at a time: this file is named to be collected
-before every other GPU test, while the test process itself has not yet
-launched a cooperative kernel.
+driver grants one process at a time: tests/conftest.py runs this test before
+every other one, while the test process itself has not yet launched a
+cooperative kernel. (Were the launch refused, the library would run the same
+ops as per-phase kernels, with the same bits.)
 """
 import os
 import subprocess

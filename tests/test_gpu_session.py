@@ -329,3 +329,28 @@ def test_model_load_from_safetensors(tmp_path):
     c2, d2 = gm2.new_cache(64), ref2.new_cache(64)
     la, lb = gm2.forward(9, c2), ref2.forward(9, d2)
     assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+
+
+def test_full_cache_step_at_temperature_reports_context(tiny):
+    """A session whose cache is full, stepped at T > 0: the context error
+    with the reference's message (model.rs:420-422), the history unchanged,
+    and the rng position one word further on, because Session::step samples
+    (one word) before feed fails (engine.rs:113-117). generate past the end
+    commits the tokens that fit, then reports the same error."""
+    cfg, w, gm, om = tiny
+    prompt = synthetic.make_prompt(cfg["vocab_size"], 8, seed=2)
+    s = H.Session(gm, H.seed_from_u64(5), 0.9, capacity=12)
+    s.prompt(prompt)
+    toks = s.generate(4)
+    assert len(toks) == 4 and s.rng_word_pos == 4
+    hist = s.history
+    with pytest.raises(H.DeferHostError, match="context length"):
+        s.step()
+    assert s.history == hist and s.rng_word_pos == 5
+    s2 = H.Session(gm, H.seed_from_u64(5), 0.9, capacity=12)
+    s2.prompt(prompt)
+    with pytest.raises(H.DeferHostError, match="context length"):
+        s2.generate(10)
+    assert s2.history == hist and s2.rng_word_pos == 5
+    s.close()
+    s2.close()
