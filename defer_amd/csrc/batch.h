@@ -1171,9 +1171,15 @@ __global__ __launch_bounds__(BLOCK) void k_b_sample(const Args* __restrict__ lar
   // A row whose wait runs out still leaves a token in range (0), so a
   // following batched embedding never reads outside the table.
   if (threadIdx.x == 0) out[j] = 0u;
-  if (T != 0.0f && !sample_stage_a<SAMP_CPW, 8>(a, tick[j], tag0 + j, T, 0, 1, s)) return;
   uint32_t tok = 0;
-  if (!sample_stage_b(a, tick[j], tag0 + j, T, T != 0.0f ? words[j] : 0u, s, &tok)) return;
+  if (T != 0.0f) {
+    float m;
+    uint32_t bi;
+    if (!sample_stage_a<SAMP_CPW, 8>(a, tick[j], tag0 + j, T, 0, 1, s, &m, &bi)) return;
+    if (!sample_exact(a, tag0 + j, m, bi, words[j], 0, 1, true, s, &tok)) return;
+  } else if (!sample_greedy(a, tick[j], s, &tok)) {
+    return;
+  }
   if (threadIdx.x == 0) out[j] = tok;
 }
 

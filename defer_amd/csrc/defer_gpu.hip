@@ -110,8 +110,10 @@ __global__ __launch_bounds__(BLOCK) void k_samp_a(const Args* __restrict__ ap,
   if (st->halt) return;
   const uint32_t i = st->op;
   if (i < run->sample_from || run->temperature == 0.0f) return;
+  float m;
+  uint32_t bi;
   sample_stage_a(a, st->tick, run->samp_tag0 + (i - run->sample_from), run->temperature,
-                 blockIdx.x, gridDim.x, s);
+                 blockIdx.x, gridDim.x, s, &m, &bi);
 }
 
 // One workgroup: sampler stage B (if the op samples) and the token to feed.
@@ -126,8 +128,7 @@ __global__ __launch_bounds__(BLOCK) void k_op(const Args* __restrict__ ap,
   uint32_t tok;
   if (i >= r.sample_from) {
     const uint32_t word = r.temperature != 0.0f ? r.words[i - r.sample_from] : 0u;
-    if (!sample_stage_b(a, st->tick, r.samp_tag0 + (i - r.sample_from), r.temperature, word, s,
-                        &tok))
+    if (!sample_one_wg(a, st->tick, r.samp_tag0 + (i - r.sample_from), r.temperature, word, s, &tok))
       return;
     if (r.mode == RUN_REPLAY) {
       if (tok != r.tokens[i]) {
@@ -372,14 +373,14 @@ struct defer_gpu_model {
   double pstat[6] = {0, 0, 0, 0, 0, 0};
 };
 
-// k_b_sample's LDS: the rows layout, with stage A's chunk area (NWA *
-// SAMP_CPW chunks from 2 * nvc floats into the scratch) wherever it runs
-// past that layout's end.
+// k_b_sample's LDS: the rows layout, with the sampler's region (stage A's
+// chunk area holds NWA * SAMP_CPW chunks) wherever it runs past that
+// layout's end.
 static size_t samp_lds_bytes(const defer_gpu_model* m) {
   const Dims& d = m->d;
-  const size_t chunk_end =
-      (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + 2 * d.nvc + NWA * SAMP_CPW * VCHUNK) * sizeof(float);
-  return std::max(m->lds_rows, chunk_end);
+  const size_t samp_end =
+      (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + samp_lds_floats(d.nvc, NWA * SAMP_CPW)) * sizeof(float);
+  return std::max(m->lds_rows, samp_end);
 }
 
 // A persistent kernel compiled for this exact shape, if there is one. The
@@ -489,7 +490,7 @@ static int apply_layout(defer_gpu_model* m, uint32_t G) {
                             MAX_GROUP * attn_chunk(d.cap - 1) + NCW * d.hd * d.group;
   const uint32_t scr_o = INLINE_COMB_MAX + rmax;
   const uint32_t scr_comb = MAX_ACHUNKS * hs;
-  const uint32_t scr_samp = 3 * d.nvc + VCHUNK + NWAVES + 2 + NWA * VCHUNK;
+  const uint32_t scr_samp = samp_lds_floats(d.nvc, NWA);
   const uint32_t scr_lm = ((d.nvc + G - 1) / G) * VCHUNK;
   d.lds_scr = (std::max({scr_attn, scr_o, scr_comb, scr_samp, scr_lm, 2 * NWAVES}) + 3) & ~3u;
   // O rows skip the workgroups that take the attention items at positions
@@ -869,9 +870,9 @@ static int cache_alloc(const defer_gpu_model* m, uint32_t cap, defer_gpu_cache* 
   HIP_TRY(hipMalloc(&c->vc, kvn * sizeof(float)));
   const size_t hs = d.hd + 2;
   // xo, xd, g: MB_REPS replicas of one block, each on its own 32 KB boundary
-  const size_t rep_words = ((size_t)2 * d.h + d.ff + 1 + 4095) / 4096 * 4096;
+  const size_t rep_words = ((size_t)2 * d.h + d.ff + 4095) / 4096 * 4096;
   const size_t base_words = (d.qkv_rows + (size_t)d.nh * MAX_ACHUNKS * hs + d.q + 2 * (size_t)d.V +
-                             3 * (size_t)d.nvc + 64 + 4095) / 4096 * 4096;
+                             5 * (size_t)d.nvc + 64 + 4095) / 4096 * 4096;
   const size_t words = base_words + MB_REPS * rep_words;
   c->mb_words = words;
   HIP_TRY(hipMalloc(&c->mb, words * sizeof(u64)));
@@ -900,11 +901,12 @@ static int cache_alloc(const defer_gpu_model* m, uint32_t cap, defer_gpu_cache* 
   a.mb_varg = p; p += d.nvc;
   a.mb_vsum = p; p += d.nvc;
   a.mb_p = p; p += d.V;
+  a.mb_psum = p; p += d.nvc;
+  a.mb_qsum = p; p += d.nvc;
   p = c->mb + base_words;
   a.mb_xo = p;
   a.mb_xd = p + d.h;
   a.mb_g = p + 2 * d.h;
-  a.mb_tok = p + 2 * d.h + d.ff;
   a.rep_words = (uint32_t)rep_words;
   a.st = c->st;
   a.mask = nullptr;
@@ -1805,7 +1807,7 @@ static int ensure_ws(defer_gpu_model* m, uint32_t rows, uint32_t lm) {
   HIP_TRY(hipMalloc(&w.LOGT, (size_t)L1 * d.V * sizeof(u64)));
   HIP_TRY(hipMalloc(&w.VMAX, (size_t)L1 * d.nvc * sizeof(u64)));
   HIP_TRY(hipMalloc(&w.VARG, (size_t)L1 * d.nvc * sizeof(u64)));
-  HIP_TRY(hipMalloc(&w.VSUM, (size_t)L1 * d.nvc * sizeof(u64)));
+  HIP_TRY(hipMalloc(&w.VSUM, (size_t)L1 * 3 * d.nvc * sizeof(u64)));
   HIP_TRY(hipMalloc(&w.VP, (size_t)L1 * d.V * sizeof(u64)));
   HIP_TRY(hipMalloc(&w.largs, (size_t)L1 * sizeof(Args)));
   HIP_TRY(hipMalloc(&w.sel, (size_t)L1 * sizeof(uint32_t)));
@@ -1817,7 +1819,7 @@ static int ensure_ws(defer_gpu_model* m, uint32_t rows, uint32_t lm) {
   HIP_TRY(hipMemset(w.st, 0, sizeof(DevState)));
   // Tags start at 1, so zeroed sums never match a wait; sampled tokens
   // start in range.
-  HIP_TRY(hipMemset(w.VSUM, 0, (size_t)L1 * d.nvc * sizeof(u64)));
+  HIP_TRY(hipMemset(w.VSUM, 0, (size_t)L1 * 3 * d.nvc * sizeof(u64)));
   HIP_TRY(hipMemset(w.VP, 0, (size_t)L1 * d.V * sizeof(u64)));
   HIP_TRY(hipMemset(w.sout, 0, (size_t)L1 * sizeof(uint32_t)));
   w.rows = R;
@@ -2201,7 +2203,9 @@ static int batch_sample(defer_gpu_model* m, defer_gpu_cache* const* ocache, cons
       a.mb_vmax = w.VMAX + (size_t)lrow[j] * d.nvc;
       a.mb_varg = w.VARG + (size_t)lrow[j] * d.nvc;
     }
-    a.mb_vsum = w.VSUM + (size_t)j * d.nvc;
+    a.mb_vsum = w.VSUM + (size_t)j * 3 * d.nvc;
+    a.mb_psum = a.mb_vsum + d.nvc;
+    a.mb_qsum = a.mb_vsum + 2 * d.nvc;
     a.mb_p = w.VP + (size_t)j * d.V;
     a.st = w.st;
     a.mask = nullptr;

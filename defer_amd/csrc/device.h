@@ -133,9 +133,8 @@ struct Args {
   u64* mb_qkv;           // [qkv_rows]
   u64* mb_part;          // [nh][MAX_ACHUNKS][hd + 2]  (m, l, acc[hd])
   u64* mb_att;           // [q] combined attention (separate-combine path)
-  // xo, xd, g and the sampled token have MB_REPS replicas, rep_words apart:
-  // a word is published to every replica and a workgroup reads its XCD's
-  // (wg % 8)
+  // xo, xd and g have MB_REPS replicas, rep_words apart: a word is
+  // published to every replica and a workgroup reads its XCD's (wg % 8)
   u64* mb_xo;            // [h] residual after attention
   u64* mb_xd;            // [h] residual after the MLP
   u64* mb_g;             // [ff]
@@ -145,7 +144,8 @@ struct Args {
   u64* mb_varg;          // [nvc] chunk argmax (index bits)
   u64* mb_vsum;          // [nvc] chunk sum of exp(logit/T - m)
   u64* mb_p;             // [V] exp(logit/T - m) of the sampling event in flight
-  u64* mb_tok;           // the token sampled at T > 0 (replicated like xo: one word per replica)
+  u64* mb_psum;          // [nvc] chunk summary words of the sequential total (exact sampler)
+  u64* mb_qsum;          // [nvc] chunk summary words of the sequential CDF (exact sampler)
   DevState* st;
   const uint32_t* mask;  // bitmask over positions, or null
   RunDesc run;

@@ -43,9 +43,8 @@ __device__ __forceinline__ bool is_stop(const RunDesc& r, uint32_t tok) {
   return false;
 }
 
-// Every op of a run in one launch. Greedy sampling runs on every workgroup
-// (same inputs, same code, same token); sampling at T > 0 on workgroup 0,
-// which hands the token to the others.
+// Every op of a run in one launch. Every workgroup samples (same inputs, same
+// code, same token), so no broadcast is needed.
 __global__ __launch_bounds__(BLOCK) void k_persistent(const Args* __restrict__ ap,
                                                       const RunDesc* __restrict__ run) {
   const Args& a = *ap;
@@ -70,20 +69,11 @@ __global__ __launch_bounds__(BLOCK) void k_persistent(const Args* __restrict__ a
       const uint32_t word = r.temperature != 0.0f ? cptr(r.words)[i - r.sample_from] : 0u;
       const uint32_t gsum = r.samp_tag0 + (i - r.sample_from);
       if (r.temperature != 0.0f) {
-        if (!sample_stage_a(a, tick, gsum, r.temperature, wg, G, s)) break;
-        // Workgroup 0 forms the token with the reference's arithmetic
-        // (sample_exact) and hands it to the others in a replicated tagged
-        // word, one replica per XCD.
-        if (wg == 0) {
-          if (!sample_exact(a, tick, gsum, r.temperature, word, s, &tok)) break;
-          if (threadIdx.x < MB_REPS)
-            mb_put(a.mb_tok + (size_t)threadIdx.x * a.rep_words, __uint_as_float(tok), gsum);
-        } else {
-          if (!poll_gather<1>(gather_vec(rep_of(a, a.mb_tok, wg), 1, gsum, s.red), 1, a.st, s.ctl)) break;
-          tok = __float_as_uint(lds_ld(s.red));
-          __syncthreads();
-        }
-      } else if (!sample_stage_b(a, tick, gsum, 0.0f, 0u, s, &tok)) {
+        float m;
+        uint32_t bi;
+        if (!sample_stage_a(a, tick, gsum, r.temperature, wg, G, s, &m, &bi)) break;
+        if (!sample_exact(a, gsum, m, bi, word, wg, G, true, s, &tok)) break;
+      } else if (!sample_greedy(a, tick, s, &tok)) {
         break;
       }
       if (r.mode == RUN_REPLAY) {

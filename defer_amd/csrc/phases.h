@@ -1528,33 +1528,126 @@ __device__ __forceinline__ float unit_f32(uint32_t word) {
   return (float)(word >> 8) * (1.0f / 16777216.0f);
 }
 
-// Sampler stage A (temperature > 0): the global max m from the chunk maxima,
-// then, for this workgroup's chunks, every p_v = exp(l_v/T - m) with the
-// reference's exp (exact.h) and each chunk's sum of them (any order: the
-// exact sampler uses it only to guess where the running sum's float spacing
-// changes). The p_v and the sums are published under the tag gsum, unique
-// to one sampling event (a per-cache or per-workspace sequence number handed
-// in by the host), so values left in the mailboxes by an earlier sample of
-// the same logits -- at another temperature, say -- never carry the tag the
-// exact sampler waits for.
-// CPW: chunks per polling/computing wave per round (the chunk area holds
-// NWA * CPW chunks); PA: words per lane per poll round.
+// ------------------------------------------------------------ exact sampler
+//
+// sample_token (sampler.rs:78-109) for T > 0 with the reference's
+// arithmetic: p_v = exp(l_v/T - m) (exact.h's expf), the sequential float
+// total of the p_v, inv = 1/total, q_v = p_v * inv, and the first v with
+// r < (the sequential float sum of q_0..q_v), else the last v with q_v > 0.
+// Both sequential sums are formed as exact.h describes, in stages that every
+// participating workgroup runs (G of them, workgroup wg owning the chunks
+// c = wg + G*k):
+//   A   the chunk maxima give m; each owner forms its chunks' p_v (kept in
+//       LDS where they fit) and publishes them and each chunk's float sum;
+//   A2  every workgroup reads all chunk sums and forms the same approximate
+//       prefix; owners publish each chunk's total in units of the float
+//       spacing the running sum is expected to have there (a summary word,
+//       or "term by term" where a spacing change or a tie falls inside);
+//       every workgroup fetches the terms of the chunks expected to change
+//       spacing while the others finish;
+//   W1  every workgroup reads the summaries and walks them (exact_walk):
+//       the exact total, hence inv;
+//   C   owners publish the summaries of q_v = p_v * inv in the spacing the
+//       CDF is expected to have; the terms of the chunks around spacing
+//       changes and around r are fetched;
+//   W2  every workgroup walks those: the token.
+// A summary is used only where the exact running sum is in the spacing it
+// was formed for and stays there, so a wrong guess costs time, never bits;
+// every workgroup computes the same token. With G = 1 one workgroup does it
+// all (the batched sampler, the per-phase kernels).
+
+constexpr double SAMP_MARGIN = 1.0 / 16384;  // relative slack of the spacing guesses
+constexpr uint32_t OWN_MAX = 16;             // owned chunks whose p_v stay in LDS
+constexpr uint32_t NEV_MAX = 48;             // term-by-term chunks fetched ahead of a walk
+static_assert(NEV_MAX % NWA == 0, "fetch slots split evenly over the waves");
+constexpr uint16_t NO_SLOT = 0xFFFF;
+
+// The sampler's LDS (from s.scr): stage A's chunk maxima and logits, then
+// the state that lives from stage A2 to the token.
+struct SampLds {
+  float* ownp;    // [OWN_MAX * VCHUNK] this workgroup's p_v
+  float* vmx;     // stage A: [nvc] chunk maxima, [nvc] argmaxes, then the
+  float* varg;    //   logits of the chunks in flight (overlapping A ..)
+  float* chunk;
+  float* A;       // [nvc] chunk sums of p
+  float* pre;     // [nvc] approximate exclusive prefix of the chunk sums
+  uint32_t* sw;   // [nvc] summary words of the walk in hand
+  uint32_t* PI;   // [nvc] inclusive prefix of the usable chunk totals (mod 2^32)
+  uint16_t* nxt;  // [nvc] the first segment start after chunk c
+  uint32_t* nev;  // number of fetched chunks
+  uint32_t* evc;  // [NEV_MAX] the chunk in each fetch slot
+  uint16_t* slot; // [nvc] where chunk c's p_v are in evp (NO_SLOT: not fetched)
+  float* evp;     // [NEV_MAX * VCHUNK] p_v of the fetched chunks
+  double* dred;   // [NWAVES]
+  uint32_t* res;  // [4]
+};
+__host__ __device__ inline uint32_t samp_lds_floats(uint32_t nvc, uint32_t stage_a_chunks) {
+  const uint32_t a = OWN_MAX * VCHUNK + 2 * nvc + stage_a_chunks * VCHUNK;
+  const uint32_t w = OWN_MAX * VCHUNK + 4 * nvc + 1 + NEV_MAX + 2 * ((nvc + 1) / 2) + NEV_MAX * VCHUNK + 1 +
+                     2 * NWAVES + 4;
+  return a > w ? a : w;
+}
+__device__ __forceinline__ SampLds samp_lds(const Lds& s, uint32_t nvc) {
+  SampLds L;
+  float* b = s.scr;
+  L.ownp = b;
+  b += OWN_MAX * VCHUNK;
+  L.vmx = b;
+  L.varg = b + nvc;
+  L.chunk = b + 2 * nvc;
+  L.A = b;
+  b += nvc;
+  L.pre = b;
+  b += nvc;
+  L.sw = reinterpret_cast<uint32_t*>(b);
+  b += nvc;
+  L.PI = reinterpret_cast<uint32_t*>(b);
+  b += nvc;
+  L.nxt = reinterpret_cast<uint16_t*>(b);
+  b += (nvc + 1) / 2;
+  L.nev = reinterpret_cast<uint32_t*>(b);
+  b += 1;
+  L.evc = reinterpret_cast<uint32_t*>(b);
+  b += NEV_MAX;
+  L.slot = reinterpret_cast<uint16_t*>(b);
+  b += (nvc + 1) / 2;
+  L.evp = b;
+  b += NEV_MAX * VCHUNK;
+  b += (uint32_t)((uintptr_t)b & 4u) ? 1 : 0;  // 8-byte alignment (s.scr is 16-byte aligned)
+  L.dred = reinterpret_cast<double*>(b);
+  b += 2 * NWAVES;
+  L.res = reinterpret_cast<uint32_t*>(b);
+  return L;
+}
+
+// Sampler stage A (temperature > 0): the global max m from the chunk maxima
+// (*m and the argmax *bi out; every workgroup forms the same), then, for
+// this workgroup's chunks, every p_v with the reference's exp, kept in LDS
+// where they fit and published, and each chunk's sum of them (any order:
+// only the spacing guesses use it). Everything is published under the tag
+// gsum, unique to one sampling event (a per-cache or per-workspace sequence
+// number handed in by the host), so values an earlier sample left in the
+// mailboxes never carry the tag a later stage waits for.
+// CPW: chunks per polling/computing wave per round; PA: words per lane per
+// poll round.
 template <uint32_t CPW = 1, uint32_t PA = 2>
 __device__ __forceinline__ bool sample_stage_a(const Args& a, uint32_t tick, uint32_t gsum, float T,
-                                               uint32_t wg, uint32_t G, const Lds& s) {
+                                               uint32_t wg, uint32_t G, const Lds& s, float* m_out,
+                                               uint32_t* bi_out) {
   const Dims d = shape_dims(a.d);
   const uint32_t nvc = d.nvc;
   const uint32_t gl = gen_lm(d, tick - 1u);
-  float* vmx = s.scr;
-  float* varg = vmx + nvc;
-  float* chunk = varg + nvc;  // [NWA * CPW][VCHUNK]
-  if (!poll_gather<2, 2>(gather_vec(a.mb_vmax, nvc, gl, vmx), gather_vec(a.mb_varg, nvc, gl, varg),
-                   NWA, a.st, s.ctl))
+  const SampLds L = samp_lds(s, nvc);
+  if (!poll_gather<2, 2>(gather_vec(a.mb_vmax, nvc, gl, L.vmx), gather_vec(a.mb_varg, nvc, gl, L.varg),
+                         NWA, a.st, s.ctl))
     return false;
   float bv;
   uint32_t bi;
-  global_argmax(vmx, varg, nvc, s.red, &bv, &bi);
+  global_argmax(L.vmx, L.varg, nvc, s.red, &bv, &bi);
   const float m = (bi == NO_INDEX) ? -INFINITY : bv / T;
+  *m_out = m;
+  *bi_out = bi;
+  if (!isfinite(m)) return true;  // the reference falls back to argmax
   const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
   const uint32_t nown = wg < nvc ? (nvc - wg + G - 1) / G : 0;
   for (uint32_t k0 = 0; k0 < nown; k0 += NWA * CPW) {
@@ -1564,16 +1657,17 @@ __device__ __forceinline__ bool sample_stage_a(const Args& a, uint32_t tick, uin
     const uint32_t clast = wg + G * (k0 + nb - 1);
     // a short last chunk is gathered separately so no slot past V is read
     const bool short_last = (clast + 1) * VCHUNK > d.V;
-    const Gather ga = gather_strided(src0, VCHUNK, short_last ? nb - 1 : nb, G * VCHUNK, gl, chunk);
+    const Gather ga = gather_strided(src0, VCHUNK, short_last ? nb - 1 : nb, G * VCHUNK, gl, L.chunk);
     const Gather gb = short_last ? gather_vec(a.mb_logit + (size_t)clast * VCHUNK,
-                                              d.V - clast * VCHUNK, gl, chunk + (nb - 1) * VCHUNK)
+                                              d.V - clast * VCHUNK, gl, L.chunk + (nb - 1) * VCHUNK)
                                  : no_gather();
     if (!poll_gather<PA, 1>(ga, gb, NWA, a.st, s.ctl)) return false;
     for (uint32_t b = wave; wave < NWA && b < nb; b += NWA) {
       const uint32_t c = wg + G * (k0 + b);
       const uint32_t v = c * VCHUNK + lane;
-      const float e = (v < d.V) ? prob_term(chunk[b * VCHUNK + lane], T, m) : 0.0f;
+      const float e = (v < d.V) ? prob_term(L.chunk[b * VCHUNK + lane], T, m) : 0.0f;
       if (v < d.V) mb_put(a.mb_p + v, e, gsum);
+      if (nown <= OWN_MAX) L.ownp[(k0 + b) * VCHUNK + lane] = e;
       const float S = wave_sum(e);
       if (lane == 0) mb_put(a.mb_vsum + c, S, gsum);
     }
@@ -1581,21 +1675,6 @@ __device__ __forceinline__ bool sample_stage_a(const Args& a, uint32_t tick, uin
   }
   return true;
 }
-
-// ------------------------------------------------------------ exact sampler
-//
-// sample_token (sampler.rs:78-109) for T > 0, on one workgroup, with the
-// reference's arithmetic: p_v = exp(l_v/T - m) (exact.h's expf), the
-// sequential float total of the p_v, inv = 1/total, q_v = p_v * inv, and the
-// first v with r < (the sequential float sum of q_0..q_v), else the last v
-// with q_v > 0. Both sequential sums are formed as exact.h describes: chunks
-// of 64 terms are summarised in parallel as integer totals in the units of
-// the float spacing their running sum is expected to have, one wave walks
-// the summaries and uses a chunk's total only where the exact running sum
-// is in that spacing and stays in it; any other chunk it sums term by term
-// (chunk_exact). The result does not depend on the guesses.
-
-constexpr double SAMP_MARGIN = 1.0 / 16384;  // relative slack of the region guesses
 
 // This lane's words ptr[k] (k < N) once each carries `tag`; false (uniform
 // over the wave) if the run was aborted meanwhile.
@@ -1634,143 +1713,344 @@ __device__ __forceinline__ bool load_tagged(const u64* const (&ptr)[N], uint32_t
   return true;
 }
 
-// The terms of one chunk (n <= 64 of them, lane j the j-th), added to the
+// The block-wide approximate exclusive prefix of the chunk sums A (double
+// partials, any fixed order), as floats in pre. Thread t owns a contiguous
+// run of chunks.
+__device__ __forceinline__ void approx_prefix(const float* A, float* pre, uint32_t nvc, double* dred) {
+  const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+  const uint32_t cpt = (nvc + BLOCK - 1) / BLOCK;
+  const uint32_t ca = min(threadIdx.x * cpt, nvc), cb = min(ca + cpt, nvc);
+  double own = 0.0;
+  for (uint32_t c = ca; c < cb; ++c) own += (double)A[c];
+  double incl = own;
+#pragma unroll
+  for (uint32_t o = 1; o < WAVE; o <<= 1) {
+    const double y = __shfl_up(incl, o);
+    if (lane >= o) incl += y;
+  }
+  __syncthreads();
+  if (lane == WAVE - 1) dred[wave] = incl;
+  __syncthreads();
+  double p = incl - own;
+  for (uint32_t w = 0; w < wave; ++w) p += dred[w];
+  for (uint32_t c = ca; c < cb; ++c) {
+    pre[c] = (float)p;
+    p += (double)A[c];
+  }
+  __syncthreads();
+}
+
+// The spacing guess of chunk c for the terms x = p * scale: the grid its
+// running sum is expected to start in, and whether a spacing change is
+// expected inside it (then it goes term by term).
+__device__ __forceinline__ int chunk_guess(const SampLds& L, uint32_t c, float scale, bool* change) {
+  const double lo = (double)L.pre[c] * scale * (1.0 - SAMP_MARGIN);
+  const double hi = ((double)L.pre[c] + (double)L.A[c]) * scale * (1.0 + SAMP_MARGIN);
+  const int E = grid_of((float)lo);
+  *change = E != grid_of((float)hi);
+  return E;
+}
+
+// Owned chunks' summary words of x = p (FIND false) or p * inv, published
+// to `dst` under gsum: one wave per chunk, a lane per term. own_in_lds: this
+// kernel ran stage A with the same (wg, G), so the owned p_v are in LDS
+// where they fit; else they are read back from the mailbox. Chunks starting
+// past r (FIND) are not needed by a walk that finds r and are published as
+// term-by-term without being formed.
+template <bool FIND>
+__device__ __forceinline__ bool publish_summaries(const Args& a, u64* dst, uint32_t gsum, float inv, float r,
+                                                  uint32_t wg, uint32_t G, bool own_in_lds, const SampLds& L,
+                                                  const Lds& s) {
+  const Dims d = shape_dims(a.d);
+  const uint32_t nvc = d.nvc, V = d.V;
+  const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+  const uint32_t nown = wg < nvc ? (nvc - wg + G - 1) / G : 0;
+  // The 135M kernel runs only at its full grid, where the owned p_v fit.
+  const bool lds_p = STAGED_ONLY || (own_in_lds && nown <= OWN_MAX);
+  constexpr uint32_t B = 4;  // chunks per wave in flight
+  bool ok = true;
+  for (uint32_t k0 = wave * B; wave < NWA && k0 < nown; k0 += NWA * B) {
+    float p[B];
+    if (lds_p) {
+#pragma unroll
+      for (uint32_t e = 0; e < B; ++e) p[e] = L.ownp[min(k0 + e, nown - 1) * VCHUNK + lane];
+    } else {
+      const u64* ptr[B];
+#pragma unroll
+      for (uint32_t e = 0; e < B; ++e) ptr[e] = a.mb_p + min((wg + G * min(k0 + e, nown - 1)) * VCHUNK + lane, V - 1);
+      if (!load_tagged<B>(ptr, gsum, p, a.st, s.ctl)) {
+        ok = false;
+        break;
+      }
+    }
+#pragma unroll
+    for (uint32_t e = 0; e < B; ++e) {
+      const uint32_t k = k0 + e;
+      if (k >= nown) break;
+      const uint32_t c = wg + G * k;
+      bool change;
+      const int E = chunk_guess(L, c, FIND ? inv : 1.0f, &change);
+      const bool past = FIND && (double)L.pre[c] * inv * (1.0 - SAMP_MARGIN) > (double)r;
+      uint32_t w = sum_word(E, SUM_EVENT);
+      if (!change && !past) {
+        const uint32_t v = c * VCHUNK + lane;
+        const float x = v < V ? (FIND ? p[e] * inv : p[e]) : 0.0f;
+        const GridTerm g = grid_term(x, E);
+        const uint32_t tot = lane_u32(wave_scan_u32(g.big ? 0u : g.rho), 63);
+        const bool flag = __ballot(g.big || g.tie) != 0;
+        w = sum_word(E, flag ? SUM_EVENT : tot);
+      }
+      if (lane == 0) mb_put(dst + c, __uint_as_float(w), gsum);
+    }
+  }
+  if (!ok && lane == 0) s.ctl->abort_seen = 1;
+  __syncthreads();
+  return s.ctl->abort_seen == 0;
+}
+
+// The p_v of the chunks a walk is expected to sum term by term, fetched
+// into LDS (at most NEV_MAX chunks; a walk reads any other from the
+// mailbox). Round 0 (while the other workgroups finish their summaries):
+// the chunks with a spacing change expected inside, and their neighbours,
+// where a guess off by a little puts the change; FIND also the chunks
+// around r. Round 1 (once the summary words are in L.sw): every chunk whose
+// word says term by term and that round 0 did not fetch. The slot map
+// L.slot says where each fetched chunk went.
+template <bool FIND>
+__device__ __forceinline__ bool fetch_events(const Args& a, uint32_t gsum, float inv, float r, uint32_t round,
+                                             const SampLds& L, const Lds& s) {
+  const Dims d = shape_dims(a.d);
+  const uint32_t nvc = d.nvc, V = d.V;
+  const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+  const uint32_t cpt = (nvc + BLOCK - 1) / BLOCK;
+  const uint32_t ca = min(threadIdx.x * cpt, nvc), cb = min(ca + cpt, nvc);
+  auto past = [&](uint32_t c) {
+    return FIND && (double)L.pre[c] * inv * (1.0 - SAMP_MARGIN) > (double)r;
+  };
+  auto change = [&](uint32_t c) {
+    bool ch;
+    (void)chunk_guess(L, c, FIND ? inv : 1.0f, &ch);
+    if (FIND) {
+      const double lo = (double)L.pre[c] * inv, hi = ((double)L.pre[c] + (double)L.A[c]) * inv;
+      ch = ch || (lo * (1.0 - SAMP_MARGIN) <= (double)r && hi * (1.0 + SAMP_MARGIN) >= (double)r);
+    }
+    return ch;
+  };
+  auto wanted = [&](uint32_t c) {
+    if (past(c)) return false;
+    if (round == 0) return change(c) || (c > 0 && change(c - 1)) || (c + 1 < nvc && change(c + 1));
+    return L.slot[c] == NO_SLOT && sum_total(L.sw[c]) == SUM_EVENT;
+  };
+  if (round == 0) {
+    for (uint32_t c = threadIdx.x; c < nvc; c += BLOCK) L.slot[c] = NO_SLOT;
+    __syncthreads();
+  }
+  const uint32_t base_n = round == 0 ? 0u : *L.nev;
+  uint32_t cnt = 0;
+  for (uint32_t c = ca; c < cb; ++c) cnt += wanted(c) ? 1u : 0u;
+  const uint32_t incl = wave_scan_u32(cnt);
+  uint32_t* wtot = reinterpret_cast<uint32_t*>(L.dred);
+  __syncthreads();
+  if (lane == WAVE - 1) wtot[wave] = incl;
+  __syncthreads();
+  uint32_t pos = base_n + incl - cnt, total = 0;
+  for (uint32_t w = 0; w < NWAVES; ++w) {
+    if (w < wave) pos += wtot[w];
+    total += wtot[w];
+  }
+  for (uint32_t c = ca; c < cb; ++c)
+    if (wanted(c)) {
+      if (pos < NEV_MAX) {
+        L.slot[c] = (uint16_t)pos;
+        L.evc[pos] = c;
+      }
+      ++pos;
+    }
+  const uint32_t n_after = min(base_n + total, NEV_MAX);
+  __syncthreads();
+  if (threadIdx.x == 0) *L.nev = n_after;
+  // The fetch: slots base_n .. n_after-1, a lane per term, FB slots per wave
+  // in flight (NWA * FB = NEV_MAX: one round).
+  constexpr uint32_t FB = NEV_MAX / NWA;
+  bool ok = true;
+  const uint32_t s0 = base_n + wave * FB;
+  if (wave < NWA && s0 < n_after) {
+    const u64* ptr[FB];
+    float t[FB];
+#pragma unroll
+    for (uint32_t e = 0; e < FB; ++e)
+      ptr[e] = a.mb_p + min(L.evc[min(s0 + e, n_after - 1)] * VCHUNK + lane, V - 1);
+    ok = load_tagged<FB>(ptr, gsum, t, a.st, s.ctl);
+#pragma unroll
+    for (uint32_t e = 0; e < FB; ++e)
+      if (ok && s0 + e < n_after) L.evp[(s0 + e) * VCHUNK + lane] = t[e];
+  }
+  if (!ok && lane == 0) s.ctl->abort_seen = 1;
+  __syncthreads();
+  return s.ctl->abort_seen == 0;
+}
+
+// The terms of one chunk (n <= 64 of them, lane j the j-th, x), added to the
 // exact running sum s one rounded step at a time, in parallel: with s in
 // grid E, the steps before the first term that leaves the region (or is a
 // tie) are an integer prefix sum; that term is one float addition; repeat.
 // FIND: stops at the first term j with r < the sum after it (hit = j; 64 if
-// none). Wave-uniform; returns false on abort.
+// none). Wave-uniform.
 template <bool FIND>
-__device__ __forceinline__ bool chunk_exact(const u64* pw, uint32_t n, uint32_t tag, float inv, float r,
-                                            float& s, uint32_t& hit, DevState* st, WaitCtl* ctl) {
+__device__ __forceinline__ void chunk_exact(float x, uint32_t n, float r, float& s, uint32_t& hit) {
   const uint32_t lane = threadIdx.x % WAVE;
-  const u64* ptr[1] = {pw + min(lane, n - 1)};
-  float v[1];
   hit = 64;
-  if (!load_tagged<1>(ptr, tag, v, st, ctl)) return false;
-  const float x = lane < n ? (FIND ? v[0] * inv : v[0]) : 0.0f;
   uint32_t jstart = 0;
+  int E = grid_of(s);
+  GridTerm g = grid_term(x, E);
+  // Where several terms leave the running sum's region at once (the first
+  // chunk, whose sum starts at 0), one float addition per term is cheaper
+  // than a restart per term.
+  if (__popcll(__ballot(lane < n && (g.big || g.tie))) >= 4) {
+    for (uint32_t j = 0; j < n; ++j) {
+      s = s + lane_f32(x, j);
+      if (FIND && r < s) {
+        hit = j;
+        return;
+      }
+    }
+    return;
+  }
+  // Each round forms the terms in grid E and in the next grid E + 1 (where
+  // the sum goes when it leaves E upwards), so a chunk whose sum changes
+  // spacing once is done in one round.
   for (;;) {
-    const int E = grid_of(s);
     const uint32_t k = grid_units(s, E);
     const bool act = lane >= jstart && lane < n;
-    const GridTerm g = grid_term(x, E);
+    const GridTerm h = grid_term(x, E + 1);
     const uint32_t rho = (act && !g.big) ? g.rho : 0u, aa = (act && !g.big) ? g.a : 0u;
-    const uint32_t P = wave_scan_u32(rho), Pex = P - rho;
+    const uint32_t rho1 = (act && !h.big) ? h.rho : 0u;
+    const uint32_t P = wave_scan_u32(rho), P1 = wave_scan_u32(rho1);
+    const uint32_t Pex = P - rho;
     const bool bad = act && (g.big || g.tie || k + Pex + aa >= GRID_TOP);
     const uint32_t jb = first_lane(__ballot(bad));
     if (FIND) {
-      const bool h = act && lane < jb && r < __builtin_ldexpf((float)(k + P), E);
-      const uint32_t jh = first_lane(__ballot(h));
+      const bool hh = act && lane < jb && r < __builtin_ldexpf((float)(k + P), E);
+      const uint32_t jh = first_lane(__ballot(hh));
       if (jh < 64) {
         hit = jh;
         s = __builtin_ldexpf((float)(k + lane_u32(P, jh)), E);
-        return true;
+        return;
       }
     }
     if (jb >= 64) {
       s = __builtin_ldexpf((float)(k + lane_u32(P, 63)), E);
-      return true;
+      return;
     }
     s = __builtin_ldexpf((float)(k + lane_u32(Pex, jb)), E);
     s = s + lane_f32(x, jb);
     if (FIND && r < s) {
       hit = jb;
-      return true;
+      return;
     }
     jstart = jb + 1;
-    if (jstart >= n) return true;
+    if (jstart >= n) return;
+    const int E2 = grid_of(s);
+    if (E2 == E + 1) {
+      // the terms after jb in grid E + 1, from the same round
+      const uint32_t k2 = grid_units(s, E2), base = lane_u32(P1, jb);
+      const bool act2 = lane >= jstart && lane < n;
+      const uint32_t Q = P1 - base, Qex = Q - rho1;
+      const bool bad2 = act2 && (h.big || h.tie || k2 + Qex + (h.big ? 0u : h.a) >= GRID_TOP);
+      const uint32_t jb2 = first_lane(__ballot(bad2));
+      if (FIND) {
+        const bool hh = act2 && lane < jb2 && r < __builtin_ldexpf((float)(k2 + Q), E2);
+        const uint32_t jh = first_lane(__ballot(hh));
+        if (jh < 64) {
+          hit = jh;
+          s = __builtin_ldexpf((float)(k2 + lane_u32(Q, jh)), E2);
+          return;
+        }
+      }
+      if (jb2 >= 64) {
+        s = __builtin_ldexpf((float)(k2 + lane_u32(Q, 63)), E2);
+        return;
+      }
+      s = __builtin_ldexpf((float)(k2 + lane_u32(Qex, jb2)), E2);
+      s = s + lane_f32(x, jb2);
+      if (FIND && r < s) {
+        hit = jb2;
+        return;
+      }
+      jstart = jb2 + 1;
+      if (jstart >= n) return;
+    }
+    E = grid_of(s);
+    g = grid_term(x, E);
   }
 }
 
-// One sequential sum over the V terms x_v = p_v (FIND false) or p_v * inv
-// (FIND true), on one workgroup. A: the chunk sums of p from stage A (LDS);
-// sw: nvc summary words (LDS); dred: NWAVES doubles of LDS; res: two words.
-// Returns the total (FIND false) or the index sample_token returns (FIND
-// true) in *out (float bits / index). false on abort.
+// Segments of the summary words in L.sw: a segment is a maximal run of
+// usable chunks (an integer total) in one grid, and each term-by-term chunk
+// is one of its own. L.PI gets the inclusive prefix of the usable totals, so
+// a segment's total is a difference of two entries; L.nxt[c] the first
+// segment start after c (nvc past the last). A walk at a segment's start
+// whose running sum is in the segment's grid and stays there takes the whole
+// segment as one integer step.
+__device__ __forceinline__ void build_segments(const SampLds& L, uint32_t nvc) {
+  const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+  const uint32_t cpt = (nvc + BLOCK - 1) / BLOCK;
+  const uint32_t ca = min(threadIdx.x * cpt, nvc), cb = min(ca + cpt, nvc);
+  auto ev = [&](uint32_t c) { return sum_total(L.sw[c]) == SUM_EVENT; };
+  auto start = [&](uint32_t c) {
+    return c == 0 || ev(c) || ev(c - 1) || sum_grid(L.sw[c]) != sum_grid(L.sw[c - 1]);
+  };
+  uint32_t own = 0, first = nvc;
+  for (uint32_t c = ca; c < cb; ++c) {
+    own += ev(c) ? 0u : sum_total(L.sw[c]);
+    if (first == nvc && start(c)) first = c;
+  }
+  // exclusive prefix of the totals over threads; suffix minimum of the
+  // first starts over the following threads
+  const uint32_t incl = wave_scan_u32(own);
+  uint32_t later;  // first start in the following lanes and waves
+  {
+    uint32_t m = first;  // suffix minimum including this lane
+#pragma unroll
+    for (uint32_t o = 1; o < WAVE; o <<= 1) {
+      const uint32_t y = __shfl_down(m, o);
+      if (lane + o < WAVE) m = min(m, y);
+    }
+    later = __shfl_down(m, 1);
+    if (lane == WAVE - 1) later = nvc;
+    uint32_t* wsum = reinterpret_cast<uint32_t*>(L.dred);  // [NWAVES] totals, [NWAVES] minima
+    __syncthreads();
+    if (lane == WAVE - 1) wsum[wave] = incl;
+    if (lane == 0) wsum[NWAVES + wave] = m;
+    __syncthreads();
+    uint32_t base = incl - own;
+    for (uint32_t w = 0; w < wave; ++w) base += wsum[w];
+    for (uint32_t w = wave + 1; w < NWAVES; ++w) later = min(later, wsum[NWAVES + w]);
+    uint32_t run = base;
+    for (uint32_t c = ca; c < cb; ++c) {
+      run += ev(c) ? 0u : sum_total(L.sw[c]);
+      L.PI[c] = run;
+    }
+    uint32_t nx = later;
+    for (uint32_t c = cb; c-- > ca;) {
+      L.nxt[c] = (uint16_t)nx;
+      if (start(c)) nx = c;
+    }
+  }
+  __syncthreads();
+}
+
+// One walk over the summary words L.sw (wave 0; the block waits): the total
+// of the terms (FIND false: *out = its bits) or the index sample_token
+// returns (FIND true). Windows of 64 summaries: the usable prefix of a window
+// is one integer sum, its first unusable chunk goes term by term from LDS
+// (fetched) or the mailbox.
 template <bool FIND>
-__device__ __forceinline__ bool exact_walk(const Args& a, uint32_t tag, float inv, float r, const float* A, uint32_t* sw,
-                           double* dred, uint32_t* res, const Lds& s, uint32_t* out) {
+__device__ __forceinline__ bool exact_walk(const Args& a, uint32_t gsum, float inv, float r, const SampLds& L,
+                                           const Lds& s, uint32_t* out) {
   const Dims d = shape_dims(a.d);
   const uint32_t nvc = d.nvc, V = d.V;
   const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
-  // 1. Guess each chunk's grid from an approximate prefix of the chunk sums;
-  // a chunk whose approximate range meets a region boundary (or, FIND,
-  // lies past r) is summed term by term if the walk reaches it.
-  {
-    const uint32_t cpt = (nvc + BLOCK - 1) / BLOCK;
-    const uint32_t ca = min(threadIdx.x * cpt, nvc), cb = min(ca + cpt, nvc);
-    double own = 0.0;
-    for (uint32_t c = ca; c < cb; ++c) own += (double)lds_ld(A + c);
-    double incl = own;
-#pragma unroll
-    for (uint32_t o = 1; o < WAVE; o <<= 1) {
-      const double y = __shfl_up(incl, o);
-      if (lane >= o) incl += y;
-    }
-    if (lane == WAVE - 1) dred[wave] = incl;
-    __syncthreads();
-    double pre = incl - own;
-    for (uint32_t w = 0; w < wave; ++w) pre += dred[w];
-    const double scale = FIND ? (double)inv : 1.0;
-    for (uint32_t c = ca; c < cb; ++c) {
-      const double ac = (double)lds_ld(A + c);
-      const double lo = pre * scale * (1.0 - SAMP_MARGIN), hi = (pre + ac) * scale * (1.0 + SAMP_MARGIN);
-      const int El = grid_of((float)lo);
-      bool ev = El != grid_of((float)hi);
-      if (FIND && lo > (double)r) ev = true;
-      sw[c] = sum_word(El, ev ? SUM_EVENT : 0u);
-      pre += ac;
-    }
-    __syncthreads();
-  }
-  // 2. Integer totals of the other chunks in their guessed grid: eight lanes
-  // per chunk, eight terms per lane, on the polling and computing waves (the
-  // loader waves of the persistent kernel issue only their staging loads).
-  // A tie or a term past the region makes the chunk a term-by-term one.
-  {
-    const uint32_t grp = lane / 8, sub = lane % 8;
-    bool ok = true;
-    for (uint32_t c0 = wave * 8; wave < NWA && c0 < nvc; c0 += NWA * 8) {
-      const uint32_t c = min(c0 + grp, nvc - 1);
-      const uint32_t w0 = sw[c];
-      const bool ev = c0 + grp >= nvc || sum_total(w0) == SUM_EVENT;
-      if (__all(ev)) continue;
-      const uint32_t j0 = c * VCHUNK + sub * 8;
-      const u64* ptr[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ptr[e] = a.mb_p + min(j0 + e, V - 1);
-      float x[8];
-      if (!load_tagged<8>(ptr, tag, x, a.st, s.ctl)) {
-        ok = false;
-        break;
-      }
-      const int E = sum_grid(w0);
-      uint32_t tot = 0;
-      bool flag = false;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float xv = (j0 + e < V) ? (FIND ? x[e] * inv : x[e]) : 0.0f;
-        const GridTerm g = grid_term(xv, E);
-        flag = flag || g.big || g.tie;
-        tot += g.big ? 0u : g.rho;
-      }
-      tot += __shfl_xor(tot, 1);
-      tot += __shfl_xor(tot, 2);
-      tot += __shfl_xor(tot, 4);
-      uint32_t fl = flag ? 1u : 0u;
-      fl |= __shfl_xor(fl, 1);
-      fl |= __shfl_xor(fl, 2);
-      fl |= __shfl_xor(fl, 4);
-      if (!ev && sub == 0) sw[c] = sum_word(E, fl ? SUM_EVENT : tot);
-    }
-    if (!ok && lane == 0) s.ctl->abort_seen = 1;
-    __syncthreads();
-    if (s.ctl->abort_seen) return false;
-  }
-  // 3. The walk, on wave 0: windows of 64 chunk summaries; the usable prefix
-  // of a window is one integer sum, the first unusable chunk goes term by
-  // term.
   if (wave == 0) {
     float sum = 0.0f;
     uint32_t found = NO_INDEX;
@@ -1779,25 +2059,54 @@ __device__ __forceinline__ bool exact_walk(const Args& a, uint32_t tag, float in
     while (c0 < nvc) {
       const int E = grid_of(sum);
       const uint32_t k = grid_units(sum, E);
-      const uint32_t c = c0 + lane;
-      const uint32_t w = c < nvc ? sw[c] : SUM_EVENT;
-      const uint32_t I = sum_total(w);
-      bool use = c < nvc && I != SUM_EVENT && sum_grid(w) == E;
-      const uint32_t P = wave_scan_u32(use ? I : 0u);
-      use = use && k + P < GRID_TOP;
-      bool stop = !use;
-      if (FIND) stop = stop || r < __builtin_ldexpf((float)(k + P), E);
-      const uint32_t fb = first_lane(__ballot(stop));
-      const uint32_t pre = fb ? lane_u32(P, fb - 1) : 0u;
-      sum = __builtin_ldexpf((float)(k + pre), E);
-      c0 += fb;
-      if (fb < 64 && c0 < nvc) {
-        const uint32_t base = c0 * VCHUNK;
-        uint32_t hit;
-        if (!chunk_exact<FIND>(a.mb_p + base, min(VCHUNK, V - base), tag, inv, r, sum, hit, a.st, s.ctl)) {
-          ok = false;
-          break;
+      bool exact_here = false;  // c0 goes term by term without a window scan
+      {
+        // the rest of c0's segment as one integer step, where it applies
+        const uint32_t w0 = L.sw[c0];
+        exact_here = sum_total(w0) == SUM_EVENT;
+        if (!exact_here && sum_grid(w0) == E) {
+          const uint32_t e = L.nxt[c0];
+          const uint32_t T = L.PI[e - 1] - (c0 ? L.PI[c0 - 1] : 0u);
+          if (T < GRID_TOP && k + T < GRID_TOP && !(FIND && r < __builtin_ldexpf((float)(k + T), E))) {
+            sum = __builtin_ldexpf((float)(k + T), E);
+            c0 = e;
+            continue;
+          }
         }
+      }
+      uint32_t fb = 0;
+      if (!exact_here) {
+        const uint32_t c = c0 + lane;
+        const uint32_t w = c < nvc ? L.sw[c] : SUM_EVENT;
+        const uint32_t I = sum_total(w);
+        bool use = c < nvc && I != SUM_EVENT && sum_grid(w) == E;
+        const uint32_t P = wave_scan_u32(use ? I : 0u);
+        use = use && k + P < GRID_TOP;
+        bool stop = !use;
+        if (FIND) stop = stop || r < __builtin_ldexpf((float)(k + P), E);
+        fb = first_lane(__ballot(stop));
+        const uint32_t pre = fb ? lane_u32(P, fb - 1) : 0u;
+        sum = __builtin_ldexpf((float)(k + pre), E);
+        c0 += fb;
+      }
+      if (fb < 64 && c0 < nvc) {
+        const uint32_t base = c0 * VCHUNK, n = min(VCHUNK, V - base);
+        const uint32_t sl = L.slot[c0];
+        float p;
+        if (sl != NO_SLOT) {
+          p = L.evp[sl * VCHUNK + lane];
+        } else {
+          const u64* ptr[1] = {a.mb_p + base + min(lane, n - 1)};
+          float t[1];
+          if (!load_tagged<1>(ptr, gsum, t, a.st, s.ctl)) {
+            ok = false;
+            break;
+          }
+          p = t[0];
+        }
+        const float x = lane < n ? (FIND ? p * inv : p) : 0.0f;
+        uint32_t hit;
+        chunk_exact<FIND>(x, n, r, sum, hit);
         if (FIND && hit < 64) {
           found = base + hit;
           break;
@@ -1810,67 +2119,71 @@ __device__ __forceinline__ bool exact_walk(const Args& a, uint32_t tag, float in
     for (uint32_t cc = nvc; FIND && ok && found == NO_INDEX && cc-- > 0;) {
       const uint32_t base = cc * VCHUNK, n = min(VCHUNK, V - base);
       const u64* ptr[1] = {a.mb_p + base + min(lane, n - 1)};
-      float v[1];
-      if (!load_tagged<1>(ptr, tag, v, a.st, s.ctl)) {
+      float t[1];
+      if (!load_tagged<1>(ptr, gsum, t, a.st, s.ctl)) {
         ok = false;
         break;
       }
-      const unsigned long long nz = __ballot(lane < n && v[0] * inv > 0.0f);
+      const unsigned long long nz = __ballot(lane < n && t[0] * inv > 0.0f);
       if (nz) found = base + 63u - (uint32_t)__clzll((long long)nz);
     }
     if (FIND && ok && found == NO_INDEX) found = 0;
     if (lane == 0) {
-      res[0] = FIND ? found : __float_as_uint(sum);
-      res[1] = ok ? 1u : 0u;
+      L.res[0] = FIND ? found : __float_as_uint(sum);
+      L.res[1] = ok ? 1u : 0u;
     }
   }
   __syncthreads();
-  const bool ok = res[1] != 0;
-  *out = res[0];
+  const bool ok = L.res[1] != 0;
+  *out = L.res[0];
   __syncthreads();
   return ok;
 }
 
-// sample_token for T > 0 on one workgroup (stage A has run on every
-// workgroup): the chunk maxima give m; where m is not finite the reference's
-// total is NaN or 0 and it falls back to argmax (sampler.rs:60-69); else
-// the exact total, then the exact CDF scan.
-__device__ __forceinline__ bool sample_exact(const Args& a, uint32_t tick, uint32_t gsum, float T, uint32_t word, const Lds& s,
-                             uint32_t* tok_out) {
-  const Dims d = shape_dims(a.d);
-  const uint32_t nvc = d.nvc;
-  const uint32_t gl = gen_lm(d, tick - 1u);
-  float* vmx = s.scr;
-  float* varg = vmx + nvc;
-  float* A = varg + nvc;
-  uint32_t* sw = reinterpret_cast<uint32_t*>(vmx);  // reused once the argmax is formed
-  double* dred = reinterpret_cast<double*>(s.scr + ((3 * nvc + 1) & ~1u));
-  uint32_t* res = reinterpret_cast<uint32_t*>(dred + NWAVES);
-  if (!poll_gather<2, 2, 2>(gather_vec(a.mb_vmax, nvc, gl, vmx), gather_vec(a.mb_varg, nvc, gl, varg),
-                            gather_vec(a.mb_vsum, nvc, gsum, A), NWA, a.st, s.ctl))
-    return false;
-  float bv;
-  uint32_t bi;
-  global_argmax(vmx, varg, nvc, s.red, &bv, &bi);
-  const float m = (bi == NO_INDEX) ? -INFINITY : bv / T;
+// Stages A2 to W2 (stage A has run on every participating workgroup; m and
+// the argmax bi are its results): the token sample_token returns (and, if
+// total_bits is given, the bits of the sequential total). Where m is not
+// finite the reference's total is NaN or 0 and it falls back to argmax
+// (sampler.rs:60-69).
+__device__ __forceinline__ bool sample_exact(const Args& a, uint32_t gsum, float m, uint32_t bi, uint32_t word,
+                                             uint32_t wg, uint32_t G, bool own_in_lds, const Lds& s,
+                                             uint32_t* tok_out, uint32_t* total_bits = nullptr) {
   if (!isfinite(m)) {
     *tok_out = (bi == NO_INDEX) ? 0u : bi;
     return true;
   }
-  uint32_t sum_bits, tok;
-  if (!exact_walk<false>(a, gsum, 1.0f, 0.0f, A, sw, dred, res, s, &sum_bits)) return false;
+  const Dims d = shape_dims(a.d);
+  const uint32_t nvc = d.nvc;
+  const SampLds L = samp_lds(s, nvc);
+  // A2
+  if (!poll_gather<2>(gather_vec(a.mb_vsum, nvc, gsum, L.A), NWA, a.st, s.ctl)) return false;
+  approx_prefix(L.A, L.pre, nvc, L.dred);
+  if (!publish_summaries<false>(a, a.mb_psum, gsum, 1.0f, 0.0f, wg, G, own_in_lds, L, s)) return false;
+  if (!fetch_events<false>(a, gsum, 1.0f, 0.0f, 0, L, s)) return false;
+  // W1
+  if (!poll_gather<2>(gather_vec(a.mb_psum, nvc, gsum, reinterpret_cast<float*>(L.sw)), NWA, a.st, s.ctl))
+    return false;
+  if (!fetch_events<false>(a, gsum, 1.0f, 0.0f, 1, L, s)) return false;
+  build_segments(L, nvc);
+  uint32_t sum_bits;
+  if (!exact_walk<false>(a, gsum, 1.0f, 0.0f, L, s, &sum_bits)) return false;
+  if (total_bits) *total_bits = sum_bits;
   const float inv = 1.0f / __uint_as_float(sum_bits);
-  if (!exact_walk<true>(a, gsum, inv, unit_f32(word), A, sw, dred, res, s, &tok)) return false;
-  *tok_out = tok;
-  return true;
+  const float r = unit_f32(word);
+  // C
+  if (!publish_summaries<true>(a, a.mb_qsum, gsum, inv, r, wg, G, own_in_lds, L, s)) return false;
+  if (!fetch_events<true>(a, gsum, inv, r, 0, L, s)) return false;
+  // W2
+  if (!poll_gather<2>(gather_vec(a.mb_qsum, nvc, gsum, reinterpret_cast<float*>(L.sw)), NWA, a.st, s.ctl))
+    return false;
+  if (!fetch_events<true>(a, gsum, inv, r, 1, L, s)) return false;
+  build_segments(L, nvc);
+  return exact_walk<true>(a, gsum, inv, r, L, s, tok_out);
 }
 
-// Sampler stage B: the token (sampler.rs:78-109). Greedy is the global argmax
-// of the chunk maxima (0 when every logit is NaN), on every workgroup that
-// calls it; T > 0 is sample_exact, on one workgroup.
-__device__ __forceinline__ bool sample_stage_b(const Args& a, uint32_t tick, uint32_t gsum, float T,
-                                               uint32_t word, const Lds& s, uint32_t* tok_out) {
-  if (T != 0.0f) return sample_exact(a, tick, gsum, T, word, s, tok_out);
+// The greedy token: the global argmax of the chunk maxima (0 when every
+// logit is NaN), on every workgroup that calls it.
+__device__ __forceinline__ bool sample_greedy(const Args& a, uint32_t tick, const Lds& s, uint32_t* tok_out) {
   const Dims d = shape_dims(a.d);
   const uint32_t nvc = d.nvc;
   const uint32_t gl = gen_lm(d, tick - 1u);
@@ -1884,6 +2197,26 @@ __device__ __forceinline__ bool sample_stage_b(const Args& a, uint32_t tick, uin
   global_argmax(vmx, varg, nvc, s.red, &bv, &bi);
   *tok_out = (bi == NO_INDEX) ? 0u : bi;
   return true;
+}
+
+// The whole sampler on one workgroup after stage A ran on G workgroups (the
+// per-phase kernels): m from the chunk maxima, then stages A2 to W2 with this
+// workgroup owning every chunk.
+__device__ __forceinline__ bool sample_one_wg(const Args& a, uint32_t tick, uint32_t gsum, float T, uint32_t word,
+                                              const Lds& s, uint32_t* tok_out) {
+  if (T == 0.0f) return sample_greedy(a, tick, s, tok_out);
+  const Dims d = shape_dims(a.d);
+  const uint32_t nvc = d.nvc;
+  const uint32_t gl = gen_lm(d, tick - 1u);
+  const SampLds L = samp_lds(s, nvc);
+  if (!poll_gather<2, 2>(gather_vec(a.mb_vmax, nvc, gl, L.vmx), gather_vec(a.mb_varg, nvc, gl, L.varg), NWA,
+                         a.st, s.ctl))
+    return false;
+  float bv;
+  uint32_t bi;
+  global_argmax(L.vmx, L.varg, nvc, s.red, &bv, &bi);
+  const float m = (bi == NO_INDEX) ? -INFINITY : bv / T;
+  return sample_exact(a, gsum, m, bi, word, 0, 1, false, s, tok_out);
 }
 
 }  // namespace DG_NS

@@ -6,8 +6,9 @@
 //                      every stride-th float bit pattern from first on;
 //   probe_expf_device  the device expf_ref on an array;
 //   probe_scan_device  wave_scan_u32 on 64-lane groups of an array;
-//   probe_walk         the exact walker on an arbitrary term sequence p:
-//                      the sequential float total of p, and the index
+//   probe_walk         the exact sampler's stages A2 to W2 (sample_exact,
+//                      one workgroup) on an arbitrary term sequence p: the
+//                      sequential float total of p, and the index
 //                      sample_token's scan returns over q = p * (1/total)
 //                      for the draw r = (word >> 8) * 2^-24.
 #include <hip/hip_runtime.h>
@@ -79,12 +80,12 @@ extern "C" int probe_scan_device(const uint32_t* x, uint32_t* y, uint32_t n) {
   return rc;
 }
 
-// One workgroup: the chunk sums from the mailbox, then both walks.
+// One workgroup: the sampler's stages A2 to W2 (sample_exact) on terms p
+// already published with their chunk sums, as the batched sampler runs them.
 __global__ __launch_bounds__(BLOCK) void k_walk(const Args* __restrict__ ap, uint32_t tag, uint32_t word,
                                                 uint32_t* out) {
   extern __shared__ float lds_raw[];
   const Args& a = *ap;
-  const uint32_t nvc = a.d.nvc;
   Lds s;
   memset(&s, 0, sizeof(s));
   s.ctl = reinterpret_cast<WaitCtl*>(lds_raw);
@@ -92,46 +93,34 @@ __global__ __launch_bounds__(BLOCK) void k_walk(const Args* __restrict__ ap, uin
   s.scr = lds_raw + 4 + 64;
   if (threadIdx.x == 0) s.ctl->abort_seen = 0;
   __syncthreads();
-  float* A = s.scr;
-  uint32_t* sw = reinterpret_cast<uint32_t*>(A + nvc);
-  double* dred = reinterpret_cast<double*>(s.scr + ((2 * nvc + 1) & ~1u));
-  uint32_t* res = reinterpret_cast<uint32_t*>(dred + NWAVES);
-  if (!poll_gather<2>(gather_vec(a.mb_vsum, nvc, tag, A), NWA, a.st, s.ctl)) return;
   uint32_t sum_bits = 0, tok = 0;
-  if (!exact_walk<false>(a, tag, 1.0f, 0.0f, A, sw, dred, res, s, &sum_bits)) return;
-  const float inv = 1.0f / __uint_as_float(sum_bits);
-  if (!exact_walk<true>(a, tag, inv, unit_f32(word), A, sw, dred, res, s, &tok)) return;
+  if (!sample_exact(a, tag, 0.0f, 0u, word, 0, 1, false, s, &tok, &sum_bits)) return;
   if (threadIdx.x == 0) {
     out[0] = sum_bits;
     out[1] = tok;
   }
 }
 
-// p: n terms >= 0 (finite); words: n_words draws. For each draw: out[2i] the
-// total's bits, out[2i + 1] the index.
+// p: n terms >= 0 (finite); words: n_words draws, each its own sampling
+// event (its own tag). For each draw: out[2i] the total's bits, out[2i + 1]
+// the index.
 extern "C" int probe_walk(const float* p, uint32_t n, const uint32_t* words, uint32_t n_words, uint32_t* out) {
   const uint32_t nvc = (n + VCHUNK - 1) / VCHUNK;
-  const uint32_t tag = 7;
   std::vector<u64> hp(n), hs(nvc);
+  std::vector<uint32_t> sums(nvc), bits(n);
   for (uint32_t c = 0; c < nvc; ++c) {
-    float sum = 0.0f;  // any order: only the region guesses use it
+    float sum = 0.0f;  // any order: only the spacing guesses use it
     for (uint32_t j = c * VCHUNK; j < n && j < (c + 1) * VCHUNK; ++j) sum += p[j];
-    uint32_t b;
-    memcpy(&b, &sum, 4);
-    hs[c] = ((u64)tag << 32) | b;
+    memcpy(&sums[c], &sum, 4);
   }
-  for (uint32_t j = 0; j < n; ++j) {
-    uint32_t b;
-    memcpy(&b, p + j, 4);
-    hp[j] = ((u64)tag << 32) | b;
-  }
-  u64 *dp = nullptr, *ds = nullptr;
+  memcpy(bits.data(), p, (size_t)n * 4);
+  u64 *dp = nullptr, *ds = nullptr;  // p words; chunk sums, then the two summary arrays
   DevState* st = nullptr;
   Args* da = nullptr;
   uint32_t* dout = nullptr;
   int rc = 1;
-  if (hipMalloc(&dp, n * 8) || hipMalloc(&ds, nvc * 8) || hipMalloc(&st, sizeof(DevState)) ||
-      hipMalloc(&da, sizeof(Args)) || hipMalloc(&dout, 8))
+  if (hipMalloc(&dp, (size_t)n * 8) || hipMalloc(&ds, 3 * (size_t)nvc * 8) ||
+      hipMalloc(&st, sizeof(DevState)) || hipMalloc(&da, sizeof(Args)) || hipMalloc(&dout, 8))
     goto done;
   {
     Args a;
@@ -140,15 +129,21 @@ extern "C" int probe_walk(const float* p, uint32_t n, const uint32_t* words, uin
     a.d.nvc = nvc;
     a.mb_p = dp;
     a.mb_vsum = ds;
+    a.mb_psum = ds + nvc;
+    a.mb_qsum = ds + 2 * nvc;
     a.st = st;
-    (void)hipMemcpy(dp, hp.data(), n * 8, hipMemcpyHostToDevice);
-    (void)hipMemcpy(ds, hs.data(), nvc * 8, hipMemcpyHostToDevice);
+    (void)hipMemset(ds, 0, 3 * (size_t)nvc * 8);
     (void)hipMemset(st, 0, sizeof(DevState));
     (void)hipMemcpy(da, &a, sizeof(Args), hipMemcpyHostToDevice);
-    const size_t lds = (4 + 64 + 2 * nvc + 2 + 2 * NWAVES + 4) * sizeof(float);
+    const size_t lds = (4 + 64 + samp_lds_floats(nvc, 0)) * sizeof(float);
     for (uint32_t i = 0; i < n_words; ++i) {
+      const u64 tag = 7 + i;
+      for (uint32_t c = 0; c < nvc; ++c) hs[c] = (tag << 32) | sums[c];
+      for (uint32_t j = 0; j < n; ++j) hp[j] = (tag << 32) | bits[j];
+      (void)hipMemcpy(dp, hp.data(), (size_t)n * 8, hipMemcpyHostToDevice);
+      (void)hipMemcpy(ds, hs.data(), (size_t)nvc * 8, hipMemcpyHostToDevice);
       (void)hipMemset(dout, 0xff, 8);
-      k_walk<<<1, BLOCK, lds>>>(da, tag, words[i], dout);
+      k_walk<<<1, BLOCK, lds>>>(da, (uint32_t)tag, words[i], dout);
       if (hipMemcpy(out + 2 * i, dout, 8, hipMemcpyDeviceToHost) != hipSuccess) goto done;
     }
     DevState h;
