@@ -133,18 +133,26 @@ def cpu_baseline_c1(cfg: dict, weights, prompt, budget_s: float = 15.0) -> dict:
     }
 
 
-def c1_step(model, prompt, H) -> tuple:
+def c1_step(model, prompt, H, wal_dir) -> tuple:
     """One step of the decode workload: sessions A (greedy) and B (T = 0.7,
-    seed 42), 128 generated tokens each. Returns (host seconds of the two
-    generate calls, device ms of their two launches, tokens of A, tokens of B)."""
+    seed 42), 128 generated tokens each, every token logged to the session's
+    WAL as the device commits it (one 29-byte record written and flushed,
+    wal.rs:241-250), inside the timed region as `defer run` times its
+    generate loop with its appends (main.rs:261-303); the WAL is created
+    before, as cmd_run creates it before run_generation. Returns (host
+    seconds of the two generate calls, device ms of their two launches,
+    tokens of A, tokens of B)."""
     wall, dev, out = 0.0, 0.0, []
-    for T in (0.0, TEMPERATURE):
+    for k, T in enumerate((0.0, TEMPERATURE)):
         s = H.Session(model, H.seed_from_u64(42), T, capacity=512)
         s.prompt(prompt)
+        wal = H.Wal.create(os.path.join(wal_dir, f"session{k}.wal"), bytes(32), H.seed_from_u64(42), T,
+                           len(prompt), 0, prompt)
         t0 = time.perf_counter()
-        toks = s.generate(128)
+        toks = s.generate(128, wal=wal)
         wall += time.perf_counter() - t0
         dev += model.last_device_ms()
+        wal.close()
         assert len(toks) == 128
         out.append(toks)
         s.close()
@@ -600,11 +608,14 @@ def main() -> int:
     model.set_exec(EXEC_MODES[args.exec])
     model.set_batching(0)
     ref = None
+    import tempfile
+
+    wal_dir = tempfile.mkdtemp(prefix="defer-bench-")
     for _ in range(args.warmup):
-        ref = c1_step(model, prompt, H)[2:]
+        ref = c1_step(model, prompt, H, wal_dir)[2:]
     wall, dev = 0.0, 0.0
     for _ in range(args.steps):
-        w, d, ta, tb = c1_step(model, prompt, H)
+        w, d, ta, tb = c1_step(model, prompt, H, wal_dir)
         wall += w
         dev += d
         if ref is not None and (ta, tb) != ref:
@@ -634,7 +645,8 @@ def main() -> int:
         "data": "synthetic (N(0,0.02) weights from seed 0, uniform-random prompt ids)",
         "config": {
             "workload": "SmolLM2-135M-shaped batch-1 decode: 32-token prompt; session A 128 "
-                        "greedy tokens, session B 128 tokens at T=0.7 (seed 42); one step = both "
+                        "greedy tokens, session B 128 tokens at T=0.7 (seed 42), every token "
+                        "appended to the session's WAL inside the timed region; one step = both "
                         "sessions (256 tokens at positions 32..160, prompts untimed)",
             "tokens_per_step": 256,
             "exec": args.exec,

@@ -67,28 +67,62 @@ def _fingerprint_of_rows(cache) -> bytes:
 def test_cache_fingerprint_and_repeat_runs(tiny):
     """KvCache::fingerprint on a device cache equals an independent SHA-256
     of its rows, an empty cache hashes 8 zero bytes, and repeated sessions
-    give the same tokens and the same fingerprint (verification.rs:46-59,
-    here 5 runs)."""
+    give the same tokens, the same fingerprint, bit-equal last logits and
+    the same rng word position (verification.rs:46-59: 100 runs)."""
     import hashlib
 
     cfg, w, gm, om = tiny
-    say("tiny: cache fingerprint vs hashlib, empty cache, 5 repeat runs of prompt 7 + 24 at T=0.9")
+    say("tiny: cache fingerprint vs hashlib, empty cache, 100 repeat runs of prompt 7 + 24 at T=0.9")
     empty = gm.new_cache(16)
     assert H.cache_fingerprint(empty) == hashlib.sha256(bytes(8)).digest()
     assert empty.shape() == (cfg["num_layers"], cfg["num_kv_heads"] * cfg["head_dim"])
     prompt = [int(x) for x in synthetic.make_prompt(cfg["vocab_size"], 7, seed=3)]
     runs = []
-    for _ in range(5):
+    for k in range(100):
+        if k:
+            s.close()
         s = H.Session(gm, H.seed_from_u64(21), 0.9)
         s.prompt(prompt)
         toks = s.generate(24)
         fp = H.cache_fingerprint(s.cache)
-        assert fp == _fingerprint_of_rows(s.cache)
-        runs.append((toks, fp))
+        if k < 3:
+            assert fp == _fingerprint_of_rows(s.cache)
+        runs.append((toks, fp, bits_of(s.cache.last_logits()).tobytes(), s.rng_word_pos))
     assert all(r == runs[0] for r in runs)
+    assert runs[0][3] == 24
     c = s.cache
     c.truncate(10)
     assert H.cache_fingerprint(c) == _fingerprint_of_rows(c) != runs[0][1]
+
+
+def bits_of(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+@pytest.mark.parametrize("T", [0.0, 0.7, 1.5])
+def test_checkout_cache_is_bit_identical(tiny, T):
+    """verification.rs:84-107 at T in {0, 0.7, 1.5}: a checkout of a live
+    session's checkpoint (history, rng position) gives the live cache, the
+    cache of the whole history fed as one prompt, bit-equal last logits and
+    the same rng word position."""
+    cfg, w, gm, om = tiny
+    seed = H.seed_from_u64(4242)
+    prompt = [int(x) for x in synthetic.make_prompt(cfg["vocab_size"], 9, seed=8)]
+    live = H.Session(gm, seed, T)
+    live.prompt(prompt)
+    live.generate(30)
+    rep = H.Session.checkout(gm, seed, T, live.history, len(prompt), live.rng_word_pos)
+    fresh = H.Session(gm, seed, T)
+    fresh.prompt(live.history)
+    assert rep.rng_word_pos == live.rng_word_pos == (30 if T else 0)
+    for other in (rep, fresh):
+        for layer in range(cfg["num_layers"]):
+            for x, y in zip(other.cache.read(layer), live.cache.read(layer)):
+                assert np.array_equal(bits_of(x), bits_of(y))
+        assert np.array_equal(bits_of(other.cache.last_logits()), bits_of(live.cache.last_logits()))
+    assert H.cache_fingerprint(rep.cache) == H.cache_fingerprint(live.cache)
+    for x in (live, rep, fresh):
+        x.close()
 
 
 def test_session_steps_equal_generate(tiny):
