@@ -379,7 +379,7 @@ struct defer_gpu_model {
 static size_t samp_lds_bytes(const defer_gpu_model* m) {
   const Dims& d = m->d;
   const size_t samp_end =
-      (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + samp_lds_floats(d.nvc, NWA * SAMP_CPW)) * sizeof(float);
+      (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + samp_lds_floats(d.nvc, NWA * SAMP_CPW, d.lds_vec)) * sizeof(float);
   return std::max(m->lds_rows, samp_end);
 }
 
@@ -490,7 +490,7 @@ static int apply_layout(defer_gpu_model* m, uint32_t G) {
                             MAX_GROUP * attn_chunk(d.cap - 1) + NCW * d.hd * d.group;
   const uint32_t scr_o = INLINE_COMB_MAX + rmax;
   const uint32_t scr_comb = MAX_ACHUNKS * hs;
-  const uint32_t scr_samp = samp_lds_floats(d.nvc, NWA);
+  const uint32_t scr_samp = samp_lds_floats(d.nvc, NWA, d.lds_vec);
   const uint32_t scr_lm = ((d.nvc + G - 1) / G) * VCHUNK;
   d.lds_scr = (std::max({scr_attn, scr_o, scr_comb, scr_samp, scr_lm, 2 * NWAVES}) + 3) & ~3u;
   // O rows skip the workgroups that take the attention items at positions

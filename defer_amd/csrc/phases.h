@@ -1558,7 +1558,7 @@ __device__ __forceinline__ float unit_f32(uint32_t word) {
 
 constexpr double SAMP_MARGIN = 1.0 / 16384;  // relative slack of the spacing guesses
 constexpr uint32_t OWN_MAX = 16;             // owned chunks whose p_v stay in LDS
-constexpr uint32_t NEV_MAX = 48;             // term-by-term chunks fetched ahead of a walk
+constexpr uint32_t NEV_MAX = 36;             // term-by-term chunks fetched ahead of a walk
 static_assert(NEV_MAX % NWA == 0, "fetch slots split evenly over the waves");
 constexpr uint16_t NO_SLOT = 0xFFFF;
 
@@ -1572,33 +1572,36 @@ struct SampLds {
   float* A;       // [nvc] chunk sums of p
   float* pre;     // [nvc] approximate exclusive prefix of the chunk sums
   uint32_t* sw;   // [nvc] summary words of the walk in hand
-  uint32_t* PI;   // [nvc] inclusive prefix of the usable chunk totals (mod 2^32)
+  uint32_t* PI;   // [nvc] build_segments: the integer total of chunk c's segment from c on
   uint16_t* nxt;  // [nvc] the first segment start after chunk c
   uint32_t* nev;  // number of fetched chunks
   uint32_t* evc;  // [NEV_MAX] the chunk in each fetch slot
   uint16_t* slot; // [nvc] where chunk c's p_v are in evp (NO_SLOT: not fetched)
   float* evp;     // [NEV_MAX * VCHUNK] p_v of the fetched chunks
+  uint32_t* pw;   // [NEV_MAX][2][VCHUNK] their terms' prefix words in grids E and E + 1 (pack_prefix)
+  int32_t* slE;   // [NEV_MAX] the grid E each fetched chunk's prefix words are for
   double* dred;   // [NWAVES]
   uint32_t* res;  // [4]
 };
-__host__ __device__ inline uint32_t samp_lds_floats(uint32_t nvc, uint32_t stage_a_chunks) {
+// A and pre live in the matvec input region (s.vec, free from the lm_head
+// to the next token's first gather) where they fit, else after the rest.
+__host__ __device__ inline bool samp_ap_in_vec(uint32_t nvc, uint32_t lds_vec) { return 2 * nvc <= lds_vec; }
+__host__ __device__ inline uint32_t samp_lds_floats(uint32_t nvc, uint32_t stage_a_chunks, uint32_t lds_vec) {
   const uint32_t a = OWN_MAX * VCHUNK + 2 * nvc + stage_a_chunks * VCHUNK;
-  const uint32_t w = OWN_MAX * VCHUNK + 4 * nvc + 1 + NEV_MAX + 2 * ((nvc + 1) / 2) + NEV_MAX * VCHUNK + 1 +
-                     2 * NWAVES + 4;
+  const uint32_t w = OWN_MAX * VCHUNK + 2 * nvc + 2 * ((nvc + 1) / 2) + 1 + NEV_MAX + 3 * NEV_MAX * VCHUNK +
+                     NEV_MAX + 1 + 2 * NWAVES + 4 + (samp_ap_in_vec(nvc, lds_vec) ? 0 : 2 * nvc);
   return a > w ? a : w;
 }
-__device__ __forceinline__ SampLds samp_lds(const Lds& s, uint32_t nvc) {
+__device__ __forceinline__ SampLds samp_lds(const Lds& s, uint32_t nvc, uint32_t lds_vec) {
   SampLds L;
   float* b = s.scr;
   L.ownp = b;
   b += OWN_MAX * VCHUNK;
+  // stage A: chunk maxima, argmaxes, then the logits of the chunks in flight
   L.vmx = b;
   L.varg = b + nvc;
   L.chunk = b + 2 * nvc;
-  L.A = b;
-  b += nvc;
-  L.pre = b;
-  b += nvc;
+  // from stage A2 on
   L.sw = reinterpret_cast<uint32_t*>(b);
   b += nvc;
   L.PI = reinterpret_cast<uint32_t*>(b);
@@ -1613,10 +1616,18 @@ __device__ __forceinline__ SampLds samp_lds(const Lds& s, uint32_t nvc) {
   b += (nvc + 1) / 2;
   L.evp = b;
   b += NEV_MAX * VCHUNK;
+  L.pw = reinterpret_cast<uint32_t*>(b);
+  b += 2 * NEV_MAX * VCHUNK;
+  L.slE = reinterpret_cast<int32_t*>(b);
+  b += NEV_MAX;
   b += (uint32_t)((uintptr_t)b & 4u) ? 1 : 0;  // 8-byte alignment (s.scr is 16-byte aligned)
   L.dred = reinterpret_cast<double*>(b);
   b += 2 * NWAVES;
   L.res = reinterpret_cast<uint32_t*>(b);
+  b += 4;
+  float* ap = samp_ap_in_vec(nvc, lds_vec) ? s.vec : b;
+  L.A = ap;
+  L.pre = ap + nvc;
   return L;
 }
 
@@ -1637,7 +1648,7 @@ __device__ __forceinline__ bool sample_stage_a(const Args& a, uint32_t tick, uin
   const Dims d = shape_dims(a.d);
   const uint32_t nvc = d.nvc;
   const uint32_t gl = gen_lm(d, tick - 1u);
-  const SampLds L = samp_lds(s, nvc);
+  const SampLds L = samp_lds(s, nvc, a.d.lds_vec);
   if (!poll_gather<2, 2>(gather_vec(a.mb_vmax, nvc, gl, L.vmx), gather_vec(a.mb_varg, nvc, gl, L.varg),
                          NWA, a.st, s.ctl))
     return false;
@@ -1808,6 +1819,19 @@ __device__ __forceinline__ bool publish_summaries(const Args& a, u64* dst, uint3
   return s.ctl->abort_seen == 0;
 }
 
+// A chunk's terms in grid E, summarised per lane j in one word: bits 0-29
+// the inclusive prefix sum of rho over lanes <= j, bit 30 whether term j
+// rounds up (rho = a + 1, so the crossing test k + Pex + a is k + P - bit),
+// bit 31 whether term j leaves the region by itself or is a tie. Lanes at
+// or past n hold zero terms.
+constexpr uint32_t PW_P = 0x3FFFFFFFu, PW_UP = 1u << 30, PW_BAD = 1u << 31;
+__device__ __forceinline__ uint32_t pack_prefix(float x, int E) {
+  const GridTerm g = grid_term(x, E);
+  const uint32_t rho = g.big ? 0u : g.rho;
+  const uint32_t P = wave_scan_u32(rho);
+  return P | (!g.big && g.rho != g.a ? PW_UP : 0u) | (g.big || g.tie ? PW_BAD : 0u);
+}
+
 // The p_v of the chunks a walk is expected to sum term by term, fetched
 // into LDS (at most NEV_MAX chunks; a walk reads any other from the
 // mailbox). Round 0 (while the other workgroups finish their summaries):
@@ -1882,8 +1906,20 @@ __device__ __forceinline__ bool fetch_events(const Args& a, uint32_t gsum, float
       ptr[e] = a.mb_p + min(L.evc[min(s0 + e, n_after - 1)] * VCHUNK + lane, V - 1);
     ok = load_tagged<FB>(ptr, gsum, t, a.st, s.ctl);
 #pragma unroll
-    for (uint32_t e = 0; e < FB; ++e)
-      if (ok && s0 + e < n_after) L.evp[(s0 + e) * VCHUNK + lane] = t[e];
+    for (uint32_t e = 0; e < FB; ++e) {
+      const uint32_t sl = s0 + e;
+      if (!ok || sl >= n_after) break;
+      L.evp[sl * VCHUNK + lane] = t[e];
+      // the terms' prefix words in the grid the chunk is expected to start
+      // in and the next one, off the walk's path
+      const uint32_t c = L.evc[sl];
+      bool ch;
+      const int E = chunk_guess(L, c, FIND ? inv : 1.0f, &ch);
+      const float x = c * VCHUNK + lane < V ? (FIND ? t[e] * inv : t[e]) : 0.0f;
+      L.pw[(2 * sl) * VCHUNK + lane] = pack_prefix(x, E);
+      L.pw[(2 * sl + 1) * VCHUNK + lane] = pack_prefix(x, E + 1);
+      if (lane == 0) L.slE[sl] = E;
+    }
   }
   if (!ok && lane == 0) s.ctl->abort_seen = 1;
   __syncthreads();
@@ -1897,17 +1933,17 @@ __device__ __forceinline__ bool fetch_events(const Args& a, uint32_t gsum, float
 // FIND: stops at the first term j with r < the sum after it (hit = j; 64 if
 // none). Wave-uniform.
 template <bool FIND>
-__device__ __forceinline__ void chunk_exact(float x, uint32_t n, float r, float& s, uint32_t& hit) {
+__device__ __forceinline__ void chunk_exact(float x, uint32_t n, float r, float& s, uint32_t& hit,
+                                            uint32_t jstart = 0) {
   const uint32_t lane = threadIdx.x % WAVE;
   hit = 64;
-  uint32_t jstart = 0;
   int E = grid_of(s);
   GridTerm g = grid_term(x, E);
   // Where several terms leave the running sum's region at once (the first
   // chunk, whose sum starts at 0), one float addition per term is cheaper
   // than a restart per term.
-  if (__popcll(__ballot(lane < n && (g.big || g.tie))) >= 4) {
-    for (uint32_t j = 0; j < n; ++j) {
+  if (__popcll(__ballot(lane >= jstart && lane < n && (g.big || g.tie))) >= 4) {
+    for (uint32_t j = jstart; j < n; ++j) {
       s = s + lane_f32(x, j);
       if (FIND && r < s) {
         hit = j;
@@ -1985,6 +2021,67 @@ __device__ __forceinline__ void chunk_exact(float x, uint32_t n, float r, float&
   }
 }
 
+// chunk_exact for a fetched chunk whose running sum starts in the grid E
+// its prefix words wE (grid E) and wE1 (grid E + 1) were formed for: the
+// terms up to the first that leaves E (or is a tie) are one integer step,
+// that term one float addition, and where the sum lands in E + 1 the rest up
+// to the next such term another integer step. Returns the lane from which
+// chunk_exact must go on (64 when the chunk is done).
+template <bool FIND>
+__device__ __forceinline__ uint32_t chunk_fast(uint32_t wE, uint32_t wE1, float x, uint32_t n, int E, float r,
+                                               float& s, uint32_t& hit) {
+  const uint32_t lane = threadIdx.x % WAVE;
+  hit = 64;
+  const uint32_t k = grid_units(s, E);
+  const uint32_t P = wE & PW_P;
+  const bool bad = lane < n && ((wE & PW_BAD) || k + P - ((wE & PW_UP) ? 1u : 0u) >= GRID_TOP);
+  const uint32_t jb = first_lane(__ballot(bad));
+  if (FIND) {
+    const uint32_t jh = first_lane(__ballot(lane < jb && lane < n && r < __builtin_ldexpf((float)(k + P), E)));
+    if (jh < 64) {
+      hit = jh;
+      s = __builtin_ldexpf((float)(k + lane_u32(P, jh)), E);
+      return 64;
+    }
+  }
+  if (jb >= 64) {
+    s = __builtin_ldexpf((float)(k + lane_u32(P, 63)), E);
+    return 64;
+  }
+  s = __builtin_ldexpf((float)(k + (jb ? lane_u32(P, jb - 1) : 0u)), E);
+  s = s + lane_f32(x, jb);
+  if (FIND && r < s) {
+    hit = jb;
+    return 64;
+  }
+  if (jb + 1 >= n) return 64;
+  if (grid_of(s) != E + 1) return jb + 1;
+  const uint32_t k2 = grid_units(s, E + 1);
+  const uint32_t Q = (wE1 & PW_P) - lane_u32(wE1 & PW_P, jb);
+  const bool after = lane > jb && lane < n;
+  const bool bad2 = after && ((wE1 & PW_BAD) || k2 + Q - ((wE1 & PW_UP) ? 1u : 0u) >= GRID_TOP);
+  const uint32_t jb2 = first_lane(__ballot(bad2));
+  if (FIND) {
+    const uint32_t jh = first_lane(__ballot(after && lane < jb2 && r < __builtin_ldexpf((float)(k2 + Q), E + 1)));
+    if (jh < 64) {
+      hit = jh;
+      s = __builtin_ldexpf((float)(k2 + lane_u32(Q, jh)), E + 1);
+      return 64;
+    }
+  }
+  if (jb2 >= 64) {
+    s = __builtin_ldexpf((float)(k2 + lane_u32(Q, 63)), E + 1);
+    return 64;
+  }
+  s = __builtin_ldexpf((float)(k2 + lane_u32(Q, jb2 - 1)), E + 1);
+  s = s + lane_f32(x, jb2);
+  if (FIND && r < s) {
+    hit = jb2;
+    return 64;
+  }
+  return jb2 + 1;
+}
+
 // Segments of the summary words in L.sw: a segment is a maximal run of
 // usable chunks (an integer total) in one grid, and each term-by-term chunk
 // is one of its own. L.PI gets the inclusive prefix of the usable totals, so
@@ -2038,6 +2135,20 @@ __device__ __forceinline__ void build_segments(const SampLds& L, uint32_t nvc) {
     }
   }
   __syncthreads();
+  // PI[c] becomes the total of c's segment from c on: PI[nxt - 1] - PI[c - 1]
+  // (read by every thread before any is overwritten)
+  constexpr uint32_t CPT_MAX = 4;  // chunks per thread: nvc <= 2048
+  uint32_t rest[CPT_MAX];
+#pragma unroll
+  for (uint32_t q = 0; q < CPT_MAX; ++q) {
+    const uint32_t c = ca + q;
+    rest[q] = c < cb ? L.PI[L.nxt[c] - 1] - (c ? L.PI[c - 1] : 0u) : 0u;
+  }
+  __syncthreads();
+#pragma unroll
+  for (uint32_t q = 0; q < CPT_MAX; ++q)
+    if (ca + q < cb) L.PI[ca + q] = rest[q];
+  __syncthreads();
 }
 
 // One walk over the summary words L.sw (wave 0; the block waits): the total
@@ -2059,20 +2170,19 @@ __device__ __forceinline__ bool exact_walk(const Args& a, uint32_t gsum, float i
     while (c0 < nvc) {
       const int E = grid_of(sum);
       const uint32_t k = grid_units(sum, E);
-      bool exact_here = false;  // c0 goes term by term without a window scan
-      {
-        // the rest of c0's segment as one integer step, where it applies
-        const uint32_t w0 = L.sw[c0];
-        exact_here = sum_total(w0) == SUM_EVENT;
-        if (!exact_here && sum_grid(w0) == E) {
-          const uint32_t e = L.nxt[c0];
-          const uint32_t T = L.PI[e - 1] - (c0 ? L.PI[c0 - 1] : 0u);
-          if (T < GRID_TOP && k + T < GRID_TOP && !(FIND && r < __builtin_ldexpf((float)(k + T), E))) {
-            sum = __builtin_ldexpf((float)(k + T), E);
-            c0 = e;
-            continue;
-          }
-        }
+      // one round of reads for c0: its summary, segment end, the segment's
+      // total from c0 on, and its fetch slot
+      const uint32_t w0 = L.sw[c0];
+      const uint32_t e = L.nxt[c0];
+      const uint32_t T = L.PI[c0];
+      const uint32_t sl = L.slot[c0];
+      const bool exact_here = sum_total(w0) == SUM_EVENT;  // term by term, no window scan
+      if (!exact_here && sum_grid(w0) == E && T < GRID_TOP && k + T < GRID_TOP &&
+          !(FIND && r < __builtin_ldexpf((float)(k + T), E))) {
+        // the rest of c0's segment as one integer step
+        sum = __builtin_ldexpf((float)(k + T), E);
+        c0 = e;
+        continue;
       }
       uint32_t fb = 0;
       if (!exact_here) {
@@ -2091,10 +2201,22 @@ __device__ __forceinline__ bool exact_walk(const Args& a, uint32_t gsum, float i
       }
       if (fb < 64 && c0 < nvc) {
         const uint32_t base = c0 * VCHUNK, n = min(VCHUNK, V - base);
-        const uint32_t sl = L.slot[c0];
+        const uint32_t sc = fb ? L.slot[c0] : sl;  // a window stop moved c0
         float p;
-        if (sl != NO_SLOT) {
-          p = L.evp[sl * VCHUNK + lane];
+        uint32_t from = 0;  // the lane chunk_exact goes on from
+        uint32_t hit = 64;
+        if (sc != NO_SLOT) {
+          p = L.evp[sc * VCHUNK + lane];
+          const uint32_t w0s = L.pw[(2 * sc) * VCHUNK + lane], w1s = L.pw[(2 * sc + 1) * VCHUNK + lane];
+          const int Es = L.slE[sc], Eg = grid_of(sum);
+          const float xf = lane < n ? (FIND ? p * inv : p) : 0.0f;
+          if (Es == Eg) {
+            from = chunk_fast<FIND>(w0s, w1s, xf, n, Es, r, sum, hit);
+          } else if (Es + 1 == Eg) {
+            // the sum starts one spacing above the guess: grid E + 1's words
+            // serve the first step, chunk_exact the rest after a change
+            from = chunk_fast<FIND>(w1s, PW_BAD, xf, n, Eg, r, sum, hit);
+          }
         } else {
           const u64* ptr[1] = {a.mb_p + base + min(lane, n - 1)};
           float t[1];
@@ -2105,8 +2227,7 @@ __device__ __forceinline__ bool exact_walk(const Args& a, uint32_t gsum, float i
           p = t[0];
         }
         const float x = lane < n ? (FIND ? p * inv : p) : 0.0f;
-        uint32_t hit;
-        chunk_exact<FIND>(x, n, r, sum, hit);
+        if (hit == 64 && from < n) chunk_exact<FIND>(x, n, r, sum, hit, from);
         if (FIND && hit < 64) {
           found = base + hit;
           break;
@@ -2154,7 +2275,7 @@ __device__ __forceinline__ bool sample_exact(const Args& a, uint32_t gsum, float
   }
   const Dims d = shape_dims(a.d);
   const uint32_t nvc = d.nvc;
-  const SampLds L = samp_lds(s, nvc);
+  const SampLds L = samp_lds(s, nvc, a.d.lds_vec);
   // A2
   if (!poll_gather<2>(gather_vec(a.mb_vsum, nvc, gsum, L.A), NWA, a.st, s.ctl)) return false;
   approx_prefix(L.A, L.pre, nvc, L.dred);
@@ -2208,7 +2329,7 @@ __device__ __forceinline__ bool sample_one_wg(const Args& a, uint32_t tick, uint
   const Dims d = shape_dims(a.d);
   const uint32_t nvc = d.nvc;
   const uint32_t gl = gen_lm(d, tick - 1u);
-  const SampLds L = samp_lds(s, nvc);
+  const SampLds L = samp_lds(s, nvc, a.d.lds_vec);
   if (!poll_gather<2, 2>(gather_vec(a.mb_vmax, nvc, gl, L.vmx), gather_vec(a.mb_varg, nvc, gl, L.varg), NWA,
                          a.st, s.ctl))
     return false;

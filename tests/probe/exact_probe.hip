@@ -135,7 +135,7 @@ extern "C" int probe_walk(const float* p, uint32_t n, const uint32_t* words, uin
     (void)hipMemset(ds, 0, 3 * (size_t)nvc * 8);
     (void)hipMemset(st, 0, sizeof(DevState));
     (void)hipMemcpy(da, &a, sizeof(Args), hipMemcpyHostToDevice);
-    const size_t lds = (4 + 64 + samp_lds_floats(nvc, 0)) * sizeof(float);
+    const size_t lds = (4 + 64 + samp_lds_floats(nvc, 0, 0)) * sizeof(float);
     for (uint32_t i = 0; i < n_words; ++i) {
       const u64 tag = 7 + i;
       for (uint32_t c = 0; c < nvc; ++c) hs[c] = (tag << 32) | sums[c];
