@@ -9,6 +9,8 @@
 //   eager:      the same kernels launched one by one.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -59,6 +61,20 @@ static int fail(int code, const char* fmt, ...) {
   } while (0)
 
 extern "C" const char* defer_gpu_last_error(void) { return g_last_error.c_str(); }
+
+// Every device and pinned host allocation of the library goes through these,
+// so defer_gpu_allocation_count can show a call allocated nothing.
+static std::atomic<uint64_t> g_allocations{0};
+template <class T>
+static hipError_t counted_malloc(T** p, size_t n) {
+  g_allocations.fetch_add(1, std::memory_order_relaxed);
+  return hipMalloc(reinterpret_cast<void**>(p), n);
+}
+static hipError_t counted_host_malloc(void** p, size_t n, unsigned flags) {
+  g_allocations.fetch_add(1, std::memory_order_relaxed);
+  return hipHostMalloc(p, n, flags);
+}
+extern "C" uint64_t defer_gpu_allocation_count(void) { return g_allocations.load(std::memory_order_relaxed); }
 
 // ------------------------------------------------------------------ kernels
 
@@ -679,7 +695,7 @@ extern "C" int defer_gpu_model_create(const defer_gpu_config* cfg, const float* 
 
   e = hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking);
   if (e != hipSuccess) return cleanup(fail(DEFER_GPU_E_HIP, "stream: %s", hipGetErrorString(e)));
-  e = hipMalloc(&m->wbuf, total);
+  e = counted_malloc(&m->wbuf, total);
   if (e != hipSuccess)
     return cleanup(fail(DEFER_GPU_E_HIP, "hipMalloc(%zu) for weights: %s", total,
                         hipGetErrorString(e)));
@@ -754,7 +770,7 @@ extern "C" int defer_gpu_model_create(const defer_gpu_config* cfg, const float* 
   m->embed = at(o_embed);
   m->norm = at(o_norm);
   m->head = at(o_head);
-  e = hipMalloc(&m->d_layers, sizeof(LayerW) * d.L);
+  e = counted_malloc(&m->d_layers, sizeof(LayerW) * d.L);
   if (e == hipSuccess)
     e = hipMemcpy(m->d_layers, m->layers.data(), sizeof(LayerW) * d.L, hipMemcpyHostToDevice);
   if (e != hipSuccess) return cleanup(fail(DEFER_GPU_E_HIP, "layer table: %s", hipGetErrorString(e)));
@@ -772,7 +788,7 @@ extern "C" int defer_gpu_model_create(const defer_gpu_config* cfg, const float* 
       const float angle = (float)p * inv_freq[i];
       rope[(size_t)p * d.half + i] = make_float2(cosf(angle), sinf(angle));
     }
-  e = hipMalloc(&m->rope, rope.size() * sizeof(float2));
+  e = counted_malloc(&m->rope, rope.size() * sizeof(float2));
   if (e == hipSuccess)
     e = hipMemcpy(m->rope, rope.data(), rope.size() * sizeof(float2), hipMemcpyHostToDevice);
   if (e != hipSuccess) return cleanup(fail(DEFER_GPU_E_HIP, "rope table: %s", hipGetErrorString(e)));
@@ -866,8 +882,8 @@ static int cache_alloc(const defer_gpu_model* m, uint32_t cap, defer_gpu_cache* 
   ++const_cast<defer_gpu_model*>(m)->n_caches;
   c->cap = cap;
   const size_t kvn = (size_t)d.L * d.nkv * cap * d.kvs;
-  HIP_TRY(hipMalloc(&c->kc, kvn * sizeof(float)));
-  HIP_TRY(hipMalloc(&c->vc, kvn * sizeof(float)));
+  HIP_TRY(counted_malloc(&c->kc, kvn * sizeof(float)));
+  HIP_TRY(counted_malloc(&c->vc, kvn * sizeof(float)));
   const size_t hs = d.hd + 2;
   // xo, xd, g: MB_REPS replicas of one block, each on its own 32 KB boundary
   const size_t rep_words = ((size_t)2 * d.h + d.ff + 4095) / 4096 * 4096;
@@ -875,13 +891,13 @@ static int cache_alloc(const defer_gpu_model* m, uint32_t cap, defer_gpu_cache* 
                              5 * (size_t)d.nvc + 64 + 4095) / 4096 * 4096;
   const size_t words = base_words + MB_REPS * rep_words;
   c->mb_words = words;
-  HIP_TRY(hipMalloc(&c->mb, words * sizeof(u64)));
+  HIP_TRY(counted_malloc(&c->mb, words * sizeof(u64)));
   HIP_TRY(hipMemset(c->mb, 0, words * sizeof(u64)));
-  HIP_TRY(hipMalloc(&c->st, sizeof(DevState)));
+  HIP_TRY(counted_malloc(&c->st, sizeof(DevState)));
   HIP_TRY(hipMemset(c->st, 0, sizeof(DevState)));
-  HIP_TRY(hipMalloc(&c->d_run, sizeof(RunDesc)));
-  HIP_TRY(hipMalloc(&c->d_mask, ((cap + 31) / 32) * sizeof(uint32_t)));
-  HIP_TRY(hipMalloc(&c->d_logits, (size_t)d.V * sizeof(float)));
+  HIP_TRY(counted_malloc(&c->d_run, sizeof(RunDesc)));
+  HIP_TRY(counted_malloc(&c->d_mask, ((cap + 31) / 32) * sizeof(uint32_t)));
+  HIP_TRY(counted_malloc(&c->d_logits, (size_t)d.V * sizeof(float)));
   Args& a = c->args;
   a.d = d;
   a.d.cap = cap;
@@ -910,7 +926,7 @@ static int cache_alloc(const defer_gpu_model* m, uint32_t cap, defer_gpu_cache* 
   a.rep_words = (uint32_t)rep_words;
   a.st = c->st;
   a.mask = nullptr;
-  HIP_TRY(hipMalloc(&c->d_args, sizeof(Args)));
+  HIP_TRY(counted_malloc(&c->d_args, sizeof(Args)));
   HIP_TRY(hipMemcpy(c->d_args, &a, sizeof(Args), hipMemcpyHostToDevice));
   return DEFER_GPU_OK;
 }
@@ -1025,7 +1041,7 @@ extern "C" int defer_gpu_cache_read(const defer_gpu_cache* cc, uint32_t layer, f
   if (layer >= d.L) return fail(DEFER_GPU_E_INVALID, "layer %u out of range", layer);
   const size_t n = (size_t)c->pos * d.kv;
   if (n == 0) return DEFER_GPU_OK;
-  if (!c->d_tmp) HIP_TRY(hipMalloc(&c->d_tmp, (size_t)c->cap * d.kv * sizeof(float)));
+  if (!c->d_tmp) HIP_TRY(counted_malloc(&c->d_tmp, (size_t)c->cap * d.kv * sizeof(float)));
   const hipStream_t s = c->m->stream;
   const size_t per_layer = (size_t)d.nkv * c->cap * d.kvs;
   for (int which = 0; which < 2; ++which) {
@@ -1060,7 +1076,7 @@ extern "C" int defer_gpu_value_norms(const defer_gpu_cache* cc, uint32_t t0, uin
   if (nt == 0) return DEFER_GPU_OK;
   const size_t n = (size_t)d.L * nt * d.nh;
   float* dout = nullptr;
-  HIP_TRY(hipMalloc(&dout, n * sizeof(float)));
+  HIP_TRY(counted_malloc(&dout, n * sizeof(float)));
   const hipStream_t s = m->stream;
   k_value_norms<<<dim3(d.nh, nt, d.L), 256, (d.hd + d.h) * sizeof(float), s>>>(
       m->d_layers, c->vc, d, c->cap, t0, nt, dout);
@@ -1084,9 +1100,9 @@ static int ensure_run_buffers(defer_gpu_cache* c, size_t n_ops, size_t n_stop) {
     c->d_tokens = c->d_words = c->d_out = nullptr;
     c->run_cap = 0;
     const size_t cap = std::max<size_t>(n_ops, 1024);
-    HIP_TRY(hipMalloc(&c->d_tokens, cap * sizeof(uint32_t)));
-    HIP_TRY(hipMalloc(&c->d_words, cap * sizeof(uint32_t)));
-    HIP_TRY(hipMalloc(&c->d_out, cap * sizeof(uint32_t)));
+    HIP_TRY(counted_malloc(&c->d_tokens, cap * sizeof(uint32_t)));
+    HIP_TRY(counted_malloc(&c->d_words, cap * sizeof(uint32_t)));
+    HIP_TRY(counted_malloc(&c->d_out, cap * sizeof(uint32_t)));
     c->run_cap = cap;
   }
   if (n_stop > c->stop_cap || !c->d_stop) {
@@ -1094,7 +1110,7 @@ static int ensure_run_buffers(defer_gpu_cache* c, size_t n_ops, size_t n_stop) {
     c->d_stop = nullptr;
     c->stop_cap = 0;
     const size_t cap = std::max<size_t>(n_stop, 16);
-    HIP_TRY(hipMalloc(&c->d_stop, cap * sizeof(uint32_t)));
+    HIP_TRY(counted_malloc(&c->d_stop, cap * sizeof(uint32_t)));
     c->stop_cap = cap;
   }
   return DEFER_GPU_OK;
@@ -1290,7 +1306,7 @@ extern "C" int defer_gpu_forward(const defer_gpu_model* m, defer_gpu_cache* c, u
   const uint32_t pos0 = c->pos;
   if (trace_out) {
     if (!c->d_trace)
-      HIP_TRY(hipMalloc(&c->d_trace, (size_t)m->d.L * m->d.nh * c->cap * sizeof(float)));
+      HIP_TRY(counted_malloc(&c->d_trace, (size_t)m->d.L * m->d.nh * c->cap * sizeof(float)));
     c->trace_to = c->d_trace;
   }
   rc = feed_tokens(m, c, &token, 1, use_mask || trace_out);
@@ -1427,7 +1443,7 @@ static int ensure_ring(defer_gpu_cache* c, size_t n) {
   const size_t cap = std::max<size_t>(n, 1024);
   // Coherent pinned memory: the device's system-scope stores land where the
   // host thread polls them while the run goes on.
-  HIP_TRY(hipHostMalloc((void**)&c->h_ring, cap * sizeof(u64), hipHostMallocCoherent));
+  HIP_TRY(counted_host_malloc((void**)&c->h_ring, cap * sizeof(u64), hipHostMallocCoherent));
   HIP_TRY(hipHostGetDevicePointer((void**)&c->d_ring, c->h_ring, 0));
   c->ring_cap = cap;
   return DEFER_GPU_OK;
@@ -1787,35 +1803,35 @@ static int ensure_ws(defer_gpu_model* m, uint32_t rows, uint32_t lm) {
   const uint32_t R = std::max(rows, w.rows), Lm = std::max(lm, w.lm);
   batch_ws_release(&w);
   const uint32_t kmax = std::max({d.h, d.q, d.ff});
-  HIP_TRY(hipMalloc(&w.X, (size_t)R * d.h * sizeof(float)));
-  HIP_TRY(hipMalloc(&w.Y, (size_t)R * batch_ldy(d) * sizeof(float)));
-  HIP_TRY(hipMalloc(&w.QS, (size_t)4 * std::min(R, 64u) * batch_ldy(d) * sizeof(float)));
-  HIP_TRY(hipMalloc(&w.INV, (size_t)R * sizeof(float)));
-  HIP_TRY(hipMalloc(&w.XP, panel_floats(R, d.h) * sizeof(float)));
-  HIP_TRY(hipMalloc(&w.QKVT, (size_t)R * d.qkv_rows * sizeof(u64)));
-  HIP_TRY(hipMalloc(&w.PART, (size_t)R * part_words(d) * sizeof(u64)));
-  HIP_TRY(hipMalloc(&w.drows, (size_t)R * sizeof(BRow)));
-  HIP_TRY(hipMalloc(&w.rargs, (size_t)R * sizeof(Args)));
-  HIP_TRY(hipMalloc(&w.items, (size_t)R * d.nkv * MAX_ACHUNKS * d.group * sizeof(uint32_t)));
-  HIP_TRY(hipMalloc(&w.tiles, ((size_t)R / 16 + 2) * sizeof(uint32_t)));
-  HIP_TRY(hipMalloc(&w.CNT, (size_t)R * d.nkv * sizeof(uint32_t)));
+  HIP_TRY(counted_malloc(&w.X, (size_t)R * d.h * sizeof(float)));
+  HIP_TRY(counted_malloc(&w.Y, (size_t)R * batch_ldy(d) * sizeof(float)));
+  HIP_TRY(counted_malloc(&w.QS, (size_t)4 * std::min(R, 64u) * batch_ldy(d) * sizeof(float)));
+  HIP_TRY(counted_malloc(&w.INV, (size_t)R * sizeof(float)));
+  HIP_TRY(counted_malloc(&w.XP, panel_floats(R, d.h) * sizeof(float)));
+  HIP_TRY(counted_malloc(&w.QKVT, (size_t)R * d.qkv_rows * sizeof(u64)));
+  HIP_TRY(counted_malloc(&w.PART, (size_t)R * part_words(d) * sizeof(u64)));
+  HIP_TRY(counted_malloc(&w.drows, (size_t)R * sizeof(BRow)));
+  HIP_TRY(counted_malloc(&w.rargs, (size_t)R * sizeof(Args)));
+  HIP_TRY(counted_malloc(&w.items, (size_t)R * d.nkv * MAX_ACHUNKS * d.group * sizeof(uint32_t)));
+  HIP_TRY(counted_malloc(&w.tiles, ((size_t)R / 16 + 2) * sizeof(uint32_t)));
+  HIP_TRY(counted_malloc(&w.CNT, (size_t)R * d.nkv * sizeof(uint32_t)));
   HIP_TRY(hipMemset(w.CNT, 0, (size_t)R * d.nkv * sizeof(uint32_t)));
-  HIP_TRY(hipMalloc(&w.sets, (size_t)R * sizeof(StateSet)));
+  HIP_TRY(counted_malloc(&w.sets, (size_t)R * sizeof(StateSet)));
   const uint32_t L1 = std::max(Lm, 1u);
-  HIP_TRY(hipMalloc(&w.XQ, panel_floats(std::max(R, L1), kmax) * sizeof(float)));
-  HIP_TRY(hipMalloc(&w.LINV, (size_t)L1 * sizeof(float)));
-  HIP_TRY(hipMalloc(&w.LOGT, (size_t)L1 * d.V * sizeof(u64)));
-  HIP_TRY(hipMalloc(&w.VMAX, (size_t)L1 * d.nvc * sizeof(u64)));
-  HIP_TRY(hipMalloc(&w.VARG, (size_t)L1 * d.nvc * sizeof(u64)));
-  HIP_TRY(hipMalloc(&w.VSUM, (size_t)L1 * 3 * d.nvc * sizeof(u64)));
-  HIP_TRY(hipMalloc(&w.VP, (size_t)L1 * d.V * sizeof(u64)));
-  HIP_TRY(hipMalloc(&w.largs, (size_t)L1 * sizeof(Args)));
-  HIP_TRY(hipMalloc(&w.sel, (size_t)L1 * sizeof(uint32_t)));
-  HIP_TRY(hipMalloc(&w.lgen, (size_t)L1 * sizeof(uint32_t)));
-  HIP_TRY(hipMalloc(&w.stick, (size_t)L1 * sizeof(uint32_t)));
-  HIP_TRY(hipMalloc(&w.swords, (size_t)L1 * sizeof(uint32_t)));
-  HIP_TRY(hipMalloc(&w.sout, (size_t)L1 * sizeof(uint32_t)));
-  HIP_TRY(hipMalloc(&w.st, sizeof(DevState)));
+  HIP_TRY(counted_malloc(&w.XQ, panel_floats(std::max(R, L1), kmax) * sizeof(float)));
+  HIP_TRY(counted_malloc(&w.LINV, (size_t)L1 * sizeof(float)));
+  HIP_TRY(counted_malloc(&w.LOGT, (size_t)L1 * d.V * sizeof(u64)));
+  HIP_TRY(counted_malloc(&w.VMAX, (size_t)L1 * d.nvc * sizeof(u64)));
+  HIP_TRY(counted_malloc(&w.VARG, (size_t)L1 * d.nvc * sizeof(u64)));
+  HIP_TRY(counted_malloc(&w.VSUM, (size_t)L1 * 3 * d.nvc * sizeof(u64)));
+  HIP_TRY(counted_malloc(&w.VP, (size_t)L1 * d.V * sizeof(u64)));
+  HIP_TRY(counted_malloc(&w.largs, (size_t)L1 * sizeof(Args)));
+  HIP_TRY(counted_malloc(&w.sel, (size_t)L1 * sizeof(uint32_t)));
+  HIP_TRY(counted_malloc(&w.lgen, (size_t)L1 * sizeof(uint32_t)));
+  HIP_TRY(counted_malloc(&w.stick, (size_t)L1 * sizeof(uint32_t)));
+  HIP_TRY(counted_malloc(&w.swords, (size_t)L1 * sizeof(uint32_t)));
+  HIP_TRY(counted_malloc(&w.sout, (size_t)L1 * sizeof(uint32_t)));
+  HIP_TRY(counted_malloc(&w.st, sizeof(DevState)));
   HIP_TRY(hipMemset(w.st, 0, sizeof(DevState)));
   // Tags start at 1, so zeroed sums never match a wait; sampled tokens
   // start in range.
@@ -1842,7 +1858,7 @@ static int ensure_panels(defer_gpu_model* m) {
                pg = panel_floats(2 * d.ff, d.h), pd = panel_floats(d.h, d.ff),
                pl = panel_floats(d.V, d.h);
   const size_t total = (pq + po + pg + pd) * d.L + pl;
-  HIP_TRY(hipMalloc(&m->panels, total * sizeof(float)));
+  HIP_TRY(counted_malloc(&m->panels, total * sizeof(float)));
   const hipStream_t s = m->stream;
   float* p = m->panels;
   m->p_qkv.assign(d.L, nullptr);

@@ -131,6 +131,8 @@ def lib() -> ctypes.CDLL:
     L.defer_gpu_replay.restype = ctypes.c_int
     L.defer_gpu_last_error.argtypes = []
     L.defer_gpu_last_error.restype = ctypes.c_char_p
+    L.defer_gpu_allocation_count.argtypes = []
+    L.defer_gpu_allocation_count.restype = ctypes.c_uint64
     L.defer_gpu_last_device_ms.argtypes = [vp]
     L.defer_gpu_last_device_ms.restype = ctypes.c_double
     L.defer_gpu_model_set_batching.argtypes = [vp, u32]
@@ -165,6 +167,11 @@ def _u32(a) -> np.ndarray:
 
 def _ptr(a: Optional[np.ndarray]):
     return None if a is None else ctypes.c_void_p(a.ctypes.data)
+
+
+def allocation_count() -> int:
+    """Device and pinned host allocations the library has made so far."""
+    return int(lib().defer_gpu_allocation_count())
 
 
 def tensor_count(cfg: Config) -> int:

@@ -150,6 +150,11 @@ int defer_gpu_generate(const defer_gpu_model* m, defer_gpu_cache* c, uint32_t ma
  * past it are truncated away; the logits are then not kept). */
 typedef int (*defer_gpu_token_fn)(void* user, uint32_t index, uint32_t token);
 
+/* Device and pinned host allocations the library has made since the process
+ * started (a diagnostic with no counterpart in the reference: tests use it
+ * to show that defer_gpu_generate_static allocates nothing). */
+uint64_t defer_gpu_allocation_count(void);
+
 /* defer_gpu_generate with on_token (nullable) called per committed token. */
 int defer_gpu_generate_cb(const defer_gpu_model* m, defer_gpu_cache* c, uint32_t max_tokens,
                           float temperature, const uint32_t* rng_words, const uint32_t* stop,
@@ -157,14 +162,16 @@ int defer_gpu_generate_cb(const defer_gpu_model* m, defer_gpu_cache* c, uint32_t
                           defer_gpu_token_fn on_token, void* user);
 
 /* defer_gpu_generate without any allocation. No counterpart in the
- * reference: it is for callers that cannot allocate device memory (code
- * under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc). The rng words, stop list and tokens of the run are staged in a
- * static device array of 513 KB per GPU, kept until the process ends, so a
- * call takes at most 65536 tokens and 256 stop tokens (more is rejected with
- * DEFER_GPU_E_INVALID before anything runs). Same arguments, results and
- * errors as defer_gpu_generate, bit for bit. Calls that overlap on one GPU
- * (from several host threads, on any caches) share that array and race. */
+ * reference: it is for callers that cannot allocate device memory (tight
+ * serving loops, harnesses that forbid hipMalloc). It launches kernels,
+ * synchronises the stream and copies the tokens back, so it must be called
+ * outside any stream capture. The rng words, stop list and tokens of the run
+ * are staged in a static device array of 513 KB per GPU, kept until the
+ * process ends, so a call takes at most 65536 tokens and 256 stop tokens
+ * (more is rejected with DEFER_GPU_E_INVALID before anything runs). Same
+ * arguments, results and errors as defer_gpu_generate, bit for bit. Calls
+ * that overlap on one GPU (from several host threads, on any caches) share
+ * that array and race. */
 int defer_gpu_generate_static(const defer_gpu_model* m, defer_gpu_cache* c, uint32_t max_tokens,
                               float temperature, const uint32_t* rng_words, const uint32_t* stop,
                               size_t n_stop, uint32_t* tokens_out, uint32_t* n_out);

@@ -434,3 +434,37 @@ def test_results_independent_of_grid(name, grids):
             assert np.array_equal(bits(x), bits(y))
         for x, y in zip(r[5], base[5]):
             assert np.array_equal(bits(x), bits(y))
+
+
+@pytest.mark.parametrize("gemm_cus", [96, 48])
+def test_lockstep_1b_independent_of_grid(gemm_cus):
+    """C4's launch mix at other GEMM shapes: the 1B shape (2 of its layers)
+    with 64 sessions stepping together, so the narrow GEMMs take the
+    quarter-split tasks (QKV, O, down) and the four-tile tasks (gate/up,
+    lm_head), greedy and at T = 0.7, with the GEMMs shaped for all the
+    device's CUs and for gemm_cus of them: same tokens, same bits."""
+    cfg = dict(synthetic.CONFIGS["llama-3.2-1b"])
+    cfg["num_layers"] = 2
+    w = synthetic.make_weights(cfg, 21)
+    V = cfg["vocab_size"]
+    prompts = [synthetic.make_prompt(V, 17 + (k % 9), seed=300 + k) for k in range(64)]
+    words = H.chacha8_words(H.seed_from_u64(8), 0, 2 * 64)
+    results = []
+    for gemm in (0, gemm_cus):
+        say(f"1b x 2 layers: 64 lockstep sessions, GEMMs for {gemm or 'all'} CUs")
+        gm = G.GpuModel(G.Config.from_dict(cfg), w)
+        gm.set_grid(0, gemm)
+        cs = [gm.new_cache(64) for _ in range(64)]
+        for c, p in zip(cs, prompts):
+            gm.prompt(c, p)
+        toks = [gm.step_batch(cs, 0.0) for _ in range(3)]
+        toks += [gm.step_batch(cs, 0.7, words[64 * i:64 * (i + 1)]) for i in range(2)]
+        results.append((toks, [bits(c.last_logits()).copy() for c in cs], cs[5].read(1)))
+        for c in cs:
+            c.close()
+        gm.close()
+    assert results[0][0] == results[1][0]
+    for x, y in zip(results[0][1], results[1][1]):
+        assert np.array_equal(x, y)
+    for x, y in zip(results[0][2], results[1][2]):
+        assert np.array_equal(bits(x), bits(y))
