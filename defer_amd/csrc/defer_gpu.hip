@@ -30,6 +30,7 @@ using namespace dg;
   namespace NS {                                              \
   struct Args;                                                \
   struct RunDesc;                                             \
+  template <bool RANDOM>                                      \
   __global__ void k_persistent(const Args* ap, const RunDesc* run); \
   }
 DG_DECLARE_SPECIALISED(dg135)
@@ -367,7 +368,7 @@ struct defer_gpu_model {
   const float* head = nullptr;
   float2* rope = nullptr;
   uint32_t exec_mode = DEFER_GPU_EXEC_PERSISTENT;
-  const void* persistent = nullptr;  // the persistent kernel for this shape
+  const void* persistent[2] = {};  // the persistent kernel for this shape: greedy, random
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   double last_ms = 0.0;
   // Batched path (built on first use): weight panels and the workspace.
@@ -406,13 +407,14 @@ static bool has_shape(const Dims& d, const Dims& f) {
   return d.h == f.h && d.nh == f.nh && d.nkv == f.nkv && d.hd == f.hd && d.ff == f.ff &&
          d.V == f.V && d.L == f.L && d.act == f.act && d.has_bias == f.has_bias && d.tied == f.tied;
 }
+template <bool RANDOM>
 static const void* persistent_kernel_for(const Dims& d) {
   if (has_shape(d, fix_shape(d, DG_SHAPE_ARGS_135M)) && d.stg_mask == 0xFu)
-    return (const void*)dg135::k_persistent;
-  if (has_shape(d, fix_shape(d, DG_SHAPE_ARGS_360M))) return (const void*)dg360::k_persistent;
-  if (has_shape(d, fix_shape(d, DG_SHAPE_ARGS_1B))) return (const void*)dg1b::k_persistent;
-  if (has_shape(d, fix_shape(d, DG_SHAPE_ARGS_8B))) return (const void*)dg8b::k_persistent;
-  return (const void*)k_persistent;
+    return (const void*)dg135::k_persistent<RANDOM>;
+  if (has_shape(d, fix_shape(d, DG_SHAPE_ARGS_360M))) return (const void*)dg360::k_persistent<RANDOM>;
+  if (has_shape(d, fix_shape(d, DG_SHAPE_ARGS_1B))) return (const void*)dg1b::k_persistent<RANDOM>;
+  if (has_shape(d, fix_shape(d, DG_SHAPE_ARGS_8B))) return (const void*)dg8b::k_persistent<RANDOM>;
+  return (const void*)k_persistent<RANDOM>;
 }
 
 struct defer_gpu_cache {
@@ -575,7 +577,8 @@ static int apply_layout(defer_gpu_model* m, uint32_t G) {
     d.stg_mask = mask;
     d.lds_stg = stg;
   }
-  m->persistent = persistent_kernel_for(d);
+  m->persistent[0] = persistent_kernel_for<false>(d);
+  m->persistent[1] = persistent_kernel_for<true>(d);
   m->lds_bytes = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr + d.lds_stg) * sizeof(float) +
                  (size_t)d.lds_pub * 2 * sizeof(u64) + (d.lds_stg ? 0 : 1024);
   m->lds_rows = (size_t)(4 + 64 + d.lds_vec + d.lds_vec2 + d.lds_scr) * sizeof(float);
@@ -584,7 +587,7 @@ static int apply_layout(defer_gpu_model* m, uint32_t G) {
   m->lds_attn = (size_t)(4 + 64 + ((std::max(scr_attn, scr_fcomb) + 3) & ~3u)) * sizeof(float);
 
   m->G = G;
-  const void* kernels[] = {m->persistent, (const void*)k_phase, (const void*)k_samp_a,
+  const void* kernels[] = {m->persistent[0], m->persistent[1], (const void*)k_phase, (const void*)k_samp_a,
                            (const void*)k_op};
   for (const void* kf : kernels) {
     const hipError_t e =
@@ -606,11 +609,12 @@ static int apply_layout(defer_gpu_model* m, uint32_t G) {
     if (e != hipSuccess)
       return fail(DEFER_GPU_E_HIP, "LDS attribute (%zu bytes): %s", m->lds_attn, hipGetErrorString(e));
   }
-  int occ = 0;
-  const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, m->persistent, BLOCK,
-                                                                     m->lds_bytes);
-  if (e != hipSuccess || occ < 1)
-    return fail(DEFER_GPU_E_HIP, "persistent kernel does not fit a CU (occupancy %d)", occ);
+  for (const void* kf : m->persistent) {
+    int occ = 0;
+    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kf, BLOCK, m->lds_bytes);
+    if (e != hipSuccess || occ < 1)
+      return fail(DEFER_GPU_E_HIP, "persistent kernel does not fit a CU (occupancy %d)", occ);
+  }
   return DEFER_GPU_OK;
 }
 
@@ -1152,7 +1156,8 @@ static int run_launch(defer_gpu_cache* c, RunDesc r, bool force_eager) {
       const Args* a = c->d_args;
       const RunDesc* dr = c->d_run;
       void* params[] = {&a, &dr};
-      const hipError_t e = hipLaunchCooperativeKernel(m->persistent, dim3(m->G), dim3(BLOCK), params,
+      const hipError_t e = hipLaunchCooperativeKernel(m->persistent[r.temperature != 0.0f], dim3(m->G),
+                                                      dim3(BLOCK), params,
                                                       (unsigned)m->lds_bytes, s);
       if (e != hipSuccess) {
         // Refused at launch (nothing ran): the device grants cooperative

@@ -44,7 +44,11 @@ __device__ __forceinline__ bool is_stop(const RunDesc& r, uint32_t tok) {
 }
 
 // Every op of a run in one launch. Every workgroup samples (same inputs, same
-// code, same token), so no broadcast is needed.
+// code, same token), so no broadcast is needed. RANDOM: the run samples at a
+// temperature above 0 (the host launches the instance that matches the run's
+// temperature); the greedy instance holds none of the random sampler's code,
+// whose registers would otherwise crowd the forward's.
+template <bool RANDOM>
 __global__ __launch_bounds__(BLOCK) void k_persistent(const Args* __restrict__ ap,
                                                       const RunDesc* __restrict__ run) {
   const Args& a = *ap;
@@ -66,9 +70,9 @@ __global__ __launch_bounds__(BLOCK) void k_persistent(const Args* __restrict__ a
   for (; i < r.n_ops; ++i) {
     uint32_t tok;
     if (i >= r.sample_from) {
-      const uint32_t word = r.temperature != 0.0f ? cptr(r.words)[i - r.sample_from] : 0u;
-      const uint32_t gsum = r.samp_tag0 + (i - r.sample_from);
-      if (r.temperature != 0.0f) {
+      if constexpr (RANDOM) {
+        const uint32_t word = cptr(r.words)[i - r.sample_from];
+        const uint32_t gsum = r.samp_tag0 + (i - r.sample_from);
         float m;
         uint32_t bi;
         if (!sample_stage_a(a, tick, gsum, r.temperature, wg, G, s, &m, &bi)) break;
@@ -111,5 +115,7 @@ __global__ __launch_bounds__(BLOCK) void k_persistent(const Args* __restrict__ a
   // Staged loads of a layer that will not run land before the wave ends.
   if (sg.on && sg.loader) stage_wait(0);
 }
+template __global__ void k_persistent<false>(const Args* __restrict__, const RunDesc* __restrict__);
+template __global__ void k_persistent<true>(const Args* __restrict__, const RunDesc* __restrict__);
 
 }  // namespace DG_NS
