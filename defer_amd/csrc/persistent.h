@@ -96,7 +96,22 @@ __global__ __launch_bounds__(BLOCK) void k_persistent(const Args* __restrict__ a
     } else {
       tok = cptr(r.tokens)[i];
     }
-    if (!forward_all(a, tok, pos, tick, wg, G, s, sg)) break;
+    if constexpr (RANDOM) {
+      // The forward's LDS layout and stager formed afresh per token from
+      // values the optimiser cannot see through, so nothing derived from
+      // them is held across the sampler (whose registers would push it to
+      // scratch, reloaded inside the forward).
+      Dims dl = a.d;
+      uint32_t wgt = wg;
+      asm volatile("" : "+s"(dl.lds_vec), "+s"(dl.lds_vec2), "+s"(dl.lds_scr), "+s"(dl.lds_stg),
+                   "+s"(dl.lds_pub), "+s"(wgt));
+      extern __shared__ float lds_raw[];
+      const Lds sf = lds_layout(lds_raw, dl);
+      const Stager sgt = make_stager(a, sf, wgt, G, a.d.lds_stg != 0);
+      if (!forward_all(a, tok, pos, tick, wgt, G, sf, sgt)) break;
+    } else if (!forward_all(a, tok, pos, tick, wg, G, s, sg)) {
+      break;
+    }
     ++pos;
     ++tick;
     if (r.ring && r.mode == RUN_GENERATE && wg == 0 && threadIdx.x == 0) ring_commit(r.ring, i, tok);
