@@ -678,5 +678,9 @@ def main() -> int:
 
 if __name__ == "__main__":
     rc = main()
+    if "defer_amd.gpu" in sys.modules and "torch" not in sys.modules:
+        # Every handle is closed: release the device (the runtime's queues,
+        # the cooperative one included) before the interpreter exits.
+        sys.modules["defer_amd.gpu"].shutdown()
     if rc:
         sys.exit(rc)

@@ -77,6 +77,10 @@ static hipError_t counted_host_malloc(void** p, size_t n, unsigned flags) {
 }
 extern "C" uint64_t defer_gpu_allocation_count(void) { return g_allocations.load(std::memory_order_relaxed); }
 
+// Live models and caches, and the devices models were made on (a bit each):
+// defer_gpu_shutdown resets only those devices, and only once nothing is live.
+static std::atomic<uint64_t> g_live_models{0}, g_live_caches{0}, g_devices_used{0};
+
 // ------------------------------------------------------------------ kernels
 
 #include "persistent.h"
@@ -632,6 +636,7 @@ extern "C" int defer_gpu_model_create(const defer_gpu_config* cfg, const float* 
     if (!tensors[i]) return fail(DEFER_GPU_E_INVALID, "tensor %zu is null", i);
 
   defer_gpu_model* m = new defer_gpu_model();
+  ++g_live_models;
   m->cfg = *cfg;
   Dims& d = m->d;
   d.h = cfg->hidden_size;
@@ -661,6 +666,7 @@ extern "C" int defer_gpu_model_create(const defer_gpu_config* cfg, const float* 
   };
   hipError_t e = hipGetDevice(&m->device);
   if (e != hipSuccess) return cleanup(fail(DEFER_GPU_E_HIP, "hipGetDevice: %s", hipGetErrorString(e)));
+  if (m->device >= 0 && m->device < 64) g_devices_used |= 1ull << m->device;
   hipDeviceProp_t prop;
   e = hipGetDeviceProperties(&prop, m->device);
   if (e != hipSuccess)
@@ -856,6 +862,7 @@ extern "C" void defer_gpu_model_destroy(defer_gpu_model* m) {
   if (m->ev1) (void)hipEventDestroy(m->ev1);
   if (m->stream) (void)hipStreamDestroy(m->stream);
   delete m;
+  --g_live_models;
 }
 
 extern "C" int defer_gpu_model_set_exec(defer_gpu_model* m, uint32_t mode) {
@@ -884,6 +891,7 @@ static int cache_alloc(const defer_gpu_model* m, uint32_t cap, defer_gpu_cache* 
   const Dims& d = m->d;
   c->m = m;
   ++const_cast<defer_gpu_model*>(m)->n_caches;
+  ++g_live_caches;
   c->cap = cap;
   const size_t kvn = (size_t)d.L * d.nkv * cap * d.kvs;
   HIP_TRY(counted_malloc(&c->kc, kvn * sizeof(float)));
@@ -942,6 +950,7 @@ static int sync_args(defer_gpu_cache* c) {
 
 static void cache_free(defer_gpu_cache* c) {
   if (!c) return;
+  --g_live_caches;  // every cache_free follows a cache_alloc
   if (c->m) --const_cast<defer_gpu_model*>(c->m)->n_caches;
   if (c->m && c->m->stream) (void)hipStreamSynchronize(c->m->stream);
   if (c->graph) (void)hipGraphExecDestroy(c->graph);
@@ -1590,6 +1599,29 @@ static int scratch_on(int device, uint32_t** out) {
     g_scratch[device] = p;
   }
   *out = g_scratch[device];
+  return DEFER_GPU_OK;
+}
+
+// Process teardown: every device a model was made on is synchronised and
+// reset (hipDeviceReset), releasing the HIP runtime's queues, including the
+// one it keeps for cooperative launches, while the process is still whole
+// rather than in the runtime's exit handlers.
+extern "C" int defer_gpu_shutdown(void) {
+  const uint64_t nm = g_live_models.load(), nc = g_live_caches.load();
+  if (nm || nc)
+    return fail(DEFER_GPU_E_INVALID, "%llu models and %llu caches are still live: destroy them first",
+                (unsigned long long)nm, (unsigned long long)nc);
+  int cur = 0;
+  HIP_TRY(hipGetDevice(&cur));
+  const uint64_t used = g_devices_used.exchange(0);
+  for (int dev = 0; dev < 64; ++dev) {
+    if (!(used >> dev & 1u)) continue;
+    HIP_TRY(hipSetDevice(dev));
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(hipDeviceReset());
+    if (dev < STATIC_MAX_DEVICES) g_scratch[dev] = nullptr;  // the array may move once reloaded
+  }
+  HIP_TRY(hipSetDevice(cur));
   return DEFER_GPU_OK;
 }
 

@@ -133,6 +133,8 @@ def lib() -> ctypes.CDLL:
     L.defer_gpu_last_error.restype = ctypes.c_char_p
     L.defer_gpu_allocation_count.argtypes = []
     L.defer_gpu_allocation_count.restype = ctypes.c_uint64
+    L.defer_gpu_shutdown.argtypes = []
+    L.defer_gpu_shutdown.restype = ctypes.c_int
     L.defer_gpu_last_device_ms.argtypes = [vp]
     L.defer_gpu_last_device_ms.restype = ctypes.c_double
     L.defer_gpu_model_set_batching.argtypes = [vp, u32]
@@ -172,6 +174,13 @@ def _ptr(a: Optional[np.ndarray]):
 def allocation_count() -> int:
     """Device and pinned host allocations the library has made so far."""
     return int(lib().defer_gpu_allocation_count())
+
+
+def shutdown() -> None:
+    """Synchronise and reset every device the library made a model on, once
+    every model and cache is closed (raises DeferGpuError otherwise). The reset
+    frees every allocation of the process on those devices: call it last."""
+    _check(lib().defer_gpu_shutdown())
 
 
 def tensor_count(cfg: Config) -> int:

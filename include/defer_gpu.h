@@ -155,6 +155,16 @@ typedef int (*defer_gpu_token_fn)(void* user, uint32_t index, uint32_t token);
  * to show that defer_gpu_generate_static allocates nothing). */
 uint64_t defer_gpu_allocation_count(void);
 
+/* Process teardown (no counterpart in the reference, whose CPU path holds no
+ * device state): once every model and cache is destroyed, synchronises and
+ * resets (hipDeviceReset) each device the library made a model on, so the HIP
+ * runtime's queues are released before the process exits rather than in the
+ * runtime's exit handlers. DEFER_GPU_E_INVALID while any handle is live. The
+ * reset frees every allocation of the process on those devices, the library's
+ * or not: call it last, when nothing else in the process uses them. The
+ * library may be used again afterwards. */
+int defer_gpu_shutdown(void);
+
 /* defer_gpu_generate with on_token (nullable) called per committed token. */
 int defer_gpu_generate_cb(const defer_gpu_model* m, defer_gpu_cache* c, uint32_t max_tokens,
                           float temperature, const uint32_t* rng_words, const uint32_t* stop,
