@@ -1724,29 +1724,24 @@ __device__ __forceinline__ bool load_tagged(const u64* const (&ptr)[N], uint32_t
   return true;
 }
 
-// The block-wide approximate exclusive prefix of the chunk sums A (double
-// partials, any fixed order), as floats in pre. Thread t owns a contiguous
-// run of chunks.
-__device__ __forceinline__ void approx_prefix(const float* A, float* pre, uint32_t nvc, double* dred) {
+// The block-wide approximate exclusive prefix of the chunk sums A (float
+// partials in a fixed tree: a few roundings of 2^-24, far inside the
+// guesses' margin), in pre. Thread t owns a contiguous run of chunks.
+__device__ __forceinline__ void approx_prefix(const float* A, float* pre, uint32_t nvc, float* wred) {
   const uint32_t lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
   const uint32_t cpt = (nvc + BLOCK - 1) / BLOCK;
   const uint32_t ca = min(threadIdx.x * cpt, nvc), cb = min(ca + cpt, nvc);
-  double own = 0.0;
-  for (uint32_t c = ca; c < cb; ++c) own += (double)A[c];
-  double incl = own;
-#pragma unroll
-  for (uint32_t o = 1; o < WAVE; o <<= 1) {
-    const double y = __shfl_up(incl, o);
-    if (lane >= o) incl += y;
-  }
+  float own = 0.0f;
+  for (uint32_t c = ca; c < cb; ++c) own += A[c];
+  const float incl = wave_scan_f32(own);
   __syncthreads();
-  if (lane == WAVE - 1) dred[wave] = incl;
+  if (lane == WAVE - 1) wred[wave] = incl;
   __syncthreads();
-  double p = incl - own;
-  for (uint32_t w = 0; w < wave; ++w) p += dred[w];
+  float p = incl - own;
+  for (uint32_t w = 0; w < wave; ++w) p += wred[w];
   for (uint32_t c = ca; c < cb; ++c) {
-    pre[c] = (float)p;
-    p += (double)A[c];
+    pre[c] = p;
+    p += A[c];
   }
   __syncthreads();
 }
@@ -1778,14 +1773,31 @@ __device__ __forceinline__ bool publish_summaries(const Args& a, u64* dst, uint3
   const uint32_t nown = wg < nvc ? (nvc - wg + G - 1) / G : 0;
   // The 135M kernel runs only at its full grid, where the owned p_v fit.
   const bool lds_p = STAGED_ONLY || (own_in_lds && nown <= OWN_MAX);
-  constexpr uint32_t B = 4;  // chunks per wave in flight
+  // chunk k's summary word from its terms pk (one wave, a lane per term)
+  auto one = [&](uint32_t k, float pk) {
+    const uint32_t c = wg + G * k;
+    bool change;
+    const int E = chunk_guess(L, c, FIND ? inv : 1.0f, &change);
+    const bool past = FIND && (double)L.pre[c] * inv * (1.0 - SAMP_MARGIN) > (double)r;
+    uint32_t w = sum_word(E, SUM_EVENT);
+    if (!change && !past) {
+      const uint32_t v = c * VCHUNK + lane;
+      const float x = v < V ? (FIND ? pk * inv : pk) : 0.0f;
+      const GridTerm g = grid_term(x, E);
+      const uint32_t tot = lane_u32(wave_scan_u32(g.big ? 0u : g.rho), 63);
+      const bool flag = __ballot(g.big || g.tie) != 0;
+      w = sum_word(E, flag ? SUM_EVENT : tot);
+    }
+    if (lane == 0) mb_put(dst + c, __uint_as_float(w), gsum);
+  };
   bool ok = true;
-  for (uint32_t k0 = wave * B; wave < NWA && k0 < nown; k0 += NWA * B) {
-    float p[B];
-    if (lds_p) {
-#pragma unroll
-      for (uint32_t e = 0; e < B; ++e) p[e] = L.ownp[min(k0 + e, nown - 1) * VCHUNK + lane];
-    } else {
+  if (lds_p) {
+    // from LDS: one chunk per wave at a time, the chunks spread over the waves
+    for (uint32_t k = wave; wave < NWA && k < nown; k += NWA) one(k, L.ownp[k * VCHUNK + lane]);
+  } else {
+    constexpr uint32_t B = 4;  // chunks per wave in flight from the mailbox
+    for (uint32_t k0 = wave * B; wave < NWA && k0 < nown; k0 += NWA * B) {
+      float p[B];
       const u64* ptr[B];
 #pragma unroll
       for (uint32_t e = 0; e < B; ++e) ptr[e] = a.mb_p + min((wg + G * min(k0 + e, nown - 1)) * VCHUNK + lane, V - 1);
@@ -1793,25 +1805,9 @@ __device__ __forceinline__ bool publish_summaries(const Args& a, u64* dst, uint3
         ok = false;
         break;
       }
-    }
 #pragma unroll
-    for (uint32_t e = 0; e < B; ++e) {
-      const uint32_t k = k0 + e;
-      if (k >= nown) break;
-      const uint32_t c = wg + G * k;
-      bool change;
-      const int E = chunk_guess(L, c, FIND ? inv : 1.0f, &change);
-      const bool past = FIND && (double)L.pre[c] * inv * (1.0 - SAMP_MARGIN) > (double)r;
-      uint32_t w = sum_word(E, SUM_EVENT);
-      if (!change && !past) {
-        const uint32_t v = c * VCHUNK + lane;
-        const float x = v < V ? (FIND ? p[e] * inv : p[e]) : 0.0f;
-        const GridTerm g = grid_term(x, E);
-        const uint32_t tot = lane_u32(wave_scan_u32(g.big ? 0u : g.rho), 63);
-        const bool flag = __ballot(g.big || g.tie) != 0;
-        w = sum_word(E, flag ? SUM_EVENT : tot);
-      }
-      if (lane == 0) mb_put(dst + c, __uint_as_float(w), gsum);
+      for (uint32_t e = 0; e < B; ++e)
+        if (k0 + e < nown) one(k0 + e, p[e]);
     }
   }
   if (!ok && lane == 0) s.ctl->abort_seen = 1;
@@ -1860,13 +1856,18 @@ __device__ __forceinline__ bool fetch_events(const Args& a, uint32_t gsum, float
     }
     return ch;
   };
+  // Round 0: each chunk's change flag, formed once into L.sw (free until the
+  // summary words arrive), read for the chunk and its neighbours.
   auto wanted = [&](uint32_t c) {
     if (past(c)) return false;
-    if (round == 0) return change(c) || (c > 0 && change(c - 1)) || (c + 1 < nvc && change(c + 1));
+    if (round == 0) return L.sw[c] != 0 || (c > 0 && L.sw[c - 1] != 0) || (c + 1 < nvc && L.sw[c + 1] != 0);
     return L.slot[c] == NO_SLOT && sum_total(L.sw[c]) == SUM_EVENT;
   };
   if (round == 0) {
-    for (uint32_t c = threadIdx.x; c < nvc; c += BLOCK) L.slot[c] = NO_SLOT;
+    for (uint32_t c = ca; c < cb; ++c) {
+      L.slot[c] = NO_SLOT;
+      L.sw[c] = change(c) ? 1u : 0u;
+    }
     __syncthreads();
   }
   const uint32_t base_n = round == 0 ? 0u : *L.nev;
@@ -2021,65 +2022,49 @@ __device__ __forceinline__ void chunk_exact(float x, uint32_t n, float r, float&
   }
 }
 
-// chunk_exact for a fetched chunk whose running sum starts in the grid E
-// its prefix words wE (grid E) and wE1 (grid E + 1) were formed for: the
-// terms up to the first that leaves E (or is a tie) are one integer step,
-// that term one float addition, and where the sum lands in E + 1 the rest up
-// to the next such term another integer step. Returns the lane from which
-// chunk_exact must go on (64 when the chunk is done).
+// The terms of a fetched chunk from lane j0 on, added to the running sum s
+// with the chunk's prefix words in grid E (wE) and grid E + 1 (wE1): while s
+// lies in one of those two grids, the terms up to the next that leaves it
+// (or is a tie there) are one integer step and that term one float
+// addition, as often as the chunk needs. Returns the lane from which
+// chunk_exact must go on once s is in neither grid (64 when the chunk is
+// done).
 template <bool FIND>
-__device__ __forceinline__ uint32_t chunk_fast(uint32_t wE, uint32_t wE1, float x, uint32_t n, int E, float r,
-                                               float& s, uint32_t& hit) {
+__device__ __forceinline__ uint32_t chunk_words(uint32_t wE, uint32_t wE1, float x, uint32_t n, int E, float r,
+                                                float& s, uint32_t& hit, uint32_t j0 = 0) {
   const uint32_t lane = threadIdx.x % WAVE;
   hit = 64;
-  const uint32_t k = grid_units(s, E);
-  const uint32_t P = wE & PW_P;
-  const bool bad = lane < n && ((wE & PW_BAD) || k + P - ((wE & PW_UP) ? 1u : 0u) >= GRID_TOP);
-  const uint32_t jb = first_lane(__ballot(bad));
-  if (FIND) {
-    const uint32_t jh = first_lane(__ballot(lane < jb && lane < n && r < __builtin_ldexpf((float)(k + P), E)));
-    if (jh < 64) {
-      hit = jh;
-      s = __builtin_ldexpf((float)(k + lane_u32(P, jh)), E);
+  for (;;) {
+    const int Ec = grid_of(s);
+    if (Ec != E && Ec != E + 1) return j0;
+    const uint32_t w = Ec == E ? wE : wE1;
+    const uint32_t k = grid_units(s, Ec);
+    const uint32_t P = w & PW_P;
+    const uint32_t Q = P - (j0 ? lane_u32(P, j0 - 1) : 0u);  // from lane j0 on
+    const bool act = lane >= j0 && lane < n;
+    const bool bad = act && ((w & PW_BAD) || k + Q - ((w & PW_UP) ? 1u : 0u) >= GRID_TOP);
+    const uint32_t jb = first_lane(__ballot(bad));
+    if (FIND) {
+      const uint32_t jh = first_lane(__ballot(act && lane < jb && r < __builtin_ldexpf((float)(k + Q), Ec)));
+      if (jh < 64) {
+        hit = jh;
+        s = __builtin_ldexpf((float)(k + lane_u32(Q, jh)), Ec);
+        return 64;
+      }
+    }
+    if (jb >= 64) {  // lanes at or past n hold zero terms
+      s = __builtin_ldexpf((float)(k + lane_u32(Q, 63)), Ec);
       return 64;
     }
-  }
-  if (jb >= 64) {
-    s = __builtin_ldexpf((float)(k + lane_u32(P, 63)), E);
-    return 64;
-  }
-  s = __builtin_ldexpf((float)(k + (jb ? lane_u32(P, jb - 1) : 0u)), E);
-  s = s + lane_f32(x, jb);
-  if (FIND && r < s) {
-    hit = jb;
-    return 64;
-  }
-  if (jb + 1 >= n) return 64;
-  if (grid_of(s) != E + 1) return jb + 1;
-  const uint32_t k2 = grid_units(s, E + 1);
-  const uint32_t Q = (wE1 & PW_P) - lane_u32(wE1 & PW_P, jb);
-  const bool after = lane > jb && lane < n;
-  const bool bad2 = after && ((wE1 & PW_BAD) || k2 + Q - ((wE1 & PW_UP) ? 1u : 0u) >= GRID_TOP);
-  const uint32_t jb2 = first_lane(__ballot(bad2));
-  if (FIND) {
-    const uint32_t jh = first_lane(__ballot(after && lane < jb2 && r < __builtin_ldexpf((float)(k2 + Q), E + 1)));
-    if (jh < 64) {
-      hit = jh;
-      s = __builtin_ldexpf((float)(k2 + lane_u32(Q, jh)), E + 1);
+    s = __builtin_ldexpf((float)(k + (jb > j0 ? lane_u32(Q, jb - 1) : 0u)), Ec);
+    s = s + lane_f32(x, jb);
+    if (FIND && r < s) {
+      hit = jb;
       return 64;
     }
+    j0 = jb + 1;
+    if (j0 >= n) return 64;
   }
-  if (jb2 >= 64) {
-    s = __builtin_ldexpf((float)(k2 + lane_u32(Q, 63)), E + 1);
-    return 64;
-  }
-  s = __builtin_ldexpf((float)(k2 + lane_u32(Q, jb2 - 1)), E + 1);
-  s = s + lane_f32(x, jb2);
-  if (FIND && r < s) {
-    hit = jb2;
-    return 64;
-  }
-  return jb2 + 1;
 }
 
 // Segments of the summary words in L.sw: a segment is a maximal run of
@@ -2151,11 +2136,46 @@ __device__ __forceinline__ void build_segments(const SampLds& L, uint32_t nvc) {
   __syncthreads();
 }
 
+// One chunk summed term by term at the running sum: from its fetch slot sc
+// with the prefix words (the sum starting in the grid they were formed for
+// or the next), else from the mailbox. FIND: *hit the lane where r falls.
+template <bool FIND>
+__device__ __forceinline__ bool walk_chunk(const Args& a, uint32_t gsum, float inv, float r, const SampLds& L,
+                                           const Lds& s, uint32_t c, uint32_t sc, uint32_t V, float& sum,
+                                           uint32_t& hit) {
+  const uint32_t lane = threadIdx.x % WAVE;
+  const uint32_t base = c * VCHUNK, n = min(VCHUNK, V - base);
+  float p;
+  uint32_t from = 0;  // the lane chunk_exact goes on from
+  hit = 64;
+  if (sc != NO_SLOT) {
+    p = L.evp[sc * VCHUNK + lane];
+    const uint32_t w0s = L.pw[(2 * sc) * VCHUNK + lane], w1s = L.pw[(2 * sc + 1) * VCHUNK + lane];
+    const int Es = L.slE[sc], Eg = grid_of(sum);
+    const float xf = lane < n ? (FIND ? p * inv : p) : 0.0f;
+    if (Eg == Es || Eg == Es + 1) from = chunk_words<FIND>(w0s, w1s, xf, n, Es, r, sum, hit);
+  } else {
+    const u64* ptr[1] = {a.mb_p + base + min(lane, n - 1)};
+    float t[1];
+    if (!load_tagged<1>(ptr, gsum, t, a.st, s.ctl)) return false;
+    p = t[0];
+  }
+  const float x = lane < n ? (FIND ? p * inv : p) : 0.0f;
+  if (hit == 64 && from < n) chunk_exact<FIND>(x, n, r, sum, hit, from);
+  return true;
+}
+
 // One walk over the summary words L.sw (wave 0; the block waits): the total
 // of the terms (FIND false: *out = its bits) or the index sample_token
-// returns (FIND true). Windows of 64 summaries: the usable prefix of a window
-// is one integer sum, its first unusable chunk goes term by term from LDS
-// (fetched) or the mailbox.
+// returns (FIND true). The expected path visits the segment starts in order:
+// a segment (its grid the running sum's, no crossing inside) is one integer
+// step, a term-by-term chunk goes through walk_chunk. The path is read a
+// window of 64 chunks at a time into registers (the starts as a ballot, each
+// start's summary, segment total and fetch slot in a lane), so a step reads
+// no LDS but the chunk's terms. Where a step does not hold (a spacing guess
+// off, a segment whose total overflows the grid, r inside a segment) the
+// walk goes on from that chunk chunk by chunk: windows of 64 summaries whose
+// usable prefix is one integer sum, the first unusable chunk term by term.
 template <bool FIND>
 __device__ __forceinline__ bool exact_walk(const Args& a, uint32_t gsum, float inv, float r, const SampLds& L,
                                            const Lds& s, uint32_t* out) {
@@ -2166,18 +2186,54 @@ __device__ __forceinline__ bool exact_walk(const Args& a, uint32_t gsum, float i
     float sum = 0.0f;
     uint32_t found = NO_INDEX;
     bool ok = true;
-    uint32_t c0 = 0;
-    while (c0 < nvc) {
+    uint32_t c0 = nvc;  // where the chunk-by-chunk walk starts (nvc: not needed)
+    for (uint32_t wb = 0; wb < nvc; wb += WAVE) {
+      const uint32_t c = wb + lane;
+      const bool in = c < nvc;
+      const uint32_t vW = in ? L.sw[c] : 0u;
+      const uint32_t vT = in ? L.PI[c] : 0u;
+      const uint32_t vS = in ? L.slot[c] : NO_SLOT;
+      unsigned long long starts = __ballot(in && (c == 0 || L.nxt[c - 1] == c));
+      bool stop = false;
+      while (starts) {
+        const uint32_t j = first_lane(starts);
+        starts &= starts - 1;
+        const uint32_t cc = wb + j;
+        const uint32_t w = lane_u32(vW, j);
+        const int E = grid_of(sum);
+        const uint32_t k = grid_units(sum, E);
+        if (sum_total(w) != SUM_EVENT) {
+          const uint32_t T = lane_u32(vT, j);
+          if (sum_grid(w) == E && T < GRID_TOP && k + T < GRID_TOP &&
+              !(FIND && r < __builtin_ldexpf((float)(k + T), E))) {
+            sum = __builtin_ldexpf((float)(k + T), E);
+            continue;
+          }
+          c0 = cc;
+          stop = true;
+          break;
+        }
+        uint32_t hit;
+        if (!walk_chunk<FIND>(a, gsum, inv, r, L, s, cc, lane_u32(vS, j), V, sum, hit)) {
+          ok = false;
+          stop = true;
+          break;
+        }
+        if (FIND && hit < 64) {
+          found = cc * VCHUNK + hit;
+          stop = true;
+          break;
+        }
+      }
+      if (stop) break;
+    }
+    while (ok && found == NO_INDEX && c0 < nvc) {
       const int E = grid_of(sum);
       const uint32_t k = grid_units(sum, E);
-      // one round of reads for c0: its summary, segment end, the segment's
-      // total from c0 on, and its fetch slot
       const uint32_t w0 = L.sw[c0];
       const uint32_t e = L.nxt[c0];
       const uint32_t T = L.PI[c0];
-      const uint32_t sl = L.slot[c0];
-      const bool exact_here = sum_total(w0) == SUM_EVENT;  // term by term, no window scan
-      if (!exact_here && sum_grid(w0) == E && T < GRID_TOP && k + T < GRID_TOP &&
+      if (sum_total(w0) != SUM_EVENT && sum_grid(w0) == E && T < GRID_TOP && k + T < GRID_TOP &&
           !(FIND && r < __builtin_ldexpf((float)(k + T), E))) {
         // the rest of c0's segment as one integer step
         sum = __builtin_ldexpf((float)(k + T), E);
@@ -2185,7 +2241,7 @@ __device__ __forceinline__ bool exact_walk(const Args& a, uint32_t gsum, float i
         continue;
       }
       uint32_t fb = 0;
-      if (!exact_here) {
+      if (sum_total(w0) != SUM_EVENT) {
         const uint32_t c = c0 + lane;
         const uint32_t w = c < nvc ? L.sw[c] : SUM_EVENT;
         const uint32_t I = sum_total(w);
@@ -2200,36 +2256,13 @@ __device__ __forceinline__ bool exact_walk(const Args& a, uint32_t gsum, float i
         c0 += fb;
       }
       if (fb < 64 && c0 < nvc) {
-        const uint32_t base = c0 * VCHUNK, n = min(VCHUNK, V - base);
-        const uint32_t sc = fb ? L.slot[c0] : sl;  // a window stop moved c0
-        float p;
-        uint32_t from = 0;  // the lane chunk_exact goes on from
-        uint32_t hit = 64;
-        if (sc != NO_SLOT) {
-          p = L.evp[sc * VCHUNK + lane];
-          const uint32_t w0s = L.pw[(2 * sc) * VCHUNK + lane], w1s = L.pw[(2 * sc + 1) * VCHUNK + lane];
-          const int Es = L.slE[sc], Eg = grid_of(sum);
-          const float xf = lane < n ? (FIND ? p * inv : p) : 0.0f;
-          if (Es == Eg) {
-            from = chunk_fast<FIND>(w0s, w1s, xf, n, Es, r, sum, hit);
-          } else if (Es + 1 == Eg) {
-            // the sum starts one spacing above the guess: grid E + 1's words
-            // serve the first step, chunk_exact the rest after a change
-            from = chunk_fast<FIND>(w1s, PW_BAD, xf, n, Eg, r, sum, hit);
-          }
-        } else {
-          const u64* ptr[1] = {a.mb_p + base + min(lane, n - 1)};
-          float t[1];
-          if (!load_tagged<1>(ptr, gsum, t, a.st, s.ctl)) {
-            ok = false;
-            break;
-          }
-          p = t[0];
+        uint32_t hit;
+        if (!walk_chunk<FIND>(a, gsum, inv, r, L, s, c0, L.slot[c0], V, sum, hit)) {
+          ok = false;
+          break;
         }
-        const float x = lane < n ? (FIND ? p * inv : p) : 0.0f;
-        if (hit == 64 && from < n) chunk_exact<FIND>(x, n, r, sum, hit, from);
         if (FIND && hit < 64) {
-          found = base + hit;
+          found = c0 * VCHUNK + hit;
           break;
         }
         ++c0;
@@ -2278,7 +2311,7 @@ __device__ __forceinline__ bool sample_exact(const Args& a, uint32_t gsum, float
   const SampLds L = samp_lds(s, nvc, a.d.lds_vec);
   // A2
   if (!poll_gather<2>(gather_vec(a.mb_vsum, nvc, gsum, L.A), NWA, a.st, s.ctl)) return false;
-  approx_prefix(L.A, L.pre, nvc, L.dred);
+  approx_prefix(L.A, L.pre, nvc, reinterpret_cast<float*>(L.dred));
   if (!publish_summaries<false>(a, a.mb_psum, gsum, 1.0f, 0.0f, wg, G, own_in_lds, L, s)) return false;
   if (!fetch_events<false>(a, gsum, 1.0f, 0.0f, 0, L, s)) return false;
   // W1
