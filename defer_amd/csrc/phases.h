@@ -1940,15 +1940,33 @@ __device__ __forceinline__ void chunk_exact(float x, uint32_t n, float r, float&
   hit = 64;
   int E = grid_of(s);
   GridTerm g = grid_term(x, E);
-  // Where several terms leave the running sum's region at once (the first
-  // chunk, whose sum starts at 0), one float addition per term is cheaper
-  // than a restart per term.
-  if (__popcll(__ballot(lane >= jstart && lane < n && (g.big || g.tie))) >= 4) {
-    for (uint32_t j = jstart; j < n; ++j) {
-      s = s + lane_f32(x, j);
-      if (FIND && r < s) {
-        hit = j;
-        return;
+  // Where several terms leave the running sum's region at once, or the
+  // terms add up to several times the sum (the first chunk, whose sum starts
+  // at 0: a spacing change every doubling, and a tie is likely for a term
+  // not far below the sum's spacing), one float addition per term is
+  // cheaper than a restart per term. The terms are read into scalar
+  // registers 16 at a time, ahead of their additions, so the chain of
+  // additions waits on nothing else.
+  const float rest = lane_f32(wave_scan_f32(lane >= jstart && lane < n ? x : 0.0f), 63);
+  if (rest > 4.0f * s || __popcll(__ballot(lane >= jstart && lane < n && (g.big || g.tie))) >= 4) {
+    // Past n (and past lane 63) the batch adds zeros, which leave s as it is.
+    const float xm = lane < n ? x : 0.0f;
+    for (uint32_t j0 = jstart; j0 < n; j0 += 16) {
+      float t[16];
+#pragma unroll
+      for (uint32_t q = 0; q < 16; ++q) t[q] = j0 + q < WAVE ? lane_f32(xm, min(j0 + q, WAVE - 1)) : 0.0f;
+      const float s0 = s;
+#pragma unroll
+      for (uint32_t q = 0; q < 16; ++q) s = s + t[q];
+      if (FIND && r < s) {  // r falls in this batch: the same additions, checked one by one
+        s = s0;
+        for (uint32_t q = 0; q < 16; ++q) {
+          s = s + t[q];
+          if (r < s) {
+            hit = j0 + q;
+            return;
+          }
+        }
       }
     }
     return;
