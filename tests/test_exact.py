@@ -79,6 +79,38 @@ def test_oracle_sample_terms_closed_forms():
     assert tok == 0 and m == 0.0
 
 
+def test_oracle_sample_terms_against_numpy_sequential_accumulate():
+    """The oracle's two sequential f32 sums (total, then the CDF of p * inv)
+    against numpy's float32 add.accumulate, which adds strictly in index
+    order: the total's bits and the index (first r < cdf, else the last
+    positive q) agree on term sequences with ties, subnormal terms, zeros and
+    a few large terms. A tree or pairwise order fails this on most draws."""
+    rng = np.random.default_rng(5)
+    cases = [
+        rng.random(49152, dtype=np.float32),
+        np.exp(rng.normal(0.0, 2.0, 20000)).astype(np.float32),
+        (rng.integers(1, 8, 5000) * np.float32(0.125)).astype(np.float32),  # exact ties likely
+        np.where(rng.random(3000) < 0.9, 0.0, rng.random(3000)).astype(np.float32),
+        (rng.random(2000) * np.float32(1e-40)).astype(np.float32),  # subnormal terms
+    ]
+    for p in cases:
+        total = np.add.accumulate(p, dtype=np.float32)[-1]
+        inv = np.float32(1.0) / total
+        q = (p * inv).astype(np.float32)
+        cdf = np.add.accumulate(q, dtype=np.float32)
+        for word in rng.integers(0, 2 ** 32, 40, dtype=np.uint64):
+            r = np.float32((int(word) >> 8) * 2.0 ** -24)
+            above = np.nonzero(r < cdf)[0]
+            if above.size:
+                want = int(above[0])
+            else:
+                pos = np.nonzero(q > 0)[0]
+                want = int(pos[-1]) if pos.size else 0
+            tok, tot = O.sample_terms(p, int(word))
+            assert tot.view(np.uint32) == total.view(np.uint32)
+            assert tok == want
+
+
 def test_oracle_expf_is_libm():
     x = np.array([0.0, -1.0, -0.5, -87.5, -103.9, -104.0, 1.0], np.float32)
     y = O.expf(x)
