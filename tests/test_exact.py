@@ -201,11 +201,16 @@ def test_walker_against_sequential_loops():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("V,T", [(49152, 0.7), (49152, 1.5), (128256, 0.8), (300, 0.3)])
-def test_sampler_equals_sample_token_on_wide_logits(V, T):
+@pytest.mark.parametrize("V,T,quant", [(49152, 0.7, 0.0), (49152, 1.5, 0.0), (128256, 0.8, 0.0), (300, 0.3, 0.0),
+                                        (49152, 0.02, 0.0), (49152, 50.0, 0.0), (49152, 1.0, 0.25)])
+def test_sampler_equals_sample_token_on_wide_logits(V, T, quant):
     """Logits shaped like the benchmark models' (N(0, 0.5)), set on a cache,
     sampled by the device with 200 words: every token equals oracle
-    sample_token's. The model is the tiny one with its head resized to V."""
+    sample_token's. The model is the tiny one with its head resized to V.
+    T = 0.02 leaves a few terms and many subnormal or zero ones; T = 50 makes
+    the terms nearly equal (a total near V, long runs in each spacing);
+    logits rounded to multiples of `quant` repeat a few values of p, so
+    equal terms and ties in the running sums are common."""
     from defer_amd import gpu as G
     from defer_amd import synthetic
 
@@ -219,12 +224,14 @@ def test_sampler_equals_sample_token_on_wide_logits(V, T):
     n_bad = 0
     for trial in range(4):
         lg = rng.normal(0, 0.5, V).astype(np.float32)
+        if quant:
+            lg = (np.round(lg / quant) * quant).astype(np.float32)
         c.set_logits(lg)
         for word in rng.integers(0, 1 << 32, 50, dtype=np.uint64):
             tok = gm.sample(c, T, int(word))
             want = O.sample_token(lg, T, int(word))
             n_bad += tok != want
-    print(f"V={V} T={T}: 200 draws, {n_bad} differ from sample_token", flush=True)
+    print(f"V={V} T={T} quant={quant}: 200 draws, {n_bad} differ from sample_token", flush=True)
     assert n_bad == 0
     c.close()
     gm.close()
