@@ -140,9 +140,9 @@ def c1_step(model, prompt, H, wal_dir) -> tuple:
     wal.rs:241-250), inside the timed region as `defer run` times its
     generate loop with its appends (main.rs:261-303); the WAL is created
     before, as cmd_run creates it before run_generation. Returns (host
-    seconds of the two generate calls, device ms of their two launches,
-    tokens of A, tokens of B)."""
-    wall, dev, out = 0.0, 0.0, []
+    seconds of the two generate calls, device ms of their two launches as a
+    (greedy, sampled) pair, tokens of A, tokens of B)."""
+    wall, dev, out = 0.0, [], []
     for k, T in enumerate((0.0, TEMPERATURE)):
         s = H.Session(model, H.seed_from_u64(42), T, capacity=512)
         s.prompt(prompt)
@@ -151,12 +151,12 @@ def c1_step(model, prompt, H, wal_dir) -> tuple:
         t0 = time.perf_counter()
         toks = s.generate(128, wal=wal)
         wall += time.perf_counter() - t0
-        dev += model.last_device_ms()
+        dev.append(model.last_device_ms())
         wal.close()
         assert len(toks) == 128
         out.append(toks)
         s.close()
-    return wall, dev, out[0], out[1]
+    return wall, tuple(dev), out[0], out[1]
 
 
 def sessions_workload(args) -> int:
@@ -613,11 +613,13 @@ def main() -> int:
     wal_dir = tempfile.mkdtemp(prefix="defer-bench-")
     for _ in range(args.warmup):
         ref = c1_step(model, prompt, H, wal_dir)[2:]
-    wall, dev = 0.0, 0.0
+    wall, dev, dev_g, dev_t = 0.0, 0.0, 0.0, 0.0
     for _ in range(args.steps):
         w, d, ta, tb = c1_step(model, prompt, H, wal_dir)
         wall += w
-        dev += d
+        dev += d[0] + d[1]
+        dev_g += d[0]
+        dev_t += d[1]
         if ref is not None and (ta, tb) != ref:
             raise SystemExit("decode is not repeatable: tokens differ between steps")
         ref = (ta, tb)
@@ -652,6 +654,8 @@ def main() -> int:
             "exec": args.exec,
             "us_per_token": round(wall / n_tok * 1e6, 1),
             "device_us_per_token": round(dev / n_tok * 1e3, 1),
+            "device_us_per_token_greedy": round(dev_g / (n_tok / 2) * 1e3, 1),
+            "device_us_per_token_sampled": round(dev_t / (n_tok / 2) * 1e3, 1),
             "weight_bytes_per_token": wbytes,
             "weight_roofline_tok_s": round(PEAK_GBS * 1e9 / wbytes, 1),
             "weight_roofline_frac": round(value * wbytes / (PEAK_GBS * 1e9), 4),
