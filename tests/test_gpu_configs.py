@@ -458,7 +458,14 @@ def test_lockstep_1b_independent_of_grid(gemm_cus):
         for c, p in zip(cs, prompts):
             gm.prompt(c, p)
         toks = [gm.step_batch(cs, 0.0) for _ in range(3)]
-        toks += [gm.step_batch(cs, 0.7, words[64 * i:64 * (i + 1)]) for i in range(2)]
+        for i in range(2):
+            ws = words[64 * i:64 * (i + 1)]
+            want = [O.sample_token(c.last_logits(), 0.7, int(wd)) for c, wd in zip(cs, ws)]
+            got = gm.step_batch(cs, 0.7, ws)
+            # the batched sampler (one workgroup per row, V = 128256) is
+            # sample_token on each row's own logits
+            assert [int(t) for t in got] == want
+            toks.append(got)
         results.append((toks, [bits(c.last_logits()).copy() for c in cs], cs[5].read(1)))
         for c in cs:
             c.close()
