@@ -150,9 +150,14 @@ int main(void) {
 
   printf("abi_test (static library): forward max|dlogit| %.3e, %u/64 draws differ from "
          "sample_token, greedy and replay %s\n", worst, differ, failures ? "FAILED" : "ok");
+  /* teardown: refused while a cache lives, then the device reset */
+  rc = defer_gpu_shutdown();
+  CHECK(rc == DEFER_GPU_E_INVALID, "shutdown with live handles gave %d", rc);
   defer_gpu_cache_destroy(r);
   defer_gpu_cache_destroy(c);
   defer_gpu_model_destroy(m);
+  rc = defer_gpu_shutdown();
+  CHECK(rc == DEFER_GPU_OK, "shutdown %d: %s", rc, defer_gpu_last_error());
   oracle_cache_destroy(oc2);
   oracle_cache_destroy(ocache);
   oracle_model_destroy(om);
